@@ -1,0 +1,30 @@
+"""CPU oracle for the speculative-decoding hot path -- TEST INFRASTRUCTURE ONLY.
+
+This package is a plain PyTorch-CPU restatement of the reference's decode path
+(the model forward with a shared KV cache and tree masks, the level-by-level
+tree drafter, greedy / sampling verification, KV compaction and the round
+loop). It exists to check the HIP path; it is never the thing measured or
+shipped. Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline``
+leg of ``bench.py`` may import it, and only as the checker / CPU baseline.
+
+How each part is pinned (so that a plausible mistake fails a check):
+
+* ``model``: layer math against the transformers ``LlamaForCausalLM`` in the
+  image (a library routine) in fp32 to 1e-5 (tests/test_oracle_model.py),
+  zero-init bridges against plain layer skipping, incremental cache against
+  the full forward, and tree masks against decoding each root->node path
+  alone (the reference's own invariants, tests/test_forward_pass.py:109-180).
+* ``engine``: greedy SD == autoregressive == HF ``generate`` for chain, tree,
+  pruned and deep-chain drafts; draft-vocab subsets and EOS; tree-shape
+  limits; the V=8 brute-force joint for sampling (tests/test_engine.py).
+  Tree pruning order and ``warp_probs`` boundaries are also pinned by small
+  hand-derived known-answer cases (tests/test_oracle_engine.py).
+* ``kernels``: per-kernel reference functions (tree attention with ancestor
+  lists, KV compaction, the bf16 rounding chains). Each is pinned against
+  the ``model`` forward (itself pinned to HF) or a closed form.
+
+Parity unpinned: none of the functions above is left without an independent
+check; sampled *trajectories* are compared distributionally only, because the
+HIP path draws from Philox4x32-10 while the reference draws from torch's CPU
+generator (the reference cannot be run here to record its streams).
+"""
