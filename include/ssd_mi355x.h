@@ -1,0 +1,161 @@
+/* C ABI of the MI355X (gfx950) speculative-decoding hot path: libssd_mi355x.so.
+ *
+ * Conventions
+ *  - Every pointer argument is a device pointer unless stated; bf16 tensors are passed as
+ *    uint16_t bit patterns; shapes are plain integers; strides are in elements.
+ *  - Every entry point enqueues work on `stream` and returns 0 on success, or a nonzero
+ *    code (1 bad argument, 2 beyond a compiled limit, 3 HIP runtime error) with a message
+ *    from ssd_last_error(). No entry point allocates device memory or synchronises the
+ *    host; workspaces are caller-provided.
+ *  - Thread-compatible: concurrent calls on different streams must not share buffers.
+ *
+ * The reference (yotamabramson/subnetwork-speculative-decoding) is pure Python/PyTorch;
+ * each function below replaces the PyTorch op call site cited beside it.
+ */
+#ifndef SSD_MI355X_H
+#define SSD_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+#if defined(__GNUC__) || defined(__clang__)
+#pragma GCC visibility push(default)
+#endif
+
+typedef struct ihipStream_t* hipStream_t;
+
+/* ------------------------------------------------------------------ library */
+const char* ssd_last_error(void);
+int ssd_abi_version(void);
+int ssd_device_arch(char* buf, int len); /* host buffer; gcnArchName of the current device */
+
+/* ------------------------------------------------------------ weight format
+ * Packs a row-major bf16 matrix W[N_src, K] (row stride ld) into MFMA tiles: tile (nb, kb) =
+ * rows row_map[16nb .. 16nb+16) x k [32kb, 32kb+32), 64 lanes x 8 bf16. row_map[N_packed]
+ * (device int32) names the source row of each packed row (-1 = zero row); it fuses q/k/v,
+ * interleaves gate/up and pairs rotary dims. Replaces holding nn.Linear weights as-is
+ * (ssd/models/subnetwork_draft.py:80-89 references HF modules). */
+int64_t ssd_packed_weight_elems(int N, int K);
+int ssd_pack_weight_bf16(const uint16_t* src, int64_t ld, int N_src, int K, const int32_t* row_map, int N_packed,
+                         uint16_t* dst, hipStream_t stream);
+
+/* ---------------------------------------------------------------- GEMMs
+ * Y = act(X W^T + bias) [+ residual] with bf16 rounding after each step; Y may alias residual.
+ * Replaces F.linear / nn.Linear at ssd/models/subnetwork_draft.py:243 (o_proj + residual),
+ * :349 (lm_head and vocab-subset head) and the bridge linears ssd/models/bridges.py:53-54,131-135.
+ * act: 0 none, 1 silu, 2 gelu, 3 relu. Batch-invariant: a row's result does not depend on M. */
+int ssd_gemm_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int N, int K, uint16_t* Y,
+                  int64_t ldy, const uint16_t* bias, int act, const uint16_t* residual, int64_t ldr,
+                  hipStream_t stream);
+
+/* Y[M, I] = silu(X Wg^T + bg) * (X Wu^T + bu), gate/up interleaved per 16-row tile.
+ * Replaces LlamaMLP's gate/up/act (modeling_llama MLP called at ssd/models/subnetwork_draft.py:245)
+ * and the swiglu bridge (ssd/models/bridges.py:57-65). */
+int ssd_gemm_swiglu_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int I, int K,
+                         uint16_t* Y, int64_t ldy, const uint16_t* bias_gate, const uint16_t* bias_up,
+                         hipStream_t stream);
+
+/* q/k/v projection + RoPE + KV-cache write, fused. Replaces ssd/models/subnetwork_draft.py:209-222
+ * (q/k/v_proj, rotate_half RoPE, KVCache.update at ssd/engine/kv_cache.py:32-43). Row m is at
+ * rotary position row_pos[m] (cos/sin tables [rope_rows, hd/2]) and writes cache slot row_slot[m]
+ * (rows whose slot is outside [0, max_len) are not written); V is stored transposed. */
+int ssd_gemm_qkv_rope_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int K, int heads,
+                           int kv_heads, int head_dim, const uint16_t* cos_tab, const uint16_t* sin_tab,
+                           int64_t rope_rows, const int32_t* row_pos, const int32_t* row_slot, uint16_t* Q, int64_t ldq,
+                           uint16_t* k_cache, uint16_t* vt_cache, int64_t max_len, hipStream_t stream);
+
+/* ------------------------------------------------------------ tree attention
+ * Row t attends cache slots [0, prefix[t]) then anc[t][0..depth[t]) (ancestors in depth order,
+ * self included), i.e. the reference's boolean tree mask (ssd/models/subnetwork_draft.py:165-191,
+ * ssd/engine/verify.py:37-41, ssd/engine/tree_drafter.py:189-196) as a gather list. Replaces the
+ * SDPA call at ssd/models/subnetwork_draft.py:236-241 (GQA, scale 1/sqrt(hd)). Keys are folded in
+ * a canonical logical order, so a verify row equals the autoregressive step at its position. */
+int ssd_attn_workspace_floats(int M, int heads, int head_dim, int64_t max_len);
+int ssd_attn_max_depth(void);
+int ssd_tree_attention_bf16(const uint16_t* q, int64_t ldq, int M, int heads, int kv_heads, int head_dim,
+                            const uint16_t* k_cache, const uint16_t* vt_cache, int64_t max_len,
+                            const int32_t* prefix, const int32_t* depth, const int32_t* anc, int p_min, int l_max,
+                            float scale, float* ws, int64_t ws_floats, uint16_t* out, int64_t ldo,
+                            hipStream_t stream);
+
+/* ---------------------------------------------------------------- rows */
+/* HF LlamaRMSNorm / bridge RMSNorm (ssd/models/bridges.py:33-37; subnetwork_draft.py:216,245,344). */
+int ssd_rmsnorm_bf16(const uint16_t* x, int64_t ldx, int M, int D, const uint16_t* w, float eps, uint16_t* y,
+                     int64_t ldy, hipStream_t stream);
+/* embed_tokens gather (ssd/models/subnetwork_draft.py:290-291). */
+int ssd_embed_bf16(const int32_t* ids, int M, const uint16_t* table, int64_t V, int D, uint16_t* out, int64_t ldo,
+                   hipStream_t stream);
+/* KVCache.keep_positions (ssd/engine/kv_cache.py:54-70): move src[0..*n_dev) to [start, ...) in every
+ * layer in one launch; all sources are read before any destination is written. */
+int ssd_kv_compact_bf16(uint16_t* k_arena, uint16_t* vt_arena, int layers, int kv_heads, int head_dim,
+                        int64_t max_len, int start, const int32_t* src, const int32_t* n_dev, int n_max,
+                        hipStream_t stream);
+/* Row top-k over bf16 logits. mode 0: raw values (k=1 is the first-index argmax of
+ * ssd/engine/verify.py:47, speculative.py:83). mode 1: log_softmax values + logsumexp
+ * (ssd/engine/tree_drafter.py:129-133); columns map through vocab_ids (subset head,
+ * ssd/models/subnetwork_draft.py:136-144). Equal values rank lower column first. */
+int ssd_row_topk_bf16(const uint16_t* logits, int64_t ld, int M, int N, int k, int mode, const int32_t* vocab_ids,
+                      int32_t* out_tok, float* out_val, float* out_lse, hipStream_t stream);
+
+/* ------------------------------------------------------------------ tree
+ * Device-resident DraftTree (ssd/engine/tree_drafter.py:48-95). All members are device
+ * pointers of `cap` entries except meta (1 + 2*32 ints) and vmeta (1 int). */
+typedef struct SsdTree {
+  int32_t* tokens;
+  int32_t* parents;
+  int32_t* depths;
+  int32_t* ranks;
+  int32_t* draft_pos;
+  double* scores;
+  int32_t* meta; /* [0] nodes, [1+d] level start, [33+d] level size */
+  int32_t* vtokens;
+  int32_t* vparents;
+  int32_t* vdepths;
+  int32_t* vranks;
+  int32_t* vorig;
+  int32_t* vmeta; /* [0] verify nodes */
+  int32_t cap;
+} SsdTree;
+
+/* Per-row inputs of one forward: token ids, rotary positions, cache slots, and the
+ * attention rows (prefix, depth, anc[cap][32]). */
+typedef struct SsdRows {
+  int32_t* ids;
+  int32_t* pos;
+  int32_t* slot;
+  int32_t* prefix;
+  int32_t* depth;
+  int32_t* anc;
+  int32_t cap;
+} SsdRows;
+
+int ssd_tree_limits(int32_t* out3); /* host: {node capacity, max depth, max ancestors per row} */
+
+/* One level of TreeDrafter.build (ssd/engine/tree_drafter.py:165-200): candidates of the current
+ * frontier (cand_tok/cand_lp [F, k]; tok < 0 = none) -> score = parent score + lp, stable sort,
+ * width cut, append; if feed, write the next draft forward's rows (positions root_pos+d+1, slots
+ * past+j, prefix tree_start, ancestors' draft slots). */
+int ssd_tree_level(const SsdTree* tree, int d, const int32_t* cand_tok, const float* cand_lp, int F_max, int k,
+                   int width, int feed, int root_pos, int tree_start, int past, const SsdRows* rows, int rows_max,
+                   hipStream_t stream);
+
+/* max_nodes cut by (-score, depth), ancestor closure and renumbering (ssd/engine/tree_drafter.py:202-207),
+ * then the verify rows of verify_inputs (ssd/engine/verify.py:32-42); root token read from device. */
+int ssd_tree_finalize(const SsdTree* tree, int max_nodes, int committed, const int32_t* root_token,
+                      const SsdRows* rows, int rows_max, hipStream_t stream);
+
+/* greedy_verify (ssd/engine/verify.py:45-57) plus the bookkeeping of speculative.py:166-171:
+ * result = [n_new, tokens...], keep_src/n_keep for ssd_kv_compact_bf16, next root token. */
+int ssd_accept_greedy(const SsdTree* tree, const int32_t* argmax, int committed, int32_t* result,
+                      int32_t* keep_src, int32_t* n_keep, int32_t* root_token, hipStream_t stream);
+
+#if defined(__GNUC__) || defined(__clang__)
+#pragma GCC visibility pop
+#endif
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SSD_MI355X_H */

@@ -181,24 +181,11 @@ class TreeDrafter:
         tree = DraftTree(cache_start=tree_start)
         frontier, f_logits = [ROOT], logits[-1:]
         for d in range(self.cfg.depth):
-            cands = []
-            for parent, (toks, lps, q) in zip(frontier, self.propose(f_logits, self.branch[d], gen)):
+            proposals = self.propose(f_logits, self.branch[d], gen)
+            for parent, (_, _, q) in zip(frontier, proposals):
                 if q is not None:
                     tree.child_q[parent] = q
-                base = tree.scores[parent] if parent != ROOT else 0.0
-                cands += [(base + lp, parent, t, r) for r, (t, lp) in enumerate(zip(toks, lps))]
-            cands.sort(key=lambda c: -c[0])
-            if self.width[d] is not None:
-                cands = cands[: self.width[d]]
-            level = []
-            for score, parent, tok, rank in cands:
-                level.append(len(tree))
-                tree.tokens.append(tok)
-                tree.parents.append(parent)
-                tree.depths.append(d + 1)
-                tree.scores.append(score)
-                tree.ranks.append(rank)
-                tree.draft_pos.append(-1)
+            level = expand_level(tree, frontier, [(t, l) for t, l, _ in proposals], d, self.width[d])
             if d == self.cfg.depth - 1 or not level:
                 break
             past = cache.get_seq_length()
@@ -212,13 +199,43 @@ class TreeDrafter:
             ids = torch.tensor([tree.tokens[i] for i in level])
             frontier = level
             f_logits, _ = self.draft(ids, torch.full((len(level),), root_pos + d + 1), cache, mask)
-        if self.cfg.max_nodes is not None and len(tree) > self.cfg.max_nodes:
-            order = sorted(range(len(tree)), key=lambda i: (-tree.scores[i], tree.depths[i]))
-            keep = set(order[: self.cfg.max_nodes])
-            for i in list(keep):
-                keep.update(tree.ancestors(i))
-            tree = tree.subset(sorted(keep))
+        return prune_tree(tree, self.cfg.max_nodes)
+
+
+def expand_level(tree: DraftTree, frontier: list, proposals: list, d: int, width: Optional[int]) -> list:
+    """One level of TreeDrafter.build (tree_drafter.py:166-183): every frontier node's
+    proposals (tokens, log-probs) become candidates scored parent score + lp (doubles); a
+    stable sort on -score keeps (frontier order, proposal rank) among ties; the first
+    ``width`` are appended. Returns the new node indices."""
+    cands = []
+    for parent, (toks, lps) in zip(frontier, proposals):
+        base = tree.scores[parent] if parent != ROOT else 0.0
+        cands += [(base + lp, parent, t, r) for r, (t, lp) in enumerate(zip(toks, lps))]
+    cands.sort(key=lambda c: -c[0])
+    if width is not None:
+        cands = cands[:width]
+    level = []
+    for score, parent, tok, rank in cands:
+        level.append(len(tree))
+        tree.tokens.append(tok)
+        tree.parents.append(parent)
+        tree.depths.append(d + 1)
+        tree.scores.append(score)
+        tree.ranks.append(rank)
+        tree.draft_pos.append(-1)
+    return level
+
+
+def prune_tree(tree: DraftTree, max_nodes: Optional[int]) -> DraftTree:
+    """Final cut (tree_drafter.py:202-207): best ``max_nodes`` by (-score, depth), closed
+    under ancestors, renumbered in original order."""
+    if max_nodes is None or len(tree) <= max_nodes:
         return tree
+    order = sorted(range(len(tree)), key=lambda i: (-tree.scores[i], tree.depths[i]))
+    keep = set(order[:max_nodes])
+    for i in list(keep):
+        keep.update(tree.ancestors(i))
+    return tree.subset(sorted(keep))
 
 
 def prune_order(scores: list, depths: list, max_nodes: int) -> list:

@@ -1,0 +1,83 @@
+// Shared device helpers for the gfx950 (MI355X) speculative-decoding kernels.
+//
+// Storage type for bf16 is uint16_t everywhere (bit patterns); arithmetic is fp32.
+// Rounding fp32 -> bf16 is round-to-nearest-even, the same rule torch uses.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/ssd_mi355x.h"
+
+#define SSD_API extern "C" __attribute__((visibility("default")))
+
+typedef uint16_t bf16_t;
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+
+namespace ssd {
+
+// Host-side error reporting: every entry point returns 0 on success, else a
+// nonzero code and a message retrievable through ssd_last_error().
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+enum Status {
+  SSD_OK = 0,
+  SSD_EINVAL = 1,     // bad argument (shape, pointer, size)
+  SSD_ERANGE = 2,     // size beyond a compiled limit
+  SSD_EHIP = 3,       // HIP runtime error
+};
+
+__device__ __forceinline__ float bf2f(bf16_t v) { return __uint_as_float(((uint32_t)v) << 16); }
+
+__device__ __forceinline__ bf16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (bf16_t)((u >> 16) | 0x40);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+
+// Round through bf16 (the value an fp32 result takes once stored as bf16).
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+
+union Pack8 {
+  uint4 u;
+  bf16_t h[8];
+  bf16x8_t v;
+};
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 u) {
+  Pack8 p;
+  p.u = u;
+  return p.v;
+}
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// Streaming (non-temporal) 16-byte load: weights are read once per call, keep them out of the caches' way.
+__device__ __forceinline__ uint4 ld_stream(const uint4* p) {
+  const u32x4_t v = __builtin_nontemporal_load((const u32x4_t*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ f32x4_t mfma16x16x32(bf16x8_t a, bf16x8_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float gelu_f(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f)); }
+__device__ __forceinline__ float relu_f(float x) { return x > 0.f ? x : 0.f; }
+
+enum Act { ACT_NONE = 0, ACT_SILU = 1, ACT_GELU = 2, ACT_RELU = 3 };
+
+__device__ __forceinline__ float apply_act(int act, float x) {
+  switch (act) {
+    case ACT_SILU: return silu_f(x);
+    case ACT_GELU: return gelu_f(x);
+    case ACT_RELU: return relu_f(x);
+    default: return x;
+  }
+}
+
+}  // namespace ssd

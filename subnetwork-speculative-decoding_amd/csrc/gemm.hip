@@ -1,0 +1,334 @@
+// Weight-streaming bf16 GEMM for decode-sized M on gfx950 (MI355X).
+//
+//   Y[M, N] = X[M, K] . W[N, K]^T      (nn.Linear without the transpose copy)
+//
+// Design (HBM-bound: every weight byte is read exactly once per call):
+// * W is pre-packed once into MFMA-native tiles: tile (nb, kb) holds rows
+//   [16nb, 16nb+16) x k [32kb, 32kb+32) as 64 lanes x 8 bf16, in the order the
+//   v_mfma_f32_16x16x32_bf16 A operand wants it. A wave's load of one tile is
+//   one fully contiguous 1 KiB request (16 B per lane).
+// * One workgroup owns one 16-row tile of N (the whole K); its KS waves split K
+//   into fixed contiguous ranges and are summed through LDS in wave order.
+// * X (activations, row-major) is the B operand, loaded straight from L2; rows
+//   beyond M are zeros. M is covered by CT column tiles of 16.
+// * Batch invariance: the instruction, the K split and the summation order
+//   depend only on (N, K), never on M, so a row's result is bit-identical
+//   whether it is computed alone (autoregressive step) or inside a 25-row
+//   verify batch. This is what keeps speculative greedy output identical to
+//   plain greedy decoding in bf16.
+// * Epilogues mirror the reference's bf16 rounding points (linear output
+//   rounded to bf16, then each elementwise op rounded): plain store, bias +
+//   activation, residual add, SwiGLU (gate rows 0-7 / up rows 8-15 of a tile),
+//   and QKV + RoPE + KV-cache write (rotary pair dims in rows r and r+8).
+#include "common.h"
+
+#include <algorithm>
+
+namespace ssd {
+
+enum Epi { EPI_STORE = 0, EPI_SWIGLU = 1, EPI_QKV = 2 };
+
+struct GemmArgs {
+  const bf16_t* X;
+  int64_t ldx;
+  int M;
+  const uint4* W;  // packed tiles
+  int N;           // logical output columns (rows of W)
+  int kb_total;    // K / 32
+  // EPI_STORE
+  bf16_t* Y;
+  int64_t ldy;
+  const bf16_t* bias;      // [N] or null
+  int act;                 // Act
+  const bf16_t* residual;  // [M, ldr] or null (Y may alias it)
+  int64_t ldr;
+  // EPI_SWIGLU: bias for gate / up (null ok); output columns = N / 2
+  const bf16_t* bias2;
+  // EPI_QKV
+  int heads, kv_heads, head_dim;
+  const bf16_t* cos_tab;  // [max_pos, head_dim/2]
+  const bf16_t* sin_tab;
+  const int* row_pos;     // [M]
+  const int* row_slot;    // [M]
+  int64_t rope_rows;      // rows of cos_tab / sin_tab
+  bf16_t* k_cache;        // this layer: [kv_heads, max_len, head_dim]
+  bf16_t* vt_cache;       // this layer: [kv_heads, head_dim, max_len]
+  int64_t max_len;
+};
+
+template <int CT, int KS>
+struct GemmLds {
+  float4 red[KS][CT][64];
+};
+
+template <int CT, int KS, int EPI>
+__global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int nb = blockIdx.x;
+  const int kbt = a.kb_total;
+  const int kb_lo = (kbt * w) / KS;
+  const int kb_hi = (kbt * (w + 1)) / KS;
+  const int j = lane & 15, g = lane >> 4;
+
+  f32x4_t acc[CT];
+#pragma unroll
+  for (int c = 0; c < CT; ++c) acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const uint4* wp = a.W + ((size_t)nb * kbt) * 64 + lane;
+  const bf16_t* xp[CT];
+  bool xv[CT];
+#pragma unroll
+  for (int c = 0; c < CT; ++c) {
+    const int m = c * 16 + j;
+    xv[c] = m < a.M;
+    xp[c] = a.X + (size_t)(xv[c] ? m : 0) * a.ldx + g * 8;
+  }
+
+  int kb = kb_lo;
+  // Two k-blocks per trip so that four independent 16 B loads are in flight.
+  for (; kb + 1 < kb_hi; kb += 2) {
+    uint4 w0 = ld_stream(wp + (size_t)kb * 64);
+    uint4 w1 = ld_stream(wp + (size_t)(kb + 1) * 64);
+    uint4 x0[CT], x1[CT];
+#pragma unroll
+    for (int c = 0; c < CT; ++c) {
+      x0[c] = xv[c] ? *(const uint4*)(xp[c] + kb * 32) : make_uint4(0, 0, 0, 0);
+      x1[c] = xv[c] ? *(const uint4*)(xp[c] + (kb + 1) * 32) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int c = 0; c < CT; ++c) acc[c] = mfma16x16x32(as_bf16x8(w0), as_bf16x8(x0[c]), acc[c]);
+#pragma unroll
+    for (int c = 0; c < CT; ++c) acc[c] = mfma16x16x32(as_bf16x8(w1), as_bf16x8(x1[c]), acc[c]);
+  }
+  if (kb < kb_hi) {
+    uint4 w0 = ld_stream(wp + (size_t)kb * 64);
+#pragma unroll
+    for (int c = 0; c < CT; ++c) {
+      uint4 x0 = xv[c] ? *(const uint4*)(xp[c] + kb * 32) : make_uint4(0, 0, 0, 0);
+      acc[c] = mfma16x16x32(as_bf16x8(w0), as_bf16x8(x0), acc[c]);
+    }
+  }
+
+  __shared__ GemmLds<CT, KS> lds;
+#pragma unroll
+  for (int c = 0; c < CT; ++c) lds.red[w][c][lane] = make_float4(acc[c][0], acc[c][1], acc[c][2], acc[c][3]);
+  __syncthreads();
+
+  // Value of tile row r (0..15), token m, summed over the waves in wave order.
+  auto tile_val = [&](int r, int m) -> float {
+    const int c = m >> 4;
+    const int ln = (m & 15) + 16 * (r >> 2);
+    const int e = r & 3;
+    float s = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < KS; ++ww) {
+      const float4 v = lds.red[ww][c][ln];
+      const float x = e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
+      s = ww == 0 ? x : s + x;
+    }
+    return s;
+  };
+
+  const int nthreads = 64 * KS;
+  const int Mv = a.M < CT * 16 ? a.M : CT * 16;
+  if constexpr (EPI == EPI_STORE) {
+    for (int o = threadIdx.x; o < 16 * Mv; o += nthreads) {
+      const int m = o >> 4, r = o & 15;
+      const int n = nb * 16 + r;
+      if (n >= a.N) continue;
+      float t = tile_val(r, m);
+      if (a.bias) t += bf2f(a.bias[n]);
+      t = rbf(t);
+      if (a.act) t = rbf(apply_act(a.act, t));
+      if (a.residual) t = rbf(bf2f(a.residual[(size_t)m * a.ldr + n]) + t);
+      a.Y[(size_t)m * a.ldy + n] = f2bf(t);
+    }
+  } else if constexpr (EPI == EPI_SWIGLU) {
+    for (int o = threadIdx.x; o < 8 * Mv; o += nthreads) {
+      const int m = o >> 3, r = o & 7;
+      const int col = nb * 8 + r;  // intermediate index
+      if (col * 2 >= a.N) continue;
+      float gt = tile_val(r, m), up = tile_val(r + 8, m);
+      if (a.bias) gt += bf2f(a.bias[col]);
+      if (a.bias2) up += bf2f(a.bias2[col]);
+      const float gs = rbf(silu_f(rbf(gt)));
+      a.Y[(size_t)m * a.ldy + col] = f2bf(gs * rbf(up));
+    }
+  } else {  // EPI_QKV
+    const int hd = a.head_dim, half = hd >> 1, tiles_per_head = hd >> 4;
+    const int q_tiles = a.heads * tiles_per_head, k_tiles = a.kv_heads * tiles_per_head;
+    int region, head, p;
+    if (nb < q_tiles) {
+      region = 0; head = nb / tiles_per_head; p = nb % tiles_per_head;
+    } else if (nb < q_tiles + k_tiles) {
+      region = 1; head = (nb - q_tiles) / tiles_per_head; p = (nb - q_tiles) % tiles_per_head;
+    } else {
+      region = 2; head = (nb - q_tiles - k_tiles) / tiles_per_head; p = (nb - q_tiles - k_tiles) % tiles_per_head;
+    }
+    for (int o = threadIdx.x; o < 8 * Mv; o += nthreads) {
+      const int m = o >> 3, r = o & 7;
+      const int dlo = p * 8 + r, dhi = dlo + half;
+      const float xlo = rbf(tile_val(r, m)), xhi = rbf(tile_val(r + 8, m));
+      const int slot = a.row_slot[m];
+      if (region != 0 && (slot < 0 || slot >= a.max_len)) continue;  // never write outside the cache
+      if (region == 2) {
+        bf16_t* vt = a.vt_cache + (size_t)head * hd * a.max_len;
+        vt[(size_t)dlo * a.max_len + slot] = f2bf(xlo);
+        vt[(size_t)dhi * a.max_len + slot] = f2bf(xhi);
+        continue;
+      }
+      const int pos = min(max(a.row_pos[m], 0), (int)a.rope_rows - 1);
+      const float cs = bf2f(a.cos_tab[(size_t)pos * half + dlo]);
+      const float sn = bf2f(a.sin_tab[(size_t)pos * half + dlo]);
+      const float olo = rbf(rbf(xlo * cs) - rbf(xhi * sn));
+      const float ohi = rbf(rbf(xhi * cs) + rbf(xlo * sn));
+      if (region == 0) {
+        bf16_t* q = a.Y + (size_t)m * a.ldy + (size_t)head * hd;
+        q[dlo] = f2bf(olo);
+        q[dhi] = f2bf(ohi);
+      } else {
+        bf16_t* kr = a.k_cache + ((size_t)head * a.max_len + slot) * hd;
+        kr[dlo] = f2bf(olo);
+        kr[dhi] = f2bf(ohi);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- packing
+// dst tile (nb, kb), lane l, element t  <-  W[row_map[16 nb + l%16]][32 kb + 8 (l/16) + t]
+// (row_map entry < 0 or beyond K -> zero).
+__global__ void pack_kernel(const bf16_t* __restrict__ src, int64_t ld, int K, const int* __restrict__ row_map,
+                            int n_tiles_n, int kb_total, uint4* __restrict__ dst) {
+  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (tile >= (int64_t)n_tiles_n * kb_total) return;
+  const int nb = (int)(tile / kb_total), kb = (int)(tile % kb_total);
+  const int row = row_map[nb * 16 + (lane & 15)];
+  const int k0 = kb * 32 + (lane >> 4) * 8;
+  Pack8 p;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) p.h[t] = (row >= 0 && k0 + t < K) ? src[(size_t)row * ld + k0 + t] : (bf16_t)0;
+  dst[tile * 64 + lane] = p.u;
+}
+
+static int choose_ks(int kb_total) {
+  if (kb_total >= 16) return 8;
+  if (kb_total >= 8) return 4;
+  if (kb_total >= 2) return 2;
+  return 1;
+}
+
+template <int EPI>
+static int launch_gemm(GemmArgs a, hipStream_t s) {
+  const int ks = choose_ks(a.kb_total);
+  const int n_tiles = EPI == EPI_STORE ? (a.N + 15) / 16 : (a.N + 15) / 16;
+  // Rows beyond 64 are processed in chunks of 64; each chunk is computed exactly as it would be alone.
+  for (int m0 = 0; m0 < a.M; m0 += 64) {
+    GemmArgs b = a;
+    b.M = std::min(64, a.M - m0);
+    b.X = a.X + (size_t)m0 * a.ldx;
+    if (a.Y) b.Y = a.Y + (size_t)m0 * a.ldy;
+    if (a.residual) b.residual = a.residual + (size_t)m0 * a.ldr;
+    if (a.row_pos) b.row_pos = a.row_pos + m0;
+    if (a.row_slot) b.row_slot = a.row_slot + m0;
+    const int ct = (b.M + 15) / 16;
+    dim3 grid(n_tiles), block(64 * ks);
+#define SSD_GEMM_CASE(CT_, KS_) \
+  if (ct == CT_ && ks == KS_) { hipLaunchKernelGGL((gemm_kernel<CT_, KS_, EPI>), grid, block, 0, s, b); }
+#define SSD_GEMM_KS(CT_) SSD_GEMM_CASE(CT_, 1) SSD_GEMM_CASE(CT_, 2) SSD_GEMM_CASE(CT_, 4) SSD_GEMM_CASE(CT_, 8)
+    SSD_GEMM_KS(1) SSD_GEMM_KS(2) SSD_GEMM_KS(3) SSD_GEMM_KS(4)
+#undef SSD_GEMM_KS
+#undef SSD_GEMM_CASE
+    int rc = check_launch("gemm");
+    if (rc) return rc;
+  }
+  return SSD_OK;
+}
+
+static int check_common(const bf16_t* X, int64_t ldx, int M, const void* W, int N, int K) {
+  if (!X || !W) return set_error(SSD_EINVAL, "gemm: null X or W");
+  if (M < 0 || N <= 0 || K <= 0) return set_error(SSD_EINVAL, "gemm: bad shape M=%d N=%d K=%d", M, N, K);
+  if (K % 32) return set_error(SSD_EINVAL, "gemm: K=%d must be a multiple of 32", K);
+  if (((uintptr_t)X & 15) || (ldx % 8)) return set_error(SSD_EINVAL, "gemm: X must be 16-byte aligned with ldx %% 8 == 0");
+  if (((uintptr_t)W & 15)) return set_error(SSD_EINVAL, "gemm: packed W must be 16-byte aligned");
+  return SSD_OK;
+}
+
+}  // namespace ssd
+
+using namespace ssd;
+
+SSD_API int64_t ssd_packed_weight_elems(int N, int K) {
+  return (int64_t)((N + 15) / 16) * 16 * (int64_t)((K + 31) / 32) * 32;
+}
+
+SSD_API int ssd_pack_weight_bf16(const uint16_t* src, int64_t ld, int N_src, int K, const int32_t* row_map,
+                                 int N_packed, uint16_t* dst, hipStream_t stream) {
+  if (!src || !dst || !row_map) return set_error(SSD_EINVAL, "pack: null pointer");
+  if (N_packed <= 0 || N_packed % 16 || K <= 0 || N_src <= 0)
+    return set_error(SSD_EINVAL, "pack: N_packed=%d must be a positive multiple of 16 (K=%d)", N_packed, K);
+  const int n_tiles_n = N_packed / 16, kb_total = (K + 31) / 32;
+  const int64_t tiles = (int64_t)n_tiles_n * kb_total;
+  hipLaunchKernelGGL(pack_kernel, dim3((unsigned)((tiles + 3) / 4)), dim3(256), 0, stream, src, ld, K, row_map,
+                     n_tiles_n, kb_total, (uint4*)dst);
+  return check_launch("pack");
+}
+
+// Y = act(X W^T + bias) [+ residual], bf16 rounding after each step. Y may alias residual.
+SSD_API int ssd_gemm_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int N, int K,
+                          uint16_t* Y, int64_t ldy, const uint16_t* bias, int act, const uint16_t* residual,
+                          int64_t ldr, hipStream_t stream) {
+  int rc = check_common(X, ldx, M, W_packed, N, K);
+  if (rc) return rc;
+  if (!Y) return set_error(SSD_EINVAL, "gemm: null Y");
+  if (act < 0 || act > 3) return set_error(SSD_EINVAL, "gemm: bad activation %d", act);
+  if (residual && act) return set_error(SSD_EINVAL, "gemm: residual and activation are exclusive");
+  if (M == 0) return SSD_OK;
+  GemmArgs a{};
+  a.X = X; a.ldx = ldx; a.M = M; a.W = (const uint4*)W_packed; a.N = N; a.kb_total = K / 32;
+  a.Y = Y; a.ldy = ldy; a.bias = bias; a.act = act; a.residual = residual; a.ldr = ldr;
+  return launch_gemm<EPI_STORE>(a, stream);
+}
+
+// Y[M, I] = silu(X Wg^T + bg) * (X Wu^T + bu); W_packed holds, per 16-row tile i, gate rows
+// [8i, 8i+8) then up rows [8i, 8i+8). N = 2 I.
+SSD_API int ssd_gemm_swiglu_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int I, int K,
+                                 uint16_t* Y, int64_t ldy, const uint16_t* bias_gate, const uint16_t* bias_up,
+                                 hipStream_t stream) {
+  int rc = check_common(X, ldx, M, W_packed, 2 * I, K);
+  if (rc) return rc;
+  if (!Y || I % 8) return set_error(SSD_EINVAL, "gemm_swiglu: null Y or I=%d not a multiple of 8", I);
+  if (M == 0) return SSD_OK;
+  GemmArgs a{};
+  a.X = X; a.ldx = ldx; a.M = M; a.W = (const uint4*)W_packed; a.N = 2 * I; a.kb_total = K / 32;
+  a.Y = Y; a.ldy = ldy; a.bias = bias_gate; a.bias2 = bias_up;
+  return launch_gemm<EPI_SWIGLU>(a, stream);
+}
+
+// Fused q/k/v projection + RoPE + KV-cache write. W_packed: q heads, k heads, v heads; each
+// head as head_dim/16 tiles whose rows 0-7 are dims [8p, 8p+8) and rows 8-15 dims
+// [hd/2 + 8p, hd/2 + 8p + 8). q -> Q[m, heads*hd]; k -> k_cache[kvh, slot, :];
+// v -> vt_cache[kvh, :, slot] (V is kept transposed).
+SSD_API int ssd_gemm_qkv_rope_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int K,
+                                   int heads, int kv_heads, int head_dim, const uint16_t* cos_tab,
+                                   const uint16_t* sin_tab, int64_t rope_rows, const int32_t* row_pos,
+                                   const int32_t* row_slot,
+                                   uint16_t* Q, int64_t ldq, uint16_t* k_cache, uint16_t* vt_cache,
+                                   int64_t max_len, hipStream_t stream) {
+  const int N = (heads + 2 * kv_heads) * head_dim;
+  int rc = check_common(X, ldx, M, W_packed, N, K);
+  if (rc) return rc;
+  if (head_dim % 16 || head_dim > 256) return set_error(SSD_EINVAL, "qkv: head_dim=%d unsupported", head_dim);
+  if (!Q || !k_cache || !vt_cache || !cos_tab || !sin_tab || !row_pos || !row_slot)
+    return set_error(SSD_EINVAL, "qkv: null pointer");
+  if (M == 0) return SSD_OK;
+  GemmArgs a{};
+  a.X = X; a.ldx = ldx; a.M = M; a.W = (const uint4*)W_packed; a.N = N; a.kb_total = K / 32;
+  a.Y = Q; a.ldy = ldq; a.heads = heads; a.kv_heads = kv_heads; a.head_dim = head_dim;
+  if (rope_rows <= 0) return set_error(SSD_EINVAL, "qkv: empty rope table");
+  a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.rope_rows = rope_rows; a.row_pos = row_pos; a.row_slot = row_slot;
+  a.k_cache = k_cache; a.vt_cache = vt_cache; a.max_len = max_len;
+  return launch_gemm<EPI_QKV>(a, stream);
+}

@@ -1,0 +1,236 @@
+// Row kernels: RMSNorm, embedding gather, KV compaction, and the vocabulary
+// reductions that close the lm_head (argmax / log-softmax top-k).
+//
+// Every reduction runs in a fixed order that depends only on the row length,
+// so each row's result is independent of how many rows share the launch.
+#include "common.h"
+
+#include <math.h>
+
+namespace ssd {
+
+// Deterministic 256-thread sum: butterfly inside each wave, then waves in order.
+__device__ __forceinline__ float block_sum_256(float v, float* sh) {
+  v += __shfl_xor(v, 1);
+  v += __shfl_xor(v, 2);
+  v += __shfl_xor(v, 4);
+  v += __shfl_xor(v, 8);
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const float r = ((sh[0] + sh[1]) + sh[2]) + sh[3];
+  __syncthreads();
+  return r;
+}
+
+// HF LlamaRMSNorm / bridge RMSNorm: y = w * bf16(x * rsqrt(mean(x^2) + eps)) (ssd/models/bridges.py:33-37).
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const bf16_t* __restrict__ x, int64_t ldx,
+                                                      const bf16_t* __restrict__ w, bf16_t* __restrict__ y,
+                                                      int64_t ldy, int D, float eps) {
+  __shared__ float sh[4];
+  const bf16_t* xr = x + (size_t)blockIdx.x * ldx;
+  bf16_t* yr = y + (size_t)blockIdx.x * ldy;
+  float ss = 0.f;
+  for (int k = threadIdx.x * 8; k < D; k += 256 * 8) {
+    Pack8 p;
+    p.u = *(const uint4*)(xr + k);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const float f = bf2f(p.h[t]);
+      ss += f * f;
+    }
+  }
+  const float tot = block_sum_256(ss, sh);
+  const float r = rsqrtf(tot / (float)D + eps);
+  for (int k = threadIdx.x * 8; k < D; k += 256 * 8) {
+    Pack8 p, q, o;
+    p.u = *(const uint4*)(xr + k);
+    q.u = *(const uint4*)(w + k);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) o.h[t] = f2bf(bf2f(q.h[t]) * rbf(bf2f(p.h[t]) * r));
+    *(uint4*)(yr + k) = o.u;
+  }
+}
+
+__global__ __launch_bounds__(256) void embed_kernel(const int* __restrict__ ids, const bf16_t* __restrict__ table,
+                                                    int64_t V, int D, bf16_t* __restrict__ out, int64_t ldo) {
+  const int m = blockIdx.x;
+  int id = ids[m];
+  id = id < 0 ? 0 : (id >= V ? (int)V - 1 : id);
+  const uint4* src = (const uint4*)(table + (size_t)id * D);
+  uint4* dst = (uint4*)(out + (size_t)m * ldo);
+  for (int k = threadIdx.x; k < D / 8; k += 256) dst[k] = src[k];
+}
+
+// Move cache entries src[0..n) to [start, start+n) in every layer and kv head
+// (ssd/engine/kv_cache.py:54-70). All sources are read before any destination is
+// written: a destination may be the source of a later entry (start=10, src=[10,12,13]).
+// K is [L][kvh][max_len][hd]; V is transposed, [L][kvh][hd][max_len]. n is read from
+// device memory (n_ptr) so the launch needs no host round trip; n <= n_max.
+__global__ __launch_bounds__(256) void kv_compact_kernel(bf16_t* __restrict__ kc, bf16_t* __restrict__ vt, int kv_heads,
+                                                         int hd, int64_t max_len, int start, const int* __restrict__ src,
+                                                         const int* __restrict__ n_ptr, int n_max) {
+  extern __shared__ bf16_t stage[];  // [2][n_max][hd]
+  const int lh = blockIdx.x;         // layer * kv_heads + head
+  const int n = max(0, min(*n_ptr, n_max));
+  bf16_t* kbase = kc + (size_t)lh * max_len * hd;
+  bf16_t* vbase = vt + (size_t)lh * hd * max_len;
+  const int tot = n * hd;
+  for (int e = threadIdx.x; e < tot; e += 256) {
+    const int i = e / hd, d = e % hd;
+    int s = src[i];
+    s = (s >= 0 && s < max_len) ? s : start + i;  // out-of-range source: leave the slot as is
+    stage[e] = kbase[(size_t)s * hd + d];
+    stage[n_max * hd + e] = vbase[(size_t)d * max_len + s];
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < tot; e += 256) {
+    const int i = e / hd, d = e % hd;
+    kbase[(size_t)(start + i) * hd + d] = stage[e];
+    vbase[(size_t)d * max_len + start + i] = stage[n_max * hd + e];
+  }
+}
+
+constexpr int TOPK_MAX = 16;
+
+struct Cand {
+  float v;
+  int i;
+};
+
+// a ranks before b: larger value, then lower column (the oracle's stable-sort order).
+__device__ __forceinline__ bool better(float av, int ai, float bv, int bi) { return av > bv || (av == bv && ai < bi); }
+
+__device__ __forceinline__ void topk_insert(Cand (&c)[TOPK_MAX], int k, float v, int i) {
+  if (!better(v, i, c[k - 1].v, c[k - 1].i)) return;
+  int p = k - 1;
+  while (p > 0 && better(v, i, c[p - 1].v, c[p - 1].i)) {
+    c[p] = c[p - 1];
+    --p;
+  }
+  c[p] = Cand{v, i};
+}
+
+// One workgroup per row of bf16 logits [M, ld] (N valid columns).
+// mode 0: k best columns by raw value (argmax for k = 1).
+// mode 1: k best log-softmax values, lp = (x - max) - log(sum exp(x - max)) in fp32
+//         (ssd/engine/tree_drafter.py:129-133), plus the row's logsumexp.
+// Column c maps to token vocab_ids[c] when vocab_ids is given (vocab subset head).
+__global__ __launch_bounds__(256) void row_topk_kernel(const bf16_t* __restrict__ logits, int64_t ld, int N, int k,
+                                                       int mode, const int* __restrict__ vocab_ids,
+                                                       int* __restrict__ out_tok, float* __restrict__ out_val,
+                                                       float* __restrict__ out_lse) {
+  __shared__ float sv[256 * TOPK_MAX];
+  __shared__ int si[256 * TOPK_MAX];
+  __shared__ float sh[4];
+  const int row = blockIdx.x;
+  const bf16_t* x = logits + (size_t)row * ld;
+  Cand c[TOPK_MAX];
+#pragma unroll
+  for (int q = 0; q < TOPK_MAX; ++q) c[q] = Cand{-INFINITY, 0x7fffffff};
+  const int nvec = N / 8;
+  for (int vI = threadIdx.x; vI < nvec; vI += 256) {
+    Pack8 p;
+    p.u = *(const uint4*)(x + (size_t)vI * 8);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) topk_insert(c, k, bf2f(p.h[t]), vI * 8 + t);
+  }
+  for (int col = nvec * 8 + threadIdx.x; col < N; col += 256) topk_insert(c, k, bf2f(x[col]), col);
+  for (int q = 0; q < k; ++q) {
+    sv[threadIdx.x * TOPK_MAX + q] = c[q].v;
+    si[threadIdx.x * TOPK_MAX + q] = c[q].i;
+  }
+  __syncthreads();
+  for (int stride = 128; stride >= 1; stride >>= 1) {
+    Cand mrg[TOPK_MAX];
+    const bool act = threadIdx.x < stride;
+    if (act) {
+      const float* av = sv + threadIdx.x * TOPK_MAX;
+      const int* ai = si + threadIdx.x * TOPK_MAX;
+      const float* bv = sv + (threadIdx.x + stride) * TOPK_MAX;
+      const int* bi = si + (threadIdx.x + stride) * TOPK_MAX;
+      int pa = 0, pb = 0;
+      for (int q = 0; q < k; ++q) {
+        if (better(av[pa], ai[pa], bv[pb], bi[pb])) { mrg[q] = Cand{av[pa], ai[pa]}; ++pa; }
+        else { mrg[q] = Cand{bv[pb], bi[pb]}; ++pb; }
+      }
+    }
+    __syncthreads();
+    if (act) {
+      for (int q = 0; q < k; ++q) {
+        sv[threadIdx.x * TOPK_MAX + q] = mrg[q].v;
+        si[threadIdx.x * TOPK_MAX + q] = mrg[q].i;
+      }
+    }
+    __syncthreads();
+  }
+  float lse = 0.f;
+  if (mode == 1) {
+    const float mx = sv[0];
+    float s = 0.f;
+    for (int vI = threadIdx.x; vI < nvec; vI += 256) {
+      Pack8 p;
+      p.u = *(const uint4*)(x + (size_t)vI * 8);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) s += __expf(bf2f(p.h[t]) - mx);
+    }
+    for (int col = nvec * 8 + threadIdx.x; col < N; col += 256) s += __expf(bf2f(x[col]) - mx);
+    const float tot = block_sum_256(s, sh);
+    lse = logf(tot);
+    if (threadIdx.x == 0 && out_lse) out_lse[row] = mx + lse;
+  }
+  if (threadIdx.x < k) {
+    const int q = threadIdx.x;
+    const int col = si[q];
+    out_tok[row * k + q] = vocab_ids ? vocab_ids[col] : col;
+    if (out_val) out_val[row * k + q] = mode == 1 ? (sv[q] - sv[0]) - lse : sv[q];
+  }
+}
+
+}  // namespace ssd
+
+using namespace ssd;
+
+SSD_API int ssd_rmsnorm_bf16(const uint16_t* x, int64_t ldx, int M, int D, const uint16_t* w, float eps,
+                             uint16_t* y, int64_t ldy, hipStream_t stream) {
+  if (!x || !w || !y || M < 0 || D <= 0 || D % 8 || ldx % 8 || ldy % 8)
+    return set_error(SSD_EINVAL, "rmsnorm: bad arguments (D=%d must be a multiple of 8)", D);
+  if (M == 0) return SSD_OK;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(M), dim3(256), 0, stream, x, ldx, w, y, ldy, D, eps);
+  return check_launch("rmsnorm");
+}
+
+SSD_API int ssd_embed_bf16(const int32_t* ids, int M, const uint16_t* table, int64_t V, int D, uint16_t* out,
+                           int64_t ldo, hipStream_t stream) {
+  if (!ids || !table || !out || M < 0 || D % 8 || ldo % 8) return set_error(SSD_EINVAL, "embed: bad arguments");
+  if (M == 0) return SSD_OK;
+  hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(256), 0, stream, ids, table, V, D, out, ldo);
+  return check_launch("embed");
+}
+
+SSD_API int ssd_kv_compact_bf16(uint16_t* k_arena, uint16_t* vt_arena, int layers, int kv_heads, int head_dim,
+                                int64_t max_len, int start, const int32_t* src, const int32_t* n_dev, int n_max,
+                                hipStream_t stream) {
+  if (!k_arena || !vt_arena || !src || !n_dev || layers <= 0 || kv_heads <= 0 || head_dim <= 0 || n_max < 0)
+    return set_error(SSD_EINVAL, "kv_compact: bad arguments");
+  if (start < 0 || start + n_max > max_len) return set_error(SSD_EINVAL, "kv_compact: start %d + %d > max_len", start, n_max);
+  if (n_max == 0) return SSD_OK;
+  const size_t lds = (size_t)2 * n_max * head_dim * sizeof(bf16_t);
+  if (lds > 64 * 1024) return set_error(SSD_ERANGE, "kv_compact: n_max=%d too large", n_max);
+  hipLaunchKernelGGL(kv_compact_kernel, dim3(layers * kv_heads), dim3(256), lds, stream, (bf16_t*)k_arena,
+                     (bf16_t*)vt_arena, kv_heads, head_dim, max_len, start, src, n_dev, n_max);
+  return check_launch("kv_compact");
+}
+
+SSD_API int ssd_row_topk_bf16(const uint16_t* logits, int64_t ld, int M, int N, int k, int mode,
+                              const int32_t* vocab_ids, int32_t* out_tok, float* out_val, float* out_lse,
+                              hipStream_t stream) {
+  if (!logits || !out_tok || M < 0 || N <= 0 || k < 1 || k > TOPK_MAX || k > N || (mode != 0 && mode != 1))
+    return set_error(SSD_EINVAL, "row_topk: bad arguments (k=%d, N=%d, mode=%d)", k, N, mode);
+  if (ld % 8 || ((uintptr_t)logits & 15)) return set_error(SSD_EINVAL, "row_topk: logits must be 16-byte aligned");
+  if (M == 0) return SSD_OK;
+  hipLaunchKernelGGL(row_topk_kernel, dim3(M), dim3(256), 0, stream, logits, ld, N, k, mode, vocab_ids, out_tok,
+                     out_val, out_lse);
+  return check_launch("row_topk");
+}

@@ -1,0 +1,254 @@
+// Device-resident speculation tree: level expansion, max_nodes pruning, verify
+// inputs and greedy acceptance. These replace the host loops of
+// ssd/engine/tree_drafter.py:147-208 and ssd/engine/verify.py:32-57 so that a
+// round needs no host round trip until its committed tokens are read back.
+//
+// Ordering rules are the reference's, restated:
+// * candidates of a level sort by cumulative score (double), ties keeping the
+//   order (frontier position, proposal rank) -- Python's stable sort of
+//   tree_drafter.py:172;
+// * the final cut sorts by (-score, depth), ties keeping node index order
+//   (tree_drafter.py:203), then closes the kept set under ancestors and
+//   renumbers it in original order (tree_drafter.py:80-95, 204-207);
+// * greedy acceptance walks root -> children in rank order, taking the child
+//   whose token equals the target argmax (verify.py:45-57).
+// Each step is one small workgroup: ranks are computed by counting (every
+// thread compares its candidate against all others), which is exact and
+// deterministic.
+#include "common.h"
+
+#include <math.h>
+
+namespace ssd {
+
+constexpr int TREE_MAXDEPTH = 32;
+constexpr int TREE_CAP = 1024;
+constexpr int ROW_MAXD = 32;  // ancestors per row (matches the attention gather list)
+
+}  // namespace ssd
+
+namespace ssd {
+
+__global__ __launch_bounds__(1024) void tree_level_kernel(SsdTree t, int d, const int* __restrict__ cand_tok,
+                                                          const float* __restrict__ cand_lp, int k, int width,
+                                                          int feed, int root_pos, int tree_start, int past,
+                                                          SsdRows rows, int rows_max) {
+  __shared__ double sc[TREE_CAP];
+  __shared__ int vd[TREE_CAP];
+  __shared__ int s_nvalid;
+  const int n0 = t.meta[0];
+  const int F = d == 0 ? 1 : t.meta[1 + TREE_MAXDEPTH + (d - 1)];
+  const int prev_start = d == 0 ? 0 : t.meta[1 + (d - 1)];
+  const int C = F * k;
+  const int c = threadIdx.x;
+  if (c == 0) s_nvalid = 0;
+  int parent = -1, tok = -1;
+  double score = -INFINITY;
+  if (c < C) {
+    const int f = c / k;
+    parent = d == 0 ? -1 : prev_start + f;
+    tok = cand_tok[c];
+    if (tok >= 0) score = (parent < 0 ? 0.0 : t.scores[parent]) + (double)cand_lp[c];
+    sc[c] = score;
+    vd[c] = tok >= 0;
+  }
+  __syncthreads();
+  if (c < C && tok >= 0) atomicAdd(&s_nvalid, 1);
+  int rank = 0;
+  if (c < C && tok >= 0) {
+    for (int o = 0; o < C; ++o)
+      if (vd[o] && (sc[o] > score || (sc[o] == score && o < c))) ++rank;
+  }
+  __syncthreads();
+  const int nvalid = s_nvalid;
+  const int n_level = (width > 0 && width < nvalid) ? width : nvalid;
+  if (c < C && tok >= 0 && rank < n_level && n0 + rank < t.cap) {
+    const int node = n0 + rank;
+    t.tokens[node] = tok;
+    t.parents[node] = parent;
+    t.depths[node] = d + 1;
+    t.scores[node] = score;
+    t.ranks[node] = c % k;
+    t.draft_pos[node] = feed ? past + rank : -1;
+  }
+  __syncthreads();
+  if (c == 0) {
+    t.meta[0] = min(n0 + n_level, t.cap);
+    t.meta[1 + d] = n0;
+    t.meta[1 + TREE_MAXDEPTH + d] = n_level;
+  }
+  if (feed && c < rows_max) {
+    const int j = c;
+    rows.pos[j] = root_pos + d + 1;
+    rows.slot[j] = past + j;
+    rows.prefix[j] = tree_start;
+    int* anc = rows.anc + (size_t)j * ROW_MAXD;
+    if (j < n_level && n0 + j < t.cap) {
+      int cur = n0 + j;
+      rows.ids[j] = t.tokens[cur];
+      rows.depth[j] = d + 1;
+      for (int i = d; i >= 0 && cur >= 0; --i) {
+        anc[i] = t.draft_pos[cur];
+        cur = t.parents[cur];
+      }
+    } else {  // padding row (fewer candidates than the launch assumed): attends the prefix only
+      rows.ids[j] = 0;
+      rows.depth[j] = 0;
+    }
+  }
+}
+
+__global__ __launch_bounds__(1024) void tree_finalize_kernel(SsdTree t, int max_nodes, int committed,
+                                                             const int* __restrict__ root_token, SsdRows rows,
+                                                             int rows_max) {
+  __shared__ int keep[TREE_CAP];
+  __shared__ int newidx[TREE_CAP];
+  const int n = t.meta[0];
+  const int i = threadIdx.x;
+  const bool prune = max_nodes > 0 && n > max_nodes;
+  if (i < n) {
+    int k = 1;
+    if (prune) {
+      const double s = t.scores[i];
+      const int dep = t.depths[i];
+      int rank = 0;
+      for (int o = 0; o < n; ++o) {
+        const double so = t.scores[o];
+        const int dpo = t.depths[o];
+        if (so > s || (so == s && (dpo < dep || (dpo == dep && o < i)))) ++rank;
+      }
+      k = rank < max_nodes;
+    }
+    keep[i] = k;
+  }
+  __syncthreads();
+  // Ancestor closure (a no-op unless float ties broke it; kept for parity with the reference).
+  if (i < n && keep[i]) {
+    int p = t.parents[i];
+    for (int step = 0; p >= 0 && p < n && step < TREE_MAXDEPTH; ++step) {
+      keep[p] = 1;
+      p = t.parents[p];
+    }
+  }
+  __syncthreads();
+  if (i < n) {
+    int idx = 0;
+    for (int o = 0; o < i; ++o) idx += keep[o];
+    newidx[i] = idx;
+  }
+  __syncthreads();
+  int vn = 0;
+  for (int o = 0; o < n; ++o) vn += keep[o];
+  if (i < n && keep[i]) {
+    const int v = newidx[i];
+    t.vtokens[v] = t.tokens[i];
+    const int p = t.parents[i];
+    t.vparents[v] = p < 0 ? -1 : newidx[p];
+    t.vdepths[v] = t.depths[i];
+    t.vranks[v] = t.ranks[i];
+    t.vorig[v] = i;
+  }
+  if (i == 0) t.vmeta[0] = vn;
+  __syncthreads();
+  // Verify rows (verify.py:32-42): row 0 is the root; row 1+v is verify node v.
+  if (i < rows_max) {
+    rows.slot[i] = committed + i;
+    rows.prefix[i] = committed + 1;
+    int* anc = rows.anc + (size_t)i * ROW_MAXD;
+    if (i == 0) {
+      rows.ids[0] = *root_token;
+      rows.pos[0] = committed;
+      rows.depth[0] = 0;
+    } else if (i <= vn) {
+      const int v = i - 1;
+      const int dep = t.vdepths[v];
+      rows.ids[i] = t.vtokens[v];
+      rows.pos[i] = committed + dep;
+      rows.depth[i] = dep;
+      int cur = v;
+      for (int q = min(dep, ROW_MAXD) - 1; q >= 0 && cur >= 0; --q) {
+        anc[q] = committed + 1 + cur;
+        cur = t.vparents[cur];
+      }
+    } else {
+      rows.ids[i] = 0;
+      rows.pos[i] = committed;
+      rows.depth[i] = 0;
+    }
+  }
+}
+
+// Greedy acceptance over the verify tree. argmax[r] is the target's first-index argmax
+// for verify row r. Writes result = [n_new, tok_0..tok_{n_new-1}], keep_src = compaction
+// sources ([committed] + [committed + 1 + accepted]), n_keep, and the next root token.
+__global__ void accept_greedy_kernel(SsdTree t, const int* __restrict__ argmax, int committed, int* result,
+                                     int* keep_src, int* n_keep, int* root_token) {
+  if (threadIdx.x != 0) return;
+  const int vn = t.vmeta[0];
+  int cur = -1, n_acc = 0;
+  int want;
+  for (int step = 0; step <= TREE_MAXDEPTH; ++step) {  // one accepted node per depth at most
+    want = argmax[cur + 1];
+    int best = -1, best_rank = 0x7fffffff;
+    for (int v = 0; v < vn; ++v)
+      if (t.vparents[v] == cur && t.vtokens[v] == want && t.vranks[v] < best_rank) {
+        best = v;
+        best_rank = t.vranks[v];
+      }
+    if (best < 0) break;
+    result[1 + n_acc] = t.vtokens[best];
+    keep_src[1 + n_acc] = committed + 1 + best;
+    ++n_acc;
+    cur = best;
+  }
+  result[1 + n_acc] = want;
+  result[0] = n_acc + 1;
+  keep_src[0] = committed;
+  *n_keep = n_acc + 1;
+  *root_token = want;
+}
+
+}  // namespace ssd
+
+using namespace ssd;
+
+SSD_API int ssd_tree_limits(int32_t* out) {
+  if (!out) return set_error(SSD_EINVAL, "tree_limits: null");
+  out[0] = TREE_CAP;
+  out[1] = TREE_MAXDEPTH;
+  out[2] = ROW_MAXD;
+  return SSD_OK;
+}
+
+SSD_API int ssd_tree_level(const SsdTree* tree, int d, const int32_t* cand_tok, const float* cand_lp, int F_max,
+                           int k, int width, int feed, int root_pos, int tree_start, int past, const SsdRows* rows,
+                           int rows_max, hipStream_t stream) {
+  if (!tree || !cand_tok || !cand_lp || (feed && !rows)) return set_error(SSD_EINVAL, "tree_level: null pointer");
+  if (d < 0 || d >= TREE_MAXDEPTH || d + 1 > ROW_MAXD) return set_error(SSD_ERANGE, "tree_level: depth %d too deep", d);
+  if (F_max * k > TREE_CAP || k < 1) return set_error(SSD_ERANGE, "tree_level: %d x %d candidates > %d", F_max, k, TREE_CAP);
+  if (tree->cap > TREE_CAP) return set_error(SSD_ERANGE, "tree_level: capacity %d > %d", tree->cap, TREE_CAP);
+  if (feed && (rows_max > rows->cap || rows_max > TREE_CAP)) return set_error(SSD_ERANGE, "tree_level: rows_max too big");
+  SsdRows r = feed ? *rows : SsdRows{};
+  hipLaunchKernelGGL(tree_level_kernel, dim3(1), dim3(1024), 0, stream, *tree, d, cand_tok, cand_lp, k, width, feed,
+                     root_pos, tree_start, past, r, feed ? rows_max : 0);
+  return check_launch("tree_level");
+}
+
+SSD_API int ssd_tree_finalize(const SsdTree* tree, int max_nodes, int committed, const int32_t* root_token,
+                              const SsdRows* rows, int rows_max, hipStream_t stream) {
+  if (!tree || !root_token || !rows) return set_error(SSD_EINVAL, "tree_finalize: null pointer");
+  if (rows_max > rows->cap || rows_max > TREE_CAP + 1 || tree->cap > TREE_CAP)
+    return set_error(SSD_ERANGE, "tree_finalize: rows_max %d too big", rows_max);
+  hipLaunchKernelGGL(tree_finalize_kernel, dim3(1), dim3(1024), 0, stream, *tree, max_nodes, committed, root_token,
+                     *rows, rows_max);
+  return check_launch("tree_finalize");
+}
+
+SSD_API int ssd_accept_greedy(const SsdTree* tree, const int32_t* argmax, int committed, int32_t* result,
+                              int32_t* keep_src, int32_t* n_keep, int32_t* root_token, hipStream_t stream) {
+  if (!tree || !argmax || !result || !keep_src || !n_keep || !root_token)
+    return set_error(SSD_EINVAL, "accept_greedy: null pointer");
+  hipLaunchKernelGGL(accept_greedy_kernel, dim3(1), dim3(64), 0, stream, *tree, argmax, committed, result, keep_src,
+                     n_keep, root_token);
+  return check_launch("accept_greedy");
+}

@@ -1,0 +1,87 @@
+"""Loader for the gfx950 C-ABI library (``libssd_mi355x.so``, declared in include/ssd_mi355x.h).
+
+There is no fallback: if the library is missing or cannot be loaded, every hot-path call
+raises. Build it with ``python subnetwork-speculative-decoding_amd/build.py``.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libssd_mi355x.so")
+
+P = C.c_void_p
+I32 = C.c_int
+I64 = C.c_int64
+F32 = C.c_float
+
+
+class SsdTree(C.Structure):
+    _fields_ = [(n, P) for n in ("tokens", "parents", "depths", "ranks", "draft_pos", "scores", "meta", "vtokens",
+                                 "vparents", "vdepths", "vranks", "vorig", "vmeta")] + [("cap", C.c_int32)]
+
+
+class SsdRows(C.Structure):
+    _fields_ = [(n, P) for n in ("ids", "pos", "slot", "prefix", "depth", "anc")] + [("cap", C.c_int32)]
+
+
+_PROTOS = {
+    "ssd_last_error": (C.c_char_p, []),
+    "ssd_abi_version": (I32, []),
+    "ssd_device_arch": (I32, [C.c_char_p, I32]),
+    "ssd_packed_weight_elems": (I64, [I32, I32]),
+    "ssd_pack_weight_bf16": (I32, [P, I64, I32, I32, P, I32, P, P]),
+    "ssd_gemm_bf16": (I32, [P, I64, I32, P, I32, I32, P, I64, P, I32, P, I64, P]),
+    "ssd_gemm_swiglu_bf16": (I32, [P, I64, I32, P, I32, I32, P, I64, P, P, P]),
+    "ssd_gemm_qkv_rope_bf16": (I32, [P, I64, I32, P, I32, I32, I32, I32, P, P, I64, P, P, P, I64, P, P, I64, P]),
+    "ssd_attn_workspace_floats": (I32, [I32, I32, I32, I64]),
+    "ssd_attn_max_depth": (I32, []),
+    "ssd_tree_attention_bf16": (I32, [P, I64, I32, I32, I32, I32, P, P, I64, P, P, P, I32, I32, F32, P, I64, P,
+                                      I64, P]),
+    "ssd_rmsnorm_bf16": (I32, [P, I64, I32, I32, P, F32, P, I64, P]),
+    "ssd_embed_bf16": (I32, [P, I32, P, I64, I32, P, I64, P]),
+    "ssd_kv_compact_bf16": (I32, [P, P, I32, I32, I32, I64, I32, P, P, I32, P]),
+    "ssd_row_topk_bf16": (I32, [P, I64, I32, I32, I32, I32, P, P, P, P, P]),
+    "ssd_tree_limits": (I32, [P]),
+    "ssd_tree_level": (I32, [C.POINTER(SsdTree), I32, P, P, I32, I32, I32, I32, I32, I32, I32, C.POINTER(SsdRows),
+                             I32, P]),
+    "ssd_tree_finalize": (I32, [C.POINTER(SsdTree), I32, I32, P, C.POINTER(SsdRows), I32, P]),
+    "ssd_accept_greedy": (I32, [C.POINTER(SsdTree), P, I32, P, P, P, P, P]),
+}
+
+EXPORTED = tuple(_PROTOS)
+
+_lib = None
+
+
+class SsdError(RuntimeError):
+    pass
+
+
+def load(path: str = LIB_PATH):
+    """Load the library (once). Raises if it is absent: there is no non-HIP path."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise ImportError(f"{path} not found: build it with `python subnetwork-speculative-decoding_amd/build.py`")
+    lib = C.CDLL(path)
+    for name, (res, args) in _PROTOS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def call(name: str, *args) -> int:
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.ssd_last_error().decode(errors="replace")
+        if rc == 1:
+            raise ValueError(f"{name}: {msg}")
+        raise SsdError(f"{name}: {msg}")
+    return rc

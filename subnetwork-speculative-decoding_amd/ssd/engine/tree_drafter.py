@@ -1,0 +1,212 @@
+"""Dynamic tree drafting with the sub-network draft, built on the device.
+
+Same algorithm and API as the reference's ssd/engine/tree_drafter.py: feed the root; at
+depth d every kept node proposes ``branch[d]`` children (top log-probs for greedy); the
+``width[d]`` best by cumulative draft log-prob are kept and, unless d is the last depth,
+fed through the draft in one batched forward where each attends to the committed prefix
+and its own ancestors; finally the best ``max_nodes`` nodes go to verification.
+
+Here every step of that loop is a kernel: the draft forward, the draft head with the fused
+log-softmax top-k (``ssd_row_topk_bf16``), and the level expansion / width cut / next-level
+attention rows (``ssd_tree_level``), then the max_nodes cut and the verify rows
+(``ssd_tree_finalize``). No host round trip happens inside a round.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Optional
+
+import torch
+
+from ssd import _lib, ops
+from ssd.config import DraftingConfig
+from ssd.engine.kv_cache import KVCache
+
+ROOT = -1
+TREE_CAP = 1024
+ROW_CAP = 64
+TOPK_MAX = 16
+
+
+def warp_probs(logits: torch.Tensor, temperature: float, top_p: float) -> torch.Tensor:
+    """Temperature + nucleus warp (reference tree_drafter.py:34-45), as a tensor function for
+    callers of the reference API; the sampling engine applies the same rule in its kernels."""
+    probs = torch.softmax(logits.float() / temperature, dim=-1)
+    if top_p < 1.0:
+        sp, idx = probs.sort(dim=-1, descending=True)
+        sp = sp.masked_fill(sp.cumsum(-1) - sp > top_p, 0.0)
+        probs = torch.zeros_like(probs).scatter(-1, idx, sp)
+        probs = probs / probs.sum(-1, keepdim=True)
+    return probs
+
+
+@dataclass
+class DraftTree:
+    """Host view of a tree (reference tree_drafter.py:48-95)."""
+    tokens: list = field(default_factory=list)
+    parents: list = field(default_factory=list)
+    depths: list = field(default_factory=list)
+    scores: list = field(default_factory=list)
+    ranks: list = field(default_factory=list)
+    draft_pos: list = field(default_factory=list)
+    child_q: dict = field(default_factory=dict)
+    cache_start: int = 0
+
+    def __len__(self) -> int:
+        return len(self.tokens)
+
+    def children(self) -> dict:
+        out: dict = {}
+        for i, p in enumerate(self.parents):
+            out.setdefault(p, []).append(i)
+        for kids in out.values():
+            kids.sort(key=lambda i: self.ranks[i])
+        return out
+
+    def ancestors(self, i: int) -> list:
+        path = []
+        while i != ROOT:
+            path.append(i)
+            i = self.parents[i]
+        return path[::-1]
+
+    def subset(self, keep) -> "DraftTree":
+        keep = sorted(keep)
+        remap = {old: new for new, old in enumerate(keep)}
+        remap[ROOT] = ROOT
+        t = DraftTree(cache_start=self.cache_start)
+        for old in keep:
+            t.tokens.append(self.tokens[old])
+            t.parents.append(remap[self.parents[old]])
+            t.depths.append(self.depths[old])
+            t.scores.append(self.scores[old])
+            t.ranks.append(self.ranks[old])
+            t.draft_pos.append(self.draft_pos[old])
+        t.child_q = {remap[p]: q for p, q in self.child_q.items() if p in remap}
+        return t
+
+
+class DeviceTree:
+    """Device buffers of one tree (include/ssd_mi355x.h SsdTree)."""
+
+    def __init__(self, device, vmeta: Optional[torch.Tensor] = None, cap: int = TREE_CAP):
+        i32 = dict(dtype=torch.int32, device=device)
+        self.cap = cap
+        self.buf = torch.zeros(11, cap, **i32)
+        (self.tokens, self.parents, self.depths, self.ranks, self.draft_pos, self.vtokens, self.vparents,
+         self.vdepths, self.vranks, self.vorig, _) = self.buf.unbind(0)
+        self.scores = torch.zeros(cap, dtype=torch.float64, device=device)
+        self.meta = torch.zeros(1 + 2 * 32, **i32)
+        self.vmeta = vmeta if vmeta is not None else torch.zeros(1, **i32)
+        p = lambda t: t.data_ptr()
+        self.struct = _lib.SsdTree(p(self.tokens), p(self.parents), p(self.depths), p(self.ranks), p(self.draft_pos),
+                                   p(self.scores), p(self.meta), p(self.vtokens), p(self.vparents), p(self.vdepths),
+                                   p(self.vranks), p(self.vorig), p(self.vmeta), cap)
+
+    def reset(self) -> None:
+        self.meta.zero_()
+
+    def to_host(self) -> DraftTree:
+        """The finalized (verify) tree as a DraftTree (synchronises)."""
+        vn = int(self.vmeta[0])
+        orig = self.vorig[:vn].long()
+        return DraftTree(tokens=self.vtokens[:vn].tolist(), parents=self.vparents[:vn].tolist(),
+                         depths=self.vdepths[:vn].tolist(), scores=self.scores[orig].tolist(),
+                         ranks=self.vranks[:vn].tolist(), draft_pos=self.draft_pos[orig].tolist())
+
+
+class TreeDrafter:
+    def __init__(self, draft, cfg: DraftingConfig):
+        cfg.validate()
+        self.draft, self.cfg = draft, cfg
+        self.branch = cfg.per_depth(cfg.branch, "branch")
+        self.width = cfg.per_depth(cfg.width, "width")
+        self.greedy = cfg.temperature == 0
+        self.levels = self.max_nodes_per_level()
+        if max(self.branch) > TOPK_MAX:
+            raise ValueError(f"drafting.branch entries must be <= {TOPK_MAX} on this build")
+        if cfg.depth > 32:
+            raise ValueError("drafting.depth must be <= 32 on this build")
+        fed = self.levels[:-1]
+        if fed and max(fed) > ROW_CAP:
+            raise ValueError(f"a fed level has {max(fed)} nodes > {ROW_CAP}; set drafting.width")
+        if sum(self.levels) > TREE_CAP or max([1] + fed) * max(self.branch) > TREE_CAP:
+            raise ValueError(f"tree of {sum(self.levels)} nodes exceeds {TREE_CAP}")
+        if self.max_verify_nodes() + 1 > ROW_CAP:
+            raise ValueError(f"{self.max_verify_nodes()} verify nodes > {ROW_CAP - 1}; set drafting.max_nodes")
+
+    def max_nodes_per_level(self) -> list:
+        return self.cfg.level_sizes()
+
+    def max_tree_cache(self) -> int:
+        """Draft-cache slots one round uses after the root (the last level is never fed)."""
+        return sum(self.max_nodes_per_level()[:-1])
+
+    def max_verify_nodes(self) -> int:
+        total = sum(self.max_nodes_per_level())
+        return min(total, self.cfg.max_nodes) if self.cfg.max_nodes else total
+
+    # ------------------------------------------------------------------ device
+    def build_device(self, cache: KVCache, root_rows, root_pos: int, tree: DeviceTree, level_rows, cand_tok,
+                     cand_lp, ws) -> None:
+        """Enqueue the whole draft phase for the root held in ``root_rows.ids[0]``; leaves the
+        unpruned tree in ``tree`` (no host synchronisation)."""
+        if not self.greedy:
+            raise NotImplementedError("sampling drafts run in the sampling engine")
+        draft = self.draft
+        tree.reset()
+        tree_start = root_pos + 1
+        cache.check_room(tree_start + self.max_tree_cache())
+        root_rows.upload(None, [root_pos], [root_pos], [root_pos + 1], [0])
+        h = draft.run_rows(root_rows, 1, root_pos + 1, root_pos + 1, cache, ws)
+        logits = draft.head(draft.final_norm(h, 1, ws.x), 1, ws)
+        n = logits.shape[1]
+        ops.row_topk(logits, 1, n, self.branch[0], 1, draft._vocab_ids_i32, cand_tok, cand_lp)
+        past = tree_start
+        for d in range(self.cfg.depth):
+            feed = d < self.cfg.depth - 1
+            f_max = 1 if d == 0 else self.levels[d - 1]
+            m = self.levels[d]
+            _lib.call("ssd_tree_level", tree.struct, d, cand_tok.data_ptr(), cand_lp.data_ptr(), f_max,
+                      self.branch[d], self.width[d] or 0, int(feed), root_pos, tree_start, past,
+                      level_rows.struct, m if feed else 0, ops.stream())
+            if not feed:
+                break
+            h = draft.run_rows(level_rows, m, tree_start, tree_start + d + 1, cache, ws)
+            logits = draft.head(draft.final_norm(h, m, ws.x), m, ws)
+            ops.row_topk(logits, m, n, self.branch[d + 1], 1, draft._vocab_ids_i32, cand_tok, cand_lp)
+            past += m
+        cache.seq_len = past
+
+    def finalize_device(self, tree: DeviceTree, committed: int, root_rows, verify_rows) -> int:
+        """max_nodes cut + verify rows; returns the verify row count used for the launch."""
+        rows = self.max_verify_nodes() + 1
+        _lib.call("ssd_tree_finalize", tree.struct, self.cfg.max_nodes or 0, committed, root_rows.ids.data_ptr(),
+                  verify_rows.struct, rows, ops.stream())
+        return rows
+
+    # -------------------------------------------------------------- reference API
+    @torch.no_grad()
+    def build(self, cache: KVCache, pending: torch.Tensor, root_pos: int, generator=None) -> DraftTree:
+        """Reference signature (tree_drafter.py:147-208): ``pending`` [1, n] committed tokens not
+        yet in the cache (the last is the root at ``root_pos``). Returns the pruned tree."""
+        from ssd.models.subnetwork_draft import Rows
+
+        pend = torch.as_tensor(pending).reshape(-1).tolist()
+        dev = self.draft.model.device
+        if len(pend) > 1:  # earlier pending tokens go in first, as an ordinary causal chunk
+            self.draft(torch.tensor([pend[:-1]]), torch.arange(root_pos - len(pend) + 1, root_pos)[None], cache,
+                       compute_logits=False)
+        ws = self.draft.workspace()
+        root_rows, level_rows = Rows(ROW_CAP, dev), Rows(ROW_CAP, dev)
+        root_rows.ids[:1].fill_(pend[-1])
+        tree = DeviceTree(dev)
+        cand_tok = torch.zeros(TREE_CAP, dtype=torch.int32, device=dev)
+        cand_lp = torch.zeros(TREE_CAP, dtype=torch.float32, device=dev)
+        self.build_device(cache, root_rows, root_pos, tree, level_rows, cand_tok, cand_lp, ws)
+        verify_rows = Rows(ROW_CAP, dev)
+        self.finalize_device(tree, root_pos, root_rows, verify_rows)
+        out = tree.to_host()
+        out.cache_start = root_pos + 1
+        return out

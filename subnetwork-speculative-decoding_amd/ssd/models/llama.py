@@ -1,0 +1,226 @@
+"""Llama target weights in the MI355X layout.
+
+The reference keeps HF ``LlamaForCausalLM`` modules and calls their ``nn.Linear`` layers
+(ssd/models/subnetwork_draft.py:80-89, 193-246). Here the same weights live once in HBM in
+the layout the gfx950 kernels stream:
+
+* per layer: q/k/v fused into one packed matrix whose 16-row tiles pair rotary dims d and
+  d + hd/2 (so RoPE and the KV-cache write run in the GEMM epilogue); gate/up fused with 8
+  gate rows + the matching 8 up rows per tile (SwiGLU in the epilogue); o and down packed
+  as-is; RMSNorm weights as plain bf16 vectors;
+* the embedding table row-major (a gather), the lm_head packed (a weight-streaming GEMM);
+* RoPE cos/sin tables [positions, hd/2] computed in fp32 and rounded to bf16 exactly as HF's
+  rotary embedding does.
+
+Packed weights are built from an HF model / state dict (copied once, layer by layer) or
+generated directly on the GPU for synthetic benchmarks (``synthetic``), never duplicated.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from ssd import ops
+
+BF16 = torch.bfloat16
+
+
+@dataclass
+class LlamaShape:
+    hidden: int
+    layers: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    inter: int
+    vocab: int
+    eps: float = 1e-6
+    theta: float = 500000.0
+
+    @classmethod
+    def from_hf_config(cls, c) -> "LlamaShape":
+        hd = getattr(c, "head_dim", None) or c.hidden_size // c.num_attention_heads
+        rp = getattr(c, "rope_parameters", None) or {}
+        theta = rp.get("rope_theta", getattr(c, "rope_theta", 10000.0))
+        rtype = rp.get("rope_type", "default")
+        if rtype != "default":
+            raise ValueError(f"rope_type {rtype!r} is not supported (default RoPE only)")
+        return cls(c.hidden_size, c.num_hidden_layers, c.num_attention_heads, c.num_key_value_heads, hd,
+                   c.intermediate_size, c.vocab_size, float(c.rms_norm_eps), float(theta))
+
+    def validate(self) -> None:
+        if self.heads % self.kv_heads:
+            raise ValueError("heads must be a multiple of kv_heads")
+        if self.head_dim not in (32, 64, 128):
+            raise ValueError(f"head_dim {self.head_dim} unsupported (32, 64, 128)")
+        for name in ("hidden", "inter"):
+            if getattr(self, name) % 32:
+                raise ValueError(f"{name}={getattr(self, name)} must be a multiple of 32")
+
+
+class _Cfg:
+    """HF-config-like view (num_hidden_layers, hidden_size, ...) for API compatibility."""
+
+    def __init__(self, s: LlamaShape):
+        self.num_hidden_layers = s.layers
+        self.hidden_size = s.hidden
+        self.num_attention_heads = s.heads
+        self.num_key_value_heads = s.kv_heads
+        self.head_dim = s.head_dim
+        self.intermediate_size = s.inter
+        self.vocab_size = s.vocab
+        self.rms_norm_eps = s.eps
+        self.rope_theta = s.theta
+
+
+def qkv_row_map(heads: int, kv_heads: int, hd: int) -> torch.Tensor:
+    """Packed row -> row of cat(q, k, v): per head, tiles of (8 dims of the first rotary half,
+    the same 8 dims of the second half)."""
+    half, rows = hd // 2, []
+    for base, nh in ((0, heads), (heads * hd, kv_heads), ((heads + kv_heads) * hd, kv_heads)):
+        for h in range(nh):
+            for p in range(hd // 16):
+                b = base + h * hd + p * 8
+                rows += list(range(b, b + 8)) + list(range(b + half, b + half + 8))
+    return torch.tensor(rows, dtype=torch.int32)
+
+
+def gate_up_row_map(inter: int) -> torch.Tensor:
+    """Packed row -> row of cat(gate, up): tile i = gate rows [8i, 8i+8) then up rows [8i, 8i+8)."""
+    i = torch.arange(inter // 8, dtype=torch.int32)[:, None] * 8 + torch.arange(8, dtype=torch.int32)[None]
+    return torch.cat([i, i + inter], 1).reshape(-1)
+
+
+def rope_tables(positions: int, hd: int, theta: float, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """cos/sin [positions, hd/2] as HF computes them (fp32 inv_freq and angles, then bf16)."""
+    inv = 1.0 / (theta ** (torch.arange(0, hd, 2, dtype=torch.int64).float() / hd))
+    ang = torch.arange(positions, dtype=torch.float32)[:, None] * inv[None, :]
+    return ang.cos().to(BF16).to(device).contiguous(), ang.sin().to(BF16).to(device).contiguous()
+
+
+class Layer:
+    __slots__ = ("wqkv", "wo", "wgu", "wd", "ln1", "ln2")
+
+
+class MI355XLlama:
+    """A Llama target resident in HBM in the kernels' layout. ``config`` mimics the HF config."""
+
+    def __init__(self, shape: LlamaShape, device="cuda"):
+        shape.validate()
+        self.shape = shape
+        self.config = _Cfg(shape)
+        self.device = torch.device(device)
+        self.embed: Optional[torch.Tensor] = None
+        self.lm_head: Optional[torch.Tensor] = None
+        self.norm: Optional[torch.Tensor] = None
+        self.layers: list[Layer] = []
+        self._cos = self._sin = None
+        self._lm_head_rows: Optional[torch.Tensor] = None  # row-major lm_head kept only when requested
+
+    # ------------------------------------------------------------ construction
+    def _put(self, t: torch.Tensor) -> torch.Tensor:
+        return t.detach().to(device=self.device, dtype=BF16).contiguous()
+
+    def _set_layer(self, get) -> None:
+        s = self.shape
+        L = Layer()
+        qkv = torch.cat([self._put(get("self_attn.q_proj.weight")), self._put(get("self_attn.k_proj.weight")),
+                         self._put(get("self_attn.v_proj.weight"))], 0)
+        L.wqkv = ops.pack_weight(qkv, qkv_row_map(s.heads, s.kv_heads, s.head_dim))
+        del qkv
+        L.wo = ops.pack_weight(self._put(get("self_attn.o_proj.weight")))
+        gu = torch.cat([self._put(get("mlp.gate_proj.weight")), self._put(get("mlp.up_proj.weight"))], 0)
+        L.wgu = ops.pack_weight(gu, gate_up_row_map(s.inter))
+        del gu
+        L.wd = ops.pack_weight(self._put(get("mlp.down_proj.weight")))
+        L.ln1 = self._put(get("input_layernorm.weight"))
+        L.ln2 = self._put(get("post_attention_layernorm.weight"))
+        self.layers.append(L)
+
+    @classmethod
+    def from_state_dict(cls, sd: dict, shape: LlamaShape, device="cuda", keep_lm_head_rows: bool = False):
+        m = cls(shape, device)
+        m.embed = m._put(sd["model.embed_tokens.weight"])
+        for i in range(shape.layers):
+            m._set_layer(lambda n, i=i: sd[f"model.layers.{i}.{n}"])
+        m.norm = m._put(sd["model.norm.weight"])
+        head = sd.get("lm_head.weight", sd["model.embed_tokens.weight"])
+        head = m._put(head)
+        m.lm_head = ops.pack_weight(head)
+        if keep_lm_head_rows:
+            m._lm_head_rows = head
+        torch.cuda.synchronize(m.device)
+        return m
+
+    @classmethod
+    def from_hf(cls, model, device="cuda", keep_lm_head_rows: bool = False) -> "MI355XLlama":
+        return cls.from_state_dict(model.state_dict(), LlamaShape.from_hf_config(model.config), device,
+                                   keep_lm_head_rows)
+
+    @classmethod
+    def synthetic(cls, shape: LlamaShape, seed: int = 0, std: float = 0.02, device="cuda") -> "MI355XLlama":
+        """Random-init weights N(0, std) (norms = 1) generated on the GPU, one seeded generator
+        per tensor (seed * 1000 + tensor index), so the model is reproducible on one torch build."""
+        m = cls(shape, device)
+        counter = [0]
+
+        def rnd(*size):
+            g = torch.Generator(device=m.device).manual_seed(seed * 1000 + counter[0])
+            counter[0] += 1
+            return (torch.randn(*size, generator=g, device=m.device, dtype=torch.float32) * std).to(BF16)
+
+        s = shape
+        m.embed = rnd(s.vocab, s.hidden)
+        ones = torch.ones(s.hidden, dtype=BF16, device=m.device)
+        for _ in range(s.layers):
+            w = {
+                "self_attn.q_proj.weight": rnd(s.heads * s.head_dim, s.hidden),
+                "self_attn.k_proj.weight": rnd(s.kv_heads * s.head_dim, s.hidden),
+                "self_attn.v_proj.weight": rnd(s.kv_heads * s.head_dim, s.hidden),
+                "self_attn.o_proj.weight": rnd(s.hidden, s.heads * s.head_dim),
+                "mlp.gate_proj.weight": rnd(s.inter, s.hidden),
+                "mlp.up_proj.weight": rnd(s.inter, s.hidden),
+                "mlp.down_proj.weight": rnd(s.hidden, s.inter),
+                "input_layernorm.weight": ones,
+                "post_attention_layernorm.weight": ones,
+            }
+            m._set_layer(w.__getitem__)
+            del w
+        m.norm = ones.clone()
+        m.lm_head = ops.pack_weight(rnd(s.vocab, s.hidden))
+        torch.cuda.synchronize(m.device)
+        return m
+
+    # ---------------------------------------------------------------- helpers
+    def rope(self, max_pos: int) -> tuple[torch.Tensor, torch.Tensor]:
+        if self._cos is None or self._cos.shape[0] < max_pos:
+            n = max(max_pos, 4096)
+            self._cos, self._sin = rope_tables(n, self.shape.head_dim, self.shape.theta, self.device)
+        return self._cos, self._sin
+
+    def weight_bytes(self, layers=None) -> int:
+        """Packed bytes streamed per forward for ``layers`` (default all) plus the full lm_head."""
+        idx = range(self.shape.layers) if layers is None else layers
+        b = sum(self.layers[i].wqkv.numel() + self.layers[i].wo.numel() + self.layers[i].wgu.numel()
+                + self.layers[i].wd.numel() for i in idx)
+        return 2 * (b + self.lm_head.numel())
+
+    def lm_head_rows(self, ids: torch.Tensor) -> torch.Tensor:
+        """Row-major lm_head rows ``ids`` (for a vocabulary-subset head). Unpacks from the
+        packed tiles when the row-major copy was not kept."""
+        if self._lm_head_rows is not None:
+            return self._lm_head_rows.index_select(0, ids.to(self.device))
+        return unpack_rows(self.lm_head, self.shape.vocab, self.shape.hidden, ids.to(self.device))
+
+
+def unpack_rows(packed: torch.Tensor, n: int, k: int, ids: torch.Tensor) -> torch.Tensor:
+    """Rows ``ids`` of the row-major matrix held in MFMA tiles (inverse of the identity packing)."""
+    kb = (k + 31) // 32
+    t = packed.view(-1, kb, 4, 16, 8)  # [nb, kb, lane/16, lane%16, 8]
+    nb, r = ids // 16, ids % 16
+    rows = t[nb.long(), :, :, r.long(), :]  # [len, kb, 4, 8]
+    return rows.reshape(ids.numel(), kb * 32)[:, :k].contiguous()

@@ -1,0 +1,397 @@
+"""Draft model = a frozen subset of the target's layers joined by bridges, on gfx950 kernels.
+
+API of the reference's ``SubnetworkDraftModel`` (ssd/models/subnetwork_draft.py:101-357):
+``forward(input_ids, position_ids, past_key_values, tree_attention_mask, logits_to_keep,
+compute_logits, ...) -> DraftOutput``, ``new_cache``, ``set_vocab_subset``, bridge
+planning/placement, ``save_bridges``/``load_bridges``. With every layer selected it is the
+target (``TargetRunner``), exactly as in the reference.
+
+Each forward runs, per selected layer: [bridge] -> RMSNorm -> fused q/k/v GEMM with RoPE
+and the KV-cache write in its epilogue -> tree attention (+ split combine) -> o GEMM with
+the residual add in its epilogue -> RMSNorm -> gate/up GEMM with SwiGLU in its epilogue ->
+down GEMM with the residual add. Then [pre-norm bridge] -> RMSNorm -> lm_head GEMM (full
+vocabulary, or the draft-vocab subset). Every step is a hand-written HIP kernel; torch
+only owns the buffers.
+
+Attention rows: a dense boolean mask (True = attend) is turned into per-row
+(prefix length, ancestor slots) -- the reference's masks always have that shape: an
+all-true committed prefix plus each node's own ancestors (subnetwork_draft.py:165-191).
+"""
+
+from __future__ import annotations
+
+import os
+from dataclasses import dataclass, field
+from typing import Optional
+
+import torch
+import torch.nn as nn
+
+from ssd import _lib, ops
+from ssd.config import BridgeConfig, validate_layer_indices
+from ssd.engine.kv_cache import KVCache
+from ssd.models.bridges import TransitionBridge
+from ssd.models.llama import MI355XLlama
+
+MAXD = 32        # ancestors per row (ssd_attn_max_depth)
+CHUNK = 64       # rows per kernel launch chain (GEMM column tiles of 16 x 4)
+
+
+@dataclass
+class BridgeSpec:
+    name: str
+    src_boundary: int
+    tgt_boundary: int
+
+
+@dataclass
+class DraftOutput:
+    logits: Optional[torch.Tensor]
+    hidden_states: torch.Tensor
+    past_key_values: Optional[KVCache]
+    bridge_states: dict = field(default_factory=dict)
+    vocab_ids: Optional[torch.Tensor] = None
+    layer_inputs: dict = field(default_factory=dict)
+
+
+def plan_bridges(layer_indices: list, num_base_layers: int) -> list:
+    """Boundary i = residual stream entering base layer i (L = the final norm). A bridge maps
+    the boundary the draft has to the one the next selected module expects, wherever layers
+    are skipped (reference subnetwork_draft.py:61-73)."""
+    specs, have = [], 0
+    for idx in layer_indices:
+        if idx != have:
+            specs.append(BridgeSpec(f"into_{idx}", have, idx))
+        have = idx + 1
+    if have != num_base_layers:
+        specs.append(BridgeSpec("into_norm", have, num_base_layers))
+    return specs
+
+
+def required_boundaries(layer_indices: list, num_base_layers: int) -> set:
+    return {b for s in plan_bridges(layer_indices, num_base_layers) for b in (s.src_boundary, s.tgt_boundary)}
+
+
+def as_device_model(base) -> MI355XLlama:
+    """Accept our device model or an HF LlamaForCausalLM (packed once, cached on the object)."""
+    if isinstance(base, MI355XLlama):
+        return base
+    cached = getattr(base, "_ssd_mi355x", None)
+    if cached is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+        cached = MI355XLlama.from_hf(base, dev)
+        base._ssd_mi355x = cached
+    return cached
+
+
+class Rows:
+    """Device buffers describing the rows of one forward (include/ssd_mi355x.h SsdRows)."""
+
+    def __init__(self, cap: int, device):
+        self.cap = cap
+        self._pinned = torch.zeros(5 * cap + cap * MAXD, dtype=torch.int32, pin_memory=True)
+        self._flat = torch.zeros(5 * cap + cap * MAXD, dtype=torch.int32, device=device)
+        self.ids = self._flat[0:cap]
+        self.pos = self._flat[cap:2 * cap]
+        self.slot = self._flat[2 * cap:3 * cap]
+        self.prefix = self._flat[3 * cap:4 * cap]
+        self.depth = self._flat[4 * cap:5 * cap]
+        self.anc = self._flat[5 * cap:].view(cap, MAXD)
+        self.struct = _lib.SsdRows(self.ids.data_ptr(), self.pos.data_ptr(), self.slot.data_ptr(),
+                                   self.prefix.data_ptr(), self.depth.data_ptr(), self.anc.data_ptr(), cap)
+
+    def view(self, off: int) -> "_RowsView":
+        """Rows [off, cap) as a forward's rows (pointer offsets, no copy)."""
+        return _RowsView(self.ids[off:], self.pos[off:], self.slot[off:], self.prefix[off:], self.depth[off:],
+                         self.anc[off:])
+
+    def upload(self, ids, pos, slot, prefix, depth, anc=None) -> None:
+        """Fill rows [0, n) from host lists with one pinned async copy (the pinned staging buffer
+        is reused, so callers synchronise between uploads; the engine does, once per round)."""
+        n = len(pos)
+        if n > self.cap:
+            raise ValueError(f"{n} rows > capacity {self.cap}")
+        c = self.cap
+        p = self._pinned
+        if ids is not None:
+            p[0:n] = torch.as_tensor(ids, dtype=torch.int32)
+        p[c:c + n] = torch.as_tensor(pos, dtype=torch.int32)
+        p[2 * c:2 * c + n] = torch.as_tensor(slot, dtype=torch.int32)
+        p[3 * c:3 * c + n] = torch.as_tensor(prefix, dtype=torch.int32)
+        p[4 * c:4 * c + n] = torch.as_tensor(depth, dtype=torch.int32)
+        if anc is not None:
+            a = p[5 * c:].view(c, MAXD)
+            for r, lst in enumerate(anc):
+                if lst:
+                    a[r, :len(lst)] = torch.as_tensor(lst, dtype=torch.int32)
+        if ids is None:  # keep device ids (e.g. produced by a kernel)
+            self._flat[c:].copy_(p[c:], non_blocking=True)
+        else:
+            self._flat.copy_(p, non_blocking=True)
+
+
+@dataclass
+class _RowsView:
+    ids: torch.Tensor
+    pos: torch.Tensor
+    slot: torch.Tensor
+    prefix: torch.Tensor
+    depth: torch.Tensor
+    anc: torch.Tensor
+
+
+class Workspace:
+    """Activation buffers for forwards of up to ``m_cap`` rows."""
+
+    def __init__(self, model: MI355XLlama, m_cap: int, bridge_hidden: int = 0):
+        s, dev = model.shape, model.device
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        self.m_cap = m_cap
+        self.h = torch.zeros(m_cap, s.hidden, **bf)
+        self.x = torch.zeros(m_cap, s.hidden, **bf)
+        self.q = torch.zeros(m_cap, s.heads * s.head_dim, **bf)
+        self.attn = torch.zeros(m_cap, s.heads * s.head_dim, **bf)
+        self.mlp = torch.zeros(m_cap, s.inter, **bf)
+        bh = max(bridge_hidden, 32)
+        self.mids = [torch.zeros(m_cap, bh, **bf), torch.zeros(m_cap, bh, **bf)]
+        self.ws = torch.zeros(0, dtype=torch.float32, device=dev)
+        self.logits = torch.zeros(0, **bf)
+
+    def attn_ws(self, model: MI355XLlama, max_len: int) -> torch.Tensor:
+        s = model.shape
+        n = ops.attn_workspace_floats(self.m_cap, s.heads, s.head_dim, max_len)
+        if self.ws.numel() < n:
+            self.ws = torch.zeros(n, dtype=torch.float32, device=model.device)
+        return self.ws
+
+    def logits_buf(self, m: int, n: int) -> torch.Tensor:
+        ld = (n + 7) // 8 * 8
+        if self.logits.numel() < m * ld:
+            self.logits = torch.zeros(max(m, self.m_cap) * ld, dtype=torch.bfloat16, device=self.h.device)
+        return self.logits[: m * ld].view(m, ld)
+
+
+class _BaseRefs:
+    """Plain holder so base weights are never registered as draft parameters."""
+
+    def __init__(self, model: MI355XLlama, layer_indices: list):
+        self.model = model
+        self.layers = [model.layers[i] for i in layer_indices]
+        self.embed_tokens = model.embed
+        self.norm = model.norm
+        self.lm_head = model.lm_head
+
+
+class SubnetworkDraftModel(nn.Module):
+    def __init__(self, base_model, layer_indices: list, bridge_config: Optional[BridgeConfig] = None,
+                 freeze_base: bool = True):
+        super().__init__()
+        model = as_device_model(base_model)
+        s = model.shape
+        self.num_base_layers = s.layers
+        self.layer_indices = validate_layer_indices(layer_indices, s.layers)
+        self.d_model, self.num_heads, self.num_kv_heads, self.head_dim = s.hidden, s.heads, s.kv_heads, s.head_dim
+        self.bridge_config = bridge_config or BridgeConfig()
+        self.base = _BaseRefs(model, self.layer_indices)
+        self.bridge_specs = plan_bridges(self.layer_indices, s.layers)
+        by_tgt = {b.tgt_boundary: b.name for b in self.bridge_specs}
+        self._pre_layer_bridge = [by_tgt.get(i) for i in self.layer_indices]
+        self._pre_norm_bridge = by_tgt.get(s.layers)
+        self.bridges = nn.ModuleDict({b.name: TransitionBridge.from_config(self.d_model, self.bridge_config)
+                                      for b in self.bridge_specs})
+        self.vocab_ids: Optional[torch.Tensor] = None
+        self._vocab_ids_i32: Optional[torch.Tensor] = None
+        self._sub_head: Optional[torch.Tensor] = None
+        self._ws: Optional[Workspace] = None
+
+    # ------------------------------------------------------------------ setup
+    @property
+    def model(self) -> MI355XLlama:
+        return self.base.model
+
+    @property
+    def num_layers(self) -> int:
+        return len(self.layer_indices)
+
+    def set_vocab_subset(self, token_ids: Optional[torch.Tensor]) -> None:
+        """Score only ``token_ids`` (sorted ascending) in this model's lm_head: a packed copy of
+        those rows (|subset| x d) streamed by the same GEMM (reference :136-144)."""
+        if token_ids is None:
+            self.vocab_ids = self._sub_head = self._vocab_ids_i32 = None
+            return
+        ids = token_ids.to(self.model.device).long()
+        self.vocab_ids = ids
+        self._vocab_ids_i32 = ids.to(torch.int32)
+        self._sub_head = ops.pack_weight(self.model.lm_head_rows(ids))
+
+    def place_bridges(self) -> None:
+        """Single-GPU build: bridges run where the base weights live."""
+        self.bridges.to(self.model.device)
+
+    def new_cache(self, max_length: int) -> KVCache:
+        s = self.model.shape
+        return KVCache(s.layers, max_length, s.kv_heads, s.head_dim, self.model.device)
+
+    def workspace(self, m_cap: int = CHUNK) -> Workspace:
+        bh = max([b.hidden for b in self.bridges.values()] + [0])
+        if self._ws is None or self._ws.m_cap < m_cap or self._ws.mids[0].shape[1] < bh:
+            self._ws = Workspace(self.model, m_cap, bh)
+        return self._ws
+
+    def _packed_bridge(self, name: str):
+        br = self.bridges[name]
+        if br.norm.weight.device != self.model.device:
+            br.to(self.model.device)
+        return br.packed(self.model.device)
+
+    # ------------------------------------------------------- device forward
+    def run_rows(self, rows: Rows, m: int, p_min: int, l_max: int, cache: KVCache, ws: Workspace,
+                 bridge_states: Optional[dict] = None, ids_ready: bool = True) -> torch.Tensor:
+        """All selected layers (+ bridges) for rows [0, m) already on the device. Returns the
+        residual stream h[:m] (before the final norm)."""
+        if m > ws.m_cap:
+            raise ValueError(f"{m} rows > workspace {ws.m_cap}")
+        model, s = self.model, self.model.shape
+        cos, sin = model.rope(cache.capacity)
+        aws = ws.attn_ws(model, cache.capacity)
+        ops.embed(rows.ids, m, model.embed, ws.h)
+        for slot, layer in enumerate(self.base.layers):
+            li = self.layer_indices[slot]
+            name = self._pre_layer_bridge[slot]
+            if name is not None:
+                self._packed_bridge(name).apply_(ws.h, m, ws.x, ws.mids)
+                if bridge_states is not None:
+                    bridge_states[name] = ws.h[:m].clone()
+            kc, vt = cache.layer(li)
+            ops.rmsnorm(ws.h, m, layer.ln1, s.eps, ws.x)
+            ops.qkv_rope(ws.x, m, layer.wqkv, s.hidden, s.heads, s.kv_heads, s.head_dim, cos, sin, rows.pos,
+                         rows.slot, ws.q, kc, vt, cache.capacity)
+            ops.tree_attention(ws.q, m, s.heads, s.kv_heads, s.head_dim, kc, vt, cache.capacity, rows.prefix,
+                               rows.depth, rows.anc, p_min, l_max, aws, ws.attn)
+            ops.gemm(ws.attn, m, layer.wo, s.hidden, s.heads * s.head_dim, ws.h, residual=ws.h)
+            ops.rmsnorm(ws.h, m, layer.ln2, s.eps, ws.x)
+            ops.gemm_swiglu(ws.x, m, layer.wgu, s.inter, s.hidden, ws.mlp)
+            ops.gemm(ws.mlp, m, layer.wd, s.hidden, s.inter, ws.h, residual=ws.h)
+        if self._pre_norm_bridge is not None:
+            self._packed_bridge(self._pre_norm_bridge).apply_(ws.h, m, ws.x, ws.mids)
+            if bridge_states is not None:
+                bridge_states[self._pre_norm_bridge] = ws.h[:m].clone()
+        return ws.h
+
+    def head(self, hn: torch.Tensor, m: int, ws: Workspace) -> torch.Tensor:
+        """lm_head (or the vocab-subset head) over hn[:m] -> bf16 logits view [m, V]."""
+        if self._sub_head is not None:
+            n, w = self._sub_head_n(), self._sub_head
+        else:
+            n, w = self.model.shape.vocab, self.model.lm_head
+        out = ws.logits_buf(m, n)
+        ops.gemm(hn, m, w, n, self.d_model, out)
+        return out[:, :n]
+
+    def _sub_head_n(self) -> int:
+        return int(self.vocab_ids.numel())
+
+    def final_norm(self, h: torch.Tensor, m: int, out: torch.Tensor) -> torch.Tensor:
+        return ops.rmsnorm(h, m, self.model.norm, self.model.shape.eps, out)
+
+    # ---------------------------------------------------------- generic API
+    @staticmethod
+    def mask_to_rows(q_len: int, past: int, mask: Optional[torch.Tensor]):
+        """Reference mask semantics (subnetwork_draft.py:165-191) -> per-row (prefix, ancestors)."""
+        if mask is None:
+            if q_len == 1:
+                return [past + 1], [[]]
+            return [past + t + 1 for t in range(q_len)], [[] for _ in range(q_len)]
+        mk = mask.detach().to("cpu", torch.bool)
+        while mk.dim() > 2:
+            if mk.shape[0] != 1:
+                raise ValueError("batch size 1 only")
+            mk = mk[0]
+        if mk.shape[-1] == past + q_len and past > 0:
+            full = mk
+        else:
+            if tuple(mk.shape[-2:]) != (q_len, q_len):
+                raise ValueError(f"tree_attention_mask must be [.., {q_len}, {q_len}], got {tuple(mk.shape)}")
+            full = torch.cat([torch.ones(q_len, past, dtype=torch.bool), mk], 1)
+        prefix, anc = [], []
+        for t in range(q_len):
+            row = full[t]
+            off = torch.nonzero(~row).flatten()
+            p = int(off[0]) if off.numel() else int(row.numel())
+            rest = (torch.nonzero(row[p:]).flatten() + p).tolist()
+            if len(rest) > MAXD:
+                raise ValueError(f"row {t} attends {len(rest)} non-prefix slots (max {MAXD})")
+            if p == 0 and not rest:
+                raise ValueError(f"row {t} attends nothing")
+            prefix.append(p)
+            anc.append(rest)
+        return prefix, anc
+
+    def forward(self, input_ids: Optional[torch.Tensor] = None, position_ids: Optional[torch.Tensor] = None,
+                past_key_values: Optional[KVCache] = None, tree_attention_mask: Optional[torch.Tensor] = None,
+                inputs_embeds: Optional[torch.Tensor] = None, logits_to_keep: int = 0, compute_logits: bool = True,
+                output_bridge_states: bool = False, true_layer_inputs: Optional[dict] = None,
+                output_layer_inputs: Optional[set] = None) -> DraftOutput:
+        if true_layer_inputs is not None or output_layer_inputs:
+            raise NotImplementedError("training-mode inputs are outside the decode path")
+        if inputs_embeds is not None:
+            raise NotImplementedError("inputs_embeds: pass token ids")
+        ids = torch.as_tensor(input_ids)
+        if ids.dim() == 1:
+            ids = ids[None]
+        if ids.shape[0] != 1:
+            raise ValueError("batch size 1 only (speculative decoding is batch 1)")
+        ids = ids[0].tolist()
+        q = len(ids)
+        cache = past_key_values
+        if cache is None:
+            cache = self.new_cache(q)
+        cache.ensure(self.num_kv_heads, self.head_dim, self.model.device)
+        past = cache.get_seq_length()
+        cache.check_room(past + q)
+        pos = list(range(past, past + q)) if position_ids is None else torch.as_tensor(position_ids).reshape(-1).tolist()
+        prefix, anc = self.mask_to_rows(q, past, tree_attention_mask)
+        ws = self.workspace(CHUNK)
+        rows = Rows(CHUNK, self.model.device)
+        hidden = torch.empty(q, self.d_model, dtype=torch.bfloat16, device=self.model.device)
+        states: dict = {} if output_bridge_states else None
+        for c0 in range(0, q, CHUNK):
+            c1 = min(q, c0 + CHUNK)
+            seen = [a for lst in anc[c0:c1] for a in lst] + [p - 1 for p in prefix[c0:c1]]
+            if max(seen) >= past + c1:
+                raise ValueError("a row attends a slot written by a later chunk")
+            rows.upload(ids[c0:c1], pos[c0:c1], list(range(past + c0, past + c1)), prefix[c0:c1],
+                        [len(a) for a in anc[c0:c1]], anc[c0:c1])
+            m = c1 - c0
+            p_min = min(prefix[c0:c1])
+            l_max = max(p + len(a) for p, a in zip(prefix[c0:c1], anc[c0:c1]))
+            h = self.run_rows(rows, m, p_min, l_max, cache, ws, states)
+            self.final_norm(h, m, hidden[c0:c1])
+            torch.cuda.current_stream().synchronize()  # the pinned staging buffer is reused next chunk
+        cache.advance(q)
+        logits = None
+        if compute_logits:
+            keep = hidden[-logits_to_keep:] if logits_to_keep > 0 else hidden
+            outs = []
+            for c0 in range(0, keep.shape[0], CHUNK):
+                part = keep[c0:c0 + CHUNK]
+                outs.append(self.head(part, part.shape[0], ws).clone())
+            logits = torch.cat(outs, 0)[None]
+        return DraftOutput(logits=logits, hidden_states=hidden[None], past_key_values=past_key_values,
+                           bridge_states={k: v[None] for k, v in (states or {}).items()},
+                           vocab_ids=self.vocab_ids if compute_logits else None)
+
+    # ------------------------------------------------------------ persistence
+    def save_bridges(self, path: str, **meta) -> None:
+        """Same file format as the reference (subnetwork_draft.py:455-466)."""
+        os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
+        torch.save({"layer_indices": self.layer_indices, "bridge_config": vars(self.bridge_config),
+                    "state_dict": self.bridges.state_dict(), "meta": meta}, path)
+
+    def load_bridges(self, path: str, strict: bool = True) -> None:
+        ckpt = torch.load(path, map_location="cpu", weights_only=True)
+        if list(ckpt["layer_indices"]) != self.layer_indices:
+            raise ValueError(f"checkpoint layer_indices {ckpt['layer_indices']} != {self.layer_indices}")
+        self.bridges.load_state_dict(ckpt["state_dict"], strict=strict)
+        for b in self.bridges.values():
+            b._packed = None

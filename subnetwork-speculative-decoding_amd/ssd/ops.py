@@ -1,0 +1,173 @@
+"""Torch-tensor wrappers over the C ABI (include/ssd_mi355x.h).
+
+PyTorch only supplies device memory and the current HIP stream here; every computation is a
+hand-written gfx950 kernel in ``libssd_mi355x.so``. Inputs are validated on the host (dtype,
+device, alignment, shapes) before a launch, so a bad call raises instead of faulting.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from ssd import _lib
+
+ACT = {None: 0, "none": 0, "silu": 1, "gelu": 2, "relu": 3}
+BF16 = torch.bfloat16
+
+
+def stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _p(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _check(t: torch.Tensor, name: str, dtype=BF16):
+    if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
+        raise ValueError(f"{name} must be a CUDA (HIP) tensor")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if dtype == BF16 and t.data_ptr() % 16:
+        raise ValueError(f"{name} must be 16-byte aligned")
+
+
+def _rows(t: torch.Tensor, name: str, cols: int, rows: int = 0) -> int:
+    """Row stride of a 2-D row-major tensor with unit column stride and >= ``rows`` rows."""
+    if t.dim() != 2 or t.stride(1) != 1 or t.shape[1] < cols or t.shape[0] < rows:
+        raise ValueError(f"{name} must be [>={rows}, >={cols}] with unit column stride, got {tuple(t.shape)}")
+    return t.stride(0)
+
+
+def _len(t: Optional[torch.Tensor], name: str, n: int) -> None:
+    if t is not None and t.numel() < n:
+        raise ValueError(f"{name} has {t.numel()} elements, needs {n}")
+
+
+def packed_elems(n: int, k: int) -> int:
+    return int(_lib.load().ssd_packed_weight_elems(n, k))
+
+
+def pack_weight(w: torch.Tensor, row_map: Optional[torch.Tensor] = None, n_packed: Optional[int] = None) -> torch.Tensor:
+    """Row-major bf16 W[N, K] -> MFMA tile layout. row_map[n_packed] picks the source row of
+    each packed row (-1 = zeros); default = identity padded to a multiple of 16."""
+    _check(w, "w")
+    n, k = w.shape
+    ld = _rows(w, "w", k)
+    if row_map is None:
+        n_packed = (n + 15) // 16 * 16
+        row_map = torch.arange(n_packed, dtype=torch.int32)
+        row_map[n:] = -1
+    n_packed = int(row_map.numel()) if n_packed is None else n_packed
+    rm = row_map.to(device=w.device, dtype=torch.int32)
+    out = torch.empty(packed_elems(n_packed, k), dtype=BF16, device=w.device)
+    _lib.call("ssd_pack_weight_bf16", w.data_ptr(), ld, n, k, rm.data_ptr(), n_packed, out.data_ptr(), stream())
+    return out
+
+
+def gemm(x: torch.Tensor, m: int, wp: torch.Tensor, n: int, k: int, out: torch.Tensor, bias=None, act=None,
+         residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+    _check(x, "x"); _check(wp, "w_packed"); _check(out, "out")
+    if bias is not None:
+        _check(bias, "bias")
+    ldx = _rows(x, "x", k, m)
+    ldy = _rows(out, "out", n, m)
+    _len(bias, "bias", n)
+    _len(wp, "w_packed", packed_elems(n, k))
+    ldr = 0
+    if residual is not None:
+        _check(residual, "residual")
+        ldr = _rows(residual, "residual", n, m)
+    _lib.call("ssd_gemm_bf16", x.data_ptr(), ldx, m, wp.data_ptr(), n, k, out.data_ptr(), ldy, _p(bias),
+              ACT[act], _p(residual), ldr, stream())
+    return out
+
+
+def gemm_swiglu(x: torch.Tensor, m: int, wp: torch.Tensor, inter: int, k: int, out: torch.Tensor, bias_gate=None,
+                bias_up=None) -> torch.Tensor:
+    _check(x, "x"); _check(wp, "w_packed"); _check(out, "out")
+    _len(bias_gate, "bias_gate", inter); _len(bias_up, "bias_up", inter)
+    _len(wp, "w_packed", packed_elems(2 * inter, k))
+    _lib.call("ssd_gemm_swiglu_bf16", x.data_ptr(), _rows(x, "x", k, m), m, wp.data_ptr(), inter, k, out.data_ptr(),
+              _rows(out, "out", inter, m), _p(bias_gate), _p(bias_up), stream())
+    return out
+
+
+def qkv_rope(x, m, wp, k, heads, kv_heads, head_dim, cos, sin, pos, slot, q_out, k_cache, vt_cache, max_len):
+    _check(x, "x"); _check(wp, "w_packed"); _check(q_out, "q"); _check(k_cache, "k_cache"); _check(vt_cache, "vt")
+    for t, nm in ((pos, "pos"), (slot, "slot")):
+        _check(t, nm, torch.int32)
+        _len(t, nm, m)
+    _len(wp, "w_packed", packed_elems((heads + 2 * kv_heads) * head_dim, k))
+    if k_cache.numel() < kv_heads * max_len * head_dim or vt_cache.numel() < kv_heads * max_len * head_dim:
+        raise ValueError("qkv_rope: cache smaller than kv_heads * max_len * head_dim")
+    if cos.shape != sin.shape or cos.dim() != 2 or cos.shape[1] != head_dim // 2:
+        raise ValueError("qkv_rope: cos/sin must be [rows, head_dim/2]")
+    _lib.call("ssd_gemm_qkv_rope_bf16", x.data_ptr(), _rows(x, "x", k, m), m, wp.data_ptr(), k, heads, kv_heads,
+              head_dim, cos.data_ptr(), sin.data_ptr(), cos.shape[0], pos.data_ptr(), slot.data_ptr(), q_out.data_ptr(),
+              _rows(q_out, "q", heads * head_dim, m), k_cache.data_ptr(), vt_cache.data_ptr(), max_len, stream())
+
+
+def attn_workspace_floats(m: int, heads: int, head_dim: int, max_len: int) -> int:
+    return int(_lib.load().ssd_attn_workspace_floats(m, heads, head_dim, max_len))
+
+
+def tree_attention(q, m, heads, kv_heads, head_dim, k_cache, vt_cache, max_len, prefix, depth, anc, p_min, l_max,
+                   ws, out, scale=None):
+    _check(q, "q"); _check(k_cache, "k_cache"); _check(vt_cache, "vt_cache"); _check(out, "out")
+    _check(ws, "ws", torch.float32)
+    for t, nm, n in ((prefix, "prefix", m), (depth, "depth", m), (anc, "anc", m * 32)):
+        _check(t, nm, torch.int32)
+        _len(t, nm, n)
+    if k_cache.numel() < kv_heads * max_len * head_dim or vt_cache.numel() < kv_heads * max_len * head_dim:
+        raise ValueError("tree_attention: cache smaller than kv_heads * max_len * head_dim")
+    scale = head_dim ** -0.5 if scale is None else scale
+    _lib.call("ssd_tree_attention_bf16", q.data_ptr(), _rows(q, "q", heads * head_dim, m), m, heads, kv_heads, head_dim,
+              k_cache.data_ptr(), vt_cache.data_ptr(), max_len, prefix.data_ptr(), depth.data_ptr(), anc.data_ptr(),
+              int(p_min), int(l_max), float(scale), ws.data_ptr(), ws.numel(), out.data_ptr(),
+              _rows(out, "out", heads * head_dim, m), stream())
+
+
+def rmsnorm(x, m, w, eps, out):
+    _check(x, "x"); _check(w, "w"); _check(out, "out")
+    d = w.numel()
+    _lib.call("ssd_rmsnorm_bf16", x.data_ptr(), _rows(x, "x", d, m), m, d, w.data_ptr(), float(eps), out.data_ptr(),
+              _rows(out, "out", d, m), stream())
+    return out
+
+
+def embed(ids, m, table, out):
+    _check(ids, "ids", torch.int32); _check(table, "table"); _check(out, "out")
+    v, d = table.shape
+    _len(ids, "ids", m)
+    _lib.call("ssd_embed_bf16", ids.data_ptr(), m, table.data_ptr(), v, d, out.data_ptr(), _rows(out, "out", d, m),
+              stream())
+    return out
+
+
+def kv_compact(k_arena, vt_arena, layers, kv_heads, head_dim, max_len, start, src, n_dev, n_max):
+    _check(k_arena, "k_arena"); _check(vt_arena, "vt_arena")
+    _check(src, "src", torch.int32); _check(n_dev, "n", torch.int32)
+    _len(src, "src", n_max)
+    if k_arena.numel() < layers * kv_heads * max_len * head_dim or vt_arena.numel() < k_arena.numel():
+        raise ValueError("kv_compact: arenas smaller than layers * kv_heads * max_len * head_dim")
+    _lib.call("ssd_kv_compact_bf16", k_arena.data_ptr(), vt_arena.data_ptr(), layers, kv_heads, head_dim, max_len,
+              int(start), src.data_ptr(), n_dev.data_ptr(), int(n_max), stream())
+
+
+def row_topk(logits, m, n, k, mode, vocab_ids, out_tok, out_val=None, out_lse=None):
+    _check(logits, "logits"); _check(out_tok, "out_tok", torch.int32)
+    if vocab_ids is not None:
+        _check(vocab_ids, "vocab_ids", torch.int32)
+        _len(vocab_ids, "vocab_ids", n)
+    _len(out_tok, "out_tok", m * k)
+    if out_val is not None:
+        _check(out_val, "out_val", torch.float32)
+        _len(out_val, "out_val", m * k)
+    if out_lse is not None:
+        _check(out_lse, "out_lse", torch.float32)
+        _len(out_lse, "out_lse", m)
+    _lib.call("ssd_row_topk_bf16", logits.data_ptr(), _rows(logits, "logits", n, m), m, n, k, mode, _p(vocab_ids),
+              out_tok.data_ptr(), _p(out_val), _p(out_lse), stream())

@@ -1,0 +1,52 @@
+"""The C-ABI library loads and exports every entry point include/ssd_mi355x.h declares (CPU only,
+no compute calls), and the Python binding covers exactly that set."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import REPO
+
+HEADER = os.path.join(REPO, "include", "ssd_mi355x.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+char\s*\*|int64_t|int)\s+(ssd_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_entry_points():
+    names = declared()
+    assert "ssd_tree_attention_bf16" in names and "ssd_kv_compact_bf16" in names and len(names) >= 18
+
+
+def test_library_exports_every_declared_symbol():
+    from ssd import _lib
+
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail("libssd_mi355x.so is not built (run subnetwork-speculative-decoding_amd/build.py)")
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in declared() if not hasattr(lib, n)]
+    assert not missing, f"not exported: {missing}"
+
+
+def test_binding_matches_header():
+    from ssd import _lib
+
+    assert sorted(_lib.EXPORTED) == declared()
+
+
+def test_host_only_entry_points():
+    from ssd import _lib
+
+    lib = _lib.load()
+    assert lib.ssd_abi_version() == 1
+    assert lib.ssd_packed_weight_elems(17, 40) == 32 * 64
+    lim = (ctypes.c_int32 * 3)()
+    assert lib.ssd_tree_limits(lim) == 0 and list(lim) == [1024, 32, 32]
+    assert lib.ssd_attn_max_depth() == 32
+    # argument validation happens on the host, before any launch
+    rc = lib.ssd_gemm_bf16(None, 0, 1, None, 16, 32, None, 0, None, 0, None, 0, None)
+    assert rc == 1 and b"null" in lib.ssd_last_error()

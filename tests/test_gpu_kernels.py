@@ -1,0 +1,365 @@
+"""Per-kernel parity of the HIP C-ABI library against the CPU oracle (oracle/kernels.py).
+
+Tolerances: integer / index work is bit-exact; bf16 outputs of fp32-accumulated GEMMs may
+differ from the oracle's fp32 sum by one bf16 rounding step (different summation order),
+so they are compared at atol/rtol 1e-2 with >= 97% exact matches; attention (fp32 softmax,
+bf16 P) at the per-node logit tolerance rel 2e-2 / abs 1e-2 relative to the output scale.
+The batch-invariance and canonical-attention tests are bitwise: they are what makes greedy
+speculative decoding identical to greedy decoding.
+"""
+
+import math
+import random
+
+import pytest
+import torch
+
+from oracle import engine as oe
+from oracle import kernels as ok
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _ops():
+    from ssd import ops
+    return ops
+
+
+def bf(t):
+    return t.to(torch.bfloat16)
+
+
+def rand(*shape, std=1.0, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g) * std
+
+
+def close_bf16(got, ref, frac=0.97, atol=1e-2, rtol=1e-2):
+    got, ref = got.float().cpu(), ref.float().cpu()
+    torch.testing.assert_close(got, ref, atol=atol, rtol=rtol)
+    exact = (got == ref).float().mean().item()
+    assert exact >= frac, f"only {exact:.3f} of outputs match the oracle exactly"
+
+
+# ---------------------------------------------------------------------------- GEMM
+@pytest.mark.parametrize("m", [1, 5, 16, 17, 33, 64, 70])
+@pytest.mark.parametrize("n,k", [(48, 64), (1040, 2048), (272, 4096)])
+def test_gemm_matches_oracle(m, n, k):
+    ops = _ops()
+    x, w = bf(rand(m, k, seed=1)), bf(rand(n, k, std=0.02, seed=2))
+    wp = ops.pack_weight(w.to(DEV))
+    y = torch.zeros(m, n, dtype=torch.bfloat16, device=DEV)
+    ops.gemm(x.to(DEV), m, wp, n, k, y)
+    close_bf16(y, ok.linear(x, w))
+
+
+def test_gemm_batch_invariance_bitwise():
+    """A row's output is identical whether it is computed alone or at any position of a
+    64-row batch (MFMA column slot, column tile and K split all change nothing)."""
+    ops = _ops()
+    n, k = 1040, 4096
+    x = bf(rand(64, k, seed=3)).to(DEV)
+    wp = ops.pack_weight(bf(rand(n, k, std=0.02, seed=4)).to(DEV))
+    full = torch.zeros(64, n, dtype=torch.bfloat16, device=DEV)
+    ops.gemm(x, 64, wp, n, k, full)
+    for m in (1, 5, 25, 33):
+        part = torch.zeros(m, n, dtype=torch.bfloat16, device=DEV)
+        ops.gemm(x, m, wp, n, k, part)
+        assert torch.equal(part, full[:m])
+    for r in (0, 7, 16, 31, 63):
+        one = torch.zeros(1, n, dtype=torch.bfloat16, device=DEV)
+        ops.gemm(x[r:r + 1].contiguous(), 1, wp, n, k, one)
+        assert torch.equal(one[0], full[r]), f"row {r} differs alone"
+
+
+@pytest.mark.parametrize("act", ["silu", "gelu", "relu"])
+def test_gemm_bias_act_and_residual(act):
+    ops = _ops()
+    m, n, k = 9, 96, 256
+    x, w = bf(rand(m, k, seed=5)), bf(rand(n, k, std=0.05, seed=6))
+    b, r = bf(rand(n, std=0.1, seed=7)), bf(rand(m, n, seed=8))
+    wp = ops.pack_weight(w.to(DEV))
+    y = torch.zeros(m, n, dtype=torch.bfloat16, device=DEV)
+    ops.gemm(x.to(DEV), m, wp, n, k, y, bias=b.to(DEV), act=act)
+    close_bf16(y, ok.linear(x, w, b, act=act))
+    h = r.to(DEV).clone()
+    ops.gemm(x.to(DEV), m, wp, n, k, h, bias=b.to(DEV), residual=h)  # in place, like h = h + o_proj(attn)
+    close_bf16(h, ok.linear(x, w, b, residual=r))
+
+
+def test_gemm_swiglu():
+    ops = _ops()
+    from ssd.models.llama import gate_up_row_map
+
+    m, inter, k = 21, 192, 256
+    x = bf(rand(m, k, seed=9))
+    wg, wu = bf(rand(inter, k, std=0.05, seed=10)), bf(rand(inter, k, std=0.05, seed=11))
+    wp = ops.pack_weight(torch.cat([wg, wu]).to(DEV), gate_up_row_map(inter))
+    y = torch.zeros(m, inter, dtype=torch.bfloat16, device=DEV)
+    ops.gemm_swiglu(x.to(DEV), m, wp, inter, k, y)
+    close_bf16(y, ok.swiglu(x, wg, wu), frac=0.95)
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_qkv_rope_and_cache_write(hd):
+    ops = _ops()
+    from ssd.models.llama import qkv_row_map, rope_tables
+
+    heads, kvh, d, m, max_len = 4, 2, 256, 6, 64
+    x = bf(rand(m, d, seed=12))
+    wq, wk, wv = (bf(rand(h * hd, d, std=0.05, seed=13 + i)) for i, h in enumerate((heads, kvh, kvh)))
+    wp = ops.pack_weight(torch.cat([wq, wk, wv]).to(DEV), qkv_row_map(heads, kvh, hd))
+    cos, sin = rope_tables(max_len, hd, 500000.0, DEV)
+    pos = torch.tensor([3, 3, 9, 40, 0, 63], dtype=torch.int32)
+    slot = torch.tensor([10, 11, 12, 13, 20, 63], dtype=torch.int32)
+    q = torch.zeros(m, heads * hd, dtype=torch.bfloat16, device=DEV)
+    kc = torch.zeros(kvh, max_len, hd, dtype=torch.bfloat16, device=DEV)
+    vt = torch.zeros(kvh, hd, max_len, dtype=torch.bfloat16, device=DEV)
+    ops.qkv_rope(x.to(DEV), m, wp, d, heads, kvh, hd, cos, sin, pos.to(DEV), slot.to(DEV), q, kc, vt, max_len)
+    rq, rk, rv = ok.qkv_rope(x, wq, wk, wv, heads, kvh, hd, pos.long(), 500000.0)
+    close_bf16(q.view(m, heads, hd), rq, frac=0.95)
+    close_bf16(kc[:, slot.long()].transpose(0, 1), rk, frac=0.95)
+    close_bf16(vt[:, :, slot.long()].permute(2, 0, 1), rv, frac=0.97)
+    untouched = torch.ones(max_len, dtype=torch.bool)
+    untouched[slot.long()] = False
+    assert kc[:, untouched].abs().sum() == 0 and vt[:, :, untouched].abs().sum() == 0
+
+
+# ----------------------------------------------------------------------- rows
+def test_rmsnorm_and_embed():
+    ops = _ops()
+    x, w = bf(rand(7, 512, seed=20)), bf(1 + rand(512, std=0.1, seed=21))
+    y = torch.zeros(7, 512, dtype=torch.bfloat16, device=DEV)
+    ops.rmsnorm(x.to(DEV), 7, w.to(DEV), 1e-6, y)
+    close_bf16(y, ok.rmsnorm(x, w, 1e-6), frac=0.98)
+    table = bf(rand(100, 64, seed=22)).to(DEV)
+    ids = torch.tensor([5, 0, 99, 5], dtype=torch.int32, device=DEV)
+    out = torch.zeros(4, 64, dtype=torch.bfloat16, device=DEV)
+    ops.embed(ids, 4, table, out)
+    assert torch.equal(out, table[ids.long()])
+
+
+def test_kv_compact_overlapping_and_all_layers():
+    ops = _ops()
+    L, kvh, hd, S = 3, 2, 64, 40
+    k = bf(rand(L, kvh, S, hd, seed=23)).to(DEV)
+    vt = bf(rand(L, kvh, hd, S, seed=24)).to(DEV)
+    k0, vt0 = k.clone().cpu(), vt.clone().cpu()
+    src = [10, 12, 13, 17]
+    buf = torch.tensor(src + [33], dtype=torch.int32, device=DEV)  # capacity 5, device count 4
+    ops.kv_compact(k, vt, L, kvh, hd, S, 10, buf, torch.tensor([4], dtype=torch.int32, device=DEV), 5)
+    assert torch.equal(k.cpu(), ok.kv_compact(k0, 10, src))
+    assert torch.equal(vt.cpu().transpose(-1, -2), ok.kv_compact(vt0.transpose(-1, -2), 10, src))
+
+
+def test_row_topk_argmax_and_logsoftmax():
+    ops = _ops()
+    m, n = 6, 5000
+    x = bf(rand(m, n, seed=25) * 3)
+    x[1, 100] = x[1, 4000] = x[1].max() + 1  # exact tie: first index wins
+    x[2, :] = 0.0  # all equal
+    xd = x.to(DEV)
+    tok = torch.zeros(m, dtype=torch.int32, device=DEV)
+    ops.row_topk(xd, m, n, 1, 0, None, tok)
+    assert tok.cpu().tolist() == ok.argmax_first(x).tolist()
+    k = 5
+    tk = torch.zeros(m * k, dtype=torch.int32, device=DEV)
+    lp = torch.zeros(m * k, dtype=torch.float32, device=DEV)
+    lse = torch.zeros(m, dtype=torch.float32, device=DEV)
+    ops.row_topk(xd, m, n, k, 1, None, tk, lp, lse)
+    rv, ri, rlse = ok.log_softmax_topk(x, k)
+    assert tk.view(m, k).cpu().tolist() == ri.tolist()
+    torch.testing.assert_close(lp.view(m, k).cpu(), rv, atol=2e-5, rtol=1e-5)
+    torch.testing.assert_close(lse.cpu(), rlse, atol=2e-5, rtol=1e-5)
+    ids = torch.arange(n, dtype=torch.int32, device=DEV) * 3 + 1
+    ops.row_topk(xd, m, n, k, 1, ids, tk, lp, lse)
+    assert tk.view(m, k).cpu().tolist() == (ri * 3 + 1).tolist()
+
+
+# ------------------------------------------------------------------ attention
+def _attn_case(m, heads, kvh, hd, S, prefix, anc, seed):
+    q = bf(rand(m, heads, hd, seed=seed))
+    k = bf(rand(kvh, S, hd, seed=seed + 1))
+    v = bf(rand(kvh, S, hd, seed=seed + 2))
+    return q, k, v
+
+
+def _run_attn(q, k, v, prefix, anc, S, m_cap=None):
+    ops = _ops()
+    m, heads, hd = q.shape
+    kvh = k.shape[0]
+    qd = q.reshape(m, heads * hd).to(DEV).contiguous()
+    kd = k.to(DEV).contiguous()
+    vtd = v.transpose(1, 2).to(DEV).contiguous()
+    pre = torch.tensor(prefix, dtype=torch.int32, device=DEV)
+    dep = torch.tensor([len(a) for a in anc], dtype=torch.int32, device=DEV)
+    an = torch.zeros(m, 32, dtype=torch.int32)
+    for t, lst in enumerate(anc):
+        an[t, :len(lst)] = torch.tensor(lst, dtype=torch.int32) if lst else an[t, :0]
+    ws = torch.zeros(ops.attn_workspace_floats(m_cap or m, heads, hd, S), dtype=torch.float32, device=DEV)
+    out = torch.zeros(m, heads * hd, dtype=torch.bfloat16, device=DEV)
+    l_max = max(p + len(a) for p, a in zip(prefix, anc))
+    ops.tree_attention(qd, m, heads, kvh, hd, kd, vtd, S, pre, dep, an.to(DEV), min(prefix), l_max, ws, out)
+    return out.view(m, heads, hd).cpu()
+
+
+@pytest.mark.parametrize("hd,heads,kvh", [(64, 4, 2), (128, 8, 2), (128, 32, 8)])
+@pytest.mark.parametrize("P", [1, 63, 64, 200, 1000, 4100])
+def test_tree_attention_matches_oracle(hd, heads, kvh, P):
+    rng = random.Random(P * 7 + hd)
+    S = P + 80
+    S = (S + 7) // 8 * 8
+    m = 9
+    prefix, anc = [], []
+    for t in range(m):
+        if t == 0:
+            prefix.append(P); anc.append([])
+        else:
+            d = rng.randint(1, 6)
+            prefix.append(P)
+            anc.append(sorted(rng.sample(range(P, S), d)))
+    q, k, v = _attn_case(m, heads, kvh, hd, S, prefix, anc, seed=P + hd)
+    got = _run_attn(q, k, v, prefix, anc, S)
+    ref = ok.tree_attention(q, k, v, prefix, anc)
+    scale = ref.abs().max().item()
+    torch.testing.assert_close(got.float(), ref, atol=1e-2 * max(scale, 1e-3), rtol=2e-2)
+
+
+@pytest.mark.parametrize("P,depth", [(5, 3), (63, 2), (64, 4), (250, 6), (255, 1), (511, 8), (1300, 5)])
+def test_tree_attention_verify_row_equals_autoregressive_row_bitwise(P, depth):
+    """A tree row (prefix P, ancestors scattered among decoys) equals the autoregressive row
+    that sees the same keys at contiguous slots P..P+depth-1, bit for bit, even when the tree
+    row shares the launch with other rows."""
+    hd, heads, kvh = 128, 8, 2
+    g = torch.Generator().manual_seed(P)
+    S_tree = (P + 3 * depth + 16 + 7) // 8 * 8
+    k_tree = bf(torch.randn(kvh, S_tree, hd, generator=g))
+    v_tree = bf(torch.randn(kvh, S_tree, hd, generator=g))
+    anc = sorted(random.Random(P).sample(range(P, S_tree), depth))
+    # autoregressive layout: same prefix, ancestors moved to P..P+depth-1
+    S_ar = (P + depth + 7) // 8 * 8
+    k_ar = torch.zeros(kvh, S_ar, hd, dtype=torch.bfloat16)
+    v_ar = torch.zeros(kvh, S_ar, hd, dtype=torch.bfloat16)
+    k_ar[:, :P], v_ar[:, :P] = k_tree[:, :P], v_tree[:, :P]
+    k_ar[:, P:P + depth], v_ar[:, P:P + depth] = k_tree[:, anc], v_tree[:, anc]
+    q = bf(torch.randn(4, heads, hd, generator=g))
+    other = [sorted(random.Random(P + i).sample(range(P, S_tree), 2)) for i in range(3)]
+    tree_out = _run_attn(q, k_tree, v_tree, [P] * 4, [other[0], anc, other[1], other[2]], S_tree)
+    ar_out = _run_attn(q[1:2].contiguous(), k_ar, v_ar, [P + depth], [[]], S_ar)
+    assert torch.equal(tree_out[1], ar_out[0])
+
+
+# ----------------------------------------------------------------------- tree
+def _device_tree(cap=1024):
+    from ssd.engine.tree_drafter import DeviceTree
+    return DeviceTree(DEV, cap=cap)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_tree_level_and_finalize_match_oracle(seed):
+    from ssd import _lib, ops
+    from ssd.models.subnetwork_draft import Rows
+
+    rng = random.Random(seed)
+    depth = rng.randint(2, 5)
+    branch = [rng.randint(1, 4) for _ in range(depth)]
+    width = [rng.choice([None, 3, 5, 8]) for _ in range(depth)]
+    max_nodes = rng.choice([None, 4, 7, 12])
+    committed, tree_start = 50, 51
+    tree = _device_tree()
+    level_rows, root_rows, vrows = Rows(64, DEV), Rows(64, DEV), Rows(64, DEV)
+    root_rows.ids[:1].fill_(777)
+    ref = oe.DraftTree()
+    frontier = [oe.ROOT]
+    past = tree_start
+    for d in range(depth):
+        k = branch[d]
+        F = len(frontier)
+        # log-probs on a coarse grid so that exact ties occur
+        lps = [[-rng.randint(0, 6) * 0.25 for _ in range(k)] for _ in range(F)]
+        lps = [sorted(r, reverse=True) for r in lps]
+        toks = [[rng.randint(0, 999) for _ in range(k)] for _ in range(F)]
+        ct = torch.tensor(toks, dtype=torch.int32).reshape(-1).to(DEV)
+        cl = torch.tensor(lps, dtype=torch.float32).reshape(-1).to(DEV)
+        feed = d < depth - 1
+        m = oe.level_sizes(oe.Drafting(depth=depth, branch=branch, width=width))[d]
+        _lib.call("ssd_tree_level", tree.struct, d, ct.data_ptr(), cl.data_ptr(), F, k, width[d] or 0, int(feed),
+                  committed, tree_start, past, level_rows.struct, m if feed else 0, ops.stream())
+        level = oe.expand_level(ref, frontier, [(t, [float(torch.tensor(x, dtype=torch.float32)) for x in l])
+                                                for t, l in zip(toks, lps)], d, width[d])
+        if feed:
+            for j, i in enumerate(level):
+                ref.draft_pos[i] = past + j
+            torch.cuda.synchronize()
+            assert level_rows.ids[:m].tolist() == [ref.tokens[i] for i in level]
+            assert level_rows.depth[:m].tolist() == [d + 1] * m
+            for j, i in enumerate(level):
+                assert level_rows.anc[j, :d + 1].tolist() == [ref.draft_pos[a] for a in ref.ancestors(i)]
+            past += m
+        frontier = level
+    n = len(ref)
+    torch.cuda.synchronize()
+    assert int(tree.meta[0]) == n
+    assert tree.tokens[:n].tolist() == ref.tokens and tree.parents[:n].tolist() == ref.parents
+    assert tree.scores[:n].tolist() == ref.scores and tree.ranks[:n].tolist() == ref.ranks
+    rows = min(n, max_nodes or n) + 1
+    _lib.call("ssd_tree_finalize", tree.struct, max_nodes or 0, committed, root_rows.ids.data_ptr(), vrows.struct,
+              rows, ops.stream())
+    pruned = oe.prune_tree(ref, max_nodes)
+    torch.cuda.synchronize()
+    vn = int(tree.vmeta[0])
+    assert vn == len(pruned)
+    assert tree.vtokens[:vn].tolist() == pruned.tokens and tree.vparents[:vn].tolist() == pruned.parents
+    ids, pos, mask = oe.verify_inputs(pruned, 777, committed, committed)
+    assert vrows.ids[:vn + 1].tolist() == ids.tolist() and vrows.pos[:vn + 1].tolist() == pos.tolist()
+    for r in range(vn + 1):
+        p, dep = int(vrows.prefix[r]), int(vrows.depth[r])
+        attended = list(range(p)) + vrows.anc[r, :dep].tolist()
+        assert attended == torch.nonzero(mask[r]).flatten().tolist()
+
+
+@pytest.mark.parametrize("seed", range(5))
+def test_accept_greedy_matches_oracle(seed):
+    from ssd import _lib, ops
+
+    rng = random.Random(100 + seed)
+    n = rng.randint(1, 20)
+    t = oe.DraftTree()
+    for i in range(n):
+        p = rng.randint(-1, i - 1)
+        t.tokens.append(rng.randint(0, 5))
+        t.parents.append(p)
+        t.depths.append(1 if p < 0 else t.depths[p] + 1)
+        t.scores.append(0.0)
+        t.ranks.append(sum(1 for j in range(i) if t.parents[j] == p))
+        t.draft_pos.append(-1)
+    # distinct tokens among siblings (as drafts propose)
+    seen = {}
+    for i in range(n):
+        s = seen.setdefault(t.parents[i], set())
+        while t.tokens[i] in s:
+            t.tokens[i] += 7
+        s.add(t.tokens[i])
+    argmax = [rng.choice([rng.randint(0, 5), t.tokens[rng.randrange(n)]]) for _ in range(n + 1)]
+    logits = torch.full((n + 1, 256), -1.0)
+    for r, a in enumerate(argmax):
+        logits[r, a] = 1.0
+    acc_ref, bonus_ref = oe.greedy_verify(t, logits)
+    tree = _device_tree()
+    i32 = lambda v: torch.tensor(v, dtype=torch.int32, device=DEV)
+    tree.vtokens[:n] = i32(t.tokens)
+    tree.vparents[:n] = i32(t.parents)
+    tree.vranks[:n] = i32(t.ranks)
+    tree.vmeta[0] = n
+    result = torch.zeros(40, dtype=torch.int32, device=DEV)
+    keep = torch.zeros(40, dtype=torch.int32, device=DEV)
+    nkeep = torch.zeros(1, dtype=torch.int32, device=DEV)
+    root = torch.zeros(1, dtype=torch.int32, device=DEV)
+    _lib.call("ssd_accept_greedy", tree.struct, i32(argmax).data_ptr(), 30, result.data_ptr(), keep.data_ptr(),
+              nkeep.data_ptr(), root.data_ptr(), ops.stream())
+    torch.cuda.synchronize()
+    nn_ = int(result[0])
+    assert nn_ == len(acc_ref) + 1
+    assert result[1:1 + nn_].tolist() == [t.tokens[i] for i in acc_ref] + [bonus_ref]
+    assert keep[:nn_].tolist() == [30] + [31 + i for i in acc_ref] and int(nkeep) == nn_ and int(root) == bonus_ref
