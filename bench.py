@@ -1,0 +1,285 @@
+"""Benchmark: speculative decoding rounds of a Llama-3-8B-shaped bf16 model on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-cpu]
+
+A *step* is one speculative round (draft tree -> verify -> commit) of the hot path. The
+workload (default ``llama3_8b_tree``): random-init Llama-3-8B shapes (hidden 4096, 32 layers,
+32/8 heads, head_dim 128, SwiGLU 14336, vocab 128256) in bf16, draft_layers [0, 15, 31] with
+two untrained bridges, tree depth 4 / branch [3, 2, 2, 1] / max_nodes 24, greedy, a 4096-token
+uniform random prompt, full-vocabulary draft head. W untimed rounds, then exactly K timed
+rounds bracketed by device synchronisation. ``value`` = committed tokens / timed seconds.
+
+Per-kernel figures are measured live with HIP events on the launch stream (same shapes as in
+the timed rounds: verify M = 25 rows at the reached context). ``cpu_baseline`` times the CPU
+oracle (this repo's PyTorch restatement of the reference path) on the host cores for a few
+rounds of the same model shape and tree after a shortened prompt.
+
+Prints one JSON line. More than one GPU is not part of this build: --gpus > 1 exits.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for _p in (REPO, os.path.join(REPO, "subnetwork-speculative-decoding_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "decode tokens/s + ms/round, Llama-3-8B bf16 tree spec; tree-attn HBM GB/s"
+
+WORKLOADS = {
+    # name: (shape, draft_layers, drafting kwargs, prompt, draft_vocab)
+    "llama3_8b_tree": ("llama3_8b", [0, 15, 31], dict(depth=4, branch=[3, 2, 2, 1], max_nodes=24), 4096, None),
+    "llama3_8b_c": ("llama3_8b", [0, 15, 31], dict(depth=6, branch=[4, 2, 2, 1, 1, 1], max_nodes=32), 4096, None),
+    "llama32_1b_b": ("llama32_1b", [0, 7, 15], dict(depth=4, branch=[3, 2, 2, 1], width=8, max_nodes=24), 512, 32768),
+}
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def time_launches(fn, reps: int) -> float:
+    """Average duration (ms) of ``fn``'s launches, HIP events on the current stream."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for a, b in evs:
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in evs) / reps
+
+
+def kernel_figures(gen, sess, reps: int) -> dict:
+    """Live per-kernel timings at the verify shape of the last timed round."""
+    import torch
+
+    from ssd import ops
+
+    target, cache, ws = gen.target, sess.cache, sess.ws
+    s = target.model.shape
+    m = gen.drafter.max_verify_nodes() + 1
+    committed = cache.get_seq_length()
+    L0 = target.model.layers[0]
+    kc, vt = cache.layer(0)
+    aws = ws.attn_ws(target.model, cache.capacity)
+    p = committed + 1
+    rows = sess.verify_rows
+    gen.drafter.finalize_device(sess.tree, committed, sess.root_rows, rows)
+    out = {}
+
+    def attn():
+        ops.tree_attention(ws.q, m, s.heads, s.kv_heads, s.head_dim, kc, vt, cache.capacity, rows.prefix, rows.depth,
+                           rows.anc, p, p + gen.cfg.depth, aws, ws.attn)
+
+    t = time_launches(attn, reps)
+    kv_bytes = 2 * s.kv_heads * (p + m) * s.head_dim * 2
+    qo_bytes = 2 * m * s.heads * s.head_dim * 2
+    b = kv_bytes + qo_bytes + m * 32 * 4
+    out["tree_attention"] = dict(ms=t, bytes=b, gbs=b / t / 1e6, frac=b / t / 1e6 / HBM_PEAK_GBS, rows=m,
+                                 context=p)
+
+    def gateup():
+        ops.gemm_swiglu(ws.x, m, L0.wgu, s.inter, s.hidden, ws.mlp)
+
+    t = time_launches(gateup, reps)
+    b = 2 * s.inter * s.hidden * 2 + m * s.hidden * 2 + m * s.inter * 2
+    out["gemm_gate_up"] = dict(ms=t, bytes=b, gbs=b / t / 1e6, frac=b / t / 1e6 / HBM_PEAK_GBS, rows=m,
+                               flops=2 * m * 2 * s.inter * s.hidden)
+
+    def down():
+        ops.gemm(ws.mlp, m, L0.wd, s.hidden, s.inter, ws.h, residual=ws.h)
+
+    t = time_launches(down, reps)
+    b = s.hidden * s.inter * 2 + m * (s.hidden + s.inter) * 2 + m * s.hidden * 2
+    out["gemm_down"] = dict(ms=t, bytes=b, gbs=b / t / 1e6, frac=b / t / 1e6 / HBM_PEAK_GBS, rows=m)
+
+    logits = ws.logits_buf(m, s.vocab)
+
+    def head():
+        ops.gemm(ws.x, m, target.model.lm_head, s.vocab, s.hidden, logits)
+
+    t = time_launches(head, reps)
+    b = s.vocab * s.hidden * 2 + m * s.hidden * 2 + m * s.vocab * 2
+    out["lm_head"] = dict(ms=t, bytes=b, gbs=b / t / 1e6, frac=b / t / 1e6 / HBM_PEAK_GBS, rows=m)
+
+    n = gen.cfg.depth + 1
+    src = torch.arange(committed, committed + n, dtype=torch.int32, device=kc.device) + torch.tensor(
+        [0] + [1] * (n - 1), dtype=torch.int32, device=kc.device)
+    nd = torch.tensor([n], dtype=torch.int32, device=kc.device)
+
+    def compact():
+        cache.compact_device(committed, src, nd, n)
+
+    t = time_launches(compact, reps)
+    b = 2 * n * s.layers * 2 * s.kv_heads * s.head_dim * 2
+    out["kv_compact"] = dict(ms=t, bytes=b, gbs=b / t / 1e6, frac=b / t / 1e6 / HBM_PEAK_GBS, rows=n)
+    return out
+
+
+def cpu_baseline(model, layers: list, dcfg: dict, rounds: int, prompt_len: int) -> dict:
+    """The CPU oracle (PyTorch restatement of the reference path) on the host cores. Its weights
+    are the GPU model's packed tensors copied to the host and viewed as row-major matrices of the
+    same shapes (a permutation of the same N(0, 0.02) values): the timing does not depend on
+    which permutation is used, and the copy takes seconds instead of minutes of CPU sampling."""
+    import torch
+
+    from oracle import engine as oe
+    from oracle import model as om
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    s = model.shape
+    shape = om.LlamaShape(s.hidden, s.layers, s.heads, s.kv_heads, s.head_dim, s.inter, s.vocab, s.eps, s.theta)
+    t0 = time.perf_counter()
+    host = lambda t, n, k: t[: n * k].view(n, k).cpu()
+    sd = {"model.embed_tokens.weight": model.embed.cpu(), "model.norm.weight": model.norm.cpu(),
+          "lm_head.weight": host(model.lm_head, s.vocab, s.hidden)}
+    nq, nkv = s.heads * s.head_dim, s.kv_heads * s.head_dim
+    for i, L in enumerate(model.layers):
+        p = f"model.layers.{i}."
+        qkv = host(L.wqkv, nq + 2 * nkv, s.hidden)
+        sd[p + "self_attn.q_proj.weight"] = qkv[:nq]
+        sd[p + "self_attn.k_proj.weight"] = qkv[nq:nq + nkv]
+        sd[p + "self_attn.v_proj.weight"] = qkv[nq + nkv:]
+        sd[p + "self_attn.o_proj.weight"] = host(L.wo, s.hidden, nq)
+        gu = host(L.wgu, 2 * s.inter, s.hidden)
+        sd[p + "mlp.gate_proj.weight"], sd[p + "mlp.up_proj.weight"] = gu[:s.inter], gu[s.inter:]
+        sd[p + "mlp.down_proj.weight"] = host(L.wd, s.hidden, s.inter)
+        sd[p + "input_layernorm.weight"] = L.ln1.cpu()
+        sd[p + "post_attention_layernorm.weight"] = L.ln2.cpu()
+    base = om.Llama(sd, shape, torch.bfloat16)
+    del sd
+    specs = om.plan_bridges(layers, s.layers)
+    draft = om.Subnetwork(base, layers, om.random_bridges(specs, s.hidden, seed=1, dtype=torch.bfloat16))
+    target = om.Target(base)
+    log(f"cpu oracle ready in {time.perf_counter() - t0:.1f}s on {cores} threads")
+    gen = oe.SpeculativeGenerator(target, draft, oe.Drafting(**dcfg), s.vocab)
+    ids = torch.randint(0, s.vocab, (prompt_len,), generator=torch.Generator().manual_seed(1)).tolist()
+    res = gen.generate(ids, 10 ** 6, {-1}, max_rounds=rounds)
+    toks = sum(res.accepted_per_round)
+    secs = res.decode_seconds
+    log(f"cpu oracle: {rounds} rounds, {toks} tokens in {secs:.2f}s")
+    return dict(value=round(toks / secs, 4), unit="tokens/s", cores=cores, kind="port",
+                sample=f"{rounds} speculative rounds of the same model shape and tree after a {prompt_len}-token "
+                       f"prompt (the GPU run uses the full prompt), bf16 PyTorch CPU oracle; "
+                       f"{1000 * secs / rounds:.0f} ms/round")
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="llama3_8b_tree", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-rounds", type=int, default=4)
+    ap.add_argument("--cpu-prompt", type=int, default=128)
+    ap.add_argument("--kernel-reps", type=int, default=30)
+    ap.add_argument("--ar-tokens", type=int, default=128)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on exactly one GPU (got --gpus {args.gpus}); multi-GPU is not part of it",
+              file=sys.stderr)
+        sys.exit(3)
+
+    import torch
+
+    from ssd.config import BridgeConfig, DraftingConfig
+    from ssd.data.token_freq import top_vocab, zipf_counts
+    from ssd.engine.speculative import SpeculativeGenerator, TargetRunner, autoregressive_generate
+    from ssd.models.llama import MI355XLlama
+    from ssd.models.subnetwork_draft import SubnetworkDraftModel
+    from ssd.runtime import SHAPES
+
+    torch.cuda.set_device(0)
+    shape_name, layers, dkw, n_prompt, draft_vocab = WORKLOADS[args.workload]
+    shape = SHAPES[shape_name]
+    t0 = time.perf_counter()
+    model = MI355XLlama.synthetic(shape, seed=0)
+    target = TargetRunner(model)
+    torch.manual_seed(0)
+    draft = SubnetworkDraftModel(model, layers, BridgeConfig())
+    draft.bridges.to(torch.bfloat16)
+    if draft_vocab:
+        draft.set_vocab_subset(top_vocab(zipf_counts(shape.vocab, 1.1, seed=0), draft_vocab))
+    cfg = DraftingConfig(**dkw)
+    gen = SpeculativeGenerator(model, draft, cfg, target)
+    ids = torch.randint(0, shape.vocab, (n_prompt,), generator=torch.Generator().manual_seed(1)).tolist()
+    rounds = args.warmup + args.steps
+    sess = gen.session(n_prompt + rounds * (cfg.depth + 1) + gen.capacity(0, 0))
+    log(f"model + draft ready in {time.perf_counter() - t0:.1f}s")
+    t0 = time.perf_counter()
+    sess.prefill(ids)
+    torch.cuda.synchronize()
+    log(f"prefill {n_prompt} tokens: {time.perf_counter() - t0:.2f}s")
+    for _ in range(args.warmup):
+        sess.step()
+    sess.phases.totals.clear()
+    n_warm = len(sess.accepted_per_round)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    toks = 0
+    for _ in range(args.steps):
+        toks += len(sess.step())
+    torch.cuda.synchronize()
+    secs = time.perf_counter() - t0
+    acc = sess.accepted_per_round[n_warm:]
+    phases = {k: 1000 * v / args.steps for k, v in sess.phases.totals.items()}
+    log(f"{args.steps} rounds: {toks} tokens in {secs:.3f}s ({toks / secs:.1f} tok/s, {1000 * secs / args.steps:.3f} "
+        f"ms/round), phases {phases}")
+    kf = kernel_figures(gen, sess, args.kernel_reps)
+    log(f"kernels: { {k: (round(v['ms'] * 1000, 1), round(v['gbs'])) for k, v in kf.items()} } (us, GB/s)")
+    del sess
+    torch.cuda.empty_cache()
+    ar = autoregressive_generate(target, torch.tensor([ids]), args.ar_tokens, {-1})
+    ar_tps = (len(ar.tokens) - 1) / ar.times["decode"]
+    log(f"autoregressive baseline: {ar_tps:.1f} tok/s")
+
+    bytes_round = model.weight_bytes() + 4 * model.weight_bytes(layers)
+    g = kf["gemm_gate_up"]
+    line = {
+        "metric": METRIC,
+        "value": round(toks / secs, 3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1000 * secs / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: random-init weights N(0, 0.02) generated on the GPU, uniform random prompt ids",
+        "config": {"workload": args.workload, "shape": shape_name, "draft_layers": layers, "drafting": dkw,
+                   "prompt_tokens": n_prompt, "draft_vocab": draft_vocab or "full", "batch": 1,
+                   "parallelism": "single GPU"},
+        "mean_accepted": round(sum(acc) / len(acc), 4),
+        "ms_per_round_phases": {k: round(v, 4) for k, v in phases.items()},
+        "ar_tokens_per_s": round(ar_tps, 3),
+        "speedup_vs_ar": round((toks / secs) / ar_tps, 4),
+        "round_weight_bytes": bytes_round,
+        "round_hbm_lower_bound_ms": round(bytes_round / HBM_PEAK_GBS / 1e6, 4),
+        "roofline": {"bound": "hbm", "kernel": "gemm_swiglu (verify gate/up, M=%d)" % g["rows"],
+                     "achieved": round(g["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(g["frac"], 4), "traffic": None},
+        "kernels": {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                    for k, v in kf.items()},
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(model, layers, dkw, args.cpu_rounds, args.cpu_prompt)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

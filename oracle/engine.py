@@ -23,6 +23,7 @@ turns the fp32 log-probs into floats before they are summed.
 
 from __future__ import annotations
 
+import time
 from dataclasses import dataclass, field
 from typing import Optional
 
@@ -317,6 +318,7 @@ class Result:
     tokens: list
     accepted_per_round: list = field(default_factory=list)
     tree_sizes: list = field(default_factory=list)
+    decode_seconds: float = 0.0  # wall time of the rounds (prefill excluded)
 
     @property
     def mean_accepted(self) -> float:
@@ -350,6 +352,7 @@ class SpeculativeGenerator:
         logits, _ = self.target(torch.tensor(input_ids), None, cache, logits_to_keep=1)
         out = [first_token(logits[-1], cfg.temperature, cfg.top_p, gen)]
         res = Result(tokens=[])
+        t0 = time.perf_counter()
         while not finish(out, eos_ids, max_new)[1]:
             if max_rounds is not None and len(res.accepted_per_round) >= max_rounds:
                 break
@@ -367,6 +370,7 @@ class SpeculativeGenerator:
             out.extend(new)
             res.accepted_per_round.append(len(new))
             res.tree_sizes.append(len(tree))
+        res.decode_seconds = time.perf_counter() - t0
         res.tokens = finish(out, eos_ids, max_new)[0]
         return res
 

@@ -147,6 +147,70 @@ def autoregressive_generate(target: TargetRunner, input_ids: torch.Tensor, max_n
     return GenerationResult(tokens=_finish(out, eos_ids, max_new_tokens)[0], times=times)
 
 
+class DecodeSession:
+    """One speculative decode stream on the device: buffers, cache and the round step.
+
+    ``prefill(ids)`` runs the target over the prompt and returns the first token;
+    ``step()`` runs one round (draft -> verify -> commit) with a single host synchronisation
+    and returns the committed tokens. ``SpeculativeGenerator.generate`` is a loop over it.
+    """
+
+    def __init__(self, gen: "SpeculativeGenerator", capacity: int):
+        cfg, drafter, target, draft = gen.cfg, gen.drafter, gen.target, gen.draft
+        if cfg.temperature != 0:
+            raise NotImplementedError("sampling speculative decoding is not part of this build yet")
+        self.cfg, self.drafter, self.target, self.draft = cfg, drafter, target, draft
+        dev = target.model.device
+        self.cache = target.new_cache(capacity)
+        self.ws = draft.workspace(CHUNK)
+        self.root_rows, self.level_rows, self.verify_rows = Rows(CHUNK, dev), Rows(CHUNK, dev), Rows(CHUNK, dev)
+        self.record = torch.zeros(4 + cfg.depth + 2, dtype=torch.int32, device=dev)  # [_, vn, n_new, tokens...]
+        self.record_host = torch.zeros_like(self.record, device="cpu").pin_memory()
+        self.tree = DeviceTree(dev, vmeta=self.record[1:2])
+        self.cand_tok = torch.zeros(TREE_CAP, dtype=torch.int32, device=dev)
+        self.cand_lp = torch.zeros(TREE_CAP, dtype=torch.float32, device=dev)
+        self.argmax = torch.zeros(ROW_CAP_VERIFY, dtype=torch.int32, device=dev)
+        self.keep_src = torch.zeros(cfg.depth + 2, dtype=torch.int32, device=dev)
+        self.n_keep = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.phases = _Phases()
+        self.accepted_per_round: list = []
+        self.tree_sizes: list = []
+
+    def prefill(self, ids: list) -> int:
+        _prefill(self.target, ids, self.cache, self.ws, self.root_rows.ids[0:1])
+        return int(self.root_rows.ids[0])
+
+    def step(self) -> list:
+        cfg, drafter, target, cache, ws = self.cfg, self.drafter, self.target, self.cache, self.ws
+        committed = cache.get_seq_length()
+        ph = self.phases
+        ph.mark("draft")
+        drafter.build_device(cache, self.root_rows, committed, self.tree, self.level_rows, self.cand_tok,
+                             self.cand_lp, ws)
+        cache.crop(committed)
+        ph.mark("verify")
+        m = drafter.finalize_device(self.tree, committed, self.root_rows, self.verify_rows)
+        cache.check_room(committed + m)
+        h = target.run_rows(self.verify_rows, m, committed + 1, committed + 1 + cfg.depth, cache, ws)
+        logits = target.head(target.final_norm(h, m, ws.x), m, ws)
+        ops.row_topk(logits, m, logits.shape[1], 1, 0, None, self.argmax)
+        _lib.call("ssd_accept_greedy", self.tree.struct, self.argmax.data_ptr(), committed,
+                  self.record[2:].data_ptr(), self.keep_src.data_ptr(), self.n_keep.data_ptr(),
+                  self.root_rows.ids.data_ptr(), ops.stream())
+        ph.mark("bookkeeping")
+        cache.compact_device(committed, self.keep_src, self.n_keep, cfg.depth + 1)
+        self.record_host.copy_(self.record, non_blocking=True)
+        ph.mark(None)
+        torch.cuda.current_stream().synchronize()
+        ph.resolve()
+        n_new = int(self.record_host[2])
+        new = self.record_host[3:3 + n_new].tolist()
+        cache.seq_len = committed + n_new
+        self.accepted_per_round.append(n_new)
+        self.tree_sizes.append(int(self.record_host[1]))
+        return new
+
+
 class SpeculativeGenerator:
     def __init__(self, base: nn.Module, draft: SubnetworkDraftModel, cfg: DraftingConfig,
                  target: Optional[TargetRunner] = None):
@@ -155,71 +219,36 @@ class SpeculativeGenerator:
         self.cfg = cfg
         self.drafter = TreeDrafter(draft, cfg)
 
+    def capacity(self, n_prompt: int, max_new_tokens: int) -> int:
+        """Cache slots for a generation; one round can overshoot max_new by depth+1 tokens and
+        the draft/verify of the last round need their own room (reference speculative.py:145-147)."""
+        extra = max(self.drafter.max_verify_nodes(), self.drafter.max_tree_cache()) + 1
+        return n_prompt + max_new_tokens + self.cfg.depth + extra + 1
+
+    def session(self, capacity: int) -> DecodeSession:
+        return DecodeSession(self, capacity)
+
     @torch.no_grad()
     def generate(self, input_ids: torch.Tensor, max_new_tokens: int, eos_ids: set, seed: Optional[int] = None,
                  max_rounds: Optional[int] = None) -> GenerationResult:
-        cfg, drafter, target, draft = self.cfg, self.drafter, self.target, self.draft
-        if cfg.temperature != 0:
-            raise NotImplementedError("sampling speculative decoding is not part of this build yet")
-        dev = target.model.device
         ids = torch.as_tensor(input_ids).reshape(-1).tolist()
-        n_prompt = len(ids)
-        extra = max(drafter.max_verify_nodes(), drafter.max_tree_cache()) + 1
-        cache = target.new_cache(n_prompt + max_new_tokens + cfg.depth + extra + 1)
-        ws = draft.workspace(CHUNK)
-        root_rows, level_rows, verify_rows = Rows(CHUNK, dev), Rows(CHUNK, dev), Rows(CHUNK, dev)
-        record = torch.zeros(4 + cfg.depth + 2, dtype=torch.int32, device=dev)  # [_, vn, n_new, tokens...]
-        record_host = torch.zeros_like(record, device="cpu").pin_memory()
-        tree = DeviceTree(dev, vmeta=record[1:2])
-        cand_tok = torch.zeros(TREE_CAP, dtype=torch.int32, device=dev)
-        cand_lp = torch.zeros(TREE_CAP, dtype=torch.float32, device=dev)
-        argmax = torch.zeros(ROW_CAP_VERIFY, dtype=torch.int32, device=dev)
-        keep_src = torch.zeros(cfg.depth + 2, dtype=torch.int32, device=dev)
-        n_keep = torch.zeros(1, dtype=torch.int32, device=dev)
-
+        sess = self.session(self.capacity(len(ids), max_new_tokens))
         times: dict = {}
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        _prefill(target, ids, cache, ws, root_rows.ids[0:1])
-        first = int(root_rows.ids[0])
+        out = [sess.prefill(ids)]
         times["prefill"] = time.perf_counter() - t0
-        out = [first]
-        result = GenerationResult(tokens=[], times=times)
-        phases = _Phases()
         t_dec = time.perf_counter()
         while not _finish(out, eos_ids, max_new_tokens)[1]:
-            if max_rounds is not None and len(result.accepted_per_round) >= max_rounds:
+            if max_rounds is not None and len(sess.accepted_per_round) >= max_rounds:
                 break
-            committed = cache.get_seq_length()
-            phases.mark("draft")
-            drafter.build_device(cache, root_rows, committed, tree, level_rows, cand_tok, cand_lp, ws)
-            cache.crop(committed)
-            phases.mark("verify")
-            m = drafter.finalize_device(tree, committed, root_rows, verify_rows)
-            cache.check_room(committed + m)
-            h = target.run_rows(verify_rows, m, committed + 1, committed + 1 + cfg.depth, cache, ws)
-            logits = target.head(target.final_norm(h, m, ws.x), m, ws)
-            ops.row_topk(logits, m, logits.shape[1], 1, 0, None, argmax)
-            _lib.call("ssd_accept_greedy", tree.struct, argmax.data_ptr(), committed, record[2:].data_ptr(),
-                      keep_src.data_ptr(), n_keep.data_ptr(), root_rows.ids.data_ptr(), ops.stream())
-            phases.mark("bookkeeping")
-            cache.compact_device(committed, keep_src, n_keep, cfg.depth + 1)
-            record_host.copy_(record, non_blocking=True)
-            phases.mark(None)
-            torch.cuda.current_stream().synchronize()
-            phases.resolve()
-            n_new = int(record_host[2])
-            new = record_host[3:3 + n_new].tolist()
-            cache.seq_len = committed + n_new
-            out.extend(new)
-            result.accepted_per_round.append(n_new)
-            result.tree_sizes.append(int(record_host[1]))
+            out.extend(sess.step())
         wall = time.perf_counter() - t_dec
-        times.update(phases.totals)
+        times.update(sess.phases.totals)
         # Host time between rounds (read-back, Python) is part of decode time, as in the reference.
-        times["host"] = max(0.0, wall - sum(phases.totals.values()))
-        result.tokens = _finish(out, eos_ids, max_new_tokens)[0]
-        return result
+        times["host"] = max(0.0, wall - sum(sess.phases.totals.values()))
+        return GenerationResult(tokens=_finish(out, eos_ids, max_new_tokens)[0], times=times,
+                                accepted_per_round=sess.accepted_per_round, tree_sizes=sess.tree_sizes)
 
 
 ROW_CAP_VERIFY = 64

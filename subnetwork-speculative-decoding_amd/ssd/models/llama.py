@@ -18,7 +18,7 @@ generated directly on the GPU for synthetic benchmarks (``synthetic``), never du
 
 from __future__ import annotations
 
-import math
+import types
 from dataclasses import dataclass
 from typing import Optional
 
@@ -113,6 +113,7 @@ class MI355XLlama:
         shape.validate()
         self.shape = shape
         self.config = _Cfg(shape)
+        self.generation_config = types.SimpleNamespace(eos_token_id=None)
         self.device = torch.device(device)
         self.embed: Optional[torch.Tensor] = None
         self.lm_head: Optional[torch.Tensor] = None
@@ -158,8 +159,10 @@ class MI355XLlama:
 
     @classmethod
     def from_hf(cls, model, device="cuda", keep_lm_head_rows: bool = False) -> "MI355XLlama":
-        return cls.from_state_dict(model.state_dict(), LlamaShape.from_hf_config(model.config), device,
-                                   keep_lm_head_rows)
+        m = cls.from_state_dict(model.state_dict(), LlamaShape.from_hf_config(model.config), device,
+                                keep_lm_head_rows)
+        m.generation_config.eos_token_id = getattr(getattr(model, "generation_config", None), "eos_token_id", None)
+        return m
 
     @classmethod
     def synthetic(cls, shape: LlamaShape, seed: int = 0, std: float = 0.02, device="cuda") -> "MI355XLlama":
