@@ -33,7 +33,8 @@ int ssd_device_arch(char* buf, int len); /* host buffer; gcnArchName of the curr
 
 /* ------------------------------------------------------------ weight format
  * Packs a row-major bf16 matrix W[N_src, K] (row stride ld) into MFMA tiles: tile (nb, kb) =
- * rows row_map[16nb .. 16nb+16) x k [32kb, 32kb+32), 64 lanes x 8 bf16. row_map[N_packed]
+ * rows row_map[16nb .. 16nb+16) x k [32kb, 32kb+32), 64 lanes x 8 bf16. N_packed is a multiple
+ * of 64 (ssd_packed_weight_elems pads rows to 64 and K to 32). row_map[N_packed]
  * (device int32) names the source row of each packed row (-1 = zero row); it fuses q/k/v,
  * interleaves gate/up and pairs rotary dims. Replaces holding nn.Linear weights as-is
  * (ssd/models/subnetwork_draft.py:80-89 references HF modules). */
@@ -95,9 +96,13 @@ int ssd_kv_compact_bf16(uint16_t* k_arena, uint16_t* vt_arena, int layers, int k
 /* Row top-k over bf16 logits. mode 0: raw values (k=1 is the first-index argmax of
  * ssd/engine/verify.py:47, speculative.py:83). mode 1: log_softmax values + logsumexp
  * (ssd/engine/tree_drafter.py:129-133); columns map through vocab_ids (subset head,
- * ssd/models/subnetwork_draft.py:136-144). Equal values rank lower column first. */
+ * ssd/models/subnetwork_draft.py:136-144). Equal values rank lower column first. Each row is scanned
+ * in 4096-column chunks by separate workgroups, merged in a fixed order; workspace of
+ * ssd_row_topk_ws_bytes(M, N) bytes. */
+int64_t ssd_row_topk_ws_bytes(int M, int N);
 int ssd_row_topk_bf16(const uint16_t* logits, int64_t ld, int M, int N, int k, int mode, const int32_t* vocab_ids,
-                      int32_t* out_tok, float* out_val, float* out_lse, hipStream_t stream);
+                      int32_t* out_tok, float* out_val, float* out_lse, void* ws, int64_t ws_bytes,
+                      hipStream_t stream);
 
 /* ------------------------------------------------------------------ tree
  * Device-resident DraftTree (ssd/engine/tree_drafter.py:48-95). All members are device

@@ -209,12 +209,35 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   const bool active = key0 < a.l_max;
   const bool shared = key0 + ATT_BLK <= a.p_min;
   const int j = lane & 15, g = lane >> 4;
+  // Blocks of this superblock that must be built per token (they reach past min(P)).
+  int tail_blocks[ATT_SB];
+  int n_tail = 0;
+#pragma unroll
+  for (int ww = 0; ww < ATT_SB; ++ww) {
+    const int k0 = (sb * ATT_SB + ww) * ATT_BLK;
+    if (k0 < a.l_max && k0 + ATT_BLK > a.p_min) tail_blocks[n_tail++] = ww;
+  }
 
   __shared__ AttnLds<HD> lds;
+  __shared__ int s_anc[16][ATT_MAXD];  // ancestor slots of the tile's tokens
+  __shared__ int s_P[16], s_L[16];
   Frags<HD> f;
   if (active && shared) load_shared_frags<HD>(f, a, kvh, key0, lane);
 
   for (int t = t_lo; t < t_hi; ++t) {
+    const int tok_first = (t * 16) / rep;
+    const int tok_last = min(a.M - 1, (t * 16 + 15) / rep);
+    const int ntok = tok_last - tok_first + 1;
+    if (n_tail) {
+      for (int idx = threadIdx.x; idx < ntok * ATT_MAXD; idx += 256)
+        s_anc[idx / ATT_MAXD][idx % ATT_MAXD] = a.anc[(size_t)(tok_first + idx / ATT_MAXD) * ATT_MAXD + idx % ATT_MAXD];
+      if (threadIdx.x < ntok) {
+        const int P = a.prefix[tok_first + threadIdx.x];
+        s_P[threadIdx.x] = P;
+        s_L[threadIdx.x] = P + min(a.depth[tok_first + threadIdx.x], ATT_MAXD);
+      }
+      __syncthreads();
+    }
     const int r = t * 16 + j;
     const bool rv = r < n_rows;
     const int tok = rv ? r / rep : 0;
@@ -236,31 +259,33 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int e = 0; e < 4; ++e) lds.o[w][j][dt * 16 + 4 * g + e] = o[dt][e];
-    } else {
-      const int tok_first = (t * 16) / rep;
-      const int tok_last = min(a.M - 1, (t * 16 + 15) / rep);
-      for (int tk = tok_first; tk <= tok_last; ++tk) {
-        const int P = a.prefix[tk], L = P + a.depth[tk];
-        const int* anc_t = a.anc + (size_t)tk * ATT_MAXD;
-        load_virtual_frags<HD>(f, a, kvh, key0, P, L, anc_t, lane);
-        uint32_t bits = 0;
+    }
+    // Per-token virtual blocks, spread over the four waves.
+    const int units = n_tail * ntok;
+    for (int u = w; u < units; u += ATT_SB) {
+      const int wb = tail_blocks[u / ntok];
+      const int tl = u % ntok, tk = tok_first + tl;
+      const int kb0 = (sb * ATT_SB + wb) * ATT_BLK;
+      const int P = s_P[tl], L = s_L[tl];
+      const int* anc_t = s_anc[tl];
+      Frags<HD> fv;
+      load_virtual_frags<HD>(fv, a, kvh, kb0, P, L, anc_t, lane);
+      uint32_t bits = 0;
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
+      for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (logical_slot(key0 + perm_key(kt, 4 * g + e), P, L, anc_t, a.max_len) >= 0) bits |= 1u << (kt * 4 + e);
-        float m, l;
-        f32x4_t o[DT];
-        block_attend<HD>(f, qf, bits, a.scale_log2, m, l, o);
-        if (rv && tok == tk) {
-          if (g == 0) { lds.m[w][j] = m; lds.l[w][j] = l; }
+        for (int e = 0; e < 4; ++e)
+          if (logical_slot(kb0 + perm_key(kt, 4 * g + e), P, L, anc_t, a.max_len) >= 0) bits |= 1u << (kt * 4 + e);
+      float m, l;
+      f32x4_t o[DT];
+      block_attend<HD>(fv, qf, bits, a.scale_log2, m, l, o);
+      if (rv && tok == tk) {
+        if (g == 0) { lds.m[wb][j] = m; lds.l[wb][j] = l; }
 #pragma unroll
-          for (int dt = 0; dt < DT; ++dt)
+        for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) lds.o[w][j][dt * 16 + 4 * g + e] = o[dt][e];
-        }
+          for (int e = 0; e < 4; ++e) lds.o[wb][j][dt * 16 + 4 * g + e] = o[dt][e];
       }
-      if (!rv && g == 0) { lds.m[w][j] = -INFINITY; lds.l[w][j] = 0.f; }
     }
     __syncthreads();
 
@@ -304,6 +329,10 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   }
 }
 
+// Cross-superblock combine, one wave per (token, q head). Canonical arithmetic for a row of
+// length L with superblocks s = 0..n-1: M = max_s m_s; w_s = 2^(m_s - M); l = sum_s l_s w_s and
+// O = sum_s O_s w_s, both summed in increasing s; out = O / l. All loads are independent of
+// the running sums, so they are issued ahead of the arithmetic.
 template <int HD>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ ws, int n_sb_cap, int M,
                                                            int heads, int kv_heads, const int* __restrict__ prefix,
@@ -315,34 +344,42 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
   const int tok = wid / heads, hq = wid % heads;
   const int rep = heads / kv_heads, kvh = hq / rep;
   const int R = tok * rep + hq % rep;
-  const int L = prefix[tok] + depth[tok];
+  const int L = prefix[tok] + min(depth[tok], ATT_MAXD);
   const int nsb = min(n_sb_run, (L + ATT_BLK * ATT_SB - 1) / (ATT_BLK * ATT_SB));
   const float* base = ws + ((size_t)kvh * M * rep + R) * n_sb_cap * (HD + 2);
-  float m = -INFINITY, l = 0.f, o[PER];
-  bool first = true;
-  for (int s = 0; s < nsb; ++s) {
-    const float* p = base + (size_t)s * (HD + 2);
-    const float ms = p[HD], ls = p[HD + 1];
-    if (ms == -INFINITY) continue;
-    if (first) {
-      m = ms; l = ls;
+  // pass 1: row max over superblocks (lanes own superblocks)
+  float mx = -INFINITY;
+  for (int s0 = 0; s0 < nsb; s0 += 64) {
+    const int s = s0 + lane;
+    if (s < nsb) mx = fmaxf(mx, base[(size_t)s * (HD + 2) + HD]);
+  }
+  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+  float l = 0.f, o[PER];
 #pragma unroll
-      for (int i = 0; i < PER; ++i) o[i] = (lane + 64 * i < HD) ? p[lane + 64 * i] : 0.f;
-      first = false;
-    } else {
-      const float mN = fmaxf(m, ms);
-      const float a1 = exp2f(m - mN), a2 = exp2f(ms - mN);
-      l = l * a1 + ls * a2;
+  for (int i = 0; i < PER; ++i) o[i] = 0.f;
+  for (int s0 = 0; s0 < nsb; s0 += 64) {
+    const int s = s0 + lane;
+    float wgt = 0.f, ls = 0.f;
+    if (s < nsb) {
+      const float ms = base[(size_t)s * (HD + 2) + HD];
+      ls = base[(size_t)s * (HD + 2) + HD + 1];
+      wgt = ms == -INFINITY ? 0.f : exp2f(ms - mx);
+    }
+    const int cnt = min(64, nsb - s0);
+    for (int q = 0; q < cnt; ++q) {
+      const float wq = __shfl(wgt, q);
+      const float lq = __shfl(ls, q);
+      l += lq * wq;
+      const float* p = base + (size_t)(s0 + q) * (HD + 2);
 #pragma unroll
       for (int i = 0; i < PER; ++i)
-        if (lane + 64 * i < HD) o[i] = o[i] * a1 + p[lane + 64 * i] * a2;
-      m = mN;
+        if (lane + 64 * i < HD && wq != 0.f) o[i] += p[lane + 64 * i] * wq;
     }
   }
   bf16_t* dst = out + (size_t)tok * ldo + (size_t)hq * HD;
 #pragma unroll
   for (int i = 0; i < PER; ++i)
-    if (lane + 64 * i < HD) dst[lane + 64 * i] = f2bf(first ? 0.f : o[i] / l);
+    if (lane + 64 * i < HD) dst[lane + 64 * i] = f2bf(l > 0.f ? o[i] / l : 0.f);
 }
 
 template <int HD>

@@ -6,12 +6,18 @@
 // * W is pre-packed once into MFMA-native tiles: tile (nb, kb) holds rows
 //   [16nb, 16nb+16) x k [32kb, 32kb+32) as 64 lanes x 8 bf16, in the order the
 //   v_mfma_f32_16x16x32_bf16 A operand wants it. A wave's load of one tile is
-//   one fully contiguous 1 KiB request (16 B per lane).
-// * One workgroup owns one 16-row tile of N (the whole K); its KS waves split K
-//   into fixed contiguous ranges and are summed through LDS in wave order.
-// * X (activations, row-major) is the B operand, loaded straight from L2; rows
-//   beyond M are zeros. M is covered by CT column tiles of 16.
-// * Batch invariance: the instruction, the K split and the summation order
+//   one fully contiguous 1 KiB request (16 B per lane). Rows are padded to 64.
+// * A workgroup owns NSUB 16-row tiles of N and the whole K; its KS waves split
+//   K into fixed contiguous ranges and are summed through LDS in wave order. Each
+//   wave streams its NSUB weight tiles against one X fragment per k-block, so
+//   activation traffic from L2 is CT/NSUB of the weight traffic (CT = 16-row
+//   column tiles of M), and issues 4 k-blocks of loads (4*NSUB KiB of weights)
+//   before it waits: HBM is kept busy by bytes in flight, not by instruction
+//   count. Wide N uses NSUB=4 / 4 waves; narrow N (o, down, qkv) NSUB=1 with up
+//   to 16 waves so that every CU still streams. (K is never split across
+//   workgroups: an agent-scope fence between them costs a write-back and
+//   invalidate of the whole L2 on this chip.)
+// * Batch invariance: instruction, NSUB, KS and every summation order
 //   depend only on (N, K), never on M, so a row's result is bit-identical
 //   whether it is computed alone (autoregressive step) or inside a 25-row
 //   verify batch. This is what keeps speculative greedy output identical to
@@ -46,98 +52,30 @@ struct GemmArgs {
   const bf16_t* bias2;
   // EPI_QKV
   int heads, kv_heads, head_dim;
-  const bf16_t* cos_tab;  // [max_pos, head_dim/2]
+  const bf16_t* cos_tab;  // [rope_rows, head_dim/2]
   const bf16_t* sin_tab;
   const int* row_pos;     // [M]
   const int* row_slot;    // [M]
-  int64_t rope_rows;      // rows of cos_tab / sin_tab
+  int64_t rope_rows;
   bf16_t* k_cache;        // this layer: [kv_heads, max_len, head_dim]
   bf16_t* vt_cache;       // this layer: [kv_heads, head_dim, max_len]
   int64_t max_len;
 };
 
-template <int CT, int KS>
-struct GemmLds {
-  float4 red[KS][CT][64];
-};
+constexpr int GEMM_UNROLL = 4;
 
-template <int CT, int KS, int EPI>
-__global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-  const int nb = blockIdx.x;
-  const int kbt = a.kb_total;
-  const int kb_lo = (kbt * w) / KS;
-  const int kb_hi = (kbt * (w + 1)) / KS;
-  const int j = lane & 15, g = lane >> 4;
-
-  f32x4_t acc[CT];
-#pragma unroll
-  for (int c = 0; c < CT; ++c) acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  const uint4* wp = a.W + ((size_t)nb * kbt) * 64 + lane;
-  const bf16_t* xp[CT];
-  bool xv[CT];
-#pragma unroll
-  for (int c = 0; c < CT; ++c) {
-    const int m = c * 16 + j;
-    xv[c] = m < a.M;
-    xp[c] = a.X + (size_t)(xv[c] ? m : 0) * a.ldx + g * 8;
-  }
-
-  int kb = kb_lo;
-  // Two k-blocks per trip so that four independent 16 B loads are in flight.
-  for (; kb + 1 < kb_hi; kb += 2) {
-    uint4 w0 = ld_stream(wp + (size_t)kb * 64);
-    uint4 w1 = ld_stream(wp + (size_t)(kb + 1) * 64);
-    uint4 x0[CT], x1[CT];
-#pragma unroll
-    for (int c = 0; c < CT; ++c) {
-      x0[c] = xv[c] ? *(const uint4*)(xp[c] + kb * 32) : make_uint4(0, 0, 0, 0);
-      x1[c] = xv[c] ? *(const uint4*)(xp[c] + (kb + 1) * 32) : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int c = 0; c < CT; ++c) acc[c] = mfma16x16x32(as_bf16x8(w0), as_bf16x8(x0[c]), acc[c]);
-#pragma unroll
-    for (int c = 0; c < CT; ++c) acc[c] = mfma16x16x32(as_bf16x8(w1), as_bf16x8(x1[c]), acc[c]);
-  }
-  if (kb < kb_hi) {
-    uint4 w0 = ld_stream(wp + (size_t)kb * 64);
-#pragma unroll
-    for (int c = 0; c < CT; ++c) {
-      uint4 x0 = xv[c] ? *(const uint4*)(xp[c] + kb * 32) : make_uint4(0, 0, 0, 0);
-      acc[c] = mfma16x16x32(as_bf16x8(w0), as_bf16x8(x0), acc[c]);
-    }
-  }
-
-  __shared__ GemmLds<CT, KS> lds;
-#pragma unroll
-  for (int c = 0; c < CT; ++c) lds.red[w][c][lane] = make_float4(acc[c][0], acc[c][1], acc[c][2], acc[c][3]);
-  __syncthreads();
-
-  // Value of tile row r (0..15), token m, summed over the waves in wave order.
-  auto tile_val = [&](int r, int m) -> float {
-    const int c = m >> 4;
-    const int ln = (m & 15) + 16 * (r >> 2);
-    const int e = r & 3;
-    float s = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < KS; ++ww) {
-      const float4 v = lds.red[ww][c][ln];
-      const float x = e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
-      s = ww == 0 ? x : s + x;
-    }
-    return s;
-  };
-
-  const int nthreads = 64 * KS;
-  const int Mv = a.M < CT * 16 ? a.M : CT * 16;
+// Epilogue of one 16-row tile `nb` for rows m < Mv; val(r, m) is the fp32 dot product of tile
+// row r and token m.
+template <int EPI, int NTHREADS, class Val>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, int nb, int Mv, Val val) {
+  if (nb * 16 >= a.N) return;
+  const int nthreads = NTHREADS;
   if constexpr (EPI == EPI_STORE) {
     for (int o = threadIdx.x; o < 16 * Mv; o += nthreads) {
       const int m = o >> 4, r = o & 15;
       const int n = nb * 16 + r;
       if (n >= a.N) continue;
-      float t = tile_val(r, m);
+      float t = val(r, m);
       if (a.bias) t += bf2f(a.bias[n]);
       t = rbf(t);
       if (a.act) t = rbf(apply_act(a.act, t));
@@ -149,7 +87,7 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
       const int m = o >> 3, r = o & 7;
       const int col = nb * 8 + r;  // intermediate index
       if (col * 2 >= a.N) continue;
-      float gt = tile_val(r, m), up = tile_val(r + 8, m);
+      float gt = val(r, m), up = val(r + 8, m);
       if (a.bias) gt += bf2f(a.bias[col]);
       if (a.bias2) up += bf2f(a.bias2[col]);
       const float gs = rbf(silu_f(rbf(gt)));
@@ -169,7 +107,7 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
     for (int o = threadIdx.x; o < 8 * Mv; o += nthreads) {
       const int m = o >> 3, r = o & 7;
       const int dlo = p * 8 + r, dhi = dlo + half;
-      const float xlo = rbf(tile_val(r, m)), xhi = rbf(tile_val(r + 8, m));
+      const float xlo = rbf(val(r, m)), xhi = rbf(val(r + 8, m));
       const int slot = a.row_slot[m];
       if (region != 0 && (slot < 0 || slot >= a.max_len)) continue;  // never write outside the cache
       if (region == 2) {
@@ -196,6 +134,97 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
   }
 }
 
+template <int KS, int NSUB, int CT>
+struct GemmLds {
+  float4 red[KS][NSUB][CT][64];
+};
+
+template <int CT, int NSUB, int KS, int EPI>
+__global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int tile = blockIdx.x;
+  const int kbt = a.kb_total;
+  const int kb_lo = (kbt * w) / KS;
+  const int kb_hi = (kbt * (w + 1)) / KS;
+  const int j = lane & 15, g = lane >> 4;
+
+  f32x4_t acc[NSUB][CT];
+#pragma unroll
+  for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+    for (int c = 0; c < CT; ++c) acc[s][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const uint4* wp[NSUB];
+#pragma unroll
+  for (int s = 0; s < NSUB; ++s) wp[s] = a.W + ((size_t)(tile * NSUB + s) * kbt) * 64 + lane;
+  const bf16_t* xp[CT];
+  bool xv[CT];
+#pragma unroll
+  for (int c = 0; c < CT; ++c) {
+    const int m = c * 16 + j;
+    xv[c] = m < a.M;
+    xp[c] = a.X + (size_t)(xv[c] ? m : 0) * a.ldx + g * 8;
+  }
+
+  int kb = kb_lo;
+  for (; kb + GEMM_UNROLL - 1 < kb_hi; kb += GEMM_UNROLL) {
+    uint4 wr[GEMM_UNROLL][NSUB], xr[GEMM_UNROLL][CT];
+#pragma unroll
+    for (int u = 0; u < GEMM_UNROLL; ++u)
+#pragma unroll
+      for (int s = 0; s < NSUB; ++s) wr[u][s] = ld_stream(wp[s] + (size_t)(kb + u) * 64);
+#pragma unroll
+    for (int u = 0; u < GEMM_UNROLL; ++u)
+#pragma unroll
+      for (int c = 0; c < CT; ++c)
+        xr[u][c] = xv[c] ? *(const uint4*)(xp[c] + (kb + u) * 32) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < GEMM_UNROLL; ++u)
+#pragma unroll
+      for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+        for (int c = 0; c < CT; ++c) acc[s][c] = mfma16x16x32(as_bf16x8(wr[u][s]), as_bf16x8(xr[u][c]), acc[s][c]);
+  }
+  for (; kb < kb_hi; ++kb) {
+    uint4 wr[NSUB], xr[CT];
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s) wr[s] = ld_stream(wp[s] + (size_t)kb * 64);
+#pragma unroll
+    for (int c = 0; c < CT; ++c) xr[c] = xv[c] ? *(const uint4*)(xp[c] + kb * 32) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+      for (int c = 0; c < CT; ++c) acc[s][c] = mfma16x16x32(as_bf16x8(wr[s]), as_bf16x8(xr[c]), acc[s][c]);
+  }
+
+  __shared__ GemmLds<KS, NSUB, CT> lds;
+#pragma unroll
+  for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+    for (int c = 0; c < CT; ++c)
+      lds.red[w][s][c][lane] = make_float4(acc[s][c][0], acc[s][c][1], acc[s][c][2], acc[s][c][3]);
+  __syncthreads();
+
+  // Tile row r (0..15) of sub-tile s, token m, summed over the waves in wave order.
+  const int Mv = a.M < CT * 16 ? a.M : CT * 16;
+#pragma unroll
+  for (int s = 0; s < NSUB; ++s)
+    gemm_epilogue<EPI, 64 * KS>(a, tile * NSUB + s, Mv, [&](int r, int m) -> float {
+      const int c = m >> 4;
+      const int ln = (m & 15) + 16 * (r >> 2);
+      const int e = r & 3;
+      float v = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < KS; ++ww) {
+        const float4 q = lds.red[ww][s][c][ln];
+        const float x = e == 0 ? q.x : e == 1 ? q.y : e == 2 ? q.z : q.w;
+        v = ww == 0 ? x : v + x;
+      }
+      return v;
+    });
+}
+
 // ---------------------------------------------------------------- packing
 // dst tile (nb, kb), lane l, element t  <-  W[row_map[16 nb + l%16]][32 kb + 8 (l/16) + t]
 // (row_map entry < 0 or beyond K -> zero).
@@ -213,17 +242,30 @@ __global__ void pack_kernel(const bf16_t* __restrict__ src, int64_t ld, int K, c
   dst[tile * 64 + lane] = p.u;
 }
 
-static int choose_ks(int kb_total) {
-  if (kb_total >= 16) return 8;
-  if (kb_total >= 8) return 4;
-  if (kb_total >= 2) return 2;
-  return 1;
+struct GemmPlan {
+  int nsub, ks, tiles;
+};
+
+// Launch geometry as a function of (N, K) only (never of M): that is what keeps every row's
+// arithmetic identical for any batch size.
+static GemmPlan plan_for(int N, int K) {
+  const int kbt = K / 32;
+  GemmPlan p;
+  if (N >= 16384) {
+    p.nsub = 4; p.ks = 4;
+  } else if (N >= 8192) {
+    p.nsub = 2; p.ks = 8;
+  } else {
+    p.nsub = 1; p.ks = 16;
+  }
+  while (p.ks > 1 && kbt / p.ks < GEMM_UNROLL) p.ks >>= 1;  // keep whole unrolled trips per wave
+  p.tiles = (N + 16 * p.nsub - 1) / (16 * p.nsub);
+  return p;
 }
 
 template <int EPI>
 static int launch_gemm(GemmArgs a, hipStream_t s) {
-  const int ks = choose_ks(a.kb_total);
-  const int n_tiles = EPI == EPI_STORE ? (a.N + 15) / 16 : (a.N + 15) / 16;
+  const GemmPlan p = plan_for(a.N, a.kb_total * 32);
   // Rows beyond 64 are processed in chunks of 64; each chunk is computed exactly as it would be alone.
   for (int m0 = 0; m0 < a.M; m0 += 64) {
     GemmArgs b = a;
@@ -234,12 +276,17 @@ static int launch_gemm(GemmArgs a, hipStream_t s) {
     if (a.row_pos) b.row_pos = a.row_pos + m0;
     if (a.row_slot) b.row_slot = a.row_slot + m0;
     const int ct = (b.M + 15) / 16;
-    dim3 grid(n_tiles), block(64 * ks);
-#define SSD_GEMM_CASE(CT_, KS_) \
-  if (ct == CT_ && ks == KS_) { hipLaunchKernelGGL((gemm_kernel<CT_, KS_, EPI>), grid, block, 0, s, b); }
-#define SSD_GEMM_KS(CT_) SSD_GEMM_CASE(CT_, 1) SSD_GEMM_CASE(CT_, 2) SSD_GEMM_CASE(CT_, 4) SSD_GEMM_CASE(CT_, 8)
-    SSD_GEMM_KS(1) SSD_GEMM_KS(2) SSD_GEMM_KS(3) SSD_GEMM_KS(4)
-#undef SSD_GEMM_KS
+    dim3 grid(p.tiles);
+#define SSD_GEMM_CASE(CT_, NS_, KS_) \
+  if (ct == CT_ && p.nsub == NS_ && p.ks == KS_) {                                                   \
+    hipLaunchKernelGGL((gemm_kernel<CT_, NS_, KS_, EPI>), grid, dim3(64 * KS_), 0, s, b);           \
+  }
+#define SSD_GEMM_PLANS(CT_)                                                                             \
+  SSD_GEMM_CASE(CT_, 4, 4) SSD_GEMM_CASE(CT_, 4, 2) SSD_GEMM_CASE(CT_, 4, 1) SSD_GEMM_CASE(CT_, 2, 8) \
+  SSD_GEMM_CASE(CT_, 2, 4) SSD_GEMM_CASE(CT_, 2, 2) SSD_GEMM_CASE(CT_, 2, 1) SSD_GEMM_CASE(CT_, 1, 16) \
+  SSD_GEMM_CASE(CT_, 1, 8) SSD_GEMM_CASE(CT_, 1, 4) SSD_GEMM_CASE(CT_, 1, 2) SSD_GEMM_CASE(CT_, 1, 1)
+    SSD_GEMM_PLANS(1) SSD_GEMM_PLANS(2) SSD_GEMM_PLANS(3) SSD_GEMM_PLANS(4)
+#undef SSD_GEMM_PLANS
 #undef SSD_GEMM_CASE
     int rc = check_launch("gemm");
     if (rc) return rc;
@@ -261,14 +308,15 @@ static int check_common(const bf16_t* X, int64_t ldx, int M, const void* W, int 
 using namespace ssd;
 
 SSD_API int64_t ssd_packed_weight_elems(int N, int K) {
-  return (int64_t)((N + 15) / 16) * 16 * (int64_t)((K + 31) / 32) * 32;
+  return (int64_t)((N + 63) / 64) * 64 * (int64_t)((K + 31) / 32) * 32;
 }
+
 
 SSD_API int ssd_pack_weight_bf16(const uint16_t* src, int64_t ld, int N_src, int K, const int32_t* row_map,
                                  int N_packed, uint16_t* dst, hipStream_t stream) {
   if (!src || !dst || !row_map) return set_error(SSD_EINVAL, "pack: null pointer");
-  if (N_packed <= 0 || N_packed % 16 || K <= 0 || N_src <= 0)
-    return set_error(SSD_EINVAL, "pack: N_packed=%d must be a positive multiple of 16 (K=%d)", N_packed, K);
+  if (N_packed <= 0 || N_packed % 64 || K <= 0 || N_src <= 0)
+    return set_error(SSD_EINVAL, "pack: N_packed=%d must be a positive multiple of 64 (K=%d)", N_packed, K);
   const int n_tiles_n = N_packed / 16, kb_total = (K + 31) / 32;
   const int64_t tiles = (int64_t)n_tiles_n * kb_total;
   hipLaunchKernelGGL(pack_kernel, dim3((unsigned)((tiles + 3) / 4)), dim3(256), 0, stream, src, ld, K, row_map,

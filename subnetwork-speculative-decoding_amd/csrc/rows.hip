@@ -112,31 +112,37 @@ __device__ __forceinline__ void topk_insert(Cand (&c)[TOPK_MAX], int k, float v,
   c[p] = Cand{v, i};
 }
 
-// One workgroup per row of bf16 logits [M, ld] (N valid columns).
-// mode 0: k best columns by raw value (argmax for k = 1).
-// mode 1: k best log-softmax values, lp = (x - max) - log(sum exp(x - max)) in fp32
-//         (ssd/engine/tree_drafter.py:129-133), plus the row's logsumexp.
-// Column c maps to token vocab_ids[c] when vocab_ids is given (vocab subset head).
-__global__ __launch_bounds__(256) void row_topk_kernel(const bf16_t* __restrict__ logits, int64_t ld, int N, int k,
-                                                       int mode, const int* __restrict__ vocab_ids,
-                                                       int* __restrict__ out_tok, float* __restrict__ out_val,
-                                                       float* __restrict__ out_lse) {
+constexpr int TOPK_CHUNK = 4096;  // columns per partial workgroup
+
+struct TopkPart {
+  float mx;  // chunk maximum
+  float se;  // sum of exp(x - mx) over the chunk (mode 1)
+  float v[TOPK_MAX];
+  int i[TOPK_MAX];
+};
+
+// Partial pass: workgroup (s, row) scans columns [s*chunk, (s+1)*chunk) of one row of bf16
+// logits and writes its k best (value, column) pairs -- larger value first, lower column on
+// ties -- its maximum and (mode 1) its sum of exp(x - max).
+__global__ __launch_bounds__(256) void row_topk_partial_kernel(const bf16_t* __restrict__ logits, int64_t ld, int N,
+                                                               int k, int mode, TopkPart* __restrict__ parts) {
   __shared__ float sv[256 * TOPK_MAX];
   __shared__ int si[256 * TOPK_MAX];
   __shared__ float sh[4];
-  const int row = blockIdx.x;
+  const int s = blockIdx.x, row = blockIdx.y, S = gridDim.x;
+  const int c0 = s * TOPK_CHUNK, c1 = min(N, c0 + TOPK_CHUNK);
   const bf16_t* x = logits + (size_t)row * ld;
   Cand c[TOPK_MAX];
 #pragma unroll
   for (int q = 0; q < TOPK_MAX; ++q) c[q] = Cand{-INFINITY, 0x7fffffff};
-  const int nvec = N / 8;
-  for (int vI = threadIdx.x; vI < nvec; vI += 256) {
+  const int v1 = c0 + ((c1 - c0) / 8) * 8;
+  for (int col = c0 + threadIdx.x * 8; col < v1; col += 256 * 8) {
     Pack8 p;
-    p.u = *(const uint4*)(x + (size_t)vI * 8);
+    p.u = *(const uint4*)(x + col);
 #pragma unroll
-    for (int t = 0; t < 8; ++t) topk_insert(c, k, bf2f(p.h[t]), vI * 8 + t);
+    for (int t = 0; t < 8; ++t) topk_insert(c, k, bf2f(p.h[t]), col + t);
   }
-  for (int col = nvec * 8 + threadIdx.x; col < N; col += 256) topk_insert(c, k, bf2f(x[col]), col);
+  for (int col = v1 + threadIdx.x; col < c1; col += 256) topk_insert(c, k, bf2f(x[col]), col);
   for (int q = 0; q < k; ++q) {
     sv[threadIdx.x * TOPK_MAX + q] = c[q].v;
     si[threadIdx.x * TOPK_MAX + q] = c[q].i;
@@ -165,26 +171,60 @@ __global__ __launch_bounds__(256) void row_topk_kernel(const bf16_t* __restrict_
     }
     __syncthreads();
   }
+  const float mx = sv[0];
+  float se = 0.f;
+  if (mode == 1) {
+    float acc = 0.f;
+    for (int col = c0 + threadIdx.x * 8; col < v1; col += 256 * 8) {
+      Pack8 p;
+      p.u = *(const uint4*)(x + col);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) acc += __expf(bf2f(p.h[t]) - mx);
+    }
+    for (int col = v1 + threadIdx.x; col < c1; col += 256) acc += __expf(bf2f(x[col]) - mx);
+    se = block_sum_256(acc, sh);
+  }
+  TopkPart* out = parts + (size_t)row * S + s;
+  if (threadIdx.x == 0) { out->mx = mx; out->se = se; }
+  if (threadIdx.x < k) { out->v[threadIdx.x] = sv[threadIdx.x]; out->i[threadIdx.x] = si[threadIdx.x]; }
+}
+
+// Merge pass, one wave per row: global max M; logsumexp = M + log(sum_s se_s * exp(mx_s - M))
+// (lanes own chunks; fixed butterfly order); the k best of the chunks' sorted lists.
+// mode 0 writes raw values, mode 1 log-softmax values (x - M) - log(sum).
+__global__ __launch_bounds__(64) void row_topk_merge_kernel(const TopkPart* __restrict__ parts, int S, int k, int mode,
+                                                            const int* __restrict__ vocab_ids, int* __restrict__ out_tok,
+                                                            float* __restrict__ out_val, float* __restrict__ out_lse) {
+  const int row = blockIdx.x, lane = threadIdx.x;
+  const TopkPart* p = parts + (size_t)row * S;
+  float mx = -INFINITY;
+  for (int s = lane; s < S; s += 64) mx = fmaxf(mx, p[s].mx);
+  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
   float lse = 0.f;
   if (mode == 1) {
-    const float mx = sv[0];
-    float s = 0.f;
-    for (int vI = threadIdx.x; vI < nvec; vI += 256) {
-      Pack8 p;
-      p.u = *(const uint4*)(x + (size_t)vI * 8);
-#pragma unroll
-      for (int t = 0; t < 8; ++t) s += __expf(bf2f(p.h[t]) - mx);
-    }
-    for (int col = nvec * 8 + threadIdx.x; col < N; col += 256) s += __expf(bf2f(x[col]) - mx);
-    const float tot = block_sum_256(s, sh);
-    lse = logf(tot);
-    if (threadIdx.x == 0 && out_lse) out_lse[row] = mx + lse;
+    float acc = 0.f;
+    for (int s = lane; s < S; s += 64) acc += p[s].se * __expf(p[s].mx - mx);
+    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
+    lse = logf(acc);
   }
-  if (threadIdx.x < k) {
-    const int q = threadIdx.x;
-    const int col = si[q];
-    out_tok[row * k + q] = vocab_ids ? vocab_ids[col] : col;
-    if (out_val) out_val[row * k + q] = mode == 1 ? (sv[q] - sv[0]) - lse : sv[q];
+  if (lane == 0) {
+    int head[64];
+    for (int s = 0; s < S && s < 64; ++s) head[s] = 0;
+    for (int q = 0; q < k; ++q) {
+      int best = -1;
+      float bv = -INFINITY;
+      int bi = 0x7fffffff;
+      for (int s = 0; s < S && s < 64; ++s) {
+        if (head[s] >= k) continue;
+        const float v = p[s].v[head[s]];
+        const int ix = p[s].i[head[s]];
+        if (best < 0 || better(v, ix, bv, bi)) { best = s; bv = v; bi = ix; }
+      }
+      ++head[best];
+      out_tok[row * k + q] = vocab_ids ? vocab_ids[bi] : bi;
+      if (out_val) out_val[row * k + q] = mode == 1 ? (bv - mx) - lse : bv;
+    }
+    if (mode == 1 && out_lse) out_lse[row] = mx + lse;
   }
 }
 
@@ -223,14 +263,26 @@ SSD_API int ssd_kv_compact_bf16(uint16_t* k_arena, uint16_t* vt_arena, int layer
   return check_launch("kv_compact");
 }
 
+SSD_API int64_t ssd_row_topk_ws_bytes(int M, int N) {
+  const int S = (N + TOPK_CHUNK - 1) / TOPK_CHUNK;
+  return (int64_t)M * S * (int64_t)sizeof(TopkPart);
+}
+
 SSD_API int ssd_row_topk_bf16(const uint16_t* logits, int64_t ld, int M, int N, int k, int mode,
-                              const int32_t* vocab_ids, int32_t* out_tok, float* out_val, float* out_lse,
-                              hipStream_t stream) {
-  if (!logits || !out_tok || M < 0 || N <= 0 || k < 1 || k > TOPK_MAX || k > N || (mode != 0 && mode != 1))
+                              const int32_t* vocab_ids, int32_t* out_tok, float* out_val, float* out_lse, void* ws,
+                              int64_t ws_bytes, hipStream_t stream) {
+  if (!logits || !out_tok || !ws || M < 0 || N <= 0 || k < 1 || k > TOPK_MAX || k > N || (mode != 0 && mode != 1))
     return set_error(SSD_EINVAL, "row_topk: bad arguments (k=%d, N=%d, mode=%d)", k, N, mode);
   if (ld % 8 || ((uintptr_t)logits & 15)) return set_error(SSD_EINVAL, "row_topk: logits must be 16-byte aligned");
+  const int S = (N + TOPK_CHUNK - 1) / TOPK_CHUNK;
+  if (S > 64) return set_error(SSD_ERANGE, "row_topk: N=%d above %d columns", N, 64 * TOPK_CHUNK);
+  if (ws_bytes < ssd_row_topk_ws_bytes(M, N)) return set_error(SSD_EINVAL, "row_topk: workspace too small");
   if (M == 0) return SSD_OK;
-  hipLaunchKernelGGL(row_topk_kernel, dim3(M), dim3(256), 0, stream, logits, ld, N, k, mode, vocab_ids, out_tok,
-                     out_val, out_lse);
-  return check_launch("row_topk");
+  hipLaunchKernelGGL(row_topk_partial_kernel, dim3(S, M), dim3(256), 0, stream, logits, ld, N, k, mode,
+                     (TopkPart*)ws);
+  int rc = check_launch("row_topk_partial");
+  if (rc) return rc;
+  hipLaunchKernelGGL(row_topk_merge_kernel, dim3(M), dim3(64), 0, stream, (const TopkPart*)ws, S, k, mode, vocab_ids,
+                     out_tok, out_val, out_lse);
+  return check_launch("row_topk_merge");
 }

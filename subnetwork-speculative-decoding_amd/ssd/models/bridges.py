@@ -170,9 +170,12 @@ class TransitionBridge(nn.Module):
             self._packed = PackedBridge(self, device)
         return self._packed
 
-    def _apply(self, fn, *args, **kwargs):  # .to()/.cuda()/load: drop the packed copy
-        self._packed = None
-        return super()._apply(fn, *args, **kwargs)
+    def _apply(self, fn, *args, **kwargs):  # .to()/.cuda(): drop the packed copy if parameters changed
+        before = [(p.data_ptr(), p.dtype, p.device) for p in self.parameters()]
+        out = super()._apply(fn, *args, **kwargs)
+        if [(p.data_ptr(), p.dtype, p.device) for p in self.parameters()] != before:
+            self._packed = None
+        return out
 
     def load_state_dict(self, *args, **kwargs):
         self._packed = None

@@ -114,7 +114,10 @@ class MI355XLlama:
         self.shape = shape
         self.config = _Cfg(shape)
         self.generation_config = types.SimpleNamespace(eos_token_id=None)
-        self.device = torch.device(device)
+        dev = torch.device(device)
+        if dev.type == "cuda" and dev.index is None:
+            dev = torch.device("cuda", torch.cuda.current_device())
+        self.device = dev
         self.embed: Optional[torch.Tensor] = None
         self.lm_head: Optional[torch.Tensor] = None
         self.norm: Optional[torch.Tensor] = None

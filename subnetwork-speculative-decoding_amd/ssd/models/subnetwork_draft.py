@@ -240,7 +240,7 @@ class SubnetworkDraftModel(nn.Module):
 
     def _packed_bridge(self, name: str):
         br = self.bridges[name]
-        if br.norm.weight.device != self.model.device:
+        if br._packed is None and br.norm.weight.device != self.model.device:
             br.to(self.model.device)
         return br.packed(self.model.device)
 

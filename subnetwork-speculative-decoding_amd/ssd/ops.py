@@ -50,18 +50,19 @@ def packed_elems(n: int, k: int) -> int:
     return int(_lib.load().ssd_packed_weight_elems(n, k))
 
 
-def pack_weight(w: torch.Tensor, row_map: Optional[torch.Tensor] = None, n_packed: Optional[int] = None) -> torch.Tensor:
-    """Row-major bf16 W[N, K] -> MFMA tile layout. row_map[n_packed] picks the source row of
-    each packed row (-1 = zeros); default = identity padded to a multiple of 16."""
+def pack_weight(w: torch.Tensor, row_map: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Row-major bf16 W[N, K] -> MFMA tile layout. row_map picks the source row of each packed
+    row (-1 = zeros); default = identity. Rows are padded with zeros to a multiple of 64."""
     _check(w, "w")
     n, k = w.shape
     ld = _rows(w, "w", k)
     if row_map is None:
-        n_packed = (n + 15) // 16 * 16
-        row_map = torch.arange(n_packed, dtype=torch.int32)
-        row_map[n:] = -1
-    n_packed = int(row_map.numel()) if n_packed is None else n_packed
-    rm = row_map.to(device=w.device, dtype=torch.int32)
+        row_map = torch.arange(n, dtype=torch.int32)
+    row_map = row_map.to(torch.int32).cpu()
+    n_packed = (row_map.numel() + 63) // 64 * 64
+    if n_packed != row_map.numel():
+        row_map = torch.cat([row_map, torch.full((n_packed - row_map.numel(),), -1, dtype=torch.int32)])
+    rm = row_map.to(device=w.device)
     out = torch.empty(packed_elems(n_packed, k), dtype=BF16, device=w.device)
     _lib.call("ssd_pack_weight_bf16", w.data_ptr(), ld, n, k, rm.data_ptr(), n_packed, out.data_ptr(), stream())
     return out
@@ -157,6 +158,19 @@ def kv_compact(k_arena, vt_arena, layers, kv_heads, head_dim, max_len, start, sr
               int(start), src.data_ptr(), n_dev.data_ptr(), int(n_max), stream())
 
 
+_TOPK_WS: dict = {}
+
+
+def _topk_ws(device, nbytes: int) -> torch.Tensor:
+    """Per-device scratch for the row top-k partials (grown on demand, reused across calls)."""
+    key = str(device)
+    buf = _TOPK_WS.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _TOPK_WS[key] = buf
+    return buf
+
+
 def row_topk(logits, m, n, k, mode, vocab_ids, out_tok, out_val=None, out_lse=None):
     _check(logits, "logits"); _check(out_tok, "out_tok", torch.int32)
     if vocab_ids is not None:
@@ -169,5 +183,7 @@ def row_topk(logits, m, n, k, mode, vocab_ids, out_tok, out_val=None, out_lse=No
     if out_lse is not None:
         _check(out_lse, "out_lse", torch.float32)
         _len(out_lse, "out_lse", m)
+    nbytes = int(_lib.load().ssd_row_topk_ws_bytes(m, n))
+    ws = _topk_ws(logits.device, nbytes)
     _lib.call("ssd_row_topk_bf16", logits.data_ptr(), _rows(logits, "logits", n, m), m, n, k, mode, _p(vocab_ids),
-              out_tok.data_ptr(), _p(out_val), _p(out_lse), stream())
+              out_tok.data_ptr(), _p(out_val), _p(out_lse), ws.data_ptr(), ws.numel(), stream())

@@ -43,7 +43,7 @@ def test_host_only_entry_points():
 
     lib = _lib.load()
     assert lib.ssd_abi_version() == 1
-    assert lib.ssd_packed_weight_elems(17, 40) == 32 * 64
+    assert lib.ssd_packed_weight_elems(17, 40) == 64 * 64  # rows padded to 64, K to 32
     lim = (ctypes.c_int32 * 3)()
     assert lib.ssd_tree_limits(lim) == 0 and list(lim) == [1024, 32, 32]
     assert lib.ssd_attn_max_depth() == 32

@@ -44,8 +44,9 @@ def close_bf16(got, ref, frac=0.97, atol=1e-2, rtol=1e-2):
 
 # ---------------------------------------------------------------------------- GEMM
 @pytest.mark.parametrize("m", [1, 5, 16, 17, 33, 64, 70])
-@pytest.mark.parametrize("n,k", [(48, 64), (1040, 2048), (272, 4096)])
+@pytest.mark.parametrize("n,k", [(48, 64), (1040, 2048), (272, 4096), (16448, 512), (16384, 4096)])
 def test_gemm_matches_oracle(m, n, k):
+    """Covers 2- and 4-tile workgroups, with and without the cross-workgroup K split."""
     ops = _ops()
     x, w = bf(rand(m, k, seed=1)), bf(rand(n, k, std=0.02, seed=2))
     wp = ops.pack_weight(w.to(DEV))
@@ -54,11 +55,11 @@ def test_gemm_matches_oracle(m, n, k):
     close_bf16(y, ok.linear(x, w))
 
 
-def test_gemm_batch_invariance_bitwise():
+@pytest.mark.parametrize("n,k", [(1040, 4096), (16384, 2048)])
+def test_gemm_batch_invariance_bitwise(n, k):
     """A row's output is identical whether it is computed alone or at any position of a
     64-row batch (MFMA column slot, column tile and K split all change nothing)."""
     ops = _ops()
-    n, k = 1040, 4096
     x = bf(rand(64, k, seed=3)).to(DEV)
     wp = ops.pack_weight(bf(rand(n, k, std=0.02, seed=4)).to(DEV))
     full = torch.zeros(64, n, dtype=torch.bfloat16, device=DEV)
