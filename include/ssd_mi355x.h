@@ -156,6 +156,71 @@ int ssd_tree_finalize(const SsdTree* tree, int max_nodes, int committed, const i
 int ssd_accept_greedy(const SsdTree* tree, const int32_t* argmax, int committed, int32_t* result,
                       int32_t* keep_src, int32_t* n_keep, int32_t* root_token, hipStream_t stream);
 
+/* ---------------------------------------------------------------- forward
+ * Descriptors of one model forward; every pointer is device memory in the formats above
+ * (weights packed by ssd_pack_weight_bf16). Host structs, read during the call only. */
+typedef struct SsdLayerW {    /* one decoder layer */
+  const uint16_t* wqkv;       /* q/k/v fused, rotary-paired rows */
+  const uint16_t* wo;
+  const uint16_t* wgu;        /* gate/up interleaved per 16-row tile */
+  const uint16_t* wd;
+  const uint16_t* ln1;        /* input RMSNorm weight [hidden] */
+  const uint16_t* ln2;        /* post-attention RMSNorm weight [hidden] */
+} SsdLayerW;
+
+typedef struct SsdModel {     /* base model shared by target and draft */
+  int32_t hidden, heads, kv_heads, head_dim, inter, vocab, n_layers;
+  float eps, attn_scale;
+  const uint16_t* embed;      /* [vocab][hidden] row-major */
+  const uint16_t* norm;       /* final RMSNorm weight */
+  const uint16_t* cos;        /* bf16 rotary tables [rope_rows][head_dim/2] */
+  const uint16_t* sin;
+  int64_t rope_rows;
+  const SsdLayerW* layers;    /* host array [n_layers] */
+} SsdModel;
+
+typedef struct SsdBridgeW {   /* x + MLP(RMSNorm(x)) */
+  const uint16_t* norm;
+  float eps;
+  int32_t hidden, swiglu, n_body;
+  const uint16_t* body_w[2];  /* plain MLP: n_body linears with bias + activation */
+  const uint16_t* body_b[2];
+  int32_t body_n[2], body_act[2];
+  const uint16_t* gu;         /* swiglu: packed gate/up and biases */
+  const uint16_t* bg;
+  const uint16_t* bu;
+  const uint16_t* out;        /* output projection [hidden -> model hidden] and bias */
+  const uint16_t* out_b;
+} SsdBridgeW;
+
+typedef struct SsdPlan {      /* which layers run, with which bridges, and which head */
+  int32_t n_steps;
+  const int32_t* layer_ids;          /* host [n_steps] */
+  const SsdBridgeW* const* pre_bridge; /* host [n_steps], NULL entries = none; NULL = no bridges */
+  const SsdBridgeW* pre_norm;        /* bridge before the final norm, or NULL */
+  const uint16_t* head_w;            /* packed lm_head (full or vocabulary subset), or NULL */
+  int32_t head_n;
+} SsdPlan;
+
+typedef struct SsdBuffers {   /* activations [m_cap][...] and the layer-major KV arena */
+  uint16_t *h, *x, *q, *attn, *mlp, *mid0, *mid1;
+  int32_t m_cap, mid_cols;
+  uint16_t* k_arena;          /* [n_layers][kv_heads][cache_cap][head_dim] */
+  uint16_t* vt_arena;         /* [n_layers][kv_heads][head_dim][cache_cap] */
+  int64_t cache_cap;
+  float* attn_ws;
+  int64_t attn_ws_floats;
+  uint16_t* logits;           /* [head_rows][ld_logits] */
+  int64_t ld_logits;
+} SsdBuffers;
+
+/* Embedding, the plan's decoder layers with their bridges, final norm and the head over rows
+ * [head_first, head_first + head_rows) — one call per forward (m <= m_cap rows, attention rows
+ * as for ssd_tree_attention_bf16). Replaces SubnetworkDraftModel.forward
+ * (ssd/models/subnetwork_draft.py:249-358, layer body :193-246) and the target's forward. */
+int ssd_forward(const SsdModel* model, const SsdPlan* plan, const SsdBuffers* buf, const SsdRows* rows, int m,
+                int p_min, int l_max, int head_first, int head_rows, hipStream_t stream);
+
 #if defined(__GNUC__) || defined(__clang__)
 #pragma GCC visibility pop
 #endif

@@ -19,16 +19,12 @@
 // never on how many rows share the call or where the tree slots sit, so a
 // verify row reproduces the autoregressive step at the same position exactly.
 //
-// Kernel structure (attn_partial): workgroup = (superblock, kv head, row-tile
-// group), 4 waves, wave w owns block 4s+w. Blocks entirely below min(P) are
-// "shared": the wave loads K and V^T for its block once into MFMA operand
-// registers (16-byte HBM loads, no LDS staging) and reuses them for every
-// 16-row tile (rows = token x GQA head). Other blocks are built per token from
-// gathered slots. S^T = K Q^T and O^T = V^T P^T both run on
-// v_mfma_f32_16x16x32_bf16; the key order inside a block is permuted so the
-// score accumulators are already the P^T operand (no LDS transpose). Row
-// max/sum use cross-lane shuffles of the wave64. Block partials meet in LDS and
-// are folded; superblock partials go to a workspace and attn_combine folds them.
+// Kernel structure: attn_partial computes one (m, l, O) partial per (row, superblock) into a
+// workspace -- superblocks below min(P) by workgroups that serve every row at once, the rest by
+// one workgroup per token -- and attn_combine folds the superblocks of each row. S^T = K Q^T and
+// O^T = V^T P^T both run on v_mfma_f32_16x16x32_bf16; the key order inside a block is permuted so
+// the score accumulators are already the P^T operand (no LDS transpose). Row max/sum use
+// cross-lane shuffles of the wave64.
 #include "common.h"
 
 #include <math.h>
@@ -51,9 +47,14 @@ struct AttnArgs {
   const int* anc;     // [M, ATT_MAXD]
   int p_min, l_max;
   float scale_log2;
-  int tiles_per_group;
-  float* ws;  // [kv_heads][M*rep][n_sb_cap][hd + 2]
+  float* ws;  // O [kv_heads][M*rep][n_sb_cap][hd], then (m, l) [kv_heads][M*rep][n_sb_cap]
   int n_sb_cap;
+  // launch geometry (set by launch_attn)
+  int n_full;         // superblocks entirely below p_min (shared by every row)
+  int n_tail_sb;      // superblocks from n_full up to l_max (built per token)
+  int tail_slots;     // workgroup ids [0, tail_slots) are tail workgroups
+  int groups, tiles_per_group;  // row tile groups of the shared workgroups
+  uint32_t rep_magic;  // ceil(2^32 / (heads / kv_heads)): R / rep == umulhi(R, rep_magic) for R < 2^16
 };
 
 __device__ __forceinline__ int perm_key(int kt, int i) {
@@ -65,8 +66,8 @@ template <int HD>
 struct Frags {
   static constexpr int KS = HD / 32;  // k-steps over head_dim for Q K^T
   static constexpr int DT = HD / 16;  // 16-wide d tiles for P V
-  uint4 k[4][KS];
-  uint4 v[DT][2];
+  u32x4_t k[4][KS];
+  u32x4_t v[DT][2];
 };
 
 template <int HD>
@@ -77,14 +78,14 @@ __device__ __forceinline__ void load_shared_frags(Frags<HD>& f, const AttnArgs& 
   for (int kt = 0; kt < 4; ++kt) {
     const bf16_t* row = kb + (size_t)(key0 + perm_key(kt, i)) * HD + g * 8;
 #pragma unroll
-    for (int ks = 0; ks < Frags<HD>::KS; ++ks) f.k[kt][ks] = *(const uint4*)(row + ks * 32);
+    for (int ks = 0; ks < Frags<HD>::KS; ++ks) f.k[kt][ks] = *(const u32x4_t*)(row + ks * 32);
   }
   const bf16_t* vb = a.Vt + (size_t)kvh * HD * a.max_len;
 #pragma unroll
   for (int dt = 0; dt < Frags<HD>::DT; ++dt) {
     const bf16_t* row = vb + (size_t)(dt * 16 + i) * a.max_len + key0 + g * 8;
-    f.v[dt][0] = *(const uint4*)(row);
-    f.v[dt][1] = *(const uint4*)(row + 32);
+    f.v[dt][0] = *(const u32x4_t*)(row);
+    f.v[dt][1] = *(const u32x4_t*)(row + 32);
   }
 }
 
@@ -96,6 +97,13 @@ __device__ __forceinline__ int logical_slot(int jpos, int P, int L, const int* a
   return (s >= 0 && s < max_len) ? s : -1;
 }
 
+// One token's block at logical positions [key0, key0 + 64): positions < P are cache slots
+// themselves, positions in [P, L) are the ancestor slots anc[pos - P], the rest is empty (zero).
+// K rows are loaded per key. V^T is loaded as for a prefix block (one 16-byte run of 8 positions
+// per lane, positions >= P masked to zero); the ancestor positions are patched in afterwards by
+// patch_ancestors. Loads are unconditional (clamped, valid addresses; values masked
+// afterwards): a load under a per-lane condition compiles to a branch after which the compiler
+// waits for the value, serialising the loads.
 template <int HD>
 __device__ __forceinline__ void load_virtual_frags(Frags<HD>& f, const AttnArgs& a, int kvh, int key0, int P,
                                                    int L, const int* anc_t, int lane) {
@@ -105,31 +113,47 @@ __device__ __forceinline__ void load_virtual_frags(Frags<HD>& f, const AttnArgs&
   for (int kt = 0; kt < 4; ++kt) {
     const int slot = logical_slot(key0 + perm_key(kt, i), P, L, anc_t, a.max_len);
     const bf16_t* row = kb + (size_t)(slot < 0 ? 0 : slot) * HD + g * 8;
+    const uint32_t keep = slot >= 0 ? 0xffffffffu : 0u;
 #pragma unroll
-    for (int ks = 0; ks < Frags<HD>::KS; ++ks)
-      f.k[kt][ks] = slot >= 0 ? *(const uint4*)(row + ks * 32) : make_uint4(0, 0, 0, 0);
+    for (int ks = 0; ks < Frags<HD>::KS; ++ks) f.k[kt][ks] = *(const u32x4_t*)(row + ks * 32) & keep;
   }
   const bf16_t* vb = a.Vt + (size_t)kvh * HD * a.max_len;
+  const int lim = P < a.max_len ? P : (int)a.max_len;  // prefix positions that exist
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
-    int slots[8];
-    bool contiguous = true;
+    const int pos0 = key0 + c * 32 + g * 8;
+    const int base = pos0 + 8 <= a.max_len ? pos0 : 0;
+    u32x4_t keep;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      slots[t] = logical_slot(key0 + c * 32 + g * 8 + t, P, L, anc_t, a.max_len);
-      contiguous = contiguous && slots[t] >= 0 && slots[t] == slots[0] + t;
-    }
-    contiguous = contiguous && (slots[0] % 8 == 0);
+    for (int w2 = 0; w2 < 4; ++w2)
+      keep[w2] = (pos0 + 2 * w2 < lim ? 0x0000ffffu : 0u) | (pos0 + 2 * w2 + 1 < lim ? 0xffff0000u : 0u);
+#pragma unroll
+    for (int dt = 0; dt < Frags<HD>::DT; ++dt)
+      f.v[dt][c] = *(const u32x4_t*)(vb + (size_t)(dt * 16 + i) * a.max_len + base) & keep;
+  }
+}
+
+// Patch the ancestor positions of this block into the V^T operands from the ancestors' V^T
+// columns staged in LDS (avt[a][d], a < D): wave-uniform loop over the ancestors in the block.
+template <int HD>
+__device__ __forceinline__ void patch_ancestors(Frags<HD>& f, const bf16_t (*avt)[HD], int key0, int P, int L,
+                                                int lane) {
+  const int i = lane & 15, g = lane >> 4;
+  const int a_lo = (key0 > P ? key0 : P) - P;
+  const int a_hi = (L < key0 + ATT_BLK ? L : key0 + ATT_BLK) - P;
+  for (int an = a_lo; an < a_hi; ++an) {
+    const int off = P + an - key0;  // 0..63, uniform
+    const int c = off >> 5, grp = (off >> 3) & 3, t = off & 7;
+    const uint32_t sel = g == grp ? ((t & 1) ? 0xffff0000u : 0x0000ffffu) : 0u;
 #pragma unroll
     for (int dt = 0; dt < Frags<HD>::DT; ++dt) {
-      const bf16_t* row = vb + (size_t)(dt * 16 + i) * a.max_len;
-      if (contiguous) {
-        f.v[dt][c] = *(const uint4*)(row + slots[0]);
-      } else {
-        Pack8 p;
+      const uint32_t h = avt[an][dt * 16 + i];
+      const uint32_t v = (h | (h << 16)) & sel;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) p.h[t] = slots[t] >= 0 ? row[slots[t]] : (bf16_t)0;
-        f.v[dt][c] = p.u;
+      for (int w2 = 0; w2 < 4; ++w2) {
+        const uint32_t m = (t >> 1) == w2 ? sel : 0u;
+        if (c == 0) f.v[dt][0][w2] = (f.v[dt][0][w2] & ~m) | (v & m);
+        else f.v[dt][1][w2] = (f.v[dt][1][w2] & ~m) | (v & m);
       }
     }
   }
@@ -138,8 +162,12 @@ __device__ __forceinline__ void load_virtual_frags(Frags<HD>& f, const AttnArgs&
 // One 64-key block for a 16-row tile. valid_bits: bit (kt*4+e) says whether key perm_key(kt, 4g+e)
 // is attended (same for every row of the pass). Outputs per lane (row j = lane%16): m (log2 units,
 // -inf if nothing attended), l, and O[row j][dt*16 + 4g + e] in o[dt][e].
-template <int HD>
-__device__ __forceinline__ void block_attend(const Frags<HD>& f, const uint4 (&qf)[HD / 32], uint32_t valid_bits,
+// exp2 for the softmax: the bare hardware instruction (results below 2^-126 flush to zero, which
+// every path shares).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+template <int HD, bool MASKED>
+__device__ __forceinline__ void block_attend(const Frags<HD>& f, const u32x4_t (&qf)[HD / 32], uint32_t valid_bits,
                                              float scale_log2, float& m_out, float& l_out,
                                              f32x4_t (&o)[HD / 16]) {
   constexpr int KS = HD / 32, DT = HD / 16;
@@ -148,7 +176,7 @@ __device__ __forceinline__ void block_attend(const Frags<HD>& f, const uint4 (&q
   for (int kt = 0; kt < 4; ++kt) {
     s[kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) s[kt] = mfma16x16x32(as_bf16x8(f.k[kt][ks]), as_bf16x8(qf[ks]), s[kt]);
+    for (int ks = 0; ks < KS; ++ks) s[kt] = mfma16x16x32(bits_bf16x8(f.k[kt][ks]), bits_bf16x8(qf[ks]), s[kt]);
   }
   float sv[16];
   float mx = -INFINITY;
@@ -156,7 +184,8 @@ __device__ __forceinline__ void block_attend(const Frags<HD>& f, const uint4 (&q
   for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float v = ((valid_bits >> (kt * 4 + e)) & 1u) ? s[kt][e] * scale_log2 : -INFINITY;
+      float v = s[kt][e] * scale_log2;
+      if (MASKED) v = ((valid_bits >> (kt * 4 + e)) & 1u) ? v : -INFINITY;
       sv[kt * 4 + e] = v;
       mx = fmaxf(mx, v);
     }
@@ -165,216 +194,305 @@ __device__ __forceinline__ void block_attend(const Frags<HD>& f, const uint4 (&q
   m_out = mx;
   // A row with nothing attended gets p = 0 everywhere (m stays -inf and marks it absent).
   // No early exit: every lane must stay active for the MFMAs below.
-  const float msafe = mx == -INFINITY ? 0.f : mx;
+  const float msafe = (MASKED && mx == -INFINITY) ? 0.f : mx;
   float l = 0.f;
-  Pack8 pb[2];
+  // P^T operand: key tile kt, element e goes to half (kt & 1) * 4 + e of operand kt >> 1.
+  uint32_t pw[2][4];
 #pragma unroll
   for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float p = exp2f(sv[kt * 4 + e] - msafe);
-      l += p;
-      pb[kt >> 1].h[(kt & 1) * 4 + e] = f2bf(p);
+    for (int e = 0; e < 4; e += 2) {
+      const float p0 = fast_exp2(sv[kt * 4 + e] - msafe), p1 = fast_exp2(sv[kt * 4 + e + 1] - msafe);
+      l += p0;
+      l += p1;
+      pw[kt >> 1][(kt & 1) * 2 + e / 2] = pack_bf16x2(p0, p1);
     }
   l += __shfl_xor(l, 16);
   l += __shfl_xor(l, 32);
   l_out = l;
+  const u32x4_t pb0 = {pw[0][0], pw[0][1], pw[0][2], pw[0][3]};
+  const u32x4_t pb1 = {pw[1][0], pw[1][1], pw[1][2], pw[1][3]};
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) {
     f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    acc = mfma16x16x32(as_bf16x8(f.v[dt][0]), pb[0].v, acc);
-    acc = mfma16x16x32(as_bf16x8(f.v[dt][1]), pb[1].v, acc);
+    acc = mfma16x16x32(bits_bf16x8(f.v[dt][0]), bits_bf16x8(pb0), acc);
+    acc = mfma16x16x32(bits_bf16x8(f.v[dt][1]), bits_bf16x8(pb1), acc);
     o[dt] = acc;
   }
 }
 
+constexpr int ATT_QROWS = 128;  // query rows staged in LDS at a time
+
 template <int HD>
-struct AttnLds {
+struct alignas(16) AttnLds {
   float o[ATT_SB][16][HD + 4];
   float m[ATT_SB][16];
   float l[ATT_SB][16];
+  bf16_t q[ATT_QROWS][HD + 8];
+  bf16_t avt[ATT_MAXD][HD];  // tail: the token's ancestors' V^T columns
 };
 
+// One launch holds two kinds of workgroups (4 waves; wave w owns block 4*sb + w):
+//  * tail:   (superblock at or beyond min(P), kv head, one token), dispatched first. The wave
+//    builds its block from the token's logical keys (prefix slots, then ancestor slots) and
+//    processes the token's GQA rows.
+//  * shared: (superblock below min(P), kv head, tile group). Every row attends every key of the
+//    superblock; the wave loads its block's K and V^T into MFMA operand registers once and runs
+//    every 16-row tile of its group against them. The groups of a superblock sit on one XCD, so
+//    K/V bytes come from HBM once and the other groups read them from that XCD's L2.
+// Query rows are staged in LDS up front (their loads overlap the K/V loads). Both kinds end in
+// the same code: the four block partials of a tile meet in LDS and are folded left to right into
+// the superblock partial, so a superblock's result does not depend on which kind of workgroup
+// produced it. Ids are decoded XCD-aware: the workgroups that read one (superblock, kv head)
+// -- its tokens (tail) or tile groups (shared) -- get ids 8 apart, i.e. one XCD (workgroups are
+// dealt to the 8 XCDs round-robin), so their re-reads of that K/V hit the XCD's L2.
+//
+// Workspace: O partials [kv_heads][M*rep][n_sb_cap][HD], then (m, l) pairs [kv_heads][M*rep][n_sb_cap].
+// Every (row, superblock < n_sb) pair of the call is written; m = -inf marks "no keys".
 template <int HD>
-__global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256, 2) void attn_partial_kernel(AttnArgs a) {
   constexpr int KS = HD / 32, DT = HD / 16;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int sb = blockIdx.x, kvh = blockIdx.y, grp = blockIdx.z;
+  const int j = lane & 15, g = lane >> 4;
   const int rep = a.heads / a.kv_heads;
   const int n_rows = a.M * rep;
-  const int n_tiles = (n_rows + 15) / 16;
-  const int t_lo = grp * a.tiles_per_group;
-  const int t_hi = min(n_tiles, t_lo + a.tiles_per_group);
-  const int key0 = (sb * ATT_SB + w) * ATT_BLK;
-  const bool active = key0 < a.l_max;
-  const bool shared = key0 + ATT_BLK <= a.p_min;
-  const int j = lane & 15, g = lane >> 4;
-  // Blocks of this superblock that must be built per token (they reach past min(P)).
-  int tail_blocks[ATT_SB];
-  int n_tail = 0;
-#pragma unroll
-  for (int ww = 0; ww < ATT_SB; ++ww) {
-    const int k0 = (sb * ATT_SB + ww) * ATT_BLK;
-    if (k0 < a.l_max && k0 + ATT_BLK > a.p_min) tail_blocks[n_tail++] = ww;
+  const bool tail = (int)blockIdx.x < a.tail_slots;
+  int sb, kvh, tok = 0, grp = 0;
+  if (tail) {
+    const int bid = blockIdx.x, xcd = bid & 7, rest = bid >> 3;
+    const int u = (rest / a.M) * 8 + xcd;
+    tok = rest % a.M;
+    if (u >= a.n_tail_sb * a.kv_heads) return;
+    sb = a.n_full + u / a.kv_heads;
+    kvh = u % a.kv_heads;
+  } else {
+    const int bid = blockIdx.x - a.tail_slots, xcd = bid & 7, rest = bid >> 3;
+    const int u = (rest / a.groups) * 8 + xcd;
+    grp = rest % a.groups;
+    if (u >= a.n_full * a.kv_heads) return;
+    sb = u / a.kv_heads;
+    kvh = u % a.kv_heads;
   }
+  const int key0 = (sb * ATT_SB + w) * ATT_BLK;
+  float* ws_o = a.ws;
+  float2* ws_ml = (float2*)(a.ws + (size_t)a.kv_heads * n_rows * a.n_sb_cap * HD);
 
   __shared__ AttnLds<HD> lds;
-  __shared__ int s_anc[16][ATT_MAXD];  // ancestor slots of the tile's tokens
-  __shared__ int s_P[16], s_L[16];
+  __shared__ int s_anc[ATT_MAXD];
+  int r_begin, r_end, P = 0, L = 0, anc_v = 0;
+  if (tail) {
+    anc_v = a.anc[(size_t)tok * ATT_MAXD + (threadIdx.x & (ATT_MAXD - 1))];
+    P = a.prefix[tok];
+    L = P + min(max(a.depth[tok], 0), ATT_MAXD);
+    r_begin = tok * rep;
+    r_end = r_begin + rep;
+  } else {
+    r_begin = grp * a.tiles_per_group * 16;
+    r_end = min(n_rows, r_begin + a.tiles_per_group * 16);
+  }
+
+  // Query rows are staged through LDS in chunks of ATT_QROWS (R = token * rep + GQA head within
+  // the kv group). The first chunk's loads are issued before the K/V loads, so they land first
+  // (memory returns in issue order) and are written to LDS while K/V are still in flight.
+  constexpr int QCH = HD / 8;                     // 16-byte chunks per row
+  constexpr int QIT = ATT_QROWS * QCH / 256;
+  u32x4_t qv[QIT];
+  auto load_q = [&](int c0, int c1) {
+    const int nq = (c1 - c0) * QCH;
+#pragma unroll
+    for (int it = 0; it < QIT; ++it) {
+      const int idx = min((int)threadIdx.x + it * 256, nq - 1);
+      const int R = c0 + idx / QCH;
+      const int qt = (int)__umulhi((uint32_t)R, a.rep_magic);
+      qv[it] = *(const u32x4_t*)(a.Q + (size_t)qt * a.ldq + (size_t)(kvh * rep + R - qt * rep) * HD + (idx % QCH) * 8);
+    }
+  };
+  auto store_q = [&](int c0, int c1) {
+    const int nq = (c1 - c0) * QCH;
+#pragma unroll
+    for (int it = 0; it < QIT; ++it) {
+      const int idx = threadIdx.x + it * 256;
+      if (idx < nq) *(u32x4_t*)&lds.q[idx / QCH][(idx % QCH) * 8] = qv[it];
+    }
+  };
+  load_q(r_begin, min(r_end, r_begin + ATT_QROWS));
+
   Frags<HD> f;
-  if (active && shared) load_shared_frags<HD>(f, a, kvh, key0, lane);
-
-  for (int t = t_lo; t < t_hi; ++t) {
-    const int tok_first = (t * 16) / rep;
-    const int tok_last = min(a.M - 1, (t * 16 + 15) / rep);
-    const int ntok = tok_last - tok_first + 1;
-    if (n_tail) {
-      for (int idx = threadIdx.x; idx < ntok * ATT_MAXD; idx += 256)
-        s_anc[idx / ATT_MAXD][idx % ATT_MAXD] = a.anc[(size_t)(tok_first + idx / ATT_MAXD) * ATT_MAXD + idx % ATT_MAXD];
-      if (threadIdx.x < ntok) {
-        const int P = a.prefix[tok_first + threadIdx.x];
-        s_P[threadIdx.x] = P;
-        s_L[threadIdx.x] = P + min(a.depth[tok_first + threadIdx.x], ATT_MAXD);
+  uint32_t bits = 0xffffu;
+  bool have = true;
+  if (tail) {
+    if (sb * ATT_SB * ATT_BLK >= L) {  // the token's keys end before this superblock
+      for (int r = threadIdx.x; r < rep; r += 256)
+        ws_ml[((size_t)kvh * n_rows + r_begin + r) * a.n_sb_cap + sb] = make_float2(-INFINITY, 0.f);
+      return;
+    }
+    if (threadIdx.x < ATT_MAXD) s_anc[threadIdx.x] = anc_v;
+    __syncthreads();
+    // The ancestors' V^T columns (L - P of them) go to LDS; their loads are issued before the
+    // block's K/V loads and land while those are in flight.
+    const bool patch = L > P;
+    constexpr int AIT = ATT_MAXD * HD / 256;
+    uint32_t av[AIT];
+    const int n_av = (L - P) * HD;  // (ancestor, d) pairs to stage
+    if (patch) {
+      const bf16_t* vb = a.Vt + (size_t)kvh * HD * a.max_len;
+#pragma unroll
+      for (int it = 0; it < AIT; ++it) {
+        if (it * 256 >= n_av) break;  // uniform
+        const int idx = threadIdx.x + it * 256;
+        const int an = min(idx / HD, L - P - 1), d = idx % HD;
+        const int slot = s_anc[an];
+        const bool ok = slot >= 0 && slot < a.max_len;
+        const uint32_t h = vb[(size_t)d * a.max_len + (ok ? slot : 0)];
+        av[it] = ok ? h : 0u;
       }
-      __syncthreads();
     }
-    const int r = t * 16 + j;
-    const bool rv = r < n_rows;
-    const int tok = rv ? r / rep : 0;
-    const int hq = kvh * rep + (rv ? r % rep : 0);
-    uint4 qf[KS];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      qf[ks] = rv ? *(const uint4*)(a.Q + (size_t)tok * a.ldq + (size_t)hq * HD + ks * 32 + g * 8)
-                  : make_uint4(0, 0, 0, 0);
-
-    if (!active) {
-      if (g == 0) { lds.m[w][j] = -INFINITY; lds.l[w][j] = 0.f; }
-    } else if (shared) {
-      float m, l;
-      f32x4_t o[DT];
-      block_attend<HD>(f, qf, 0xffffu, a.scale_log2, m, l, o);
-      if (g == 0) { lds.m[w][j] = m; lds.l[w][j] = l; }
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) lds.o[w][j][dt * 16 + 4 * g + e] = o[dt][e];
-    }
-    // Per-token virtual blocks, spread over the four waves.
-    const int units = n_tail * ntok;
-    for (int u = w; u < units; u += ATT_SB) {
-      const int wb = tail_blocks[u / ntok];
-      const int tl = u % ntok, tk = tok_first + tl;
-      const int kb0 = (sb * ATT_SB + wb) * ATT_BLK;
-      const int P = s_P[tl], L = s_L[tl];
-      const int* anc_t = s_anc[tl];
-      Frags<HD> fv;
-      load_virtual_frags<HD>(fv, a, kvh, kb0, P, L, anc_t, lane);
-      uint32_t bits = 0;
+    have = key0 < L;
+    if (have) {
+      load_virtual_frags<HD>(f, a, kvh, key0, P, L, s_anc, lane);
+      bits = 0;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (logical_slot(kb0 + perm_key(kt, 4 * g + e), P, L, anc_t, a.max_len) >= 0) bits |= 1u << (kt * 4 + e);
-      float m, l;
-      f32x4_t o[DT];
-      block_attend<HD>(fv, qf, bits, a.scale_log2, m, l, o);
-      if (rv && tok == tk) {
-        if (g == 0) { lds.m[wb][j] = m; lds.l[wb][j] = l; }
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) lds.o[wb][j][dt * 16 + 4 * g + e] = o[dt][e];
-      }
+          if (logical_slot(key0 + perm_key(kt, 4 * g + e), P, L, s_anc, a.max_len) >= 0) bits |= 1u << (kt * 4 + e);
     }
-    __syncthreads();
+    if (patch) {
+#pragma unroll
+      for (int it = 0; it < AIT; ++it) {
+        if (it * 256 >= n_av) break;  // uniform
+        const int idx = threadIdx.x + it * 256;
+        lds.avt[idx / HD][idx % HD] = (bf16_t)av[it];
+      }
+      __syncthreads();
+      if (have) patch_ancestors<HD>(f, lds.avt, key0, P, L, lane);
+    }
+  } else {
+    load_shared_frags<HD>(f, a, kvh, key0, lane);
+  }
 
-    // Fold the 4 block partials of each row left to right -> superblock partial.
-    {
-      const int rr = threadIdx.x >> 4;       // tile row
-      const int dc = threadIdx.x & 15;       // d chunk
-      constexpr int DPT = HD / 16;           // d per thread
-      const int R = t * 16 + rr;
-      if (R < n_rows) {
-        float mS = -INFINITY, lS = 0.f, oS[DPT];
-        bool first = true;
-#pragma unroll
-        for (int ww = 0; ww < ATT_SB; ++ww) {
-          const float mb = lds.m[ww][rr];
-          if (mb == -INFINITY) continue;
-          const float lb = lds.l[ww][rr];
-          if (first) {
-            mS = mb; lS = lb;
-#pragma unroll
-            for (int d = 0; d < DPT; ++d) oS[d] = lds.o[ww][rr][dc * DPT + d];
-            first = false;
-          } else {
-            const float mN = fmaxf(mS, mb);
-            const float a1 = exp2f(mS - mN), a2 = exp2f(mb - mN);
-            lS = lS * a1 + lb * a2;
-#pragma unroll
-            for (int d = 0; d < DPT; ++d) oS[d] = oS[d] * a1 + lds.o[ww][rr][dc * DPT + d] * a2;
-            mS = mN;
-          }
-        }
-        float* dst = a.ws + (((size_t)kvh * n_rows + R) * a.n_sb_cap + sb) * (HD + 2);
-        if (!first) {
-#pragma unroll
-          for (int d = 0; d < DPT; ++d) dst[dc * DPT + d] = oS[d];
-        }
-        if (dc == 0) { dst[HD] = mS; dst[HD + 1] = lS; }
-      }
-    }
+  for (int c0 = r_begin; c0 < r_end; c0 += ATT_QROWS) {
+    const int c1 = min(r_end, c0 + ATT_QROWS);
+    if (c0 != r_begin) load_q(c0, c1);
+    store_q(c0, c1);
     __syncthreads();
+    for (int t0 = c0; t0 < c1; t0 += 16) {
+      const int nv = min(16, c1 - t0);
+      const bool rv = j < nv;
+      u32x4_t qf[KS];
+      const uint32_t qkeep = rv ? 0xffffffffu : 0u;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) qf[ks] = *(const u32x4_t*)&lds.q[rv ? t0 - c0 + j : 0][ks * 32 + g * 8] & qkeep;
+      if (have) {
+        float m, l;
+        f32x4_t o[DT];
+        if (tail)
+          block_attend<HD, true>(f, qf, bits, a.scale_log2, m, l, o);
+        else
+          block_attend<HD, false>(f, qf, bits, a.scale_log2, m, l, o);
+        if (g == 0) { lds.m[w][j] = m; lds.l[w][j] = l; }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) *(f32x4_t*)&lds.o[w][j][dt * 16 + 4 * g] = o[dt];
+      } else if (g == 0) {
+        lds.m[w][j] = -INFINITY;
+        lds.l[w][j] = 0.f;
+      }
+      __syncthreads();
+
+      // Fold the 4 block partials of each row: superblock max first, then the weighted sums in
+      // block order -> superblock partial.
+      {
+        const int rr = threadIdx.x >> 4;       // tile row
+        const int dc = threadIdx.x & 15;       // d chunk
+        constexpr int DPT = HD / 16;           // d per thread
+        if (rr < nv) {
+          float mb[ATT_SB], mS = -INFINITY;
+#pragma unroll
+          for (int ww = 0; ww < ATT_SB; ++ww) {
+            mb[ww] = lds.m[ww][rr];
+            mS = fmaxf(mS, mb[ww]);
+          }
+          float lS = 0.f, oS[DPT];
+#pragma unroll
+          for (int d = 0; d < DPT; ++d) oS[d] = 0.f;
+#pragma unroll
+          for (int ww = 0; ww < ATT_SB; ++ww) {
+            if (mb[ww] == -INFINITY) continue;
+            const float wgt = fast_exp2(mb[ww] - mS);
+            lS += lds.l[ww][rr] * wgt;
+#pragma unroll
+            for (int d = 0; d < DPT; ++d) oS[d] += lds.o[ww][rr][dc * DPT + d] * wgt;
+          }
+          const size_t rec = ((size_t)kvh * n_rows + t0 + rr) * a.n_sb_cap + sb;
+          if (mS != -INFINITY) {
+            float* dst = ws_o + rec * HD + dc * DPT;
+            if constexpr (DPT % 4 == 0) {
+#pragma unroll
+              for (int d = 0; d < DPT; d += 4) *(float4*)(dst + d) = make_float4(oS[d], oS[d + 1], oS[d + 2], oS[d + 3]);
+            } else {
+#pragma unroll
+              for (int d = 0; d < DPT; ++d) dst[d] = oS[d];
+            }
+          }
+          if (dc == 0) ws_ml[rec] = make_float2(mS, lS);
+        }
+      }
+      __syncthreads();
+    }
   }
 }
 
-// Cross-superblock combine, one wave per (token, q head). Canonical arithmetic for a row of
-// length L with superblocks s = 0..n-1: M = max_s m_s; w_s = 2^(m_s - M); l = sum_s l_s w_s and
-// O = sum_s O_s w_s, both summed in increasing s; out = O / l. All loads are independent of
-// the running sums, so they are issued ahead of the arithmetic.
+// Cross-superblock combine, one wave per (token, q head). Canonical arithmetic for a row with
+// superblocks s = 0..n-1: M = max_s m_s; w_s = 2^(m_s - M) (0 where m_s = -inf); l = sum_s l_s w_s
+// and O = sum_s O_s w_s, both summed in increasing s; out = O / l. The partials of up to 32
+// superblocks are loaded in one batch, issued before the max is reduced.
 template <int HD>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ ws, int n_sb_cap, int M,
-                                                           int heads, int kv_heads, const int* __restrict__ prefix,
-                                                           const int* __restrict__ depth, bf16_t* __restrict__ out,
-                                                           int64_t ldo, int n_sb_run) {
+                                                           int heads, int kv_heads, bf16_t* __restrict__ out,
+                                                           int64_t ldo, int n) {
   constexpr int PER = (HD + 63) / 64;
+  constexpr int CH = 32;
   const int wid = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (wid >= M * heads) return;
   const int tok = wid / heads, hq = wid % heads;
   const int rep = heads / kv_heads, kvh = hq / rep;
-  const int R = tok * rep + hq % rep;
-  const int L = prefix[tok] + min(depth[tok], ATT_MAXD);
-  const int nsb = min(n_sb_run, (L + ATT_BLK * ATT_SB - 1) / (ATT_BLK * ATT_SB));
-  const float* base = ws + ((size_t)kvh * M * rep + R) * n_sb_cap * (HD + 2);
-  // pass 1: row max over superblocks (lanes own superblocks)
-  float mx = -INFINITY;
-  for (int s0 = 0; s0 < nsb; s0 += 64) {
-    const int s = s0 + lane;
-    if (s < nsb) mx = fmaxf(mx, base[(size_t)s * (HD + 2) + HD]);
-  }
+  const int n_rows = M * rep;
+  const size_t row = (size_t)kvh * n_rows + tok * rep + hq % rep;
+  const float* O = ws + row * n_sb_cap * HD;
+  const float2* ml = (const float2*)(ws + (size_t)kv_heads * n_rows * n_sb_cap * HD) + row * n_sb_cap;
+  float v[CH][PER], mc[CH], lc[CH];
+  // Unconditional loads from clamped indices (a per-lane conditional load would be waited for
+  // one by one); entries past n are masked where they are used.
+  auto load_chunk = [&](int s0) {
+#pragma unroll
+    for (int q = 0; q < CH; ++q) {
+      const int sq = min(s0 + q, n - 1);
+      mc[q] = ml[sq].x;
+      lc[q] = ml[sq].y;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) v[q][i] = O[(size_t)sq * HD + min(lane + 64 * i, HD - 1)];
+    }
+  };
+  load_chunk(0);
+  float mx = ml[min(lane, n - 1)].x;
+  for (int s = lane + 64; s < n; s += 64) mx = fmaxf(mx, ml[s].x);
   for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
   float l = 0.f, o[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) o[i] = 0.f;
-  for (int s0 = 0; s0 < nsb; s0 += 64) {
-    const int s = s0 + lane;
-    float wgt = 0.f, ls = 0.f;
-    if (s < nsb) {
-      const float ms = base[(size_t)s * (HD + 2) + HD];
-      ls = base[(size_t)s * (HD + 2) + HD + 1];
-      wgt = ms == -INFINITY ? 0.f : exp2f(ms - mx);
-    }
-    const int cnt = min(64, nsb - s0);
-    for (int q = 0; q < cnt; ++q) {
-      const float wq = __shfl(wgt, q);
-      const float lq = __shfl(ls, q);
-      l += lq * wq;
-      const float* p = base + (size_t)(s0 + q) * (HD + 2);
+  for (int s0 = 0;;) {
 #pragma unroll
-      for (int i = 0; i < PER; ++i)
-        if (lane + 64 * i < HD && wq != 0.f) o[i] += p[lane + 64 * i] * wq;
+    for (int q = 0; q < CH; ++q) {
+      const float wq = (s0 + q >= n || mc[q] == -INFINITY) ? 0.f : fast_exp2(mc[q] - mx);
+      if (wq != 0.f) {
+        l += lc[q] * wq;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) o[i] += v[q][i] * wq;
+      }
     }
+    s0 += CH;
+    if (s0 >= n) break;
+    load_chunk(s0);
   }
   bf16_t* dst = out + (size_t)tok * ldo + (size_t)hq * HD;
 #pragma unroll
@@ -384,23 +502,32 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
 
 template <int HD>
 static int launch_attn(AttnArgs a, bf16_t* out, int64_t ldo, hipStream_t s) {
-  const int rep = a.heads / a.kv_heads;
-  const int n_tiles = (a.M * rep + 15) / 16;
-  const int n_sb = (a.l_max + ATT_BLK * ATT_SB - 1) / (ATT_BLK * ATT_SB);
+  constexpr int SBK = ATT_BLK * ATT_SB;
+  const int n_sb = (a.l_max + SBK - 1) / SBK;
   if (n_sb > a.n_sb_cap) return set_error(SSD_ERANGE, "attention: length %d needs %d superblocks > workspace %d",
                                           a.l_max, n_sb, a.n_sb_cap);
-  // Tile groups: enough workgroups to cover the chip, never changing the arithmetic.
-  const int units = n_sb * a.kv_heads;
-  int groups = (512 + units - 1) / units;
+  a.n_full = a.p_min / SBK < n_sb ? a.p_min / SBK : n_sb;
+  a.n_tail_sb = n_sb - a.n_full;
+  a.tail_slots = (a.n_tail_sb * a.kv_heads + 7) / 8 * 8 * a.M;
+  const uint32_t rep = (uint32_t)(a.heads / a.kv_heads);
+  a.rep_magic = (uint32_t)((((uint64_t)1 << 32) + rep - 1) / rep);
+  // Shared workgroups split their rows into tile groups when the chip has room for more
+  // workgroups (about 2 per CU resident at once); the groups of one superblock share an XCD.
+  const int units8 = (a.n_full * a.kv_heads + 7) / 8 * 8;
+  const int n_tiles = (a.M * (a.heads / a.kv_heads) + 15) / 16;
+  int groups = units8 ? (512 - a.tail_slots) / units8 : 1;
   groups = groups < 1 ? 1 : (groups > n_tiles ? n_tiles : groups);
   a.tiles_per_group = (n_tiles + groups - 1) / groups;
-  groups = (n_tiles + a.tiles_per_group - 1) / a.tiles_per_group;
-  hipLaunchKernelGGL((attn_partial_kernel<HD>), dim3(n_sb, a.kv_heads, groups), dim3(256), 0, s, a);
-  int rc = check_launch("attn_partial");
-  if (rc) return rc;
+  a.groups = (n_tiles + a.tiles_per_group - 1) / a.tiles_per_group;
+  const int grid = a.tail_slots + units8 * a.groups;
+  if (grid > 0) {
+    hipLaunchKernelGGL((attn_partial_kernel<HD>), dim3(grid), dim3(256), 0, s, a);
+    const int rc = check_launch("attn_partial");
+    if (rc) return rc;
+  }
   const int waves = a.M * a.heads;
   hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3((waves + 3) / 4), dim3(256), 0, s, a.ws, a.n_sb_cap, a.M,
-                     a.heads, a.kv_heads, a.prefix, a.depth, out, ldo, n_sb);
+                     a.heads, a.kv_heads, out, ldo, n_sb);
   return check_launch("attn_combine");
 }
 

@@ -31,12 +31,17 @@ enum Status {
 
 __device__ __forceinline__ float bf2f(bf16_t v) { return __uint_as_float(((uint32_t)v) << 16); }
 
-__device__ __forceinline__ bf16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (bf16_t)((u >> 16) | 0x40);  // quiet NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (bf16_t)(u >> 16);
+typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2_t;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
+
+// Two fp32 -> packed bf16 pair (lo in bits 0-15): one v_cvt_pk_bf16_f32 on gfx950 (round to
+// nearest even, NaN stays NaN).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
+
+__device__ __forceinline__ bf16_t f2bf(float f) { return (bf16_t)(pack_bf16x2(f, 0.f) & 0xffffu); }
 
 // Round through bf16 (the value an fp32 result takes once stored as bf16).
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
@@ -54,6 +59,9 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 u) {
 }
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// Reinterpret 8 packed bf16 (four 32-bit words) as the MFMA operand type (no memory round trip).
+__device__ __forceinline__ bf16x8_t bits_bf16x8(u32x4_t u) { return __builtin_bit_cast(bf16x8_t, u); }
 
 // Streaming (non-temporal) 16-byte load: weights are read once per call, keep them out of the caches' way.
 __device__ __forceinline__ uint4 ld_stream(const uint4* p) {

@@ -27,6 +27,34 @@ class SsdRows(C.Structure):
     _fields_ = [(n, P) for n in ("ids", "pos", "slot", "prefix", "depth", "anc")] + [("cap", C.c_int32)]
 
 
+class SsdLayerW(C.Structure):
+    _fields_ = [(n, P) for n in ("wqkv", "wo", "wgu", "wd", "ln1", "ln2")]
+
+
+class SsdModel(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("hidden", "heads", "kv_heads", "head_dim", "inter", "vocab", "n_layers")] + [
+        ("eps", F32), ("attn_scale", F32), ("embed", P), ("norm", P), ("cos", P), ("sin", P), ("rope_rows", I64),
+        ("layers", C.POINTER(SsdLayerW))]
+
+
+class SsdBridgeW(C.Structure):
+    _fields_ = [("norm", P), ("eps", F32), ("hidden", C.c_int32), ("swiglu", C.c_int32), ("n_body", C.c_int32),
+                ("body_w", P * 2), ("body_b", P * 2), ("body_n", C.c_int32 * 2), ("body_act", C.c_int32 * 2),
+                ("gu", P), ("bg", P), ("bu", P), ("out", P), ("out_b", P)]
+
+
+class SsdPlan(C.Structure):
+    _fields_ = [("n_steps", C.c_int32), ("layer_ids", C.POINTER(C.c_int32)),
+                ("pre_bridge", C.POINTER(C.POINTER(SsdBridgeW))), ("pre_norm", C.POINTER(SsdBridgeW)),
+                ("head_w", P), ("head_n", C.c_int32)]
+
+
+class SsdBuffers(C.Structure):
+    _fields_ = [(n, P) for n in ("h", "x", "q", "attn", "mlp", "mid0", "mid1")] + [
+        ("m_cap", C.c_int32), ("mid_cols", C.c_int32), ("k_arena", P), ("vt_arena", P), ("cache_cap", I64),
+        ("attn_ws", P), ("attn_ws_floats", I64), ("logits", P), ("ld_logits", I64)]
+
+
 _PROTOS = {
     "ssd_last_error": (C.c_char_p, []),
     "ssd_abi_version": (I32, []),
@@ -50,6 +78,8 @@ _PROTOS = {
                              I32, P]),
     "ssd_tree_finalize": (I32, [C.POINTER(SsdTree), I32, I32, P, C.POINTER(SsdRows), I32, P]),
     "ssd_accept_greedy": (I32, [C.POINTER(SsdTree), P, I32, P, P, P, P, P]),
+    "ssd_forward": (I32, [C.POINTER(SsdModel), C.POINTER(SsdPlan), C.POINTER(SsdBuffers), C.POINTER(SsdRows), I32,
+                          I32, I32, I32, I32, P]),
 }
 
 EXPORTED = tuple(_PROTOS)

@@ -91,18 +91,16 @@ def _prefill(target: SubnetworkDraftModel, ids: list, cache: KVCache, ws, out_de
     past = cache.get_seq_length()
     q = len(ids)
     cache.check_room(past + q)
-    hn = ws.x
+    logits = None
     for c0 in range(0, q, CHUNK):
         c1 = min(q, c0 + CHUNK)
         m = c1 - c0
         slots = list(range(past + c0, past + c1))
         rows.upload(ids[c0:c1], slots, slots, [s + 1 for s in slots], [0] * m)
-        h = target.run_rows(rows, m, past + c0 + 1, past + c1, cache, ws)
-        if c1 == q:
-            target.final_norm(h[m - 1:], 1, hn)
-        torch.cuda.current_stream().synchronize()
+        last = c1 == q
+        logits = target.forward_rows(rows, m, past + c0 + 1, past + c1, cache, ws, m - 1 if last else 0, int(last))
+        torch.cuda.current_stream().synchronize()  # the pinned staging buffer is reused next chunk
     cache.advance(q)
-    logits = target.head(hn, 1, ws)
     ops.row_topk(logits, 1, logits.shape[1], 1, 0, None, out_dev)
 
 
@@ -137,8 +135,7 @@ def autoregressive_generate(target: TargetRunner, input_ids: torch.Tensor, max_n
     while not _finish(out, eos_ids, max_new_tokens)[1] and s < steps - 1:
         stop = min(steps - 1, s + check_every)
         while s < stop:  # step s feeds token s, writes token s + 1
-            h = target.run_rows(rows.view(s), 1, n_prompt + s + 1, n_prompt + s + 1, cache, ws)
-            logits = target.head(target.final_norm(h, 1, ws.x), 1, ws)
+            logits = target.forward_rows(rows.view(s), 1, n_prompt + s + 1, n_prompt + s + 1, cache, ws)
             ops.row_topk(logits, 1, logits.shape[1], 1, 0, None, rows.ids[s + 1:s + 2])
             s += 1
         cache.seq_len = n_prompt + s
@@ -191,8 +188,7 @@ class DecodeSession:
         ph.mark("verify")
         m = drafter.finalize_device(self.tree, committed, self.root_rows, self.verify_rows)
         cache.check_room(committed + m)
-        h = target.run_rows(self.verify_rows, m, committed + 1, committed + 1 + cfg.depth, cache, ws)
-        logits = target.head(target.final_norm(h, m, ws.x), m, ws)
+        logits = target.forward_rows(self.verify_rows, m, committed + 1, committed + 1 + cfg.depth, cache, ws)
         ops.row_topk(logits, m, logits.shape[1], 1, 0, None, self.argmax)
         _lib.call("ssd_accept_greedy", self.tree.struct, self.argmax.data_ptr(), committed,
                   self.record[2:].data_ptr(), self.keep_src.data_ptr(), self.n_keep.data_ptr(),

@@ -159,8 +159,7 @@ class TreeDrafter:
         tree_start = root_pos + 1
         cache.check_room(tree_start + self.max_tree_cache())
         root_rows.upload(None, [root_pos], [root_pos], [root_pos + 1], [0])
-        h = draft.run_rows(root_rows, 1, root_pos + 1, root_pos + 1, cache, ws)
-        logits = draft.head(draft.final_norm(h, 1, ws.x), 1, ws)
+        logits = draft.forward_rows(root_rows, 1, root_pos + 1, root_pos + 1, cache, ws)
         n = logits.shape[1]
         ops.row_topk(logits, 1, n, self.branch[0], 1, draft._vocab_ids_i32, cand_tok, cand_lp)
         past = tree_start
@@ -173,8 +172,7 @@ class TreeDrafter:
                       level_rows.struct, m if feed else 0, ops.stream())
             if not feed:
                 break
-            h = draft.run_rows(level_rows, m, tree_start, tree_start + d + 1, cache, ws)
-            logits = draft.head(draft.final_norm(h, m, ws.x), m, ws)
+            logits = draft.forward_rows(level_rows, m, tree_start, tree_start + d + 1, cache, ws)
             ops.row_topk(logits, m, n, self.branch[d + 1], 1, draft._vocab_ids_i32, cand_tok, cand_lp)
             past += m
         cache.seq_len = past

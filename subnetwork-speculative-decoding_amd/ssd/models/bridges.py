@@ -18,7 +18,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from ssd import ops
+from ssd import _lib, ops
 from ssd.config import BridgeConfig
 
 _ACTS = {"silu": nn.SiLU, "gelu": nn.GELU, "relu": nn.ReLU}
@@ -93,6 +93,24 @@ class PackedBridge:
         out = bridge.mlp.out_proj
         self.out = ops.pack_weight(bf(out.weight))
         self.out_bias = bf(out.bias)
+        self._native: Optional[_lib.SsdBridgeW] = None
+
+    def native(self) -> "_lib.SsdBridgeW":
+        """C descriptor (SsdBridgeW) for ssd_forward; the tensors it points at live on this object."""
+        if self._native is None:
+            def p(t):
+                return None if t is None else t.data_ptr()
+
+            st = _lib.SsdBridgeW()
+            st.norm, st.eps, st.hidden, st.swiglu, st.n_body = p(self.norm), self.eps, self.hidden, int(self.swiglu), \
+                len(self.body)
+            for i, (w, b, n, _, act) in enumerate(self.body):
+                st.body_w[i], st.body_b[i], st.body_n[i], st.body_act[i] = p(w), p(b), n, ops.ACT[act]
+            if self.swiglu:
+                st.gu, st.bg, st.bu = p(self.gu), p(self.bg), p(self.bu)
+            st.out, st.out_b = p(self.out), p(self.out_bias)
+            self._native = st
+        return self._native
 
     def apply_(self, h: torch.Tensor, m: int, x: torch.Tensor, mids: list) -> None:
         """h[:m] <- h + MLP(RMSNorm(h)) in place. x: [>=m, d] scratch; mids: two [>=m, hidden] scratches."""

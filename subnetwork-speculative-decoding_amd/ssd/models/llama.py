@@ -24,7 +24,7 @@ from typing import Optional
 
 import torch
 
-from ssd import ops
+from ssd import _lib, ops
 
 BF16 = torch.bfloat16
 
@@ -124,6 +124,7 @@ class MI355XLlama:
         self.layers: list[Layer] = []
         self._cos = self._sin = None
         self._lm_head_rows: Optional[torch.Tensor] = None  # row-major lm_head kept only when requested
+        self._native = None
 
     # ------------------------------------------------------------ construction
     def _put(self, t: torch.Tensor) -> torch.Tensor:
@@ -207,6 +208,21 @@ class MI355XLlama:
             n = max(max_pos, 4096)
             self._cos, self._sin = rope_tables(n, self.shape.head_dim, self.shape.theta, self.device)
         return self._cos, self._sin
+
+    def native(self, max_pos: int) -> "_lib.SsdModel":
+        """C descriptor (SsdModel) of this model for ssd_forward; rebuilt only when the rotary
+        tables grow. The struct and its layer array stay alive on this object."""
+        cos, sin = self.rope(max_pos)
+        if self._native is None or self._native[0] != cos.data_ptr():
+            s = self.shape
+            arr = (_lib.SsdLayerW * s.layers)(*[
+                _lib.SsdLayerW(L.wqkv.data_ptr(), L.wo.data_ptr(), L.wgu.data_ptr(), L.wd.data_ptr(), L.ln1.data_ptr(),
+                               L.ln2.data_ptr()) for L in self.layers])
+            st = _lib.SsdModel(s.hidden, s.heads, s.kv_heads, s.head_dim, s.inter, s.vocab, s.layers, s.eps,
+                               s.head_dim ** -0.5, self.embed.data_ptr(), self.norm.data_ptr(), cos.data_ptr(),
+                               sin.data_ptr(), cos.shape[0], arr)
+            self._native = (cos.data_ptr(), st, arr)
+        return self._native[1]
 
     def weight_bytes(self, layers=None) -> int:
         """Packed bytes streamed per forward for ``layers`` (default all) plus the full lm_head."""

@@ -20,6 +20,7 @@ all-true committed prefix plus each node's own ancestors (subnetwork_draft.py:16
 
 from __future__ import annotations
 
+import ctypes
 import os
 from dataclasses import dataclass, field
 from typing import Optional
@@ -102,8 +103,11 @@ class Rows:
 
     def view(self, off: int) -> "_RowsView":
         """Rows [off, cap) as a forward's rows (pointer offsets, no copy)."""
-        return _RowsView(self.ids[off:], self.pos[off:], self.slot[off:], self.prefix[off:], self.depth[off:],
-                         self.anc[off:])
+        v = _RowsView(self.ids[off:], self.pos[off:], self.slot[off:], self.prefix[off:], self.depth[off:],
+                      self.anc[off:])
+        v.struct = _lib.SsdRows(v.ids.data_ptr(), v.pos.data_ptr(), v.slot.data_ptr(), v.prefix.data_ptr(),
+                                v.depth.data_ptr(), v.anc.data_ptr(), self.cap - off)
+        return v
 
     def upload(self, ids, pos, slot, prefix, depth, anc=None) -> None:
         """Fill rows [0, n) from host lists with one pinned async copy (the pinned staging buffer
@@ -138,6 +142,7 @@ class _RowsView:
     prefix: torch.Tensor
     depth: torch.Tensor
     anc: torch.Tensor
+    struct: Optional[_lib.SsdRows] = None
 
 
 class Workspace:
@@ -156,6 +161,7 @@ class Workspace:
         self.mids = [torch.zeros(m_cap, bh, **bf), torch.zeros(m_cap, bh, **bf)]
         self.ws = torch.zeros(0, dtype=torch.float32, device=dev)
         self.logits = torch.zeros(0, **bf)
+        self._native: dict = {}
 
     def attn_ws(self, model: MI355XLlama, max_len: int) -> torch.Tensor:
         s = model.shape
@@ -169,6 +175,25 @@ class Workspace:
         if self.logits.numel() < m * ld:
             self.logits = torch.zeros(max(m, self.m_cap) * ld, dtype=torch.bfloat16, device=self.h.device)
         return self.logits[: m * ld].view(m, ld)
+
+    def native(self, model: MI355XLlama, cache: KVCache, n: int):
+        """(SsdBuffers, logits [m_cap, ld]) for ssd_forward over these buffers, ``cache``'s arena and
+        a head of ``n`` columns. Descriptors are cached per (arena, logits, workspace) pointers."""
+        ld = (n + 7) // 8 * 8
+        if self.logits.numel() < self.m_cap * ld:
+            self.logits = torch.zeros(self.m_cap * ld, dtype=torch.bfloat16, device=self.h.device)
+        aws = self.attn_ws(model, cache.capacity)
+        key = (cache.k.data_ptr(), cache.vt.data_ptr(), cache.capacity, ld, self.logits.data_ptr(), aws.data_ptr())
+        st = self._native.get(key)
+        if st is None:
+            if len(self._native) >= 8:
+                self._native.pop(next(iter(self._native)))
+            st = _lib.SsdBuffers(self.h.data_ptr(), self.x.data_ptr(), self.q.data_ptr(), self.attn.data_ptr(),
+                                 self.mlp.data_ptr(), self.mids[0].data_ptr(), self.mids[1].data_ptr(), self.m_cap,
+                                 self.mids[0].shape[1], cache.k.data_ptr(), cache.vt.data_ptr(), cache.capacity,
+                                 aws.data_ptr(), aws.numel(), self.logits.data_ptr(), ld)
+            self._native[key] = st
+        return st, self.logits[: self.m_cap * ld].view(self.m_cap, ld)
 
 
 class _BaseRefs:
@@ -203,6 +228,7 @@ class SubnetworkDraftModel(nn.Module):
         self._vocab_ids_i32: Optional[torch.Tensor] = None
         self._sub_head: Optional[torch.Tensor] = None
         self._ws: Optional[Workspace] = None
+        self._plan = None
 
     # ------------------------------------------------------------------ setup
     @property
@@ -245,6 +271,41 @@ class SubnetworkDraftModel(nn.Module):
         return br.packed(self.model.device)
 
     # ------------------------------------------------------- device forward
+    def native_plan(self) -> "_lib.SsdPlan":
+        """C descriptor (SsdPlan): selected layers, their bridges and the head; rebuilt when a
+        bridge is repacked or the vocabulary subset changes."""
+        pre = [self._packed_bridge(n) if n is not None else None for n in self._pre_layer_bridge]
+        post = self._packed_bridge(self._pre_norm_bridge) if self._pre_norm_bridge is not None else None
+        head = self._sub_head if self._sub_head is not None else self.model.lm_head
+        key = (tuple(id(b) for b in pre), id(post), head.data_ptr())
+        if self._plan is None or self._plan[0] != key:
+            n = len(self.layer_indices)
+            ids = (ctypes.c_int32 * n)(*self.layer_indices)
+            BP = ctypes.POINTER(_lib.SsdBridgeW)
+            natives = [b.native() if b is not None else None for b in pre]
+            arr = (BP * n)(*[ctypes.pointer(x) if x is not None else BP() for x in natives])
+            st = _lib.SsdPlan(n, ids, arr if any(natives) else None,
+                              ctypes.pointer(post.native()) if post is not None else None, head.data_ptr(),
+                              self._head_n())
+            self._plan = (key, st, ids, arr, pre, post)
+        return self._plan[1]
+
+    def _head_n(self) -> int:
+        return int(self.vocab_ids.numel()) if self._sub_head is not None else self.model.shape.vocab
+
+    def forward_rows(self, rows, m: int, p_min: int, l_max: int, cache: KVCache, ws: Workspace,
+                     head_first: int = 0, head_rows: Optional[int] = None) -> Optional[torch.Tensor]:
+        """One ssd_forward call over rows [0, m) on the device: embedding, the selected layers and
+        bridges, the final norm (into ws.x) and the head over rows [head_first, head_first +
+        head_rows) (default all). Returns the bf16 logits view [head_rows, n] (None if no rows)."""
+        if head_rows is None:
+            head_rows = m
+        n = self._head_n()
+        buf, logits = ws.native(self.model, cache, n)
+        _lib.call("ssd_forward", self.model.native(cache.capacity), self.native_plan(), buf, rows.struct, m,
+                  int(p_min), int(l_max), head_first, head_rows, ops.stream())
+        return logits[:head_rows, :n] if head_rows else None
+
     def run_rows(self, rows: Rows, m: int, p_min: int, l_max: int, cache: KVCache, ws: Workspace,
                  bridge_states: Optional[dict] = None, ids_ready: bool = True) -> torch.Tensor:
         """All selected layers (+ bridges) for rows [0, m) already on the device. Returns the
@@ -280,16 +341,11 @@ class SubnetworkDraftModel(nn.Module):
 
     def head(self, hn: torch.Tensor, m: int, ws: Workspace) -> torch.Tensor:
         """lm_head (or the vocab-subset head) over hn[:m] -> bf16 logits view [m, V]."""
-        if self._sub_head is not None:
-            n, w = self._sub_head_n(), self._sub_head
-        else:
-            n, w = self.model.shape.vocab, self.model.lm_head
+        n = self._head_n()
+        w = self._sub_head if self._sub_head is not None else self.model.lm_head
         out = ws.logits_buf(m, n)
         ops.gemm(hn, m, w, n, self.d_model, out)
         return out[:, :n]
-
-    def _sub_head_n(self) -> int:
-        return int(self.vocab_ids.numel())
 
     def final_norm(self, h: torch.Tensor, m: int, out: torch.Tensor) -> torch.Tensor:
         return ops.rmsnorm(h, m, self.model.norm, self.model.shape.eps, out)
@@ -365,8 +421,12 @@ class SubnetworkDraftModel(nn.Module):
             m = c1 - c0
             p_min = min(prefix[c0:c1])
             l_max = max(p + len(a) for p, a in zip(prefix[c0:c1], anc[c0:c1]))
-            h = self.run_rows(rows, m, p_min, l_max, cache, ws, states)
-            self.final_norm(h, m, hidden[c0:c1])
+            if states is None:
+                self.forward_rows(rows, m, p_min, l_max, cache, ws, head_rows=0)
+                hidden[c0:c1].copy_(ws.x[:m])
+            else:
+                h = self.run_rows(rows, m, p_min, l_max, cache, ws, states)
+                self.final_norm(h, m, hidden[c0:c1])
             torch.cuda.current_stream().synchronize()  # the pinned staging buffer is reused next chunk
         cache.advance(q)
         logits = None

@@ -50,3 +50,30 @@ def test_host_only_entry_points():
     # argument validation happens on the host, before any launch
     rc = lib.ssd_gemm_bf16(None, 0, 1, None, 16, 32, None, 0, None, 0, None, 0, None)
     assert rc == 1 and b"null" in lib.ssd_last_error()
+
+
+def test_descriptor_structs_match_c_layout(tmp_path):
+    """The ctypes mirrors of the descriptor structs have the C compiler's sizes and offsets."""
+    import ctypes as C
+    import subprocess
+
+    from ssd import _lib
+
+    structs = {name: getattr(_lib, name) for name in ("SsdTree", "SsdRows", "SsdLayerW", "SsdModel", "SsdBridgeW",
+                                                       "SsdPlan", "SsdBuffers")}
+    lines = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void) {"]
+    for name, T in structs.items():
+        lines.append(f'printf("{name} %zu\\n", sizeof({name}));')
+        for field, *_ in T._fields_:
+            lines.append(f'printf("{name}.{field} %zu\\n", offsetof({name}, {field}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-o", str(exe), str(src)], check=True)
+    got = dict(line.split() for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                       check=True).stdout.splitlines())
+    for name, T in structs.items():
+        assert int(got[name]) == C.sizeof(T), name
+        for field, *_ in T._fields_:
+            assert int(got[f"{name}.{field}"]) == getattr(T, field).offset, f"{name}.{field}"

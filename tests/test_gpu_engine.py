@@ -118,6 +118,25 @@ def test_draft_logits_match_oracle(hf, oracle_base):
     assert_logits_close(got, ref, exact)
 
 
+@pytest.mark.parametrize("bridge", [dict(), dict(num_layers=3, activation="gelu", hidden_dim=384),
+                                    dict(mlp_type="swiglu", hidden_dim=320, bias=False)])
+def test_forward_sequencer_bitwise_equals_per_kernel_calls(hf, bridge):
+    """ssd_forward (one C call per forward) == the same kernels called one by one from Python
+    (the path taken when bridge states are requested), with bridges of every kind, a skipped
+    final layer (pre-norm bridge) and a vocabulary-subset head."""
+    _, BridgeConfig, _, SDM = ssd()
+    torch.manual_seed(5)
+    draft = SDM(hf, [1, 2, 4], BridgeConfig(init_std=0.02, **bridge))
+    ids = prompt(70, 9)
+    for subset in (None, torch.arange(0, 512, 3)):
+        draft.set_vocab_subset(subset)
+        seq = draft(ids)
+        per = draft(ids, output_bridge_states=True)
+        assert set(per.bridge_states) == {"into_1", "into_4", "into_norm"}
+        assert torch.equal(seq.hidden_states, per.hidden_states)
+        assert torch.equal(seq.logits, per.logits)
+
+
 def test_incremental_cache_bitwise_equals_full(hf):
     draft = make_draft(hf, "untrained")
     ids = prompt(100, 3)
