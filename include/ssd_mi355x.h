@@ -67,6 +67,32 @@ int ssd_gemm_qkv_rope_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t
                            int64_t rope_rows, const int32_t* row_pos, const int32_t* row_slot, uint16_t* Q, int64_t ldq,
                            uint16_t* k_cache, uint16_t* vt_cache, int64_t max_len, hipStream_t stream);
 
+/* ---------------------------------------------------------- split-K GEMMs
+ * For narrow outputs (o_proj, down_proj, q/k/v, bridge out_proj) K is split over workgroups:
+ * P[s][m][n] = sum over the s-th K range of X W^T in fp32, s < ssd_gemm_splits(N, K) (a function
+ * of the shape only, so results stay batch-invariant). P: 16-byte aligned fp32, row stride
+ * ldp >= N rounded up to 64 (multiple of 4), split stride >= M * ldp. A consumer sums the S
+ * partials in order s = 0..S-1 and applies the epilogue of the op it replaces. */
+int ssd_gemm_splits(int N, int K);
+int ssd_gemm_partial_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int N, int K, float* P,
+                          int64_t ldp, int64_t split_stride, hipStream_t stream);
+/* The ssd_gemm_bf16 epilogue (bias, activation, residual; Y may alias residual) over S partials. */
+int ssd_gemm_finalize_bf16(const float* P, int64_t ldp, int64_t split_stride, int S, int M, int N, uint16_t* Y,
+                           int64_t ldy, const uint16_t* bias, int act, const uint16_t* residual, int64_t ldr,
+                           hipStream_t stream);
+/* The RoPE + KV-cache-write epilogue of ssd_gemm_qkv_rope_bf16 over S partials of the packed q/k/v
+ * projection (ssd/models/subnetwork_draft.py:209-222). */
+int ssd_qkv_rope_finalize_bf16(const float* P, int64_t ldp, int64_t split_stride, int S, int M, int heads,
+                               int kv_heads, int head_dim, const uint16_t* cos_tab, const uint16_t* sin_tab,
+                               int64_t rope_rows, const int32_t* row_pos, const int32_t* row_slot, uint16_t* Q,
+                               int64_t ldq, uint16_t* k_cache, uint16_t* vt_cache, int64_t max_len, hipStream_t stream);
+/* Residual add of a projection's partials, then the next RMSNorm (ssd/models/subnetwork_draft.py:243-245,
+ * ssd/models/bridges.py:131-135):  h <- bf16(h + bf16(sum_s P[s] + bias));  y <- w * bf16(h * rsqrt(mean(h^2)
+ * + eps)). S = 0: y = RMSNorm(h) only; y = NULL: residual update only. D = row length (P's N). */
+int ssd_add_rmsnorm_bf16(const float* P, int64_t ldp, int64_t split_stride, int S, const uint16_t* bias, uint16_t* h,
+                         int64_t ldh, int M, int D, const uint16_t* w, float eps, uint16_t* y, int64_t ldy,
+                         hipStream_t stream);
+
 /* ------------------------------------------------------------ tree attention
  * Row t attends cache slots [0, prefix[t]) then anc[t][0..depth[t]) (ancestors in depth order,
  * self included), i.e. the reference's boolean tree mask (ssd/models/subnetwork_draft.py:165-191,
@@ -212,6 +238,8 @@ typedef struct SsdBuffers {   /* activations [m_cap][...] and the layer-major KV
   int64_t attn_ws_floats;
   uint16_t* logits;           /* [head_rows][ld_logits] */
   int64_t ld_logits;
+  float* part;                /* split-K partials of one GEMM (fp32) */
+  int64_t part_floats;
 } SsdBuffers;
 
 /* Embedding, the plan's decoder layers with their bridges, final norm and the head over rows

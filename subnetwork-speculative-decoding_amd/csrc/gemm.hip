@@ -64,72 +64,84 @@ struct GemmArgs {
 
 constexpr int GEMM_UNROLL = 4;
 
+// Per-element epilogues (fp32 dot products in, bf16 rounding points of the reference out).
+// Plain store: output column n of row m.
+__device__ __forceinline__ void epi_store(const GemmArgs& a, int n, int m, float t) {
+  if (a.bias) t += bf2f(a.bias[n]);
+  t = rbf(t);
+  if (a.act) t = rbf(apply_act(a.act, t));
+  if (a.residual) t = rbf(bf2f(a.residual[(size_t)m * a.ldr + n]) + t);
+  a.Y[(size_t)m * a.ldy + n] = f2bf(t);
+}
+
+// SwiGLU: intermediate column col of row m from its gate and up dot products.
+__device__ __forceinline__ void epi_swiglu(const GemmArgs& a, int col, int m, float gt, float up) {
+  if (a.bias) gt += bf2f(a.bias[col]);
+  if (a.bias2) up += bf2f(a.bias2[col]);
+  const float gs = rbf(silu_f(rbf(gt)));
+  a.Y[(size_t)m * a.ldy + col] = f2bf(gs * rbf(up));
+}
+
+// q/k/v tile nb, pair r (rows r and r + 8 = rotary dims p*8 + r and hd/2 + p*8 + r) of row m:
+// RoPE for q/k, then Q store or KV-cache write (V transposed).
+__device__ __forceinline__ void epi_qkv(const GemmArgs& a, int nb, int m, int r, float vlo, float vhi) {
+  const int hd = a.head_dim, half = hd >> 1, tiles_per_head = hd >> 4;
+  const int q_tiles = a.heads * tiles_per_head, k_tiles = a.kv_heads * tiles_per_head;
+  int region, head, p;
+  if (nb < q_tiles) {
+    region = 0; head = nb / tiles_per_head; p = nb % tiles_per_head;
+  } else if (nb < q_tiles + k_tiles) {
+    region = 1; head = (nb - q_tiles) / tiles_per_head; p = (nb - q_tiles) % tiles_per_head;
+  } else {
+    region = 2; head = (nb - q_tiles - k_tiles) / tiles_per_head; p = (nb - q_tiles - k_tiles) % tiles_per_head;
+  }
+  const int dlo = p * 8 + r, dhi = dlo + half;
+  const float xlo = rbf(vlo), xhi = rbf(vhi);
+  const int slot = a.row_slot[m];
+  if (region != 0 && (slot < 0 || slot >= a.max_len)) return;  // never write outside the cache
+  if (region == 2) {
+    bf16_t* vt = a.vt_cache + (size_t)head * hd * a.max_len;
+    vt[(size_t)dlo * a.max_len + slot] = f2bf(xlo);
+    vt[(size_t)dhi * a.max_len + slot] = f2bf(xhi);
+    return;
+  }
+  const int pos = min(max(a.row_pos[m], 0), (int)a.rope_rows - 1);
+  const float cs = bf2f(a.cos_tab[(size_t)pos * half + dlo]);
+  const float sn = bf2f(a.sin_tab[(size_t)pos * half + dlo]);
+  const float olo = rbf(rbf(xlo * cs) - rbf(xhi * sn));
+  const float ohi = rbf(rbf(xhi * cs) + rbf(xlo * sn));
+  if (region == 0) {
+    bf16_t* q = a.Y + (size_t)m * a.ldy + (size_t)head * hd;
+    q[dlo] = f2bf(olo);
+    q[dhi] = f2bf(ohi);
+  } else {
+    bf16_t* kr = a.k_cache + ((size_t)head * a.max_len + slot) * hd;
+    kr[dlo] = f2bf(olo);
+    kr[dhi] = f2bf(ohi);
+  }
+}
+
 // Epilogue of one 16-row tile `nb` for rows m < Mv; val(r, m) is the fp32 dot product of tile
-// row r and token m.
+// row r and token m. Threads tid, tid + NTHREADS, ... of the caller share the work.
 template <int EPI, int NTHREADS, class Val>
-__device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, int nb, int Mv, Val val) {
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, int nb, int Mv, Val val, int tid) {
   if (nb * 16 >= a.N) return;
-  const int nthreads = NTHREADS;
   if constexpr (EPI == EPI_STORE) {
-    for (int o = threadIdx.x; o < 16 * Mv; o += nthreads) {
+    for (int o = tid; o < 16 * Mv; o += NTHREADS) {
       const int m = o >> 4, r = o & 15;
       const int n = nb * 16 + r;
-      if (n >= a.N) continue;
-      float t = val(r, m);
-      if (a.bias) t += bf2f(a.bias[n]);
-      t = rbf(t);
-      if (a.act) t = rbf(apply_act(a.act, t));
-      if (a.residual) t = rbf(bf2f(a.residual[(size_t)m * a.ldr + n]) + t);
-      a.Y[(size_t)m * a.ldy + n] = f2bf(t);
+      if (n < a.N) epi_store(a, n, m, val(r, m));
     }
   } else if constexpr (EPI == EPI_SWIGLU) {
-    for (int o = threadIdx.x; o < 8 * Mv; o += nthreads) {
+    for (int o = tid; o < 8 * Mv; o += NTHREADS) {
       const int m = o >> 3, r = o & 7;
       const int col = nb * 8 + r;  // intermediate index
-      if (col * 2 >= a.N) continue;
-      float gt = val(r, m), up = val(r + 8, m);
-      if (a.bias) gt += bf2f(a.bias[col]);
-      if (a.bias2) up += bf2f(a.bias2[col]);
-      const float gs = rbf(silu_f(rbf(gt)));
-      a.Y[(size_t)m * a.ldy + col] = f2bf(gs * rbf(up));
+      if (col * 2 < a.N) epi_swiglu(a, col, m, val(r, m), val(r + 8, m));
     }
   } else {  // EPI_QKV
-    const int hd = a.head_dim, half = hd >> 1, tiles_per_head = hd >> 4;
-    const int q_tiles = a.heads * tiles_per_head, k_tiles = a.kv_heads * tiles_per_head;
-    int region, head, p;
-    if (nb < q_tiles) {
-      region = 0; head = nb / tiles_per_head; p = nb % tiles_per_head;
-    } else if (nb < q_tiles + k_tiles) {
-      region = 1; head = (nb - q_tiles) / tiles_per_head; p = (nb - q_tiles) % tiles_per_head;
-    } else {
-      region = 2; head = (nb - q_tiles - k_tiles) / tiles_per_head; p = (nb - q_tiles - k_tiles) % tiles_per_head;
-    }
-    for (int o = threadIdx.x; o < 8 * Mv; o += nthreads) {
+    for (int o = tid; o < 8 * Mv; o += NTHREADS) {
       const int m = o >> 3, r = o & 7;
-      const int dlo = p * 8 + r, dhi = dlo + half;
-      const float xlo = rbf(val(r, m)), xhi = rbf(val(r + 8, m));
-      const int slot = a.row_slot[m];
-      if (region != 0 && (slot < 0 || slot >= a.max_len)) continue;  // never write outside the cache
-      if (region == 2) {
-        bf16_t* vt = a.vt_cache + (size_t)head * hd * a.max_len;
-        vt[(size_t)dlo * a.max_len + slot] = f2bf(xlo);
-        vt[(size_t)dhi * a.max_len + slot] = f2bf(xhi);
-        continue;
-      }
-      const int pos = min(max(a.row_pos[m], 0), (int)a.rope_rows - 1);
-      const float cs = bf2f(a.cos_tab[(size_t)pos * half + dlo]);
-      const float sn = bf2f(a.sin_tab[(size_t)pos * half + dlo]);
-      const float olo = rbf(rbf(xlo * cs) - rbf(xhi * sn));
-      const float ohi = rbf(rbf(xhi * cs) + rbf(xlo * sn));
-      if (region == 0) {
-        bf16_t* q = a.Y + (size_t)m * a.ldy + (size_t)head * hd;
-        q[dlo] = f2bf(olo);
-        q[dhi] = f2bf(ohi);
-      } else {
-        bf16_t* kr = a.k_cache + ((size_t)head * a.max_len + slot) * hd;
-        kr[dlo] = f2bf(olo);
-        kr[dhi] = f2bf(ohi);
-      }
+      epi_qkv(a, nb, m, r, val(r, m), val(r + 8, m));
     }
   }
 }
@@ -158,14 +170,10 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
   const uint4* wp[NSUB];
 #pragma unroll
   for (int s = 0; s < NSUB; ++s) wp[s] = a.W + ((size_t)(tile * NSUB + s) * kbt) * 64 + lane;
+  // Rows past M load row M-1 (always valid, no per-lane branch); their columns are never stored.
   const bf16_t* xp[CT];
-  bool xv[CT];
 #pragma unroll
-  for (int c = 0; c < CT; ++c) {
-    const int m = c * 16 + j;
-    xv[c] = m < a.M;
-    xp[c] = a.X + (size_t)(xv[c] ? m : 0) * a.ldx + g * 8;
-  }
+  for (int c = 0; c < CT; ++c) xp[c] = a.X + (size_t)min(c * 16 + j, a.M - 1) * a.ldx + g * 8;
 
   int kb = kb_lo;
   for (; kb + GEMM_UNROLL - 1 < kb_hi; kb += GEMM_UNROLL) {
@@ -178,7 +186,7 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
     for (int u = 0; u < GEMM_UNROLL; ++u)
 #pragma unroll
       for (int c = 0; c < CT; ++c)
-        xr[u][c] = xv[c] ? *(const uint4*)(xp[c] + (kb + u) * 32) : make_uint4(0, 0, 0, 0);
+        xr[u][c] = *(const uint4*)(xp[c] + (kb + u) * 32);
 #pragma unroll
     for (int u = 0; u < GEMM_UNROLL; ++u)
 #pragma unroll
@@ -191,7 +199,7 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int s = 0; s < NSUB; ++s) wr[s] = ld_stream(wp[s] + (size_t)kb * 64);
 #pragma unroll
-    for (int c = 0; c < CT; ++c) xr[c] = xv[c] ? *(const uint4*)(xp[c] + kb * 32) : make_uint4(0, 0, 0, 0);
+    for (int c = 0; c < CT; ++c) xr[c] = *(const uint4*)(xp[c] + kb * 32);
 #pragma unroll
     for (int s = 0; s < NSUB; ++s)
 #pragma unroll
@@ -222,7 +230,201 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
         v = ww == 0 ? x : v + x;
       }
       return v;
-    });
+    }, threadIdx.x);
+}
+
+// ------------------------------------------------------------ split-K partials
+// P[s][m][n] = sum over the s-th K range of X[m, k] W[n, k], fp32 (s < S). Workgroup = (NW*NSUB
+// 16-row tiles of N, one K range); wave w streams its NSUB weight tiles over the whole range,
+// and all waves share the activations, staged once per workgroup in LDS (k-block major, KC
+// k-blocks per pass, the next pass's weights and activations loaded while this one computes).
+// Splitting K over workgroups keeps narrow-N GEMMs (o, down, qkv) at >= 256 workgroups with
+// NSUB = 1 while each activation byte leaves L2 once per workgroup instead of once per wave.
+// The S partials are reduced in a fixed order by the consumer (gemm_finalize_kernel,
+// add_rmsnorm_kernel); S depends only on (N, K), so results stay batch-invariant.
+template <int CT>
+struct PartCfg {
+  static constexpr int KC = CT <= 2 ? 16 : 8;  // k-blocks of activations per LDS pass (KC * CT KiB)
+};
+
+template <int CT, int NSUB, int NW>
+__global__ __launch_bounds__(64 * NW) void gemm_part_kernel(GemmArgs a, float* __restrict__ P, int64_t ldp,
+                                                            int64_t sstride, int S) {
+  constexpr int KC = PartCfg<CT>::KC;
+  constexpr int XCH = KC * CT * 64;                    // 16-byte activation chunks per pass
+  constexpr int XIT = (XCH + 64 * NW - 1) / (64 * NW); // per thread
+  __shared__ u32x4_t xs[XCH];                          // [kb][m][4 x 16 B]
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int kbt = a.kb_total;
+  const int split = blockIdx.y;
+  const int kb0 = (int)(((int64_t)kbt * split) / S), kb1 = (int)(((int64_t)kbt * (split + 1)) / S);
+  const int tile0 = (blockIdx.x * NW + w) * NSUB;
+  const bool active = tile0 * 16 < a.N;  // packed rows are padded to 64, so whole sub-tiles exist
+  const u32x4_t* W = (const u32x4_t*)a.W;
+  const u32x4_t* wp[NSUB];
+#pragma unroll
+  for (int s = 0; s < NSUB; ++s) wp[s] = W + ((size_t)(tile0 + s) * kbt) * 64 + lane;
+
+  f32x4_t acc[NSUB][CT];
+#pragma unroll
+  for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+    for (int c = 0; c < CT; ++c) acc[s][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  u32x4_t xv[XIT], wr[KC][NSUB];
+  // Loads of one pass [c0, c0 + nk): indices are clamped (no per-lane branches around loads).
+  auto load_pass = [&](int c0, int nk, u32x4_t (&xo)[XIT], u32x4_t (&wo)[KC][NSUB]) {
+    const int nx = nk * CT * 64;
+#pragma unroll
+    for (int it = 0; it < XIT; ++it) {
+      const int idx = min((int)threadIdx.x + it * 64 * NW, nx - 1);
+      const int kb = idx / (CT * 64), rem = idx % (CT * 64);
+      const int m = min(rem >> 2, a.M - 1);
+      xo[it] = *(const u32x4_t*)(a.X + (size_t)m * a.ldx + (size_t)(c0 + kb) * 32 + (rem & 3) * 8);
+    }
+    if (active) {
+#pragma unroll
+      for (int u = 0; u < KC; ++u)
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) wo[u][s] = __builtin_nontemporal_load(wp[s] + (size_t)(c0 + min(u, nk - 1)) * 64);
+    }
+  };
+  int c0 = kb0;
+  int nk = min(KC, kb1 - c0);
+  if (nk > 0) load_pass(c0, nk, xv, wr);
+  while (nk > 0) {
+    __syncthreads();  // the previous pass's readers are done with xs
+#pragma unroll
+    for (int it = 0; it < XIT; ++it) {
+      const int idx = threadIdx.x + it * 64 * NW;
+      if (idx < nk * CT * 64) xs[idx] = xv[it];
+    }
+    __syncthreads();
+    const int c1 = c0 + nk;
+    const int nk1 = min(KC, kb1 - c1);
+    u32x4_t wn[KC][NSUB];
+    if (nk1 > 0) load_pass(c1, nk1, xv, wn);
+    if (active) {
+#pragma unroll
+      for (int u = 0; u < KC; ++u) {
+        if (u < nk) {
+          u32x4_t xr[CT];
+#pragma unroll
+          for (int c = 0; c < CT; ++c) xr[c] = xs[(u * CT * 16 + c * 16 + j) * 4 + g];
+#pragma unroll
+          for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+            for (int c = 0; c < CT; ++c)
+              acc[s][c] = mfma16x16x32(bits_bf16x8(wr[u][s]), bits_bf16x8(xr[c]), acc[s][c]);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < KC; ++u)
+#pragma unroll
+      for (int s = 0; s < NSUB; ++s) wr[u][s] = wn[u][s];
+    c0 = c1;
+    nk = nk1;
+  }
+  // Lane (j, g) holds rows n = 16 tile + 4g + e of column m = 16c + j.
+  if (active) {
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+      for (int c = 0; c < CT; ++c) {
+        const int m = c * 16 + j;
+        if (m < a.M) *(f32x4_t*)(P + split * sstride + (size_t)m * ldp + (tile0 + s) * 16 + 4 * g) = acc[s][c];
+      }
+  }
+}
+
+// Epilogue over split-K partials: one thread per (row m, tile nb, pair r) -- r and r + 8 for the
+// SwiGLU / RoPE pairings, both for the plain store -- so the grid covers every output at once.
+// The S partials (S a template constant, loads issued together) are summed in order s = 0..S-1,
+// then the single-pass kernel's bf16 epilogue runs on the sums.
+template <int EPI, int S>
+__global__ __launch_bounds__(256) void gemm_finalize_kernel(GemmArgs a, const float* __restrict__ P, int64_t ldp,
+                                                            int64_t sstride) {
+  const int tiles = (a.N + 15) / 16;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)a.M * tiles * 8) return;
+  const int r = (int)(idx & 7);
+  const int nb = (int)((idx >> 3) % tiles);
+  const int m = (int)((idx >> 3) / tiles);
+  const float* p = P + (size_t)m * ldp + nb * 16 + r;
+  float lo[S], hi[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    lo[s] = p[s * sstride];
+    hi[s] = p[s * sstride + 8];
+  }
+  float vlo = lo[0], vhi = hi[0];
+#pragma unroll
+  for (int s = 1; s < S; ++s) {
+    vlo += lo[s];
+    vhi += hi[s];
+  }
+  if constexpr (EPI == EPI_STORE) {
+    if (nb * 16 + r < a.N) epi_store(a, nb * 16 + r, m, vlo);
+    if (nb * 16 + r + 8 < a.N) epi_store(a, nb * 16 + r + 8, m, vhi);
+  } else {
+    epi_qkv(a, nb, m, r, vlo, vhi);
+  }
+}
+
+template <int EPI>
+static int launch_finalize(const GemmArgs& a, const float* P, int64_t ldp, int64_t sstride, int S, hipStream_t s) {
+  const int64_t threads = (int64_t)a.M * ((a.N + 15) / 16) * 8;
+  const dim3 grid((unsigned)((threads + 255) / 256)), block(256);
+  switch (S) {
+    case 1: hipLaunchKernelGGL((gemm_finalize_kernel<EPI, 1>), grid, block, 0, s, a, P, ldp, sstride); break;
+    case 2: hipLaunchKernelGGL((gemm_finalize_kernel<EPI, 2>), grid, block, 0, s, a, P, ldp, sstride); break;
+    case 4: hipLaunchKernelGGL((gemm_finalize_kernel<EPI, 4>), grid, block, 0, s, a, P, ldp, sstride); break;
+    case 8: hipLaunchKernelGGL((gemm_finalize_kernel<EPI, 8>), grid, block, 0, s, a, P, ldp, sstride); break;
+    case 16: hipLaunchKernelGGL((gemm_finalize_kernel<EPI, 16>), grid, block, 0, s, a, P, ldp, sstride); break;
+    default: return set_error(SSD_EINVAL, "finalize: split count %d not in {1, 2, 4, 8, 16}", S);
+  }
+  return SSD_OK;
+}
+
+struct PartPlan {
+  int nsub, nw, S;
+};
+
+// Split count as a function of (N, K) only: enough workgroups for the chip (~256), each with at
+// least 8 k-blocks.
+static PartPlan part_plan(int N, int K) {
+  PartPlan p;
+  p.nsub = 1;
+  p.nw = 8;
+  const int kbt = K / 32;
+  const int groups = (N + 16 * p.nw * p.nsub - 1) / (16 * p.nw * p.nsub);
+  p.S = 1;
+  while (groups * p.S < 256 && p.S * 2 * 8 <= kbt && p.S < 16) p.S *= 2;
+  return p;
+}
+
+static int launch_part(const GemmArgs& a, float* P, int64_t ldp, int64_t sstride, hipStream_t s) {
+  const PartPlan p = part_plan(a.N, a.kb_total * 32);
+  const int groups = (a.N + 16 * p.nw * p.nsub - 1) / (16 * p.nw * p.nsub);
+  for (int m0 = 0; m0 < a.M; m0 += 64) {
+    GemmArgs b = a;
+    b.M = std::min(64, a.M - m0);
+    b.X = a.X + (size_t)m0 * a.ldx;
+    float* Pm = P + (size_t)m0 * ldp;
+    const int ct = (b.M + 15) / 16;
+    dim3 grid(groups, p.S);
+    switch (ct) {
+      case 1: hipLaunchKernelGGL((gemm_part_kernel<1, 1, 8>), grid, dim3(512), 0, s, b, Pm, ldp, sstride, p.S); break;
+      case 2: hipLaunchKernelGGL((gemm_part_kernel<2, 1, 8>), grid, dim3(512), 0, s, b, Pm, ldp, sstride, p.S); break;
+      case 3: hipLaunchKernelGGL((gemm_part_kernel<3, 1, 8>), grid, dim3(512), 0, s, b, Pm, ldp, sstride, p.S); break;
+      default: hipLaunchKernelGGL((gemm_part_kernel<4, 1, 8>), grid, dim3(512), 0, s, b, Pm, ldp, sstride, p.S); break;
+    }
+    const int rc = check_launch("gemm_part");
+    if (rc) return rc;
+  }
+  return SSD_OK;
 }
 
 // ---------------------------------------------------------------- packing
@@ -380,3 +582,68 @@ SSD_API int ssd_gemm_qkv_rope_bf16(const uint16_t* X, int64_t ldx, int M, const 
   a.k_cache = k_cache; a.vt_cache = vt_cache; a.max_len = max_len;
   return launch_gemm<EPI_QKV>(a, stream);
 }
+
+// ------------------------------------------------------------ split-K entry points
+SSD_API int ssd_gemm_splits(int N, int K) {
+  if (N <= 0 || K <= 0 || K % 32) return set_error(SSD_EINVAL, "gemm_splits: bad shape N=%d K=%d", N, K);
+  return part_plan(N, K).S;
+}
+
+static int check_partials(const void* P, int64_t ldp, int64_t sstride, int M, int N) {
+  if (!P) return set_error(SSD_EINVAL, "partials: null buffer");
+  if (((uintptr_t)P & 15) || ldp % 4 || ldp < (N + 63) / 64 * 64 || sstride < (int64_t)M * ldp || sstride % 4)
+    return set_error(SSD_EINVAL, "partials: need 16-byte alignment, ldp >= %d (multiple of 4), split stride >= M*ldp",
+                     (N + 63) / 64 * 64);
+  return SSD_OK;
+}
+
+// P[s][m][n] (s < ssd_gemm_splits(N, K)) = sum over the s-th K range of X W^T, fp32.
+SSD_API int ssd_gemm_partial_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int N, int K,
+                                  float* P, int64_t ldp, int64_t split_stride, hipStream_t stream) {
+  int rc = check_common(X, ldx, M, W_packed, N, K);
+  if (rc) return rc;
+  if ((rc = check_partials(P, ldp, split_stride, M, N))) return rc;
+  if (M == 0) return SSD_OK;
+  GemmArgs a{};
+  a.X = X; a.ldx = ldx; a.M = M; a.W = (const uint4*)W_packed; a.N = N; a.kb_total = K / 32;
+  return launch_part(a, P, ldp, split_stride, stream);
+}
+
+// The ssd_gemm_bf16 epilogue (bias, activation, residual) over S split-K partials.
+SSD_API int ssd_gemm_finalize_bf16(const float* P, int64_t ldp, int64_t split_stride, int S, int M, int N, uint16_t* Y,
+                                   int64_t ldy, const uint16_t* bias, int act, const uint16_t* residual, int64_t ldr,
+                                   hipStream_t stream) {
+  int rc = check_partials(P, ldp, split_stride, M, N);
+  if (rc) return rc;
+  if (!Y || S < 1 || M < 0 || N <= 0) return set_error(SSD_EINVAL, "gemm_finalize: null Y or bad S=%d M=%d N=%d", S, M, N);
+  if (act < 0 || act > 3 || (residual && act)) return set_error(SSD_EINVAL, "gemm_finalize: bad activation %d", act);
+  if (M == 0) return SSD_OK;
+  GemmArgs a{};
+  a.M = M; a.N = N; a.Y = Y; a.ldy = ldy; a.bias = bias; a.act = act; a.residual = residual; a.ldr = ldr;
+  rc = launch_finalize<EPI_STORE>(a, P, ldp, split_stride, S, stream);
+  return rc ? rc : check_launch("gemm_finalize");
+}
+
+// q/k/v RoPE + KV-cache write (as ssd_gemm_qkv_rope_bf16) over S split-K partials of the packed
+// q/k/v projection.
+SSD_API int ssd_qkv_rope_finalize_bf16(const float* P, int64_t ldp, int64_t split_stride, int S, int M, int heads,
+                                       int kv_heads, int head_dim, const uint16_t* cos_tab, const uint16_t* sin_tab,
+                                       int64_t rope_rows, const int32_t* row_pos, const int32_t* row_slot, uint16_t* Q,
+                                       int64_t ldq, uint16_t* k_cache, uint16_t* vt_cache, int64_t max_len,
+                                       hipStream_t stream) {
+  const int N = (heads + 2 * kv_heads) * head_dim;
+  int rc = check_partials(P, ldp, split_stride, M, N);
+  if (rc) return rc;
+  if (S < 1 || M < 0 || heads <= 0 || kv_heads <= 0) return set_error(SSD_EINVAL, "qkv_finalize: bad S/M/heads");
+  if (head_dim % 16 || head_dim > 256) return set_error(SSD_EINVAL, "qkv_finalize: head_dim=%d unsupported", head_dim);
+  if (!Q || !k_cache || !vt_cache || !cos_tab || !sin_tab || !row_pos || !row_slot || rope_rows <= 0)
+    return set_error(SSD_EINVAL, "qkv_finalize: null pointer or empty rope table");
+  if (M == 0) return SSD_OK;
+  GemmArgs a{};
+  a.M = M; a.N = N; a.Y = Q; a.ldy = ldq; a.heads = heads; a.kv_heads = kv_heads; a.head_dim = head_dim;
+  a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.rope_rows = rope_rows; a.row_pos = row_pos; a.row_slot = row_slot;
+  a.k_cache = k_cache; a.vt_cache = vt_cache; a.max_len = max_len;
+  rc = launch_finalize<EPI_QKV>(a, P, ldp, split_stride, S, stream);
+  return rc ? rc : check_launch("qkv_finalize");
+}
+

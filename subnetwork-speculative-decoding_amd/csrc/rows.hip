@@ -53,6 +53,81 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const bf16_t* __restrict__
   }
 }
 
+// Deterministic 1024-thread sum: butterfly inside each wave, then the 16 wave sums in order.
+__device__ __forceinline__ float block_sum_1024(float v, float* sh) {
+  v += __shfl_xor(v, 1);
+  v += __shfl_xor(v, 2);
+  v += __shfl_xor(v, 4);
+  v += __shfl_xor(v, 8);
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = sh[0];
+#pragma unroll
+  for (int i = 1; i < 16; ++i) r += sh[i];
+  __syncthreads();
+  return r;
+}
+
+// Residual update from split-K partials, then RMSNorm of the new residual:
+//   h <- bf16(h + bf16(sum_s P[s] + bias));  y <- w * bf16(h * rsqrt(mean(h^2) + eps))
+// (the o_proj / down_proj / bridge out_proj residual add of the reference, followed by the next
+// RMSNorm; ssd/models/subnetwork_draft.py:243-245, ssd/models/bridges.py:131-135). One 1024-thread
+// workgroup per row, 4 columns per thread per pass; the S partials (a template constant, loads
+// issued together) are summed in order s = 0..S-1. S = 0: y = RMSNorm(h) only.
+template <int S>
+__global__ __launch_bounds__(1024) void add_rmsnorm_kernel(const float* __restrict__ P, int64_t ldp, int64_t sstride,
+                                                           const bf16_t* __restrict__ bias, bf16_t* __restrict__ h,
+                                                           int64_t ldh, const bf16_t* __restrict__ w,
+                                                           bf16_t* __restrict__ y, int64_t ldy, int D, float eps) {
+  __shared__ float sh[16];
+  const int m = blockIdx.x;
+  bf16_t* hr = h + (size_t)m * ldh;
+  float ss = 0.f;
+  for (int k = threadIdx.x * 4; k < D; k += 1024 * 4) {
+    const uint2 hv = *(const uint2*)(hr + k);
+    float v[4] = {bf2f((bf16_t)(hv.x & 0xffff)), bf2f((bf16_t)(hv.x >> 16)), bf2f((bf16_t)(hv.y & 0xffff)),
+                  bf2f((bf16_t)(hv.y >> 16))};
+    if constexpr (S > 0) {
+      const float* pr = P + (size_t)m * ldp + k;
+      f32x4_t part[S];
+#pragma unroll
+      for (int s = 0; s < S; ++s) part[s] = *(const f32x4_t*)(pr + s * sstride);
+      f32x4_t o = part[0];
+#pragma unroll
+      for (int s = 1; s < S; ++s) o += part[s];
+      float bv[4] = {0.f, 0.f, 0.f, 0.f};
+      if (bias) {
+        const uint2 b = *(const uint2*)(bias + k);
+        bv[0] = bf2f((bf16_t)(b.x & 0xffff)); bv[1] = bf2f((bf16_t)(b.x >> 16));
+        bv[2] = bf2f((bf16_t)(b.y & 0xffff)); bv[3] = bf2f((bf16_t)(b.y >> 16));
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) v[t] = rbf(v[t] + rbf(bias ? o[t] + bv[t] : o[t]));
+      *(uint2*)(hr + k) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) ss += v[t] * v[t];
+  }
+  const float tot = block_sum_1024(ss, sh);
+  if (!y) return;
+  const float r = rsqrtf(tot / (float)D + eps);
+  bf16_t* yr = y + (size_t)m * ldy;
+  for (int k = threadIdx.x * 4; k < D; k += 1024 * 4) {
+    const uint2 hv = *(const uint2*)(hr + k), wv = *(const uint2*)(w + k);
+    const uint32_t hw[2] = {hv.x, hv.y}, ww[2] = {wv.x, wv.y};
+    uint32_t o[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const float a0 = bf2f((bf16_t)(ww[q] & 0xffff)) * rbf(bf2f((bf16_t)(hw[q] & 0xffff)) * r);
+      const float a1 = bf2f((bf16_t)(ww[q] >> 16)) * rbf(bf2f((bf16_t)(hw[q] >> 16)) * r);
+      o[q] = pack_bf16x2(a0, a1);
+    }
+    *(uint2*)(yr + k) = make_uint2(o[0], o[1]);
+  }
+}
+
 __global__ __launch_bounds__(256) void embed_kernel(const int* __restrict__ ids, const bf16_t* __restrict__ table,
                                                     int64_t V, int D, bf16_t* __restrict__ out, int64_t ldo) {
   const int m = blockIdx.x;
@@ -286,3 +361,31 @@ SSD_API int ssd_row_topk_bf16(const uint16_t* logits, int64_t ld, int M, int N, 
                      out_tok, out_val, out_lse);
   return check_launch("row_topk_merge");
 }
+
+SSD_API int ssd_add_rmsnorm_bf16(const float* P, int64_t ldp, int64_t split_stride, int S, const uint16_t* bias,
+                                 uint16_t* h, int64_t ldh, int M, int D, const uint16_t* w, float eps, uint16_t* y,
+                                 int64_t ldy, hipStream_t stream) {
+  if (!h || (y && !w) || (S > 0 && !P) || S < 0 || S > 16 || M < 0 || D <= 0 || D % 8)
+    return set_error(SSD_EINVAL, "add_rmsnorm: null pointer or bad S=%d M=%d D=%d", S, M, D);
+  if (((uintptr_t)h & 15) || ldh % 8 || (y && (((uintptr_t)y & 15) || ldy % 8)) || (w && ((uintptr_t)w & 15)) ||
+      (bias && ((uintptr_t)bias & 15)))
+    return set_error(SSD_EINVAL, "add_rmsnorm: bf16 tensors must be 16-byte aligned with strides %% 8 == 0");
+  if (S > 0 && (((uintptr_t)P & 15) || ldp % 4 || ldp < D || split_stride < (int64_t)M * ldp || split_stride % 4))
+    return set_error(SSD_EINVAL, "add_rmsnorm: partials need 16-byte alignment, ldp >= D, split stride >= M*ldp");
+  if (M == 0) return SSD_OK;
+#define SSD_ADD_RMS(S_)                                                                                       \
+  hipLaunchKernelGGL((add_rmsnorm_kernel<S_>), dim3(M), dim3(1024), 0, stream, P, ldp, split_stride,          \
+                     (const bf16_t*)bias, (bf16_t*)h, ldh, (const bf16_t*)w, (bf16_t*)y, ldy, D, eps)
+  switch (S) {
+    case 0: SSD_ADD_RMS(0); break;
+    case 1: SSD_ADD_RMS(1); break;
+    case 2: SSD_ADD_RMS(2); break;
+    case 4: SSD_ADD_RMS(4); break;
+    case 8: SSD_ADD_RMS(8); break;
+    case 16: SSD_ADD_RMS(16); break;
+    default: return set_error(SSD_EINVAL, "add_rmsnorm: split count %d not in {0, 1, 2, 4, 8, 16}", S);
+  }
+#undef SSD_ADD_RMS
+  return check_launch("add_rmsnorm");
+}
+

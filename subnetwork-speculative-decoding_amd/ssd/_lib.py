@@ -52,7 +52,7 @@ class SsdPlan(C.Structure):
 class SsdBuffers(C.Structure):
     _fields_ = [(n, P) for n in ("h", "x", "q", "attn", "mlp", "mid0", "mid1")] + [
         ("m_cap", C.c_int32), ("mid_cols", C.c_int32), ("k_arena", P), ("vt_arena", P), ("cache_cap", I64),
-        ("attn_ws", P), ("attn_ws_floats", I64), ("logits", P), ("ld_logits", I64)]
+        ("attn_ws", P), ("attn_ws_floats", I64), ("logits", P), ("ld_logits", I64), ("part", P), ("part_floats", I64)]
 
 
 _PROTOS = {
@@ -78,6 +78,11 @@ _PROTOS = {
                              I32, P]),
     "ssd_tree_finalize": (I32, [C.POINTER(SsdTree), I32, I32, P, C.POINTER(SsdRows), I32, P]),
     "ssd_accept_greedy": (I32, [C.POINTER(SsdTree), P, I32, P, P, P, P, P]),
+    "ssd_gemm_splits": (I32, [I32, I32]),
+    "ssd_gemm_partial_bf16": (I32, [P, I64, I32, P, I32, I32, P, I64, I64, P]),
+    "ssd_gemm_finalize_bf16": (I32, [P, I64, I64, I32, I32, I32, P, I64, P, I32, P, I64, P]),
+    "ssd_qkv_rope_finalize_bf16": (I32, [P, I64, I64, I32, I32, I32, I32, I32, P, P, I64, P, P, P, I64, P, P, I64, P]),
+    "ssd_add_rmsnorm_bf16": (I32, [P, I64, I64, I32, P, P, I64, I32, I32, P, F32, P, I64, P]),
     "ssd_forward": (I32, [C.POINTER(SsdModel), C.POINTER(SsdPlan), C.POINTER(SsdBuffers), C.POINTER(SsdRows), I32,
                           I32, I32, I32, I32, P]),
 }

@@ -112,19 +112,25 @@ class PackedBridge:
             self._native = st
         return self._native
 
-    def apply_(self, h: torch.Tensor, m: int, x: torch.Tensor, mids: list) -> None:
-        """h[:m] <- h + MLP(RMSNorm(h)) in place. x: [>=m, d] scratch; mids: two [>=m, hidden] scratches."""
-        ops.rmsnorm(h, m, self.norm, self.eps, x)
+    def body_(self, x: torch.Tensor, m: int, mids: list) -> tuple:
+        """MLP body over x[:m] (x = RMSNorm(h) already); returns (output, its width)."""
         if self.swiglu:
             ops.gemm_swiglu(x, m, self.gu, self.hidden, self.d, mids[0], self.bg, self.bu)
-            cur = mids[0]
-        else:
-            cur = x
-            for i, (w, b, n, k, act) in enumerate(self.body):
-                dst = mids[i % 2]
-                ops.gemm(cur, m, w, n, k, dst, bias=b, act=act)
-                cur = dst
-        ops.gemm(cur, m, self.out, self.d, self.hidden, h, bias=self.out_bias, residual=h)
+            return mids[0], self.hidden
+        cur, k = x, self.d
+        for i, (w, b, n, kin, act) in enumerate(self.body):
+            dst = mids[i % 2]
+            ops.gemm(cur, m, w, n, kin, dst, bias=b, act=act)
+            cur, k = dst, n
+        return cur, k
+
+    def apply_(self, h: torch.Tensor, m: int, x: torch.Tensor, mids: list, part: torch.Tensor, next_w: torch.Tensor,
+               next_eps: float) -> None:
+        """x[:m] = RMSNorm_bridge(h) on entry. h[:m] <- h + MLP(x) (out_proj as split-K partials, residual
+        add fused with the next RMSNorm), then x[:m] <- next RMSNorm(h): the kernel order of ssd_forward."""
+        cur, k = self.body_(x, m, mids)
+        s, ld = ops.gemm_partial(cur, m, self.out, self.d, k, part)
+        ops.add_rmsnorm(part, s, ld, h, m, next_w, next_eps, x, bias=self.out_bias)
 
 
 class TransitionBridge(nn.Module):

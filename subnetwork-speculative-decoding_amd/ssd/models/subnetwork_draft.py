@@ -159,6 +159,11 @@ class Workspace:
         self.mlp = torch.zeros(m_cap, s.inter, **bf)
         bh = max(bridge_hidden, 32)
         self.mids = [torch.zeros(m_cap, bh, **bf), torch.zeros(m_cap, bh, **bf)]
+        # split-K partials of the largest GEMM that writes them (q/k/v, o, down, bridge out_proj)
+        n_qkv = (s.heads + 2 * s.kv_heads) * s.head_dim
+        shapes = [(n_qkv, s.hidden), (s.hidden, s.heads * s.head_dim), (s.hidden, s.inter), (s.hidden, bh)]
+        self.part = torch.zeros(max(ops.partial_floats(m_cap, n, k) for n, k in shapes), dtype=torch.float32,
+                                device=dev)
         self.ws = torch.zeros(0, dtype=torch.float32, device=dev)
         self.logits = torch.zeros(0, **bf)
         self._native: dict = {}
@@ -191,7 +196,8 @@ class Workspace:
             st = _lib.SsdBuffers(self.h.data_ptr(), self.x.data_ptr(), self.q.data_ptr(), self.attn.data_ptr(),
                                  self.mlp.data_ptr(), self.mids[0].data_ptr(), self.mids[1].data_ptr(), self.m_cap,
                                  self.mids[0].shape[1], cache.k.data_ptr(), cache.vt.data_ptr(), cache.capacity,
-                                 aws.data_ptr(), aws.numel(), self.logits.data_ptr(), ld)
+                                 aws.data_ptr(), aws.numel(), self.logits.data_ptr(), ld, self.part.data_ptr(),
+                                 self.part.numel())
             self._native[key] = st
         return st, self.logits[: self.m_cap * ld].view(self.m_cap, ld)
 
@@ -306,35 +312,56 @@ class SubnetworkDraftModel(nn.Module):
                   int(p_min), int(l_max), head_first, head_rows, ops.stream())
         return logits[:head_rows, :n] if head_rows else None
 
+    def _norm_before(self, st: int):
+        """(weight, eps) of the RMSNorm applied to h before plan step st (st == #layers: the head)."""
+        s = self.model.shape
+        if st < len(self.layer_indices):
+            name = self._pre_layer_bridge[st]
+            if name is not None:
+                b = self._packed_bridge(name)
+                return b.norm, b.eps
+            return self.base.layers[st].ln1, s.eps
+        if self._pre_norm_bridge is not None:
+            b = self._packed_bridge(self._pre_norm_bridge)
+            return b.norm, b.eps
+        return self.model.norm, s.eps
+
     def run_rows(self, rows: Rows, m: int, p_min: int, l_max: int, cache: KVCache, ws: Workspace,
                  bridge_states: Optional[dict] = None, ids_ready: bool = True) -> torch.Tensor:
-        """All selected layers (+ bridges) for rows [0, m) already on the device. Returns the
-        residual stream h[:m] (before the final norm)."""
+        """The kernels of ssd_forward called one by one from Python, in the same order (used when
+        bridge states are requested). Leaves the residual stream in ws.h[:m] and the final-normed
+        rows in ws.x[:m]; returns ws.h."""
         if m > ws.m_cap:
             raise ValueError(f"{m} rows > workspace {ws.m_cap}")
         model, s = self.model, self.model.shape
         cos, sin = model.rope(cache.capacity)
         aws = ws.attn_ws(model, cache.capacity)
+        part = ws.part
+        n_qkv = (s.heads + 2 * s.kv_heads) * s.head_dim
         ops.embed(rows.ids, m, model.embed, ws.h)
+        w0, e0 = self._norm_before(0)
+        ops.add_rmsnorm(None, 0, 0, ws.h, m, w0, e0, ws.x)
         for slot, layer in enumerate(self.base.layers):
             li = self.layer_indices[slot]
             name = self._pre_layer_bridge[slot]
             if name is not None:
-                self._packed_bridge(name).apply_(ws.h, m, ws.x, ws.mids)
+                self._packed_bridge(name).apply_(ws.h, m, ws.x, ws.mids, part, layer.ln1, s.eps)
                 if bridge_states is not None:
                     bridge_states[name] = ws.h[:m].clone()
             kc, vt = cache.layer(li)
-            ops.rmsnorm(ws.h, m, layer.ln1, s.eps, ws.x)
-            ops.qkv_rope(ws.x, m, layer.wqkv, s.hidden, s.heads, s.kv_heads, s.head_dim, cos, sin, rows.pos,
-                         rows.slot, ws.q, kc, vt, cache.capacity)
+            sp, ld = ops.gemm_partial(ws.x, m, layer.wqkv, n_qkv, s.hidden, part)
+            ops.qkv_rope_finalize(part, sp, ld, m, s.heads, s.kv_heads, s.head_dim, cos, sin, rows.pos, rows.slot,
+                                  ws.q, kc, vt, cache.capacity)
             ops.tree_attention(ws.q, m, s.heads, s.kv_heads, s.head_dim, kc, vt, cache.capacity, rows.prefix,
                                rows.depth, rows.anc, p_min, l_max, aws, ws.attn)
-            ops.gemm(ws.attn, m, layer.wo, s.hidden, s.heads * s.head_dim, ws.h, residual=ws.h)
-            ops.rmsnorm(ws.h, m, layer.ln2, s.eps, ws.x)
+            sp, ld = ops.gemm_partial(ws.attn, m, layer.wo, s.hidden, s.heads * s.head_dim, part)
+            ops.add_rmsnorm(part, sp, ld, ws.h, m, layer.ln2, s.eps, ws.x)
             ops.gemm_swiglu(ws.x, m, layer.wgu, s.inter, s.hidden, ws.mlp)
-            ops.gemm(ws.mlp, m, layer.wd, s.hidden, s.inter, ws.h, residual=ws.h)
+            wn, en = self._norm_before(slot + 1)
+            sp, ld = ops.gemm_partial(ws.mlp, m, layer.wd, s.hidden, s.inter, part)
+            ops.add_rmsnorm(part, sp, ld, ws.h, m, wn, en, ws.x)
         if self._pre_norm_bridge is not None:
-            self._packed_bridge(self._pre_norm_bridge).apply_(ws.h, m, ws.x, ws.mids)
+            self._packed_bridge(self._pre_norm_bridge).apply_(ws.h, m, ws.x, ws.mids, part, model.norm, s.eps)
             if bridge_states is not None:
                 bridge_states[self._pre_norm_bridge] = ws.h[:m].clone()
         return ws.h
@@ -425,8 +452,8 @@ class SubnetworkDraftModel(nn.Module):
                 self.forward_rows(rows, m, p_min, l_max, cache, ws, head_rows=0)
                 hidden[c0:c1].copy_(ws.x[:m])
             else:
-                h = self.run_rows(rows, m, p_min, l_max, cache, ws, states)
-                self.final_norm(h, m, hidden[c0:c1])
+                self.run_rows(rows, m, p_min, l_max, cache, ws, states)
+                hidden[c0:c1].copy_(ws.x[:m])
             torch.cuda.current_stream().synchronize()  # the pinned staging buffer is reused next chunk
         cache.advance(q)
         logits = None

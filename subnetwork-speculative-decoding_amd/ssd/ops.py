@@ -187,3 +187,75 @@ def row_topk(logits, m, n, k, mode, vocab_ids, out_tok, out_val=None, out_lse=No
     ws = _topk_ws(logits.device, nbytes)
     _lib.call("ssd_row_topk_bf16", logits.data_ptr(), _rows(logits, "logits", n, m), m, n, k, mode, _p(vocab_ids),
               out_tok.data_ptr(), _p(out_val), _p(out_lse), ws.data_ptr(), ws.numel(), stream())
+
+
+# ------------------------------------------------------------------ split-K GEMMs
+def gemm_splits(n: int, k: int) -> int:
+    s = int(_lib.load().ssd_gemm_splits(n, k))
+    if s < 1:
+        raise ValueError(f"gemm_splits: bad shape N={n} K={k}")
+    return s
+
+
+def part_ld(n: int) -> int:
+    """Row stride of split-K partials for an N-column output."""
+    return (n + 63) // 64 * 64
+
+
+def partial_floats(m: int, n: int, k: int) -> int:
+    return gemm_splits(n, k) * m * part_ld(n)
+
+
+def gemm_partial(x, m, wp, n, k, part):
+    """part[s*m*ldp + r*ldp + c] = sum over the s-th K range of x[r] . W[c] (fp32); returns (S, ldp)."""
+    _check(x, "x"); _check(wp, "w_packed"); _check(part, "partials", torch.float32)
+    _len(wp, "w_packed", packed_elems(n, k))
+    s, ld = gemm_splits(n, k), part_ld(n)
+    _len(part, "partials", s * m * ld)
+    _lib.call("ssd_gemm_partial_bf16", x.data_ptr(), _rows(x, "x", k, m), m, wp.data_ptr(), n, k, part.data_ptr(), ld,
+              m * ld, stream())
+    return s, ld
+
+
+def gemm_finalize(part, s, ld, m, n, out, bias=None, act=None, residual=None):
+    _check(part, "partials", torch.float32); _check(out, "out")
+    if bias is not None:
+        _check(bias, "bias")
+    if residual is not None:
+        _check(residual, "residual")
+    _len(part, "partials", s * m * ld)
+    _lib.call("ssd_gemm_finalize_bf16", part.data_ptr(), ld, m * ld, s, m, n, out.data_ptr(), _rows(out, "out", n, m),
+              _p(bias), ACT[act], _p(residual), 0 if residual is None else _rows(residual, "residual", n, m), stream())
+    return out
+
+
+def qkv_rope_finalize(part, s, ld, m, heads, kv_heads, head_dim, cos, sin, pos, slot, q_out, k_cache, vt_cache, max_len):
+    _check(part, "partials", torch.float32); _check(q_out, "q"); _check(k_cache, "k_cache"); _check(vt_cache, "vt")
+    for t, nm in ((pos, "pos"), (slot, "slot")):
+        _check(t, nm, torch.int32)
+        _len(t, nm, m)
+    _len(part, "partials", s * m * ld)
+    if k_cache.numel() < kv_heads * max_len * head_dim or vt_cache.numel() < kv_heads * max_len * head_dim:
+        raise ValueError("qkv_rope_finalize: cache smaller than kv_heads * max_len * head_dim")
+    if cos.shape != sin.shape or cos.dim() != 2 or cos.shape[1] != head_dim // 2:
+        raise ValueError("qkv_rope_finalize: cos/sin must be [rows, head_dim/2]")
+    _lib.call("ssd_qkv_rope_finalize_bf16", part.data_ptr(), ld, m * ld, s, m, heads, kv_heads, head_dim,
+              cos.data_ptr(), sin.data_ptr(), cos.shape[0], pos.data_ptr(), slot.data_ptr(), q_out.data_ptr(),
+              _rows(q_out, "q", heads * head_dim, m), k_cache.data_ptr(), vt_cache.data_ptr(), max_len, stream())
+
+
+def add_rmsnorm(part, s, ld, h, m, w, eps, out, bias=None):
+    """h[:m] <- bf16(h + bf16(sum of the s partials + bias)) (s = 0: unchanged); out[:m] <- RMSNorm(h) * w."""
+    _check(h, "h")
+    d = h.shape[1]
+    if s:
+        _check(part, "partials", torch.float32)
+        _len(part, "partials", s * m * ld)
+    if bias is not None:
+        _check(bias, "bias")
+    if out is not None:
+        _check(out, "out"); _check(w, "w")
+    _lib.call("ssd_add_rmsnorm_bf16", part.data_ptr() if s else None, ld if s else 0, m * ld if s else 0, s, _p(bias),
+              h.data_ptr(), _rows(h, "h", d, m), m, d, None if out is None else w.data_ptr(), float(eps),
+              _p(out), 0 if out is None else _rows(out, "out", d, m), stream())
+    return out

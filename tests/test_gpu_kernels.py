@@ -127,6 +127,95 @@ def test_qkv_rope_and_cache_write(hd):
     assert kc[:, untouched].abs().sum() == 0 and vt[:, :, untouched].abs().sum() == 0
 
 
+# --------------------------------------------------------------- split-K GEMMs
+def _partial(ops, x, m, wp, n, k):
+    part = torch.zeros(ops.partial_floats(max(m, 1), n, k), dtype=torch.float32, device=DEV)
+    s, ld = ops.gemm_partial(x, m, wp, n, k, part)
+    return part, s, ld
+
+
+@pytest.mark.parametrize("m", [1, 7, 25, 64, 70])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (1024, 14336), (6144, 4096), (320, 512), (64, 64)])
+def test_gemm_partial_matches_oracle(m, n, k):
+    """Split-K partials summed and rounded by the finalize epilogue (bias + residual) vs the
+    oracle's bf16 linear chain; the split count is a function of (N, K)."""
+    ops = _ops()
+    x, w = bf(rand(m, k, seed=40)), bf(rand(n, k, std=0.02, seed=41))
+    b, r = bf(rand(n, std=0.1, seed=42)), bf(rand(m, n, seed=43))
+    wp = ops.pack_weight(w.to(DEV))
+    part, s, ld = _partial(ops, x.to(DEV), m, wp, n, k)
+    assert s == ops.gemm_splits(n, k) >= 1
+    y = torch.zeros(m, n, dtype=torch.bfloat16, device=DEV)
+    ops.gemm_finalize(part, s, ld, m, n, y)
+    close_bf16(y, ok.linear(x, w))
+    h = r.to(DEV).clone()
+    ops.gemm_finalize(part, s, ld, m, n, h, bias=b.to(DEV), residual=h)
+    close_bf16(h, ok.linear(x, w, b, residual=r))
+
+
+@pytest.mark.parametrize("n,k", [(4096, 4096), (6144, 4096), (4096, 14336)])
+def test_gemm_partial_batch_invariance_bitwise(n, k):
+    """Split-K partials of a row do not depend on how many rows share the call or where the row sits."""
+    ops = _ops()
+    x = bf(rand(64, k, seed=44)).to(DEV)
+    wp = ops.pack_weight(bf(rand(n, k, std=0.02, seed=45)).to(DEV))
+    full, s, ld = _partial(ops, x, 64, wp, n, k)
+    full = full[:s * 64 * ld].view(s, 64, ld)
+    for m in (1, 25, 33):
+        p, _, _ = _partial(ops, x, m, wp, n, k)
+        assert torch.equal(p[:s * m * ld].view(s, m, ld)[:, :, :n], full[:, :m, :n])
+    for r in (0, 17, 63):
+        p, _, _ = _partial(ops, x[r:r + 1].contiguous(), 1, wp, n, k)
+        assert torch.equal(p[:s * ld].view(s, 1, ld)[:, 0, :n], full[:, r, :n]), f"row {r}"
+
+
+def test_add_rmsnorm_fuses_residual_and_norm():
+    ops = _ops()
+    m, d, k = 9, 512, 1024
+    x, w = bf(rand(m, k, seed=46)), bf(rand(d, k, std=0.03, seed=47))
+    h0, g = bf(rand(m, d, seed=48)), bf(1 + rand(d, std=0.1, seed=49))
+    b = bf(rand(d, std=0.1, seed=50))
+    wp = ops.pack_weight(w.to(DEV))
+    part, s, ld = _partial(ops, x.to(DEV), m, wp, d, k)
+    h = h0.to(DEV).clone()
+    y = torch.zeros(m, d, dtype=torch.bfloat16, device=DEV)
+    ops.add_rmsnorm(part, s, ld, h, m, g.to(DEV), 1e-5, y, bias=b.to(DEV))
+    h_ref = ok.linear(x, w, b, residual=h0)
+    close_bf16(h, h_ref)
+    close_bf16(y, ok.rmsnorm(h.float().cpu(), g, 1e-5), frac=0.98)  # norm of the stored residual
+    h2 = h.clone()
+    ops.add_rmsnorm(None, 0, 0, h2, m, g.to(DEV), 1e-5, y)  # S = 0: plain RMSNorm, h untouched
+    assert torch.equal(h2, h)
+    close_bf16(y, ok.rmsnorm(h.float().cpu(), g, 1e-5), frac=0.98)
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_qkv_rope_finalize_matches_oracle(hd):
+    ops = _ops()
+    from ssd.models.llama import qkv_row_map, rope_tables
+
+    heads, kvh, d, m, max_len = 4, 2, 512, 6, 64
+    x = bf(rand(m, d, seed=51))
+    wq, wk, wv = (bf(rand(h * hd, d, std=0.05, seed=52 + i)) for i, h in enumerate((heads, kvh, kvh)))
+    n = (heads + 2 * kvh) * hd
+    wp = ops.pack_weight(torch.cat([wq, wk, wv]).to(DEV), qkv_row_map(heads, kvh, hd))
+    cos, sin = rope_tables(max_len, hd, 500000.0, DEV)
+    pos = torch.tensor([3, 3, 9, 40, 0, 63], dtype=torch.int32)
+    slot = torch.tensor([10, 11, 12, 13, 20, 63], dtype=torch.int32)
+    q = torch.zeros(m, heads * hd, dtype=torch.bfloat16, device=DEV)
+    kc = torch.zeros(kvh, max_len, hd, dtype=torch.bfloat16, device=DEV)
+    vt = torch.zeros(kvh, hd, max_len, dtype=torch.bfloat16, device=DEV)
+    part, s, ld = _partial(ops, x.to(DEV), m, wp, n, d)
+    ops.qkv_rope_finalize(part, s, ld, m, heads, kvh, hd, cos, sin, pos.to(DEV), slot.to(DEV), q, kc, vt, max_len)
+    rq, rk, rv = ok.qkv_rope(x, wq, wk, wv, heads, kvh, hd, pos.long(), 500000.0)
+    close_bf16(q.view(m, heads, hd), rq, frac=0.95)
+    close_bf16(kc[:, slot.long()].transpose(0, 1), rk, frac=0.95)
+    close_bf16(vt[:, :, slot.long()].permute(2, 0, 1), rv, frac=0.97)
+    untouched = torch.ones(max_len, dtype=torch.bool)
+    untouched[slot.long()] = False
+    assert kc[:, untouched].abs().sum() == 0 and vt[:, :, untouched].abs().sum() == 0
+
+
 # ----------------------------------------------------------------------- rows
 def test_rmsnorm_and_embed():
     ops = _ops()
