@@ -45,86 +45,119 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def time_launches(fn, reps: int) -> float:
-    """Average duration (ms) of ``fn``'s launches, HIP events on the current stream."""
+def time_launches(fn, n: int, reps: int = 3) -> float:
+    """Average duration (ms) of one launch of fn(i), i = 0..n-1: the n launches are captured once in
+    a HIP graph and replayed between two HIP events on the launching stream (no host time between
+    kernels), best of reps. Callers pass a different layer's weights per i, so every launch
+    streams its weights from HBM as in a decode round (a repeat of one layer would be served from
+    the 256 MB Infinity Cache)."""
     import torch
 
-    fn()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        for i in range(n):  # warm up outside the capture
+            fn(i)
     torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-    for a, b in evs:
-        a.record()
-        fn()
-        b.record()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        for i in range(n):
+            fn(i)
+    best = float("inf")
+    with torch.cuda.stream(st):
+        g.replay()
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(st)
+            g.replay()
+            b.record(st)
+            b.synchronize()
+            best = min(best, a.elapsed_time(b) / n)
     torch.cuda.synchronize()
-    return sum(a.elapsed_time(b) for a, b in evs) / reps
+    return best
 
 
-def kernel_figures(gen, sess, reps: int) -> dict:
-    """Live per-kernel timings at the verify shape of the last timed round."""
+def kernel_figures(gen, sess) -> dict:
+    """Live per-kernel timings at the verify shape of the last timed round (M = verify rows,
+    context = the committed length), each kernel launched once per layer like in the round."""
     import torch
 
     from ssd import ops
 
     target, cache, ws = gen.target, sess.cache, sess.ws
-    s = target.model.shape
+    model = target.model
+    s = model.shape
+    L = model.layers
+    nl = s.layers
     m = gen.drafter.max_verify_nodes() + 1
     committed = cache.get_seq_length()
-    L0 = target.model.layers[0]
-    kc, vt = cache.layer(0)
-    aws = ws.attn_ws(target.model, cache.capacity)
+    aws = ws.attn_ws(model, cache.capacity)
     p = committed + 1
     rows = sess.verify_rows
     gen.drafter.finalize_device(sess.tree, committed, sess.root_rows, rows)
+    part = ws.part
     out = {}
 
-    def attn():
+    def fig(name, t, b, **kw):
+        out[name] = dict(ms=t, bytes=b, gbs=b / t / 1e6, frac=b / t / 1e6 / HBM_PEAK_GBS, rows=m, **kw)
+
+    def attn(i):
+        kc, vt = cache.layer(i)
         ops.tree_attention(ws.q, m, s.heads, s.kv_heads, s.head_dim, kc, vt, cache.capacity, rows.prefix, rows.depth,
                            rows.anc, p, p + gen.cfg.depth, aws, ws.attn)
 
-    t = time_launches(attn, reps)
     kv_bytes = 2 * s.kv_heads * (p + m) * s.head_dim * 2
-    qo_bytes = 2 * m * s.heads * s.head_dim * 2
-    b = kv_bytes + qo_bytes + m * 32 * 4
-    out["tree_attention"] = dict(ms=t, bytes=b, gbs=b / t / 1e6, frac=b / t / 1e6 / HBM_PEAK_GBS, rows=m,
-                                 context=p)
+    fig("tree_attention", time_launches(attn, nl), kv_bytes + 2 * m * s.heads * s.head_dim * 2 + m * 32 * 4,
+        context=p)
+    n_qkv = (s.heads + 2 * s.kv_heads) * s.head_dim
 
-    def gateup():
-        ops.gemm_swiglu(ws.x, m, L0.wgu, s.inter, s.hidden, ws.mlp)
+    def qkv(i):
+        ops.gemm_partial(ws.x, m, L[i].wqkv, n_qkv, s.hidden, part)
 
-    t = time_launches(gateup, reps)
-    b = 2 * s.inter * s.hidden * 2 + m * s.hidden * 2 + m * s.inter * 2
-    out["gemm_gate_up"] = dict(ms=t, bytes=b, gbs=b / t / 1e6, frac=b / t / 1e6 / HBM_PEAK_GBS, rows=m,
-                               flops=2 * m * 2 * s.inter * s.hidden)
+    sp = ops.gemm_splits(n_qkv, s.hidden)
+    fig("gemm_qkv_partial", time_launches(qkv, nl),
+        n_qkv * s.hidden * 2 + m * s.hidden * 2 + sp * m * n_qkv * 4, splits=sp)
 
-    def down():
-        ops.gemm(ws.mlp, m, L0.wd, s.hidden, s.inter, ws.h, residual=ws.h)
+    def gateup(i):
+        ops.gemm_swiglu(ws.x, m, L[i].wgu, s.inter, s.hidden, ws.mlp)
 
-    t = time_launches(down, reps)
-    b = s.hidden * s.inter * 2 + m * (s.hidden + s.inter) * 2 + m * s.hidden * 2
-    out["gemm_down"] = dict(ms=t, bytes=b, gbs=b / t / 1e6, frac=b / t / 1e6 / HBM_PEAK_GBS, rows=m)
+    fig("gemm_gate_up", time_launches(gateup, nl), 2 * s.inter * s.hidden * 2 + m * s.hidden * 2 + m * s.inter * 2,
+        flops=2 * m * 2 * s.inter * s.hidden)
 
+    def down(i):
+        ops.gemm_partial(ws.mlp, m, L[i].wd, s.hidden, s.inter, part)
+
+    sp = ops.gemm_splits(s.hidden, s.inter)
+    fig("gemm_down_partial", time_launches(down, nl),
+        s.hidden * s.inter * 2 + m * s.inter * 2 + sp * m * s.hidden * 4, splits=sp)
     logits = ws.logits_buf(m, s.vocab)
 
-    def head():
-        ops.gemm(ws.x, m, target.model.lm_head, s.vocab, s.hidden, logits)
+    def head(i):
+        ops.gemm(ws.x, m, model.lm_head, s.vocab, s.hidden, logits)
 
-    t = time_launches(head, reps)
-    b = s.vocab * s.hidden * 2 + m * s.hidden * 2 + m * s.vocab * 2
-    out["lm_head"] = dict(ms=t, bytes=b, gbs=b / t / 1e6, frac=b / t / 1e6 / HBM_PEAK_GBS, rows=m)
-
+    fig("lm_head", time_launches(head, 4), s.vocab * s.hidden * 2 + m * s.hidden * 2 + m * s.vocab * 2)
     n = gen.cfg.depth + 1
-    src = torch.arange(committed, committed + n, dtype=torch.int32, device=kc.device) + torch.tensor(
-        [0] + [1] * (n - 1), dtype=torch.int32, device=kc.device)
-    nd = torch.tensor([n], dtype=torch.int32, device=kc.device)
+    src = torch.arange(committed, committed + n, dtype=torch.int32, device=model.device) + torch.tensor(
+        [0] + [1] * (n - 1), dtype=torch.int32, device=model.device)
+    nd = torch.tensor([n], dtype=torch.int32, device=model.device)
 
-    def compact():
+    def compact(i):
         cache.compact_device(committed, src, nd, n)
 
-    t = time_launches(compact, reps)
-    b = 2 * n * s.layers * 2 * s.kv_heads * s.head_dim * 2
-    out["kv_compact"] = dict(ms=t, bytes=b, gbs=b / t / 1e6, frac=b / t / 1e6 / HBM_PEAK_GBS, rows=n)
+    fig("kv_compact", time_launches(compact, 8), 2 * n * s.layers * 2 * s.kv_heads * s.head_dim * 2)
+    out["kv_compact"]["rows"] = n
     return out
+
+
+def load_traffic(kernel_key: str):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary
+    (profiles/*_traffic.json: FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the same counters'
+    reading for a plain copy of known size), or None if absent."""
+    path = os.path.join(REPO, "profiles", f"{kernel_key}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("traffic_bytes")
 
 
 def cpu_baseline(model, layers: list, dcfg: dict, rounds: int, prompt_len: int) -> dict:
@@ -185,8 +218,9 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-rounds", type=int, default=4)
     ap.add_argument("--cpu-prompt", type=int, default=128)
-    ap.add_argument("--kernel-reps", type=int, default=30)
     ap.add_argument("--ar-tokens", type=int, default=128)
+    ap.add_argument("--copy-probe-mb", type=int, default=0,
+                    help="also run one plain device copy of this many MiB (calibrates rocprofv3 byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on exactly one GPU (got --gpus {args.gpus}); multi-GPU is not part of it",
@@ -238,7 +272,7 @@ def main() -> None:
     phases = {k: 1000 * v / args.steps for k, v in sess.phases.totals.items()}
     log(f"{args.steps} rounds: {toks} tokens in {secs:.3f}s ({toks / secs:.1f} tok/s, {1000 * secs / args.steps:.3f} "
         f"ms/round), phases {phases}")
-    kf = kernel_figures(gen, sess, args.kernel_reps)
+    kf = kernel_figures(gen, sess)
     log(f"kernels: { {k: (round(v['ms'] * 1000, 1), round(v['gbs'])) for k, v in kf.items()} } (us, GB/s)")
     del sess
     torch.cuda.empty_cache()
@@ -272,10 +306,17 @@ def main() -> None:
         "round_hbm_lower_bound_ms": round(bytes_round / HBM_PEAK_GBS / 1e6, 4),
         "roofline": {"bound": "hbm", "kernel": "gemm_swiglu (verify gate/up, M=%d)" % g["rows"],
                      "achieved": round(g["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(g["frac"], 4), "traffic": None},
+                     "frac": round(g["frac"], 4), "traffic": load_traffic("gemm_gate_up_llama3_8b_verify")},
         "kernels": {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in kf.items()},
     }
+    if args.copy_probe_mb:
+        src = torch.ones(args.copy_probe_mb << 20, dtype=torch.uint8, device=model.device)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy probe: {args.copy_probe_mb} MiB read + {args.copy_probe_mb} MiB written")
+        del src, dst
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(model, layers, dkw, args.cpu_rounds, args.cpu_prompt)
     print(json.dumps(line), flush=True)
