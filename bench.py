@@ -110,13 +110,14 @@ def kernel_figures(gen, sess) -> dict:
     fig("tree_attention", time_launches(attn, nl), kv_bytes + 2 * m * s.heads * s.head_dim * 2 + m * 32 * 4,
         context=p)
     n_qkv = (s.heads + 2 * s.kv_heads) * s.head_dim
+    cos, sin = model.rope(cache.capacity)
 
     def qkv(i):
-        ops.gemm_partial(ws.x, m, L[i].wqkv, n_qkv, s.hidden, part)
+        kc, vt = cache.layer(i)
+        ops.qkv_rope(ws.x, m, L[i].wqkv, s.hidden, s.heads, s.kv_heads, s.head_dim, cos, sin, rows.pos, rows.slot,
+                     ws.q, kc, vt, cache.capacity)
 
-    sp = ops.gemm_splits(n_qkv, s.hidden)
-    fig("gemm_qkv_partial", time_launches(qkv, nl),
-        n_qkv * s.hidden * 2 + m * s.hidden * 2 + sp * m * n_qkv * 4, splits=sp)
+    fig("gemm_qkv_rope", time_launches(qkv, nl), n_qkv * s.hidden * 2 + m * s.hidden * 2 + m * n_qkv * 2)
 
     def gateup(i):
         ops.gemm_swiglu(ws.x, m, L[i].wgu, s.inter, s.hidden, ws.mlp)

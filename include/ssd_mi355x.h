@@ -34,13 +34,18 @@ int ssd_device_arch(char* buf, int len); /* host buffer; gcnArchName of the curr
 /* ------------------------------------------------------------ weight format
  * Packs a row-major bf16 matrix W[N_src, K] (row stride ld) into MFMA tiles: tile (nb, kb) =
  * rows row_map[16nb .. 16nb+16) x k [32kb, 32kb+32), 64 lanes x 8 bf16. N_packed is a multiple
- * of 64 (ssd_packed_weight_elems pads rows to 64 and K to 32). row_map[N_packed]
+ * of 128 (ssd_packed_weight_elems pads rows to 128 and K to 32). row_map[N_packed]
  * (device int32) names the source row of each packed row (-1 = zero row); it fuses q/k/v,
- * interleaves gate/up and pairs rotary dims. Replaces holding nn.Linear weights as-is
- * (ssd/models/subnetwork_draft.py:80-89 references HF modules). */
+ * interleaves gate/up and pairs rotary dims. Tiles are stored in groups of `group` row tiles
+ * per k-block ([nb / group][kb][nb % group]) so that a workgroup streams one contiguous region:
+ * weights for ssd_gemm_bf16 / ssd_gemm_swiglu_bf16 / ssd_gemm_qkv_rope_bf16 use
+ * group = ssd_gemm_weight_group(N, K); weights for ssd_gemm_partial_bf16 use group = 1.
+ * Replaces holding nn.Linear weights as-is (ssd/models/subnetwork_draft.py:80-89 references HF
+ * modules). */
 int64_t ssd_packed_weight_elems(int N, int K);
+int ssd_gemm_weight_group(int N, int K); /* 1, 2, 4 or 8; 0 on a bad shape */
 int ssd_pack_weight_bf16(const uint16_t* src, int64_t ld, int N_src, int K, const int32_t* row_map, int N_packed,
-                         uint16_t* dst, hipStream_t stream);
+                         int group, uint16_t* dst, hipStream_t stream);
 
 /* ---------------------------------------------------------------- GEMMs
  * Y = act(X W^T + bias) [+ residual] with bf16 rounding after each step; Y may alias residual.
@@ -68,7 +73,8 @@ int ssd_gemm_qkv_rope_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t
                            uint16_t* k_cache, uint16_t* vt_cache, int64_t max_len, hipStream_t stream);
 
 /* ---------------------------------------------------------- split-K GEMMs
- * For narrow outputs (o_proj, down_proj, q/k/v, bridge out_proj) K is split over workgroups:
+ * For narrow outputs (o_proj, down_proj, q/k/v, bridge out_proj) K is split over workgroups
+ * (weights packed with group 1):
  * P[s][m][n] = sum over the s-th K range of X W^T in fp32, s < ssd_gemm_splits(N, K) (a function
  * of the shape only, so results stay batch-invariant). P: 16-byte aligned fp32, row stride
  * ldp >= N rounded up to 64 (multiple of 4), split stride >= M * ldp. A consumer sums the S

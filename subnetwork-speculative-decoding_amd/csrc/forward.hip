@@ -5,7 +5,7 @@
 // Order per selected layer (ssd/models/subnetwork_draft.py:193-246 and :315-351 in the
 // reference), with each residual add fused with the RMSNorm that follows it:
 //   [bridge: body GEMMs -> out_proj partials -> h += out, x = ln1(h)]
-//   q/k/v partials -> RoPE + KV write -> tree attention (+ combine)
+//   q/k/v GEMM with RoPE + KV write in its epilogue -> tree attention (+ combine)
 //   -> o partials -> h += o, x = ln2(h) -> gate/up GEMM + SwiGLU
 //   -> down partials -> h += down, x = <next norm>(h)
 // where <next norm> is the next bridge's norm, the next layer's ln1, the pre-norm bridge's norm
@@ -107,7 +107,6 @@ SSD_API int ssd_forward(const SsdModel* md, const SsdPlan* plan, const SsdBuffer
       return set_error(SSD_EINVAL, "forward: layer %d", plan->layer_ids[st]);
   const int d = md->hidden, hd = md->head_dim, H = md->heads, KV = md->kv_heads;
   const int64_t qdim = (int64_t)H * hd;
-  const int n_qkv = (H + 2 * KV) * hd;
   const size_t layer_elems = (size_t)KV * buf->cache_cap * hd;
   Fwd f{md, buf, m, d, s};
   int rc = ssd_embed_bf16(rows->ids, m, md->embed, md->vocab, d, buf->h, d, s);
@@ -125,11 +124,8 @@ SSD_API int ssd_forward(const SsdModel* md, const SsdPlan* plan, const SsdBuffer
       return rc;
     uint16_t* kc = buf->k_arena + li * layer_elems;
     uint16_t* vt = buf->vt_arena + li * layer_elems;
-    int64_t ldp;
-    const int S = f.partials(buf->x, d, L.wqkv, n_qkv, d, &ldp);
-    if (S < 0) return -S;
-    if ((rc = ssd_qkv_rope_finalize_bf16(buf->part, ldp, (int64_t)m * ldp, S, m, H, KV, hd, md->cos, md->sin,
-                                         md->rope_rows, rows->pos, rows->slot, buf->q, qdim, kc, vt, buf->cache_cap, s)))
+    if ((rc = ssd_gemm_qkv_rope_bf16(buf->x, d, m, L.wqkv, d, H, KV, hd, md->cos, md->sin, md->rope_rows, rows->pos,
+                                     rows->slot, buf->q, qdim, kc, vt, buf->cache_cap, s)))
       return rc;
     if ((rc = ssd_tree_attention_bf16(buf->q, qdim, m, H, KV, hd, kc, vt, buf->cache_cap, rows->prefix, rows->depth,
                                       rows->anc, p_min, l_max, md->attn_scale, buf->attn_ws, buf->attn_ws_floats,

@@ -62,7 +62,6 @@ struct GemmArgs {
   int64_t max_len;
 };
 
-constexpr int GEMM_UNROLL = 4;
 
 // Per-element epilogues (fp32 dot products in, bf16 rounding points of the reference out).
 // Plain store: output column n of row m.
@@ -151,7 +150,7 @@ struct GemmLds {
   float4 red[KS][NSUB][CT][64];
 };
 
-template <int CT, int NSUB, int KS, int EPI>
+template <int CT, int NSUB, int KS, int U, int EPI>
 __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
@@ -167,43 +166,46 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int c = 0; c < CT; ++c) acc[s][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  const uint4* wp[NSUB];
+  const u32x4_t* wp[NSUB];
 #pragma unroll
-  for (int s = 0; s < NSUB; ++s) wp[s] = a.W + ((size_t)(tile * NSUB + s) * kbt) * 64 + lane;
+  for (int s = 0; s < NSUB; ++s) wp[s] = (const u32x4_t*)a.W + (size_t)tile * kbt * NSUB * 64 + s * 64 + lane;  // grouped layout
   // Rows past M load row M-1 (always valid, no per-lane branch); their columns are never stored.
   const bf16_t* xp[CT];
 #pragma unroll
   for (int c = 0; c < CT; ++c) xp[c] = a.X + (size_t)min(c * 16 + j, a.M - 1) * a.ldx + g * 8;
 
   int kb = kb_lo;
-  for (; kb + GEMM_UNROLL - 1 < kb_hi; kb += GEMM_UNROLL) {
-    uint4 wr[GEMM_UNROLL][NSUB], xr[GEMM_UNROLL][CT];
+  for (; kb + U - 1 < kb_hi; kb += U) {
+    u32x4_t wr[U][NSUB], xr[U][CT];
 #pragma unroll
-    for (int u = 0; u < GEMM_UNROLL; ++u)
+    for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int s = 0; s < NSUB; ++s) wr[u][s] = ld_stream(wp[s] + (size_t)(kb + u) * 64);
+      for (int s = 0; s < NSUB; ++s) wr[u][s] = __builtin_nontemporal_load(wp[s] + (size_t)(kb + u) * NSUB * 64);
 #pragma unroll
-    for (int u = 0; u < GEMM_UNROLL; ++u)
+    for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int c = 0; c < CT; ++c)
-        xr[u][c] = *(const uint4*)(xp[c] + (kb + u) * 32);
+        xr[u][c] = *(const u32x4_t*)(xp[c] + (kb + u) * 32);
+    // Keep every load of the trip ahead of its MFMAs: left alone, the scheduler sinks the later
+    // k-blocks' loads below the first MFMAs to save registers, leaving one k-block in flight.
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 0; u < GEMM_UNROLL; ++u)
+    for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int s = 0; s < NSUB; ++s)
 #pragma unroll
-        for (int c = 0; c < CT; ++c) acc[s][c] = mfma16x16x32(as_bf16x8(wr[u][s]), as_bf16x8(xr[u][c]), acc[s][c]);
+        for (int c = 0; c < CT; ++c) acc[s][c] = mfma16x16x32(bits_bf16x8(wr[u][s]), bits_bf16x8(xr[u][c]), acc[s][c]);
   }
   for (; kb < kb_hi; ++kb) {
-    uint4 wr[NSUB], xr[CT];
+    u32x4_t wr[NSUB], xr[CT];
 #pragma unroll
-    for (int s = 0; s < NSUB; ++s) wr[s] = ld_stream(wp[s] + (size_t)kb * 64);
+    for (int s = 0; s < NSUB; ++s) wr[s] = __builtin_nontemporal_load(wp[s] + (size_t)kb * NSUB * 64);
 #pragma unroll
-    for (int c = 0; c < CT; ++c) xr[c] = *(const uint4*)(xp[c] + kb * 32);
+    for (int c = 0; c < CT; ++c) xr[c] = *(const u32x4_t*)(xp[c] + kb * 32);
 #pragma unroll
     for (int s = 0; s < NSUB; ++s)
 #pragma unroll
-      for (int c = 0; c < CT; ++c) acc[s][c] = mfma16x16x32(as_bf16x8(wr[s]), as_bf16x8(xr[c]), acc[s][c]);
+      for (int c = 0; c < CT; ++c) acc[s][c] = mfma16x16x32(bits_bf16x8(wr[s]), bits_bf16x8(xr[c]), acc[s][c]);
   }
 
   __shared__ GemmLds<KS, NSUB, CT> lds;
@@ -429,9 +431,11 @@ static int launch_part(const GemmArgs& a, float* P, int64_t ldp, int64_t sstride
 
 // ---------------------------------------------------------------- packing
 // dst tile (nb, kb), lane l, element t  <-  W[row_map[16 nb + l%16]][32 kb + 8 (l/16) + t]
-// (row_map entry < 0 or beyond K -> zero).
+// (row_map entry < 0 or beyond K -> zero). Tiles are stored grouped: the `group` tiles
+// nb = g*group .. g*group+group-1 of one k-block sit next to each other ([g][kb][nb % group]), so
+// a workgroup that owns a group streams one contiguous region.
 __global__ void pack_kernel(const bf16_t* __restrict__ src, int64_t ld, int K, const int* __restrict__ row_map,
-                            int n_tiles_n, int kb_total, uint4* __restrict__ dst) {
+                            int n_tiles_n, int kb_total, int group, uint4* __restrict__ dst) {
   const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (tile >= (int64_t)n_tiles_n * kb_total) return;
@@ -441,7 +445,8 @@ __global__ void pack_kernel(const bf16_t* __restrict__ src, int64_t ld, int K, c
   Pack8 p;
 #pragma unroll
   for (int t = 0; t < 8; ++t) p.h[t] = (row >= 0 && k0 + t < K) ? src[(size_t)row * ld + k0 + t] : (bf16_t)0;
-  dst[tile * 64 + lane] = p.u;
+  const int64_t dst_tile = ((int64_t)(nb / group) * kb_total + kb) * group + nb % group;
+  dst[dst_tile * 64 + lane] = p.u;
 }
 
 struct GemmPlan {
@@ -449,18 +454,25 @@ struct GemmPlan {
 };
 
 // Launch geometry as a function of (N, K) only (never of M): that is what keeps every row's
-// arithmetic identical for any batch size.
+// arithmetic identical for any batch size (a row's sum runs over the k-blocks of each of the ks
+// waves in order, then over the waves in order; the tile grouping nsub does not enter it). The
+// per-trip unroll U may follow M: it does not change the order. Measured on MI355X with every
+// launch streaming its weights from HBM: vocabulary-wide heads stream best as 8 tiles x 2 waves,
+// gate/up-wide outputs as 4 tiles x 2 waves, q/k/v-wide outputs as 2 tiles x 8 waves, narrow
+// outputs as 1 tile x 16 waves.
 static GemmPlan plan_for(int N, int K) {
   const int kbt = K / 32;
   GemmPlan p;
-  if (N >= 16384) {
-    p.nsub = 4; p.ks = 4;
-  } else if (N >= 8192) {
+  if (N >= 65536) {
+    p.nsub = 8; p.ks = 2;
+  } else if (N >= 16384) {
+    p.nsub = 4; p.ks = 2;
+  } else if (N >= 6144) {
     p.nsub = 2; p.ks = 8;
   } else {
     p.nsub = 1; p.ks = 16;
   }
-  while (p.ks > 1 && kbt / p.ks < GEMM_UNROLL) p.ks >>= 1;  // keep whole unrolled trips per wave
+  while (p.ks > 1 && kbt / p.ks < 4) p.ks >>= 1;  // at least 4 k-blocks per wave
   p.tiles = (N + 16 * p.nsub - 1) / (16 * p.nsub);
   return p;
 }
@@ -480,13 +492,14 @@ static int launch_gemm(GemmArgs a, hipStream_t s) {
     const int ct = (b.M + 15) / 16;
     dim3 grid(p.tiles);
 #define SSD_GEMM_CASE(CT_, NS_, KS_) \
-  if (ct == CT_ && p.nsub == NS_ && p.ks == KS_) {                                                   \
-    hipLaunchKernelGGL((gemm_kernel<CT_, NS_, KS_, EPI>), grid, dim3(64 * KS_), 0, s, b);           \
+  if (ct == CT_ && p.nsub == NS_ && p.ks == KS_) {                                                            \
+    hipLaunchKernelGGL((gemm_kernel<CT_, NS_, KS_, (CT_ == 1 ? 4 : 2), EPI>), grid, dim3(64 * KS_), 0, s, b);   \
   }
-#define SSD_GEMM_PLANS(CT_)                                                                             \
-  SSD_GEMM_CASE(CT_, 4, 4) SSD_GEMM_CASE(CT_, 4, 2) SSD_GEMM_CASE(CT_, 4, 1) SSD_GEMM_CASE(CT_, 2, 8) \
-  SSD_GEMM_CASE(CT_, 2, 4) SSD_GEMM_CASE(CT_, 2, 2) SSD_GEMM_CASE(CT_, 2, 1) SSD_GEMM_CASE(CT_, 1, 16) \
-  SSD_GEMM_CASE(CT_, 1, 8) SSD_GEMM_CASE(CT_, 1, 4) SSD_GEMM_CASE(CT_, 1, 2) SSD_GEMM_CASE(CT_, 1, 1)
+#define SSD_GEMM_PLANS(CT_)                                                                                \
+  SSD_GEMM_CASE(CT_, 8, 2) SSD_GEMM_CASE(CT_, 8, 1) SSD_GEMM_CASE(CT_, 4, 2) SSD_GEMM_CASE(CT_, 4, 1)     \
+  SSD_GEMM_CASE(CT_, 2, 8) SSD_GEMM_CASE(CT_, 2, 4) SSD_GEMM_CASE(CT_, 2, 2) SSD_GEMM_CASE(CT_, 2, 1)     \
+  SSD_GEMM_CASE(CT_, 1, 16) SSD_GEMM_CASE(CT_, 1, 8) SSD_GEMM_CASE(CT_, 1, 4) SSD_GEMM_CASE(CT_, 1, 2)    \
+  SSD_GEMM_CASE(CT_, 1, 1)
     SSD_GEMM_PLANS(1) SSD_GEMM_PLANS(2) SSD_GEMM_PLANS(3) SSD_GEMM_PLANS(4)
 #undef SSD_GEMM_PLANS
 #undef SSD_GEMM_CASE
@@ -510,19 +523,29 @@ static int check_common(const bf16_t* X, int64_t ldx, int M, const void* W, int 
 using namespace ssd;
 
 SSD_API int64_t ssd_packed_weight_elems(int N, int K) {
-  return (int64_t)((N + 63) / 64) * 64 * (int64_t)((K + 31) / 32) * 32;
+  return (int64_t)((N + 127) / 128) * 128 * (int64_t)((K + 31) / 32) * 32;
+}
+
+SSD_API int ssd_gemm_weight_group(int N, int K) {
+  if (N <= 0 || K <= 0 || K % 32) {
+    set_error(SSD_EINVAL, "weight_group: bad shape N=%d K=%d", N, K);
+    return 0;
+  }
+  return plan_for(N, K).nsub;
 }
 
 
 SSD_API int ssd_pack_weight_bf16(const uint16_t* src, int64_t ld, int N_src, int K, const int32_t* row_map,
-                                 int N_packed, uint16_t* dst, hipStream_t stream) {
+                                 int N_packed, int group, uint16_t* dst, hipStream_t stream) {
   if (!src || !dst || !row_map) return set_error(SSD_EINVAL, "pack: null pointer");
-  if (N_packed <= 0 || N_packed % 64 || K <= 0 || N_src <= 0)
-    return set_error(SSD_EINVAL, "pack: N_packed=%d must be a positive multiple of 64 (K=%d)", N_packed, K);
+  if (N_packed <= 0 || N_packed % 128 || K <= 0 || N_src <= 0)
+    return set_error(SSD_EINVAL, "pack: N_packed=%d must be a positive multiple of 128 (K=%d)", N_packed, K);
+  if (group != 1 && group != 2 && group != 4 && group != 8)
+    return set_error(SSD_EINVAL, "pack: group %d not in {1, 2, 4, 8}", group);
   const int n_tiles_n = N_packed / 16, kb_total = (K + 31) / 32;
   const int64_t tiles = (int64_t)n_tiles_n * kb_total;
   hipLaunchKernelGGL(pack_kernel, dim3((unsigned)((tiles + 3) / 4)), dim3(256), 0, stream, src, ld, K, row_map,
-                     n_tiles_n, kb_total, (uint4*)dst);
+                     n_tiles_n, kb_total, group, (uint4*)dst);
   return check_launch("pack");
 }
 

@@ -60,7 +60,8 @@ _PROTOS = {
     "ssd_abi_version": (I32, []),
     "ssd_device_arch": (I32, [C.c_char_p, I32]),
     "ssd_packed_weight_elems": (I64, [I32, I32]),
-    "ssd_pack_weight_bf16": (I32, [P, I64, I32, I32, P, I32, P, P]),
+    "ssd_gemm_weight_group": (I32, [I32, I32]),
+    "ssd_pack_weight_bf16": (I32, [P, I64, I32, I32, P, I32, I32, P, P]),
     "ssd_gemm_bf16": (I32, [P, I64, I32, P, I32, I32, P, I64, P, I32, P, I64, P]),
     "ssd_gemm_swiglu_bf16": (I32, [P, I64, I32, P, I32, I32, P, I64, P, P, P]),
     "ssd_gemm_qkv_rope_bf16": (I32, [P, I64, I32, P, I32, I32, I32, I32, P, P, I64, P, P, P, I64, P, P, I64, P]),

@@ -91,7 +91,7 @@ class PackedBridge:
                 self.body.append((ops.pack_weight(bf(lin.weight)), bf(lin.bias), lin.out_features,
                                   lin.in_features, name))
         out = bridge.mlp.out_proj
-        self.out = ops.pack_weight(bf(out.weight))
+        self.out = ops.pack_weight(bf(out.weight), split=True)
         self.out_bias = bf(out.bias)
         self._native: Optional[_lib.SsdBridgeW] = None
 

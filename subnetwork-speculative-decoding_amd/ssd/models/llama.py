@@ -137,11 +137,11 @@ class MI355XLlama:
                          self._put(get("self_attn.v_proj.weight"))], 0)
         L.wqkv = ops.pack_weight(qkv, qkv_row_map(s.heads, s.kv_heads, s.head_dim))
         del qkv
-        L.wo = ops.pack_weight(self._put(get("self_attn.o_proj.weight")))
+        L.wo = ops.pack_weight(self._put(get("self_attn.o_proj.weight")), split=True)
         gu = torch.cat([self._put(get("mlp.gate_proj.weight")), self._put(get("mlp.up_proj.weight"))], 0)
         L.wgu = ops.pack_weight(gu, gate_up_row_map(s.inter))
         del gu
-        L.wd = ops.pack_weight(self._put(get("mlp.down_proj.weight")))
+        L.wd = ops.pack_weight(self._put(get("mlp.down_proj.weight")), split=True)
         L.ln1 = self._put(get("input_layernorm.weight"))
         L.ln2 = self._put(get("post_attention_layernorm.weight"))
         self.layers.append(L)
@@ -236,13 +236,15 @@ class MI355XLlama:
         packed tiles when the row-major copy was not kept."""
         if self._lm_head_rows is not None:
             return self._lm_head_rows.index_select(0, ids.to(self.device))
-        return unpack_rows(self.lm_head, self.shape.vocab, self.shape.hidden, ids.to(self.device))
+        return unpack_rows(self.lm_head, self.shape.vocab, self.shape.hidden, ids.to(self.device),
+                           ops.weight_group(self.shape.vocab, self.shape.hidden))
 
 
-def unpack_rows(packed: torch.Tensor, n: int, k: int, ids: torch.Tensor) -> torch.Tensor:
-    """Rows ``ids`` of the row-major matrix held in MFMA tiles (inverse of the identity packing)."""
+def unpack_rows(packed: torch.Tensor, n: int, k: int, ids: torch.Tensor, group: int = 1) -> torch.Tensor:
+    """Rows ``ids`` of the row-major matrix held in MFMA tiles (inverse of the identity packing
+    with tiles grouped by ``group`` per k-block)."""
     kb = (k + 31) // 32
-    t = packed.view(-1, kb, 4, 16, 8)  # [nb, kb, lane/16, lane%16, 8]
+    t = packed.view(-1, kb, group, 4, 16, 8)  # [nb // group, kb, nb % group, lane/16, lane%16, 8]
     nb, r = ids // 16, ids % 16
-    rows = t[nb.long(), :, :, r.long(), :]  # [len, kb, 4, 8]
+    rows = t[(nb // group).long(), :, (nb % group).long(), :, r.long(), :]  # [len, kb, 4, 8]
     return rows.reshape(ids.numel(), kb * 32)[:, :k].contiguous()

@@ -337,7 +337,6 @@ class SubnetworkDraftModel(nn.Module):
         cos, sin = model.rope(cache.capacity)
         aws = ws.attn_ws(model, cache.capacity)
         part = ws.part
-        n_qkv = (s.heads + 2 * s.kv_heads) * s.head_dim
         ops.embed(rows.ids, m, model.embed, ws.h)
         w0, e0 = self._norm_before(0)
         ops.add_rmsnorm(None, 0, 0, ws.h, m, w0, e0, ws.x)
@@ -349,9 +348,8 @@ class SubnetworkDraftModel(nn.Module):
                 if bridge_states is not None:
                     bridge_states[name] = ws.h[:m].clone()
             kc, vt = cache.layer(li)
-            sp, ld = ops.gemm_partial(ws.x, m, layer.wqkv, n_qkv, s.hidden, part)
-            ops.qkv_rope_finalize(part, sp, ld, m, s.heads, s.kv_heads, s.head_dim, cos, sin, rows.pos, rows.slot,
-                                  ws.q, kc, vt, cache.capacity)
+            ops.qkv_rope(ws.x, m, layer.wqkv, s.hidden, s.heads, s.kv_heads, s.head_dim, cos, sin, rows.pos, rows.slot,
+                         ws.q, kc, vt, cache.capacity)
             ops.tree_attention(ws.q, m, s.heads, s.kv_heads, s.head_dim, kc, vt, cache.capacity, rows.prefix,
                                rows.depth, rows.anc, p_min, l_max, aws, ws.attn)
             sp, ld = ops.gemm_partial(ws.attn, m, layer.wo, s.hidden, s.heads * s.head_dim, part)

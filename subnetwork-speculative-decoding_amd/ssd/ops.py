@@ -50,21 +50,34 @@ def packed_elems(n: int, k: int) -> int:
     return int(_lib.load().ssd_packed_weight_elems(n, k))
 
 
-def pack_weight(w: torch.Tensor, row_map: Optional[torch.Tensor] = None) -> torch.Tensor:
+def weight_group(n: int, k: int) -> int:
+    """Tile grouping the single-pass GEMMs (gemm, gemm_swiglu, qkv_rope) expect for an [N, K] weight."""
+    g = int(_lib.load().ssd_gemm_weight_group(n, k))
+    if g < 1:
+        raise ValueError(f"weight_group: bad shape N={n} K={k}")
+    return g
+
+
+def pack_weight(w: torch.Tensor, row_map: Optional[torch.Tensor] = None, split: bool = False,
+                n_logical: Optional[int] = None) -> torch.Tensor:
     """Row-major bf16 W[N, K] -> MFMA tile layout. row_map picks the source row of each packed
-    row (-1 = zeros); default = identity. Rows are padded with zeros to a multiple of 64."""
+    row (-1 = zeros); default = identity. Rows are padded with zeros to a multiple of 128. Tiles
+    are grouped for the single-pass GEMMs (group = weight_group(N_logical, K), N_logical = the
+    GEMM's output width, default the row_map length); split=True packs for gemm_partial (group 1)."""
     _check(w, "w")
     n, k = w.shape
     ld = _rows(w, "w", k)
     if row_map is None:
         row_map = torch.arange(n, dtype=torch.int32)
     row_map = row_map.to(torch.int32).cpu()
-    n_packed = (row_map.numel() + 63) // 64 * 64
+    n_log = n_logical if n_logical is not None else row_map.numel()
+    n_packed = (row_map.numel() + 127) // 128 * 128
     if n_packed != row_map.numel():
         row_map = torch.cat([row_map, torch.full((n_packed - row_map.numel(),), -1, dtype=torch.int32)])
     rm = row_map.to(device=w.device)
+    group = 1 if split else weight_group(n_log, k)
     out = torch.empty(packed_elems(n_packed, k), dtype=BF16, device=w.device)
-    _lib.call("ssd_pack_weight_bf16", w.data_ptr(), ld, n, k, rm.data_ptr(), n_packed, out.data_ptr(), stream())
+    _lib.call("ssd_pack_weight_bf16", w.data_ptr(), ld, n, k, rm.data_ptr(), n_packed, group, out.data_ptr(), stream())
     return out
 
 

@@ -43,7 +43,9 @@ def test_host_only_entry_points():
 
     lib = _lib.load()
     assert lib.ssd_abi_version() == 1
-    assert lib.ssd_packed_weight_elems(17, 40) == 64 * 64  # rows padded to 64, K to 32
+    assert lib.ssd_packed_weight_elems(17, 40) == 128 * 64  # rows padded to 128, K to 32
+    assert [lib.ssd_gemm_weight_group(n, 4096) for n in (4096, 8192, 28672, 128256)] == [1, 2, 4, 8]
+    assert lib.ssd_gemm_weight_group(4096, 100) == 0
     lim = (ctypes.c_int32 * 3)()
     assert lib.ssd_tree_limits(lim) == 0 and list(lim) == [1024, 32, 32]
     assert lib.ssd_attn_max_depth() == 32
@@ -77,3 +79,25 @@ def test_descriptor_structs_match_c_layout(tmp_path):
         assert int(got[name]) == C.sizeof(T), name
         for field, *_ in T._fields_:
             assert int(got[f"{name}.{field}"]) == getattr(T, field).offset, f"{name}.{field}"
+
+
+def test_unpack_rows_inverts_grouped_packing():
+    """The tile layout written by ssd_pack_weight_bf16 (restated here from its documentation) is
+    inverted by ssd.models.llama.unpack_rows for every tile grouping."""
+    import torch
+
+    from ssd.models.llama import unpack_rows
+
+    n, k = 256, 96
+    w = torch.arange(n * k, dtype=torch.float32).view(n, k).to(torch.bfloat16)
+    kb = k // 32
+    for group in (1, 2, 4, 8):
+        packed = torch.zeros(n // 16, kb, 64, 8, dtype=torch.bfloat16)
+        for nb in range(n // 16):
+            for b in range(kb):
+                for lane in range(64):
+                    packed[nb, b, lane] = w[nb * 16 + lane % 16, b * 32 + (lane // 16) * 8: b * 32 + (lane // 16) * 8 + 8]
+        grouped = packed.view(n // 16 // group, group, kb, 64, 8).transpose(1, 2).reshape(-1)  # [g][kb][nb%g]
+        ids = torch.tensor([0, 5, 17, 100, 255])
+        assert torch.equal(unpack_rows(grouped, n, k, ids, group), w[ids])
+

@@ -142,7 +142,7 @@ def test_gemm_partial_matches_oracle(m, n, k):
     ops = _ops()
     x, w = bf(rand(m, k, seed=40)), bf(rand(n, k, std=0.02, seed=41))
     b, r = bf(rand(n, std=0.1, seed=42)), bf(rand(m, n, seed=43))
-    wp = ops.pack_weight(w.to(DEV))
+    wp = ops.pack_weight(w.to(DEV), split=True)
     part, s, ld = _partial(ops, x.to(DEV), m, wp, n, k)
     assert s == ops.gemm_splits(n, k) >= 1
     y = torch.zeros(m, n, dtype=torch.bfloat16, device=DEV)
@@ -158,7 +158,7 @@ def test_gemm_partial_batch_invariance_bitwise(n, k):
     """Split-K partials of a row do not depend on how many rows share the call or where the row sits."""
     ops = _ops()
     x = bf(rand(64, k, seed=44)).to(DEV)
-    wp = ops.pack_weight(bf(rand(n, k, std=0.02, seed=45)).to(DEV))
+    wp = ops.pack_weight(bf(rand(n, k, std=0.02, seed=45)).to(DEV), split=True)
     full, s, ld = _partial(ops, x, 64, wp, n, k)
     full = full[:s * 64 * ld].view(s, 64, ld)
     for m in (1, 25, 33):
@@ -175,7 +175,7 @@ def test_add_rmsnorm_fuses_residual_and_norm():
     x, w = bf(rand(m, k, seed=46)), bf(rand(d, k, std=0.03, seed=47))
     h0, g = bf(rand(m, d, seed=48)), bf(1 + rand(d, std=0.1, seed=49))
     b = bf(rand(d, std=0.1, seed=50))
-    wp = ops.pack_weight(w.to(DEV))
+    wp = ops.pack_weight(w.to(DEV), split=True)
     part, s, ld = _partial(ops, x.to(DEV), m, wp, d, k)
     h = h0.to(DEV).clone()
     y = torch.zeros(m, d, dtype=torch.bfloat16, device=DEV)
@@ -198,7 +198,7 @@ def test_qkv_rope_finalize_matches_oracle(hd):
     x = bf(rand(m, d, seed=51))
     wq, wk, wv = (bf(rand(h * hd, d, std=0.05, seed=52 + i)) for i, h in enumerate((heads, kvh, kvh)))
     n = (heads + 2 * kvh) * hd
-    wp = ops.pack_weight(torch.cat([wq, wk, wv]).to(DEV), qkv_row_map(heads, kvh, hd))
+    wp = ops.pack_weight(torch.cat([wq, wk, wv]).to(DEV), qkv_row_map(heads, kvh, hd), split=True)
     cos, sin = rope_tables(max_len, hd, 500000.0, DEV)
     pos = torch.tensor([3, 3, 9, 40, 0, 63], dtype=torch.int32)
     slot = torch.tensor([10, 11, 12, 13, 20, 63], dtype=torch.int32)
