@@ -6,8 +6,10 @@ for like and greedy speculative output is bit-identical to greedy decoding (ever
 per-row arithmetic is independent of how many rows share a launch).
 
 One round, all enqueued on the current HIP stream with no host round trip inside:
-  draft   root forward -> draft head + log-softmax top-k -> level expansion (x depth)
+  draft   root forward -> draft head + log-softmax top-k (sampled: warp + Gumbel top-k)
+          -> level expansion (x depth)
   verify  max_nodes cut + verify rows -> target forward -> argmax -> greedy acceptance
+          (sampled: warp -> speculative-sampling walk)
   commit  KV compaction of the root + accepted path (one launch, all layers)
 then a single device->host copy of the round record (committed tokens, tree size).
 Phase times come from HIP events (no extra synchronisation); the reference's metric
@@ -27,6 +29,7 @@ import torch.nn as nn
 from ssd import _lib, ops
 from ssd.config import DraftingConfig
 from ssd.engine.kv_cache import KVCache
+from ssd.engine.sampling import Sampler
 from ssd.engine.tree_drafter import TREE_CAP, DeviceTree, TreeDrafter
 from ssd.models.subnetwork_draft import CHUNK, Rows, SubnetworkDraftModel
 
@@ -83,9 +86,11 @@ class _Phases:
         self._pending = []
 
 
-def _prefill(target: SubnetworkDraftModel, ids: list, cache: KVCache, ws, out_dev: torch.Tensor) -> None:
-    """Target forward over the prompt (chunks of 64 causal rows) and the first-index argmax of
-    the last row into out_dev[0] (reference speculative.py:149-151, :81-84)."""
+def _prefill(target: SubnetworkDraftModel, ids: list, cache: KVCache, ws, out_dev: torch.Tensor,
+             sampler: Optional[Sampler] = None) -> None:
+    """Target forward over the prompt (chunks of 64 causal rows) and the first token into
+    out_dev[0]: the first-index argmax of the last row, or with ``sampler`` a draw from its warped
+    distribution with counter 0 (reference speculative.py:149-151, :81-84)."""
     dev = target.model.device
     rows = Rows(CHUNK, dev)
     past = cache.get_seq_length()
@@ -101,20 +106,25 @@ def _prefill(target: SubnetworkDraftModel, ids: list, cache: KVCache, ws, out_de
         logits = target.forward_rows(rows, m, past + c0 + 1, past + c1, cache, ws, m - 1 if last else 0, int(last))
         torch.cuda.current_stream().synchronize()  # the pinned staging buffer is reused next chunk
     cache.advance(q)
-    ops.row_topk(logits, 1, logits.shape[1], 1, 0, None, out_dev)
+    if sampler is not None:
+        sampler.draw(logits, out_dev, counter=0)
+    else:
+        ops.row_topk(logits, 1, logits.shape[1], 1, 0, None, out_dev)
 
 
 @torch.no_grad()
 def autoregressive_generate(target: TargetRunner, input_ids: torch.Tensor, max_new_tokens: int, eos_ids: set,
                             temperature: float = 0.0, top_p: float = 1.0, seed: Optional[int] = None,
                             check_every: int = 16) -> GenerationResult:
-    """Greedy decoding with the target, one row per step (reference speculative.py:101-122).
-    Steps are enqueued back to back (the next step's input id is the previous step's argmax,
-    written on the device); the host checks EOS / length every ``check_every`` steps."""
-    if temperature != 0:
-        raise NotImplementedError("sampled autoregressive decoding is not part of this build yet")
+    """Decoding with the target, one row per step (reference speculative.py:101-122): argmax, or
+    with temperature > 0 a draw from the warped distribution (Philox counter = step, from
+    ``seed``). Steps are enqueued back to back (the next step's input id is written on the
+    device); the host checks EOS / length every ``check_every`` steps."""
     ids = torch.as_tensor(input_ids).reshape(-1).tolist()
     dev = target.model.device
+    sampler = None
+    if temperature != 0:
+        sampler = Sampler(temperature, top_p, target.model.shape.vocab, dev, 0, 1, seed)
     n_prompt = len(ids)
     cache = target.new_cache(n_prompt + max_new_tokens + 1)
     ws = target.workspace(CHUNK)
@@ -123,7 +133,7 @@ def autoregressive_generate(target: TargetRunner, input_ids: torch.Tensor, max_n
     times: dict = {}
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    _prefill(target, ids, cache, ws, rows.ids[0:1])
+    _prefill(target, ids, cache, ws, rows.ids[0:1], sampler)
     torch.cuda.synchronize()
     times["prefill"] = time.perf_counter() - t0
     # Step s feeds generated token s at position n_prompt + s.
@@ -136,7 +146,10 @@ def autoregressive_generate(target: TargetRunner, input_ids: torch.Tensor, max_n
         stop = min(steps - 1, s + check_every)
         while s < stop:  # step s feeds token s, writes token s + 1
             logits = target.forward_rows(rows.view(s), 1, n_prompt + s + 1, n_prompt + s + 1, cache, ws)
-            ops.row_topk(logits, 1, logits.shape[1], 1, 0, None, rows.ids[s + 1:s + 2])
+            if sampler is not None:
+                sampler.draw(logits, rows.ids[s + 1:s + 2], counter=s + 1)
+            else:
+                ops.row_topk(logits, 1, logits.shape[1], 1, 0, None, rows.ids[s + 1:s + 2])
             s += 1
         cache.seq_len = n_prompt + s
         out = rows.ids[: s + 1].tolist()
@@ -152,12 +165,14 @@ class DecodeSession:
     and returns the committed tokens. ``SpeculativeGenerator.generate`` is a loop over it.
     """
 
-    def __init__(self, gen: "SpeculativeGenerator", capacity: int):
+    def __init__(self, gen: "SpeculativeGenerator", capacity: int, seed: Optional[int] = None):
         cfg, drafter, target, draft = gen.cfg, gen.drafter, gen.target, gen.draft
-        if cfg.temperature != 0:
-            raise NotImplementedError("sampling speculative decoding is not part of this build yet")
         self.cfg, self.drafter, self.target, self.draft = cfg, drafter, target, draft
         dev = target.model.device
+        self.sampler = None
+        if cfg.temperature != 0:
+            self.sampler = Sampler(cfg.temperature, cfg.top_p, target.model.shape.vocab, dev,
+                                   1 + drafter.max_tree_cache(), ROW_CAP_VERIFY, seed)
         self.cache = target.new_cache(capacity)
         self.ws = draft.workspace(CHUNK)
         self.root_rows, self.level_rows, self.verify_rows = Rows(CHUNK, dev), Rows(CHUNK, dev), Rows(CHUNK, dev)
@@ -174,25 +189,31 @@ class DecodeSession:
         self.tree_sizes: list = []
 
     def prefill(self, ids: list) -> int:
-        _prefill(self.target, ids, self.cache, self.ws, self.root_rows.ids[0:1])
+        _prefill(self.target, ids, self.cache, self.ws, self.root_rows.ids[0:1], self.sampler)
         return int(self.root_rows.ids[0])
 
     def step(self) -> list:
         cfg, drafter, target, cache, ws = self.cfg, self.drafter, self.target, self.cache, self.ws
         committed = cache.get_seq_length()
         ph = self.phases
+        if self.sampler is not None:
+            self.sampler.counter = len(self.accepted_per_round) + 1
         ph.mark("draft")
         drafter.build_device(cache, self.root_rows, committed, self.tree, self.level_rows, self.cand_tok,
-                             self.cand_lp, ws)
+                             self.cand_lp, ws, self.sampler)
         cache.crop(committed)
         ph.mark("verify")
         m = drafter.finalize_device(self.tree, committed, self.root_rows, self.verify_rows)
         cache.check_room(committed + m)
         logits = target.forward_rows(self.verify_rows, m, committed + 1, committed + 1 + cfg.depth, cache, ws)
-        ops.row_topk(logits, m, logits.shape[1], 1, 0, None, self.argmax)
-        _lib.call("ssd_accept_greedy", self.tree.struct, self.argmax.data_ptr(), committed,
-                  self.record[2:].data_ptr(), self.keep_src.data_ptr(), self.n_keep.data_ptr(),
-                  self.root_rows.ids.data_ptr(), ops.stream())
+        if self.sampler is not None:
+            self.sampler.accept(self.tree, logits, m, committed, self.record[2:], self.keep_src, self.n_keep,
+                                self.root_rows.ids)
+        else:
+            ops.row_topk(logits, m, logits.shape[1], 1, 0, None, self.argmax)
+            _lib.call("ssd_accept_greedy", self.tree.struct, self.argmax.data_ptr(), committed,
+                      self.record[2:].data_ptr(), self.keep_src.data_ptr(), self.n_keep.data_ptr(),
+                      self.root_rows.ids.data_ptr(), ops.stream())
         ph.mark("bookkeeping")
         cache.compact_device(committed, self.keep_src, self.n_keep, cfg.depth + 1)
         self.record_host.copy_(self.record, non_blocking=True)
@@ -221,14 +242,14 @@ class SpeculativeGenerator:
         extra = max(self.drafter.max_verify_nodes(), self.drafter.max_tree_cache()) + 1
         return n_prompt + max_new_tokens + self.cfg.depth + extra + 1
 
-    def session(self, capacity: int) -> DecodeSession:
-        return DecodeSession(self, capacity)
+    def session(self, capacity: int, seed: Optional[int] = None) -> DecodeSession:
+        return DecodeSession(self, capacity, seed)
 
     @torch.no_grad()
     def generate(self, input_ids: torch.Tensor, max_new_tokens: int, eos_ids: set, seed: Optional[int] = None,
                  max_rounds: Optional[int] = None) -> GenerationResult:
         ids = torch.as_tensor(input_ids).reshape(-1).tolist()
-        sess = self.session(self.capacity(len(ids), max_new_tokens))
+        sess = self.session(self.capacity(len(ids), max_new_tokens), seed)
         times: dict = {}
         torch.cuda.synchronize()
         t0 = time.perf_counter()

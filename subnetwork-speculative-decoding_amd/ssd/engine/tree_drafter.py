@@ -7,7 +7,8 @@ fed through the draft in one batched forward where each attends to the committed
 and its own ancestors; finally the best ``max_nodes`` nodes go to verification.
 
 Here every step of that loop is a kernel: the draft forward, the draft head with the fused
-log-softmax top-k (``ssd_row_topk_bf16``), and the level expansion / width cut / next-level
+log-softmax top-k (``ssd_row_topk_bf16``; sampled drafts: the warp ``ssd_warp_probs_bf16`` and
+the Gumbel top-k draw ``ssd_gumbel_topk``), and the level expansion / width cut / next-level
 attention rows (``ssd_tree_level``), then the max_nodes cut and the verify rows
 (``ssd_tree_finalize``). No host round trip happens inside a round.
 """
@@ -30,15 +31,19 @@ TOPK_MAX = 16
 
 
 def warp_probs(logits: torch.Tensor, temperature: float, top_p: float) -> torch.Tensor:
-    """Temperature + nucleus warp (reference tree_drafter.py:34-45), as a tensor function for
-    callers of the reference API; the sampling engine applies the same rule in its kernels."""
-    probs = torch.softmax(logits.float() / temperature, dim=-1)
-    if top_p < 1.0:
-        sp, idx = probs.sort(dim=-1, descending=True)
-        sp = sp.masked_fill(sp.cumsum(-1) - sp > top_p, 0.0)
-        probs = torch.zeros_like(probs).scatter(-1, idx, sp)
-        probs = probs / probs.sum(-1, keepdim=True)
-    return probs
+    """Temperature + nucleus warp (reference tree_drafter.py:34-45) of device logits [..., V]
+    through ``ssd_warp_probs_bf16`` (logits are taken in bf16, the dtype the decode path
+    produces); returns fp32 probabilities of the same shape. Equal probabilities at the nucleus
+    boundary keep lower columns first."""
+    V = logits.shape[-1]
+    lg = logits.reshape(-1, V)
+    rows = lg.shape[0]
+    ld = (V + 7) // 8 * 8
+    buf = torch.zeros(rows, ld, dtype=torch.bfloat16, device=logits.device)
+    buf[:, :V] = lg
+    out = torch.empty(rows, (V + 3) // 4 * 4, dtype=torch.float32, device=logits.device)
+    ops.warp_probs(buf, rows, V, temperature, top_p, out)
+    return out[:, :V].reshape(logits.shape)
 
 
 @dataclass
@@ -107,13 +112,20 @@ class DeviceTree:
     def reset(self) -> None:
         self.meta.zero_()
 
-    def to_host(self) -> DraftTree:
-        """The finalized (verify) tree as a DraftTree (synchronises)."""
+    def to_host(self, sampler=None) -> DraftTree:
+        """The finalized (verify) tree as a DraftTree (synchronises). With the sampler of a
+        sampled draft, ``child_q`` maps every node with children (and the root) to the warped
+        draft distribution they were drawn from (device rows over the full vocabulary)."""
         vn = int(self.vmeta[0])
         orig = self.vorig[:vn].long()
-        return DraftTree(tokens=self.vtokens[:vn].tolist(), parents=self.vparents[:vn].tolist(),
-                         depths=self.vdepths[:vn].tolist(), scores=self.scores[orig].tolist(),
-                         ranks=self.vranks[:vn].tolist(), draft_pos=self.draft_pos[orig].tolist())
+        t = DraftTree(tokens=self.vtokens[:vn].tolist(), parents=self.vparents[:vn].tolist(),
+                      depths=self.vdepths[:vn].tolist(), scores=self.scores[orig].tolist(),
+                      ranks=self.vranks[:vn].tolist(), draft_pos=self.draft_pos[orig].tolist())
+        if sampler is not None:
+            V = sampler.vocab
+            for p in set(t.parents):
+                t.child_q[p] = sampler.Q[0 if p == ROOT else 1 + int(orig[p]), :V]
+        return t
 
 
 class TreeDrafter:
@@ -149,11 +161,13 @@ class TreeDrafter:
 
     # ------------------------------------------------------------------ device
     def build_device(self, cache: KVCache, root_rows, root_pos: int, tree: DeviceTree, level_rows, cand_tok,
-                     cand_lp, ws) -> None:
+                     cand_lp, ws, sampler=None) -> None:
         """Enqueue the whole draft phase for the root held in ``root_rows.ids[0]``; leaves the
-        unpruned tree in ``tree`` (no host synchronisation)."""
-        if not self.greedy:
-            raise NotImplementedError("sampling drafts run in the sampling engine")
+        unpruned tree in ``tree`` (no host synchronisation). Sampled drafting (temperature > 0)
+        needs ``sampler`` (ssd.engine.sampling.Sampler): proposals are Gumbel top-k draws from
+        the warped draft distribution, which is kept per node in ``sampler.Q``."""
+        if not self.greedy and sampler is None:
+            raise ValueError("sampled drafting needs a Sampler")
         draft = self.draft
         tree.reset()
         tree_start = root_pos + 1
@@ -161,7 +175,14 @@ class TreeDrafter:
         root_rows.upload(None, [root_pos], [root_pos], [root_pos + 1], [0])
         logits = draft.forward_rows(root_rows, 1, root_pos + 1, root_pos + 1, cache, ws)
         n = logits.shape[1]
-        ops.row_topk(logits, 1, n, self.branch[0], 1, draft._vocab_ids_i32, cand_tok, cand_lp)
+
+        def propose(logits, rows, d):
+            if self.greedy:
+                ops.row_topk(logits, rows, n, self.branch[d], 1, draft._vocab_ids_i32, cand_tok, cand_lp)
+            else:
+                sampler.propose(draft, logits, rows, d, self.branch[d], tree.meta, cand_tok, cand_lp)
+
+        propose(logits, 1, 0)
         past = tree_start
         for d in range(self.cfg.depth):
             feed = d < self.cfg.depth - 1
@@ -173,7 +194,7 @@ class TreeDrafter:
             if not feed:
                 break
             logits = draft.forward_rows(level_rows, m, tree_start, tree_start + d + 1, cache, ws)
-            ops.row_topk(logits, m, n, self.branch[d + 1], 1, draft._vocab_ids_i32, cand_tok, cand_lp)
+            propose(logits, m, d + 1)
             past += m
         cache.seq_len = past
 
@@ -202,9 +223,15 @@ class TreeDrafter:
         tree = DeviceTree(dev)
         cand_tok = torch.zeros(TREE_CAP, dtype=torch.int32, device=dev)
         cand_lp = torch.zeros(TREE_CAP, dtype=torch.float32, device=dev)
-        self.build_device(cache, root_rows, root_pos, tree, level_rows, cand_tok, cand_lp, ws)
+        sampler = None
+        if not self.greedy:
+            from ssd.engine.sampling import Sampler, seed_from_generator
+
+            sampler = Sampler(self.cfg.temperature, self.cfg.top_p, self.draft.model.shape.vocab, dev,
+                              1 + self.max_tree_cache(), 1, seed_from_generator(generator))
+        self.build_device(cache, root_rows, root_pos, tree, level_rows, cand_tok, cand_lp, ws, sampler)
         verify_rows = Rows(ROW_CAP, dev)
         self.finalize_device(tree, root_pos, root_rows, verify_rows)
-        out = tree.to_host()
+        out = tree.to_host(sampler)
         out.cache_start = root_pos + 1
         return out

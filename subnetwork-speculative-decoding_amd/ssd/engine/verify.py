@@ -54,3 +54,46 @@ def greedy_verify(tree: DraftTree, target_logits: torch.Tensor) -> tuple:
             return accepted, want
         accepted.append(nxt)
         cur = nxt
+
+
+def sample_verify(tree: DraftTree, target_logits: torch.Tensor, temperature: float, top_p: float,
+                  generator=None) -> tuple:
+    """Speculative sampling over the tree (reference verify.py:60-95) on the device: the target
+    rows are warped by ``ssd_warp_probs_bf16`` and walked by ``ssd_accept_sample``. ``tree.child_q``
+    maps each node with children (and the root, -1) to the warped draft distribution its children
+    were drawn from (trees built by a sampled ``TreeDrafter.build`` carry them). The Philox seed is
+    drawn from ``generator``. Returns (accepted node indices, bonus token)."""
+    from ssd.engine.sampling import Sampler, seed_from_generator
+    from ssd.engine.tree_drafter import DeviceTree
+
+    V = target_logits.shape[-1]
+    lg = target_logits.reshape(-1, V)
+    n = len(tree)
+    if lg.shape[0] < n + 1:
+        raise ValueError(f"target_logits has {lg.shape[0]} rows, the tree needs {n + 1}")
+    dev = lg.device
+    sampler = Sampler(temperature, top_p, V, dev, 1 + n, n + 1, seed_from_generator(generator))
+    for p in set(tree.parents):
+        sampler.Q[0 if p == ROOT else 1 + p, :V] = torch.as_tensor(tree.child_q[p], device=dev).float()
+    dt = DeviceTree(dev, cap=max(n, 1))
+    if n:
+        i32 = dict(dtype=torch.int32, device=dev)
+        dt.vtokens[:n] = torch.tensor(tree.tokens, **i32)
+        dt.vparents[:n] = torch.tensor(tree.parents, **i32)
+        dt.vranks[:n] = torch.tensor(tree.ranks, **i32)
+        dt.vdepths[:n] = torch.tensor(tree.depths, **i32)
+        dt.vorig[:n] = torch.arange(n, **i32)
+    dt.vmeta[0] = n
+    ld = (V + 7) // 8 * 8
+    buf = torch.zeros(n + 1, ld, dtype=torch.bfloat16, device=dev)
+    buf[:, :V] = lg[: n + 1]
+    depth = max(tree.depths, default=0)
+    result = torch.zeros(depth + 3, dtype=torch.int32, device=dev)
+    keep_src = torch.zeros(depth + 2, dtype=torch.int32, device=dev)
+    n_keep = torch.zeros(1, dtype=torch.int32, device=dev)
+    root = torch.zeros(1, dtype=torch.int32, device=dev)
+    sampler.accept(dt, buf[:, :V], n + 1, 0, result, keep_src, n_keep, root)
+    r = result.tolist()
+    n_new = r[0]
+    accepted = [s - 1 for s in keep_src[1:n_new].tolist()]
+    return accepted, r[n_new]

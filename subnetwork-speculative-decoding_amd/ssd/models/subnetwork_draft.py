@@ -232,6 +232,7 @@ class SubnetworkDraftModel(nn.Module):
                                       for b in self.bridge_specs})
         self.vocab_ids: Optional[torch.Tensor] = None
         self._vocab_ids_i32: Optional[torch.Tensor] = None
+        self._vocab_inv: Optional[torch.Tensor] = None
         self._sub_head: Optional[torch.Tensor] = None
         self._ws: Optional[Workspace] = None
         self._plan = None
@@ -249,11 +250,15 @@ class SubnetworkDraftModel(nn.Module):
         """Score only ``token_ids`` (sorted ascending) in this model's lm_head: a packed copy of
         those rows (|subset| x d) streamed by the same GEMM (reference :136-144)."""
         if token_ids is None:
-            self.vocab_ids = self._sub_head = self._vocab_ids_i32 = None
+            self.vocab_ids = self._sub_head = self._vocab_ids_i32 = self._vocab_inv = None
             return
         ids = token_ids.to(self.model.device).long()
         self.vocab_ids = ids
         self._vocab_ids_i32 = ids.to(torch.int32)
+        # token -> subset column (-1 outside): the sampling warp zeroes q outside the subset
+        inv = torch.full((self.model.shape.vocab,), -1, dtype=torch.int32, device=ids.device)
+        inv[ids] = torch.arange(ids.numel(), dtype=torch.int32, device=ids.device)
+        self._vocab_inv = inv
         self._sub_head = ops.pack_weight(self.model.lm_head_rows(ids))
 
     def place_bridges(self) -> None:

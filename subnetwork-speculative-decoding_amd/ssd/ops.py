@@ -272,3 +272,44 @@ def add_rmsnorm(part, s, ld, h, m, w, eps, out, bias=None):
               h.data_ptr(), _rows(h, "h", d, m), m, d, None if out is None else w.data_ptr(), float(eps),
               _p(out), 0 if out is None else _rows(out, "out", d, m), stream())
     return out
+
+
+# ------------------------------------------------------------------------ sampling
+def warp_probs(logits, rows, n, temperature, top_p, out, V=None, vocab_ids=None, vocab_inv=None, tree_meta=None,
+               level=0):
+    """softmax(logits / T) + nucleus cut per row into fp32 ``out`` [*, V] (ssd_warp_probs_bf16)."""
+    _check(logits, "logits"); _check(out, "probs", torch.float32)
+    V = n if V is None else V
+    if vocab_ids is not None:
+        _check(vocab_ids, "vocab_ids", torch.int32); _len(vocab_ids, "vocab_ids", n)
+        _check(vocab_inv, "vocab_inv", torch.int32); _len(vocab_inv, "vocab_inv", V)
+    if tree_meta is not None:
+        _check(tree_meta, "tree_meta", torch.int32)
+    elif out.shape[0] < rows:
+        raise ValueError(f"probs has {out.shape[0]} rows < {rows}")
+    _lib.call("ssd_warp_probs_bf16", logits.data_ptr(), _rows(logits, "logits", n, rows), rows, n, _p(vocab_ids),
+              _p(vocab_inv), V, float(temperature), float(top_p), _p(tree_meta), level, out.data_ptr(),
+              _rows(out, "probs", V), stream())
+    return out
+
+
+def gumbel_topk(probs, rows, V, k, seed, counter, out_tok, out_lp, tree_meta=None, level=0):
+    _check(probs, "probs", torch.float32); _check(out_tok, "out_tok", torch.int32)
+    _check(out_lp, "out_lp", torch.float32)
+    _len(out_tok, "out_tok", rows * k); _len(out_lp, "out_lp", rows * k)
+    if tree_meta is not None:
+        _check(tree_meta, "tree_meta", torch.int32)
+    _lib.call("ssd_gumbel_topk", probs.data_ptr(), _rows(probs, "probs", V), rows, V, k, _p(tree_meta), level,
+              seed & (2**64 - 1), counter & (2**64 - 1), out_tok.data_ptr(), out_lp.data_ptr(), stream())
+
+
+def sample_rows(probs, rows, V, seed, counter, out_tok):
+    _check(probs, "probs", torch.float32); _check(out_tok, "out_tok", torch.int32)
+    _len(out_tok, "out_tok", rows)
+    _lib.call("ssd_sample_rows", probs.data_ptr(), _rows(probs, "probs", V, rows), rows, V, seed & (2**64 - 1),
+              counter & (2**64 - 1), out_tok.data_ptr(), stream())
+    return out_tok
+
+
+def sample_state_bytes(rows: int) -> int:
+    return int(_lib.load().ssd_sample_state_bytes(rows))
