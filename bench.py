@@ -38,7 +38,11 @@ WORKLOADS = {
     "llama3_8b_tree": ("llama3_8b", [0, 15, 31], dict(depth=4, branch=[3, 2, 2, 1], max_nodes=24), 4096, None),
     "llama3_8b_c": ("llama3_8b", [0, 15, 31], dict(depth=6, branch=[4, 2, 2, 1, 1, 1], max_nodes=32), 4096, None),
     "llama32_1b_b": ("llama32_1b", [0, 7, 15], dict(depth=4, branch=[3, 2, 2, 1], width=8, max_nodes=24), 512, 32768),
+    "llama3_8b_sampled": ("llama3_8b", [0, 15, 31], dict(depth=3, branch=[3, 2, 1], temperature=0.7, top_p=0.9),
+                          4096, None),
 }
+# Sampled decoding measured beside the default workload (same model, draft and prompt).
+SAMPLED = dict(depth=3, branch=[3, 2, 1], temperature=0.7, top_p=0.9)
 
 
 def log(msg: str) -> None:
@@ -210,6 +214,33 @@ def cpu_baseline(model, layers: list, dcfg: dict, rounds: int, prompt_len: int) 
                        f"{1000 * secs / rounds:.0f} ms/round")
 
 
+def sampled_rounds(model, draft, target, ids: list, steps: int, warmup: int = 5) -> dict:
+    """Sampled speculative rounds (SAMPLED drafting) after the same prompt: ms/round, tokens/s,
+    mean tokens per round and phase split; Philox seed 0."""
+    import torch
+
+    from ssd.config import DraftingConfig
+    from ssd.engine.speculative import SpeculativeGenerator
+
+    cfg = DraftingConfig(**SAMPLED)
+    gen = SpeculativeGenerator(model, draft, cfg, target)
+    sess = gen.session(len(ids) + (warmup + steps) * (cfg.depth + 1) + gen.capacity(0, 0), seed=0)
+    sess.prefill(ids)
+    for _ in range(warmup):
+        sess.step()
+    sess.phases.totals.clear()
+    n0 = len(sess.accepted_per_round)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    toks = sum(len(sess.step()) for _ in range(steps))
+    torch.cuda.synchronize()
+    secs = time.perf_counter() - t0
+    acc = sess.accepted_per_round[n0:]
+    return {"drafting": SAMPLED, "rounds": steps, "tokens_per_s": round(toks / secs, 3),
+            "ms_per_round": round(1000 * secs / steps, 4), "mean_accepted": round(sum(acc) / len(acc), 4),
+            "ms_per_round_phases": {k: round(1000 * v / steps, 4) for k, v in sess.phases.totals.items()}}
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -220,6 +251,8 @@ def main() -> None:
     ap.add_argument("--cpu-rounds", type=int, default=4)
     ap.add_argument("--cpu-prompt", type=int, default=128)
     ap.add_argument("--ar-tokens", type=int, default=128)
+    ap.add_argument("--sampled-rounds", type=int, default=30,
+                    help="also time this many sampled rounds (T 0.7, top_p 0.9, d3 [3,2,1]); 0 = skip")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="also run one plain device copy of this many MiB (calibrates rocprofv3 byte counters)")
     args = ap.parse_args()
@@ -252,7 +285,7 @@ def main() -> None:
     gen = SpeculativeGenerator(model, draft, cfg, target)
     ids = torch.randint(0, shape.vocab, (n_prompt,), generator=torch.Generator().manual_seed(1)).tolist()
     rounds = args.warmup + args.steps
-    sess = gen.session(n_prompt + rounds * (cfg.depth + 1) + gen.capacity(0, 0))
+    sess = gen.session(n_prompt + rounds * (cfg.depth + 1) + gen.capacity(0, 0), seed=0)
     log(f"model + draft ready in {time.perf_counter() - t0:.1f}s")
     t0 = time.perf_counter()
     sess.prefill(ids)
@@ -277,6 +310,11 @@ def main() -> None:
     log(f"kernels: { {k: (round(v['ms'] * 1000, 1), round(v['gbs'])) for k, v in kf.items()} } (us, GB/s)")
     del sess
     torch.cuda.empty_cache()
+    sampled = None
+    if args.sampled_rounds and "temperature" not in dkw:
+        sampled = sampled_rounds(model, draft, target, ids, args.sampled_rounds)
+        log(f"sampled {SAMPLED}: {sampled}")
+        torch.cuda.empty_cache()
     ar = autoregressive_generate(target, torch.tensor([ids]), args.ar_tokens, {-1})
     ar_tps = (len(ar.tokens) - 1) / ar.times["decode"]
     log(f"autoregressive baseline: {ar_tps:.1f} tok/s")
@@ -311,6 +349,8 @@ def main() -> None:
         "kernels": {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in kf.items()},
     }
+    if sampled is not None:
+        line["sampled"] = sampled
     if args.copy_probe_mb:
         src = torch.ones(args.copy_probe_mb << 20, dtype=torch.uint8, device=model.device)
         dst = torch.empty_like(src)

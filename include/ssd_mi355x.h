@@ -190,38 +190,42 @@ int ssd_accept_greedy(const SsdTree* tree, const int32_t* argmax, int committed,
 
 /* ---------------------------------------------------------------- sampling
  * Randomness is Philox4x32-10 keyed by a 64-bit seed; `counter` separates draws (one value per
- * round / decode step). Reproducible for a given (seed, counter), independent of launch shape. */
-int ssd_sample_limits(int32_t* out2); /* host: {max children per node, sizeof the per-row state} */
+ * round / decode step). Reproducible for a given (seed, counter), independent of launch shape.
+ * Rows are processed in 4096-column chunks (one workgroup each); chunk results meet in a
+ * caller workspace of ssd_sample_ws_bytes(rows, columns) bytes (no clearing needed). */
+int ssd_sample_limits(int32_t* out2); /* host: {max children per node / draws per row, max columns} */
+int64_t ssd_sample_ws_bytes(int rows, int n);
 
 /* warp_probs (ssd/engine/tree_drafter.py:34-45) and the scatter of a draft-vocab subset back to
  * the full vocabulary (tree_drafter.py:134-137): probs[r][V] fp32 = softmax(logits / T), and with
  * top_p < 1 only the entries whose preceding (descending) mass is <= top_p, renormalised; equal
- * probabilities rank lower column first. vocab_ids (n columns -> tokens, with vocab_inv[V] the
- * inverse, -1 outside) may be NULL when n == V. With tree_meta, the rows are the frontier that
- * proposes `level` and row f is written at probs row 1 + (start of level-1) + f (row 0 for the
- * root) so each tree node keeps the q its children were drawn from. */
+ * logits rank lower column first. vocab_ids (n columns -> tokens, with vocab_inv[V] the inverse,
+ * -1 outside) may be NULL when n == V. With tree_meta, the rows are the frontier that proposes
+ * `level` and row f is written at probs row 1 + (start of level-1) + f (row 0 for the root) so
+ * each tree node keeps the q its children were drawn from. */
 int ssd_warp_probs_bf16(const uint16_t* logits, int64_t ld, int rows, int n, const int32_t* vocab_ids,
                         const int32_t* vocab_inv, int V, float temperature, float top_p, const int32_t* tree_meta,
-                        int level, float* probs, int64_t ldp, hipStream_t stream);
+                        int level, float* probs, int64_t ldp, void* ws, int64_t ws_bytes, hipStream_t stream);
 
 /* _propose, sampling branch (ssd/engine/tree_drafter.py:138-144): per row of q, min(k, |support|)
  * tokens without replacement in draw order (largest q(y)/E(y), E ~ Exp(1)) and their log q;
  * out_tok[r][k] is -1 past the support. tree_meta/level address q rows as ssd_warp_probs_bf16. */
 int ssd_gumbel_topk(const float* probs, int64_t ldp, int rows, int V, int k, const int32_t* tree_meta, int level,
-                    uint64_t seed, uint64_t counter, int32_t* out_tok, float* out_lp, hipStream_t stream);
+                    uint64_t seed, uint64_t counter, int32_t* out_tok, float* out_lp, void* ws, int64_t ws_bytes,
+                    hipStream_t stream);
 
 /* torch.multinomial(p, 1) per row (ssd/engine/speculative.py:81-84): a categorical draw from
  * each nonnegative row (need not be normalised). */
 int ssd_sample_rows(const float* probs, int64_t ldp, int rows, int V, uint64_t seed, uint64_t counter,
-                    int32_t* out_tok, hipStream_t stream);
+                    int32_t* out_tok, void* ws, int64_t ws_bytes, hipStream_t stream);
 
 /* sample_verify (ssd/engine/verify.py:60-95) over the finalized tree plus the bookkeeping of
- * ssd_accept_greedy. P[rows][V]: warped target rows (row 0 root, 1 + v verify node v);
- * Q: warped draft rows as written by ssd_warp_probs_bf16 with tree_meta (row 1 + draft index). */
-int64_t ssd_sample_state_bytes(int rows);
+ * ssd_accept_greedy. P[rows][V]: warped target rows (row 0 root, 1 + v verify node v; rows <= 64);
+ * Q: warped draft rows as written by ssd_warp_probs_bf16 with tree_meta (row 1 + draft index).
+ * max_kids: the most children any node has (<= 16); that many rejection passes are launched. */
 int ssd_accept_sample(const SsdTree* tree, const float* P, int64_t ldp, const float* Q, int64_t ldq, int V,
-                      int rows, uint64_t seed, uint64_t counter, void* state, int64_t state_bytes, int committed,
-                      int32_t* result, int32_t* keep_src, int32_t* n_keep, int32_t* root_token,
+                      int rows, int max_kids, uint64_t seed, uint64_t counter, void* ws, int64_t ws_bytes,
+                      int committed, int32_t* result, int32_t* keep_src, int32_t* n_keep, int32_t* root_token,
                       hipStream_t stream);
 
 /* ---------------------------------------------------------------- forward

@@ -19,12 +19,19 @@ How each part is pinned (so that a plausible mistake fails a check):
   limits; the V=8 brute-force joint for sampling (tests/test_engine.py).
   Tree pruning order and ``warp_probs`` boundaries are also pinned by small
   hand-derived known-answer cases (tests/test_oracle_engine.py).
+* ``sampling``: the sampling path with the kernels' Philox4x32-10 streams: the
+  generator against its published known-answer vectors, the nucleus warp against
+  hand-derived cases (ties included) and the fp32 rule, the verify.py:60-95 loop
+  against the precomputed-state formulation decision for decision, and the
+  speculative-sampling theorem (first committed token ~ warped target, chi-square,
+  with a planted-mistake negative control) (tests/test_oracle_sampling.py).
 * ``kernels``: per-kernel reference functions (tree attention with ancestor
   lists, KV compaction, the bf16 rounding chains). Each is pinned against
   the ``model`` forward (itself pinned to HF) or a closed form.
 
 Parity unpinned: none of the functions above is left without an independent
-check; sampled *trajectories* are compared distributionally only, because the
-HIP path draws from Philox4x32-10 while the reference draws from torch's CPU
-generator (the reference cannot be run here to record its streams).
+check. Sampled trajectories of the HIP path are compared draw for draw with
+``sampling`` (same Philox streams); against the reference's own torch-generator
+streams they can only be compared distributionally (the reference was not run
+here to record them).
 """

@@ -17,17 +17,22 @@
 //   draw, here as argmax_y p(y) / E(y) with E(y) ~ Exp(1) (the Gumbel-max trick).
 //
 // Randomness: Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as
-// easy as 1, 2, 3", SC 2011). Key = 64-bit seed; counter = (element or step index,
+// easy as 1, 2, 3", SC 2011). Key = 64-bit seed; counter = (element / 4 or step index,
 // row | level << 16, round counter low word, round counter high bits << 8 | purpose tag),
-// so every draw of a generation has its own counter and the result does not depend on
-// launch shapes or on how many rows share a launch.
+// so every draw of a generation has its own counter and no result depends on launch
+// shapes or on how many rows share a launch.
 //
-// Tie rules (where the reference leaves the order to torch's sort): equal probabilities
-// rank lower column first in the nucleus cut; equal Gumbel keys rank lower token first.
+// Work layout: a row is cut into chunks of 4096 columns, one 1024-thread workgroup per
+// (chunk, row), 4 consecutive columns per thread. Cross-chunk results go through a
+// caller-provided workspace between launches: integer histograms built with atomics
+// (order-independent), or per-chunk partials combined afterwards in chunk order, so every
+// result is deterministic.
 //
-// Each row is one 1024-thread workgroup making several passes over its row (fp32,
-// L2-resident after the first). Thread t always owns elements 4t + 4096 j, so a value a
-// thread stores in one pass is read back by the same thread in the next.
+// Nucleus cut: the order of a row's probabilities is the order of its bf16 logits, so the
+// cut is searched over the 16-bit logit keys: a 256-bin mass histogram of the key's high
+// byte (mass = round(p * 2^52), exact integer sums), then a 256-bin count histogram of the
+// low byte inside the cut bin, which fixes the cut key; equal logits rank lower column first
+// (per-chunk counts of the cut key give each tie its column rank).
 #include "common.h"
 
 #include <math.h>
@@ -35,15 +40,16 @@
 namespace ssd {
 
 constexpr int SMP_THREADS = 1024;
-constexpr int SMP_MAXK = 16;      // children per node considered by the acceptance walk
+constexpr int SMP_CHUNK = 4096;
+constexpr int SMP_MAXK = 16;      // children per node / draws per row
+constexpr int SMP_MAXC = 256;     // chunks per row (rows up to 1M columns)
 constexpr int SMP_MAXDEPTH = 32;  // tree depth (matches the tree kernels)
-constexpr int SMP_BINS = 1024;
 
 enum SmpTag { TAG_PROPOSE = 1, TAG_ACCEPT = 2, TAG_BONUS = 3, TAG_DRAW = 4 };
 
 struct Rng {
-  uint32_t k0, k1;        // key: seed
-  uint32_t c2, c3_base;   // counter words 2 and 3 (round counter; tag is or-ed into c3)
+  uint32_t k0, k1;       // key: seed
+  uint32_t c2, c3_base;  // counter words 2 and 3 (round counter; tag is or-ed into c3)
 };
 
 static Rng make_rng(uint64_t seed, uint64_t ctr) {
@@ -122,6 +128,8 @@ __device__ __forceinline__ bool better(float ka, int ia, float kb, int ib) {
   return ka > kb || (ka == kb && ia < ib);
 }
 
+constexpr int NO_IDX = 0x7fffffff;
+
 // Largest key, lowest index among equal keys. Every thread gets the result.
 __device__ __forceinline__ KeyIdx block_argmax(float key, int idx, KeyIdx* sh) {
 #pragma unroll
@@ -158,19 +166,83 @@ __device__ __forceinline__ uint32_t block_scan(uint32_t v, uint32_t* sh) {
   return v + add;
 }
 
+__device__ __forceinline__ uint64_t block_scan64(uint64_t v, uint64_t* sh) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint64_t n = __shfl_up(v, o);
+    if (lane >= o) v += n;
+  }
+  if (lane == 63) sh[w] = v;
+  __syncthreads();
+  uint64_t add = 0;
+  for (int i = 0; i < w; ++i) add += sh[i];
+  __syncthreads();
+  return v + add;
+}
+
+// ------------------------------------------------------------------------ workspace
+// One caller-provided buffer, carved per (rows, chunks). Histograms are cleared by the first
+// launch of each warp; every other array is fully written before it is read.
+struct SmpWs {
+  float2* stats;      // [rows][C] chunk (max, sum exp) of logits / T
+  uint64_t* coarse;   // [rows][256] mass by key high byte
+  uint32_t* fine;     // [rows][256] count by key low byte inside the cut bin
+  uint32_t* finec;    // [rows][C][256] the same per chunk (column rank of ties)
+  KeyIdx* cand;       // [rows][C][SMP_MAXK] per-chunk Gumbel top-k candidates
+  int* csupp;         // [rows][C] per-chunk support size
+  KeyIdx* arg;        // [rows][C] per-chunk categorical draw
+  double* zr;         // [rows][SMP_MAXK + 1][C] residual mass partials per rejection state
+  KeyIdx* bon;        // [rows][SMP_MAXK + 1][C] bonus draw partials per rejection state
+  double* s0;         // [rows][C] mass of q0 per chunk
+  int* supp;          // [rows][C] support of q0 per chunk
+  int C;
+};
+
+static int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
+static int64_t smp_layout(int rows, int C, char* base, SmpWs* ws) {
+  int64_t off = 0;
+  auto take = [&](int64_t bytes) -> char* {
+    char* p = base ? base + off : nullptr;
+    off += align256(bytes);
+    return p;
+  };
+  const int64_t R = rows, CC = C;
+  SmpWs w;
+  w.stats = (float2*)take(R * CC * sizeof(float2));
+  w.coarse = (uint64_t*)take(R * 256 * 8);
+  w.fine = (uint32_t*)take(R * 256 * 4);
+  w.finec = (uint32_t*)take(R * CC * 256 * 4);
+  w.cand = (KeyIdx*)take(R * CC * SMP_MAXK * sizeof(KeyIdx));
+  w.csupp = (int*)take(R * CC * 4);
+  w.arg = (KeyIdx*)take(R * CC * sizeof(KeyIdx));
+  w.zr = (double*)take(R * (SMP_MAXK + 1) * CC * 8);
+  w.bon = (KeyIdx*)take(R * (SMP_MAXK + 1) * CC * sizeof(KeyIdx));
+  w.s0 = (double*)take(R * CC * 8);
+  w.supp = (int*)take(R * CC * 4);
+  w.C = C;
+  if (ws) *ws = w;
+  return off;
+}
+
+static int chunks_of(int n) { return (n + SMP_CHUNK - 1) / SMP_CHUNK; }
+
 // ------------------------------------------------------------------------ warp
 struct WarpArgs {
   const bf16_t* logits;
   int64_t ld;
-  int rows, n;           // logit rows and columns
-  const int* vocab;      // column -> token (draft-vocab subset), or null (column = token)
-  const int* inv;        // token -> column or -1 (with vocab), length V
-  int V;                 // output row length (full vocabulary)
+  int rows, n;        // logit rows and columns
+  const int* vocab;   // column -> token (draft-vocab subset), or null (column = token)
+  const int* inv;     // token -> column or -1 (with vocab), length V
+  int V;              // output row length (full vocabulary)
   float temp, top_p;
-  const int* meta;       // tree meta: rows are the frontier proposing `level`; null: plain rows
+  uint64_t T;         // top_p in units of 2^-52
+  const int* meta;    // tree meta: rows are the frontier proposing `level`; null: plain rows
   int level;
   float* out;
   int64_t ldo;
+  SmpWs ws;
 };
 
 // Frontier size and first output row of a proposal step (tree meta layout: [0] nodes,
@@ -190,230 +262,238 @@ __device__ __forceinline__ void frontier_rows(const int* meta, int level, int ro
   }
 }
 
-struct Cut {
-  int bin;
-  uint32_t above;  // fixed-point mass ranked before the bin
-};
+// Monotone 16-bit key of a bf16 value (ascending key = ascending value) and its inverse.
+__device__ __forceinline__ uint32_t bf_key(uint32_t h) { return h ^ ((h & 0x8000u) ? 0xffffu : 0x8000u); }
+__device__ __forceinline__ uint32_t key_bf(uint32_t k) { return k ^ ((k & 0x8000u) ? 0x8000u : 0xffffu); }
 
-// The bin holding the first entry whose preceding mass exceeds T, scanning bins from the
-// largest value down; `base` is the mass ranked before every bin of this histogram.
-// Returns bin -1 when the whole histogram fits under T.
-__device__ __forceinline__ Cut find_cut(const uint32_t* hist, uint32_t base, uint32_t T, uint32_t* scan_sh,
-                                        Cut* cut_sh) {
-  const int b = SMP_BINS - 1 - (int)threadIdx.x;
-  const uint32_t v = hist[b];
-  const uint32_t incl = block_scan(v, scan_sh);
-  if (threadIdx.x == 0) *cut_sh = Cut{-1, 0};
-  __syncthreads();
-  const uint32_t above = base + incl - v;
-  if (v > 0 && above <= T && T < base + incl) *cut_sh = Cut{b, above};
-  __syncthreads();
-  const Cut c = *cut_sh;
-  __syncthreads();
-  return c;
+// The probability of a logit and its fixed-point mass: one code path for every use, so a
+// value and the mass accumulated for it always agree bit for bit.
+__device__ __forceinline__ float prob_of(uint32_t h, float temp, float M, float S) {
+  return expf(bf2f((bf16_t)h) / temp - M) / S;
+}
+__device__ __forceinline__ uint64_t mass_of(float p) { return __double2ull_rn((double)p * 0x1p52); }
+
+__device__ __forceinline__ void load4_bf16(const bf16_t* row, int i, int n, uint32_t h[4]) {
+  if (i + 3 < n) {
+    const uint2 raw = *(const uint2*)(row + i);
+    h[0] = raw.x & 0xffff;
+    h[1] = raw.x >> 16;
+    h[2] = raw.y & 0xffff;
+    h[3] = raw.y >> 16;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) h[e] = i + e < n ? row[i + e] : 0xff80u;  // -inf pads
+  }
 }
 
-__device__ __forceinline__ uint32_t mass_fixed(float p) { return __float2uint_rn(p * 0x1p31f); }
+struct WarpShared {
+  float red_f[16];
+  uint32_t red_u[16];
+  uint64_t red_l[16];
+  uint64_t histm[256];
+  uint32_t histc[256];
+  float M, S;
+  int cut;
+  uint64_t above, total;
+};
 
-__global__ __launch_bounds__(SMP_THREADS) void warp_kernel(WarpArgs a) {
-  __shared__ uint32_t hist_m[SMP_BINS];
-  __shared__ uint32_t hist_c[SMP_BINS];
-  __shared__ uint32_t scan_sh[16];
-  __shared__ float red_f[16];
-  __shared__ Cut cut_sh;
-  __shared__ int idx_cut_sh;
+// Row max and sum exp from the chunk partials (fixed order: block reduction over chunk index).
+__device__ __forceinline__ void row_stats(const float2* st, int C, WarpShared& sh, float& M, float& S) {
+  const int t = threadIdx.x;
+  const float2 v = t < C ? st[t] : make_float2(-INFINITY, 0.f);
+  M = block_max(v.x, sh.red_f);
+  S = block_sum<float>(t < C && v.x != -INFINITY ? v.y * expf(v.x - M) : 0.f, sh.red_f);
+}
+
+// Scan a 256-bin histogram (bin masses from mass_fn(bin)) from the largest key down: the bin
+// holding the first entry whose preceding mass exceeds T. Sets sh.cut (-1 when the whole
+// histogram fits under T), sh.above (mass of the bins above the cut bin, plus `base`) and
+// sh.total.
+template <typename MassFn>
+__device__ __forceinline__ void cut_scan(MassFn mass_fn, uint64_t base, uint64_t T, WarpShared& sh) {
+  const int t = threadIdx.x;
+  const int b = 255 - t;
+  const uint64_t v = t < 256 ? mass_fn(b) : 0ull;
+  const uint64_t incl = block_scan64(v, sh.red_l);
+  if (t == 0) sh.cut = -1;
+  if (t == 255) sh.total = base + incl;
+  __syncthreads();
+  if (t < 256 && v > 0 && base + incl - v <= T && T < base + incl) {
+    sh.cut = b;
+    sh.above = base + incl - v;
+  }
+  __syncthreads();
+}
+
+// L0: chunk max / sum exp; the first chunk of each row clears the row's histograms.
+__global__ __launch_bounds__(SMP_THREADS) void warp_stats_kernel(WarpArgs a) {
+  __shared__ WarpShared sh;
   int F, base;
   frontier_rows(a.meta, a.level, a.rows, F, base);
-  const int f = blockIdx.x;
+  const int f = blockIdx.y, c = blockIdx.x, t = threadIdx.x;
   if (f >= F) return;
-  const bf16_t* lg = a.logits + (size_t)f * a.ld;
-  float* out = a.out + (size_t)(base + f) * a.ldo;
-  const int t = threadIdx.x;
-  const int n = a.n;
-  const float temp = a.temp;
-  if (t == 0) idx_cut_sh = 0x7fffffff;
+  if (c == 0 && a.top_p < 1.f) {
+    if (t < 256) a.ws.coarse[(size_t)f * 256 + t] = 0;
+    if (t < 256) a.ws.fine[(size_t)f * 256 + t] = 0;
+  }
+  const int i = c * SMP_CHUNK + t * 4;
+  uint32_t h[4];
+  load4_bf16(a.logits + (size_t)f * a.ld, i, a.n, h);
+  float x[4], m = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    x[e] = i + e < a.n ? bf2f((bf16_t)h[e]) / a.temp : -INFINITY;
+    m = fmaxf(m, x[e]);
+  }
+  const float M = block_max(m, sh.red_f);
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) s += i + e < a.n ? expf(x[e] - M) : 0.f;
+  const float S = block_sum<float>(s, sh.red_f);
+  if (t == 0) a.ws.stats[(size_t)f * a.ws.C + c] = make_float2(M, S);
+}
 
-  // Pass 1: max and sum of exp (online per thread, fixed-order combine).
-  float m = -INFINITY, s = 0.f;
-  for (int i = t * 4; i < n; i += 4 * SMP_THREADS) {
-    const uint2 raw = *(const uint2*)(lg + i);
-    const bf16_t h[4] = {(bf16_t)(raw.x & 0xffff), (bf16_t)(raw.x >> 16), (bf16_t)(raw.y & 0xffff),
-                         (bf16_t)(raw.y >> 16)};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if (i + e >= n) break;
-      const float x = bf2f(h[e]) / temp;
-      if (x > m) {
-        s = s * expf(m - x) + 1.f;
-        m = x;
-      } else {
-        s += expf(x - m);
-      }
-    }
-  }
-  const float M = block_max(m, red_f);
-  const float S = block_sum<float>(m == -INFINITY ? 0.f : s * expf(m - M), red_f);
-  const bool nucleus = a.top_p < 1.f;
-  const uint32_t T = nucleus ? (uint32_t)fmin(fmax((double)a.top_p, 0.0) * 2147483648.0, 4294967295.0) : 0u;
-
-  if (nucleus) {
-    hist_m[t] = 0;
-    __syncthreads();
-  }
-  // Pass 2: probabilities into the output row; mass histogram of the top 12 value bits.
-  for (int i = t * 4; i < n; i += 4 * SMP_THREADS) {
-    const uint2 raw = *(const uint2*)(lg + i);
-    const bf16_t h[4] = {(bf16_t)(raw.x & 0xffff), (bf16_t)(raw.x >> 16), (bf16_t)(raw.y & 0xffff),
-                         (bf16_t)(raw.y >> 16)};
-    float p[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) p[e] = expf(bf2f(h[e]) / temp - M) / S;
-    if (!a.vocab && i + 3 < n) {
-      *(float4*)(out + i) = make_float4(p[0], p[1], p[2], p[3]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (i + e < n) out[a.vocab ? a.vocab[i + e] : i + e] = p[e];
-    }
-    if (nucleus) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (i + e < n) atomicAdd(&hist_m[min(__float_as_uint(p[e]) >> 20, 1023u)], mass_fixed(p[e]));
-    }
-  }
-  if (a.vocab) {  // tokens outside the subset have probability 0
-    for (int y = t; y < a.V; y += SMP_THREADS)
-      if (a.inv[y] < 0) out[y] = 0.f;
-  }
-  if (!nucleus) return;
+// L1: mass / count histogram of the key high byte.
+__global__ __launch_bounds__(SMP_THREADS) void warp_coarse_kernel(WarpArgs a) {
+  __shared__ WarpShared sh;
+  int F, base;
+  frontier_rows(a.meta, a.level, a.rows, F, base);
+  const int f = blockIdx.y, c = blockIdx.x, t = threadIdx.x;
+  if (f >= F) return;
+  float M, S;
+  row_stats(a.ws.stats + (size_t)f * a.ws.C, a.ws.C, sh, M, S);
+  if (t < 256) sh.histm[t] = 0;
   __syncthreads();
-
-  auto load_p = [&](int i, float p[4]) {
-    if (!a.vocab && i + 3 < n) {
-      const float4 v = *(const float4*)(out + i);
-      p[0] = v.x;
-      p[1] = v.y;
-      p[2] = v.z;
-      p[3] = v.w;
-    } else {
+  const int i = c * SMP_CHUNK + t * 4;
+  uint32_t h[4];
+  load4_bf16(a.logits + (size_t)f * a.ld, i, a.n, h);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) p[e] = i + e < n ? out[a.vocab ? a.vocab[i + e] : i + e] : 0.f;
-    }
-  };
+  for (int e = 0; e < 4; ++e) {
+    if (i + e >= a.n) continue;
+    const uint32_t bin = bf_key(h[e]) >> 8;
+    atomicAdd((unsigned long long*)&sh.histm[bin], (unsigned long long)mass_of(prob_of(h[e], a.temp, M, S)));
+  }
+  __syncthreads();
+  if (t < 256 && sh.histm[t])
+    atomicAdd((unsigned long long*)&a.ws.coarse[(size_t)f * 256 + t], (unsigned long long)sh.histm[t]);
+}
 
-  // Radix search for the cut: 12 + 10 + 10 value bits (probabilities are <= 1, so the top
-  // 12 bits of a float are < 1024).
-  const Cut cA = find_cut(hist_m, 0u, T, scan_sh, &cut_sh);
-  uint32_t vbits = 0, kept_mass = 0;
-  int idx_cut = 0x7fffffff;
-  if (cA.bin < 0) {  // everything fits under top_p: keep all
-    vbits = 0;
-    kept_mass = 0xffffffffu;
+// L2: inside the coarse cut bin, count histogram of the key low byte (row total and per chunk).
+__global__ __launch_bounds__(SMP_THREADS) void warp_fine_kernel(WarpArgs a) {
+  __shared__ WarpShared sh;
+  int F, base;
+  frontier_rows(a.meta, a.level, a.rows, F, base);
+  const int f = blockIdx.y, c = blockIdx.x, t = threadIdx.x;
+  if (f >= F) return;
+  const uint64_t* coarse = a.ws.coarse + (size_t)f * 256;
+  cut_scan([&](int b) { return coarse[b]; }, 0ull, a.T, sh);
+  const int cut = sh.cut;
+  if (cut < 0) return;  // everything fits under top_p (uniform per block)
+  if (t < 256) sh.histc[t] = 0;
+  __syncthreads();
+  const int i = c * SMP_CHUNK + t * 4;
+  uint32_t h[4];
+  load4_bf16(a.logits + (size_t)f * a.ld, i, a.n, h);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t k = bf_key(h[e]);
+    if (i + e < a.n && (int)(k >> 8) == cut) atomicAdd(&sh.histc[k & 255], 1u);
+  }
+  __syncthreads();
+  if (t < 256) {
+    const uint32_t v = sh.histc[t];
+    a.ws.finec[((size_t)f * a.ws.C + c) * 256 + t] = v;
+    if (v) atomicAdd(&a.ws.fine[(size_t)f * 256 + t], v);
+  }
+}
+
+// L3: probabilities out (renormalised survivors when top_p < 1); zeros outside a subset.
+__global__ __launch_bounds__(SMP_THREADS) void warp_final_kernel(WarpArgs a) {
+  __shared__ WarpShared sh;
+  __shared__ uint32_t cut_key_sh, c_keep_sh, prefix_sh;
+  __shared__ uint64_t kept_sh;
+  int F, base;
+  frontier_rows(a.meta, a.level, a.rows, F, base);
+  const int f = blockIdx.y, c = blockIdx.x, t = threadIdx.x;
+  if (f >= F) return;
+  float* out = a.out + (size_t)(base + f) * a.ldo;
+  if (a.vocab) {  // tokens outside the subset have probability 0
+    const int y0 = c * SMP_CHUNK + t * 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (y0 + e < a.V && a.inv[y0 + e] < 0) out[y0 + e] = 0.f;
+  }
+  if (c * SMP_CHUNK >= a.n) return;  // a zero-fill-only chunk (uniform per block)
+  float M, S;
+  row_stats(a.ws.stats + (size_t)f * a.ws.C, a.ws.C, sh, M, S);
+  uint32_t cut_key = 0, c_keep = 0xffffffffu, prefix = 0;
+  float scale = 1.f;
+  if (a.top_p < 1.f) {
+    const uint64_t* coarse = a.ws.coarse + (size_t)f * 256;
+    cut_scan([&](int b) { return coarse[b]; }, 0ull, a.T, sh);
+    if (sh.cut < 0) {  // keep all: renormalise by the total mass
+      scale = (float)(1.0 / ((double)sh.total * 0x1p-52));
+    } else {
+      const int cb = sh.cut;
+      const uint64_t above = sh.above;
+      const uint32_t* fine = a.ws.fine + (size_t)f * 256;
+      // mass of fine bin b = count * mass of that exact logit
+      cut_scan([&](int b) {
+        const uint32_t n = fine[b];
+        return n ? (uint64_t)n * mass_of(prob_of(key_bf(((uint32_t)cb << 8) | (uint32_t)b), a.temp, M, S)) : 0ull;
+      }, above, a.T, sh);
+      if (t == 0) {
+        const int fb = sh.cut < 0 ? 0 : sh.cut;  // always found: the coarse bin's mass straddles T
+        const uint32_t key = ((uint32_t)cb << 8) | (uint32_t)fb;
+        const uint32_t n_t = fine[fb];
+        const uint64_t w = mass_of(prob_of(key_bf(key), a.temp, M, S));
+        const uint64_t C3 = sh.cut < 0 ? above : sh.above;
+        uint64_t keep = n_t;
+        if (w > 0 && a.T >= C3) keep = min((uint64_t)n_t, (a.T - C3) / w + 1ull);
+        cut_key_sh = key;
+        c_keep_sh = (uint32_t)keep;
+        kept_sh = C3 + keep * w;
+      }
+      __syncthreads();
+      cut_key = cut_key_sh;
+      c_keep = c_keep_sh;
+      scale = (float)(1.0 / ((double)kept_sh * 0x1p-52));
+      // ties of the cut key in earlier chunks
+      const uint32_t fb = cut_key & 255;
+      const uint32_t v = t < c ? a.ws.finec[((size_t)f * a.ws.C + t) * 256 + fb] : 0u;
+      const uint32_t pre = block_sum<uint32_t>(v, (uint32_t*)sh.red_u);
+      if (t == 0) prefix_sh = pre;
+      __syncthreads();
+      prefix = prefix_sh;
+    }
+  }
+  const int i = c * SMP_CHUNK + t * 4;
+  uint32_t h[4];
+  load4_bf16(a.logits + (size_t)f * a.ld, i, a.n, h);
+  // column rank of this thread's ties of the cut key
+  uint32_t ties = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) ties += (i + e < a.n && bf_key(h[e]) == cut_key) ? 1u : 0u;
+  uint32_t rank = 0;
+  if (a.top_p < 1.f && c_keep != 0xffffffffu) rank = prefix + block_scan(ties, sh.red_u) - ties;
+  float p[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t k = bf_key(h[e]);
+    bool keep = true;
+    if (a.top_p < 1.f && c_keep != 0xffffffffu) {
+      keep = k > cut_key;
+      if (k == cut_key && i + e < a.n) keep = rank++ < c_keep;
+    }
+    const float pv = prob_of(h[e], a.temp, M, S);
+    p[e] = keep ? (a.top_p < 1.f ? pv * scale : pv) : 0.f;
+  }
+  if (!a.vocab && i + 3 < a.n) {
+    *(float4*)(out + i) = make_float4(p[0], p[1], p[2], p[3]);
   } else {
-    hist_m[t] = 0;
-    __syncthreads();
-    for (int i = t * 4; i < n; i += 4 * SMP_THREADS) {
-      float p[4];
-      load_p(i, p);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t b = __float_as_uint(p[e]);
-        if (i + e < n && (int)(b >> 20) == cA.bin) atomicAdd(&hist_m[(b >> 10) & 1023], mass_fixed(p[e]));
-      }
-    }
-    __syncthreads();
-    const Cut cB = find_cut(hist_m, cA.above, T, scan_sh, &cut_sh);
-    const uint32_t hiB = ((uint32_t)cA.bin << 10) | (uint32_t)max(cB.bin, 0);
-    hist_m[t] = 0;
-    hist_c[t] = 0;
-    __syncthreads();
-    for (int i = t * 4; i < n; i += 4 * SMP_THREADS) {
-      float p[4];
-      load_p(i, p);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t b = __float_as_uint(p[e]);
-        if (i + e < n && (b >> 10) == hiB) {
-          atomicAdd(&hist_m[b & 1023], mass_fixed(p[e]));
-          atomicAdd(&hist_c[b & 1023], 1u);
-        }
-      }
-    }
-    __syncthreads();
-    const Cut cC = find_cut(hist_m, cB.above, T, scan_sh, &cut_sh);
-    // cB / cC cannot miss when cA hit (the bin's mass straddles T); guard anyway.
-    const int binC = max(cC.bin, 0);
-    vbits = (hiB << 10) | (uint32_t)binC;
-    const uint32_t n_t = hist_c[binC];
-    const uint32_t w_v = n_t ? hist_m[binC] / n_t : 0u;
-    const uint32_t C3 = cC.bin < 0 ? cB.above : cC.above;
-    uint32_t c = n_t;
-    if (w_v > 0 && T >= C3) c = min(n_t, (T - C3) / w_v + 1u);
-    kept_mass = C3 + c * w_v;
-    if (c < n_t) {
-      // Equal probabilities straddle the cut: keep the c lowest columns among them.
-      int sh = 0;
-      while (((n - 1) >> sh) >= SMP_BINS) ++sh;
-      __syncthreads();
-      hist_c[t] = 0;
-      __syncthreads();
-      for (int i = t * 4; i < n; i += 4 * SMP_THREADS) {
-        float p[4];
-        load_p(i, p);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (i + e < n && __float_as_uint(p[e]) == vbits) atomicAdd(&hist_c[(i + e) >> sh], 1u);
-      }
-      __syncthreads();
-      const uint32_t cnt = hist_c[t];
-      const uint32_t incl = block_scan(cnt, scan_sh);
-      if (cnt > 0 && incl - cnt < c && c <= incl) {
-        cut_sh = Cut{t, c - (incl - cnt)};  // bin t holds the c-th tie, the `above`-th inside it
-      }
-      __syncthreads();
-      const Cut cd = cut_sh;
-      __syncthreads();
-      // One element per thread inside the bin (bins span at most 2^sh <= 1024 columns).
-      const int col = (cd.bin << sh) + t;
-      int tie = 0;
-      if (t < (1 << sh) && col < n) {
-        const float pv = a.vocab ? out[a.vocab[col]] : out[col];
-        tie = __float_as_uint(pv) == vbits;
-      }
-      const uint32_t rk = block_scan((uint32_t)tie, scan_sh);
-      if (tie && rk == cd.above) idx_cut_sh = col;
-      __syncthreads();
-      idx_cut = idx_cut_sh;
-    }
-  }
-  const float inv_sum = kept_mass == 0xffffffffu ? -1.f : (float)(1.0 / ((double)kept_mass * 0x1p-31));
-  float keep_sum_f = 0.f;
-  if (kept_mass == 0xffffffffu) {  // keep all: renormalise by the plain sum
-    for (int i = t * 4; i < n; i += 4 * SMP_THREADS) {
-      float p[4];
-      load_p(i, p);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) keep_sum_f += i + e < n ? p[e] : 0.f;
-    }
-    keep_sum_f = block_sum<float>(keep_sum_f, red_f);
-  }
-  // Final pass: survivors renormalised, the rest zeroed.
-  for (int i = t * 4; i < n; i += 4 * SMP_THREADS) {
-    float p[4];
-    load_p(i, p);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t b = __float_as_uint(p[e]);
-      const bool keep = b > vbits || (b == vbits && i + e <= idx_cut);
-      p[e] = keep ? (inv_sum < 0.f ? p[e] / keep_sum_f : p[e] * inv_sum) : 0.f;
-    }
-    if (!a.vocab && i + 3 < n) {
-      *(float4*)(out + i) = make_float4(p[0], p[1], p[2], p[3]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (i + e < n) out[a.vocab ? a.vocab[i + e] : i + e] = p[e];
-    }
+    for (int e = 0; e < 4; ++e)
+      if (i + e < a.n) out[a.vocab ? a.vocab[i + e] : i + e] = p[e];
   }
 }
 
@@ -427,81 +507,127 @@ struct TopkArgs {
   Rng rng;
   int* out_tok;   // [rows][k], -1 past min(k, support)
   float* out_lp;  // log q of each drawn token
+  SmpWs ws;
 };
 
-// Draws min(k, |support|) tokens without replacement from each row of q: the k largest keys
-// q(y) / E(y), E(y) ~ Exp(1) i.i.d. (equivalently log q(y) + Gumbel), in decreasing key
-// order, which is the order of the sequential draws.
-template <int K>
-__global__ __launch_bounds__(SMP_THREADS) void gumbel_topk_kernel(TopkArgs a) {
+__device__ __forceinline__ void load4_f32(const float* row, int i, int n, float v[4]) {
+  if (i + 3 < n) {
+    const float4 q = *(const float4*)(row + i);
+    v[0] = q.x;
+    v[1] = q.y;
+    v[2] = q.z;
+    v[3] = q.w;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = i + e < n ? row[i + e] : 0.f;
+  }
+}
+
+// Per chunk: the k largest keys q(y) / E(y) (E ~ Exp(1) from the PROPOSE stream) and the
+// support size. Keys of one thread are its 4 columns; the chunk's top k are popped one at a
+// time by block argmax.
+__global__ __launch_bounds__(SMP_THREADS) void gumbel_chunk_kernel(TopkArgs a) {
   __shared__ KeyIdx red[16];
   __shared__ int red_i[16];
   int F, base;
   frontier_rows(a.meta, a.level, a.rows, F, base);
-  const int f = blockIdx.x;
+  const int f = blockIdx.y, c = blockIdx.x, t = threadIdx.x;
   if (f >= F) return;
   const float* q = a.q + (size_t)(base + f) * a.ldq;
-  const int t = threadIdx.x;
-  float kk[K];
-  int ki[K];
-#pragma unroll
-  for (int j = 0; j < K; ++j) {
-    kk[j] = -1.f;
-    ki[j] = 0x7fffffff;
-  }
+  const int i = c * SMP_CHUNK + t * 4;
+  float v[4];
+  load4_f32(q, i, a.V, v);
+  const U4 r = rng_block(a.rng, (uint32_t)(i >> 2), (uint32_t)f | ((uint32_t)a.level << 16), TAG_PROPOSE);
+  float kk[4];
+  int ki[4];
   int supp = 0;
-  const uint32_t c1 = (uint32_t)f | ((uint32_t)a.level << 16);
-  for (int i = t * 4; i < a.V; i += 4 * SMP_THREADS) {
-    float p[4];
-    if (i + 3 < a.V) {
-      const float4 v = *(const float4*)(q + i);
-      p[0] = v.x;
-      p[1] = v.y;
-      p[2] = v.z;
-      p[3] = v.w;
-    } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) p[e] = i + e < a.V ? q[i + e] : 0.f;
-    }
-    const U4 r = rng_block(a.rng, (uint32_t)(i >> 2), c1, TAG_PROPOSE);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if (!(p[e] > 0.f)) continue;
-      ++supp;
-      const float key = p[e] / exp1_from_bits(u4_get(r, e));
-      if (key > kk[K - 1]) {  // insert, keeping earlier (lower) tokens first among equal keys
-        float ck = key;
-        int ci = i + e;
-#pragma unroll
-        for (int j = 0; j < K; ++j) {
-          if (ck > kk[j]) {
-            const float tk = kk[j];
-            const int ti = ki[j];
-            kk[j] = ck;
-            ki[j] = ci;
-            ck = tk;
-            ci = ti;
-          }
-        }
-      }
-    }
+  for (int e = 0; e < 4; ++e) {
+    const bool on = i + e < a.V && v[e] > 0.f;
+    supp += on;
+    kk[e] = on ? v[e] / exp1_from_bits(u4_get(r, e)) : -1.f;
+    ki[e] = on ? i + e : NO_IDX;
   }
   const int support = block_sum<int>(supp, red_i);
+  KeyIdx* cand = a.ws.cand + ((size_t)f * a.ws.C + c) * SMP_MAXK;
+  for (int j = 0; j < a.k; ++j) {
+    // this thread's best remaining column
+    int b = 0;
+#pragma unroll
+    for (int e = 1; e < 4; ++e)
+      if (better(kk[e], ki[e], kk[b], ki[b])) b = e;
+    float bk = kk[0];
+    int bi = ki[0];
+#pragma unroll
+    for (int e = 1; e < 4; ++e)
+      if (e == b) {
+        bk = kk[e];
+        bi = ki[e];
+      }
+    const KeyIdx w = block_argmax(bk, bi, red);
+    if (t == 0) cand[j] = w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (ki[e] == w.idx) {
+        kk[e] = -1.f;
+        ki[e] = NO_IDX;
+      }
+  }
+  if (t == 0) a.ws.csupp[(size_t)f * a.ws.C + c] = support;
+}
+
+// Per row: merge the chunks' candidates in chunk order; write min(k, support) tokens in draw
+// order and log q of each.
+__global__ __launch_bounds__(SMP_THREADS) void gumbel_merge_kernel(TopkArgs a) {
+  __shared__ KeyIdx red[16];
+  __shared__ int red_i[16];
+  int F, base;
+  frontier_rows(a.meta, a.level, a.rows, F, base);
+  const int f = blockIdx.x, t = threadIdx.x;
+  if (f >= F) return;
+  const int C = a.ws.C;
+  const int total = C * a.k;
+  const float* q = a.q + (size_t)(base + f) * a.ldq;
+  int support = block_sum<int>(t < C ? a.ws.csupp[(size_t)f * C + t] : 0, red_i);
   const int take = min(a.k, support);
+  // each thread holds up to 4 candidates (C * k <= 256 * 16 = 4096)
+  float kk[4];
+  int ki[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int j = t * 4 + e;
+    if (j < total) {
+      const KeyIdx v = a.ws.cand[((size_t)f * C + j / a.k) * SMP_MAXK + j % a.k];
+      kk[e] = v.key;
+      ki[e] = v.idx;
+    } else {
+      kk[e] = -1.f;
+      ki[e] = NO_IDX;
+    }
+  }
   for (int r = 0; r < a.k; ++r) {
     int tok = -1;
     if (r < take) {
-      const KeyIdx w = block_argmax(kk[0], ki[0], red);
-      tok = w.idx;
-      if (ki[0] == w.idx) {  // owner pops its head
+      int b = 0;
 #pragma unroll
-        for (int j = 0; j + 1 < K; ++j) {
-          kk[j] = kk[j + 1];
-          ki[j] = ki[j + 1];
+      for (int e = 1; e < 4; ++e)
+        if (better(kk[e], ki[e], kk[b], ki[b])) b = e;
+      float bk = kk[0];
+      int bi = ki[0];
+#pragma unroll
+      for (int e = 1; e < 4; ++e)
+        if (e == b) {
+          bk = kk[e];
+          bi = ki[e];
         }
-        kk[K - 1] = -1.f;
-        ki[K - 1] = 0x7fffffff;
-      }
+      const KeyIdx w = block_argmax(bk, bi, red);
+      tok = w.idx == NO_IDX ? -1 : w.idx;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (ki[e] == w.idx) {
+          kk[e] = -1.f;
+          ki[e] = NO_IDX;
+        }
     }
     if (t == 0) {
       a.out_tok[f * a.k + r] = tok;
@@ -511,53 +637,178 @@ __global__ __launch_bounds__(SMP_THREADS) void gumbel_topk_kernel(TopkArgs a) {
 }
 
 // ------------------------------------------------------------- categorical draws
-// One draw per row from p (any nonnegative row; normalisation is irrelevant to the argmax):
-// argmax_y p(y) / E(y), E from the DRAW stream with counter (y / 4, row).
-__global__ __launch_bounds__(SMP_THREADS) void sample_rows_kernel(const float* __restrict__ P, int64_t ldp, int V,
-                                                                  Rng rng, int* __restrict__ out_tok) {
+// One draw per row: argmax_y p(y) / E(y), E from the DRAW stream with counter (y / 4, row).
+__global__ __launch_bounds__(SMP_THREADS) void draw_chunk_kernel(const float* __restrict__ P, int64_t ldp, int V,
+                                                                 Rng rng, SmpWs ws) {
   __shared__ KeyIdx red[16];
-  const int row = blockIdx.x;
-  const float* p = P + (size_t)row * ldp;
+  const int row = blockIdx.y, c = blockIdx.x, t = threadIdx.x;
+  const int i = c * SMP_CHUNK + t * 4;
+  float v[4];
+  load4_f32(P + (size_t)row * ldp, i, V, v);
+  const U4 r = rng_block(rng, (uint32_t)(i >> 2), (uint32_t)row, TAG_DRAW);
   float best = -1.f;
-  int bi = 0x7fffffff;
-  for (int i = threadIdx.x * 4; i < V; i += 4 * SMP_THREADS) {
-    const U4 r = rng_block(rng, (uint32_t)(i >> 2), (uint32_t)row, TAG_DRAW);
+  int bi = NO_IDX;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if (i + e >= V) break;
-      const float pv = p[i + e];
-      if (!(pv > 0.f)) continue;
-      const float key = pv / exp1_from_bits(u4_get(r, e));
-      if (key > best) {
+  for (int e = 0; e < 4; ++e) {
+    if (i + e < V && v[e] > 0.f) {
+      const float key = v[e] / exp1_from_bits(u4_get(r, e));
+      if (better(key, i + e, best, bi)) {
         best = key;
         bi = i + e;
       }
     }
   }
   const KeyIdx w = block_argmax(best, bi, red);
-  if (threadIdx.x == 0) out_tok[row] = w.idx == 0x7fffffff ? 0 : w.idx;
+  if (t == 0) ws.arg[(size_t)row * ws.C + c] = w;
+}
+
+__device__ __forceinline__ KeyIdx merge_chunks(const KeyIdx* part, int C) {
+  KeyIdx b{-1.f, NO_IDX};
+  for (int c = 0; c < C; ++c)
+    if (better(part[c].key, part[c].idx, b.key, b.idx)) b = part[c];
+  return b;
+}
+
+__global__ void draw_merge_kernel(int rows, SmpWs ws, int* __restrict__ out_tok) {
+  const int row = blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= rows) return;
+  const KeyIdx b = merge_chunks(ws.arg + (size_t)row * ws.C, ws.C);
+  out_tok[row] = b.idx == NO_IDX ? 0 : b.idx;
 }
 
 // ----------------------------------------------------------- speculative acceptance
-// Per verify row (node `cur`, row cur + 1): the states the walk can reach at that node.
-// State j = after the first j children (rank order, q0(x) > 0) were rejected:
-//   q_0 = q0, q_j(y) = q0(y) [y not rejected] / zq[j] (zq[j] = sum q0 - sum of rejected q0),
+// Verify row r holds node cur = r - 1 (root: r = 0). State j of a node = after its first j
+// children (rank order, q0(x) > 0) were rejected:
+//   q_0 = q0, q_j(y) = q0(y) [y not rejected] / zq[j]  (zq[j] = sum q0 - sum of rejected q0),
 //   p_0 = p,  p_j = (p_{j-1} - q_{j-1})+ / zr[j] when zr[j] = sum (p_{j-1} - q_{j-1})+ > 0,
 //             p_j = p_{j-1} otherwise,
 // and bonus[j] = the categorical draw from p_j (one shared Exp(1) vector per round: only one
 // state's draw is ever used, and which one is decided by the acceptance uniforms alone).
-struct SampleState {
-  int n;     // children considered
-  int supp;  // |support of q0|
-  int kid[SMP_MAXK];
-  int bonus[SMP_MAXK + 1];
-  float zr[SMP_MAXK + 1];
-  float zq[SMP_MAXK + 1];
+// Pass j (one launch over all rows and chunks) produces the chunk partials of zr[j] and
+// bonus[j]; partials are combined in chunk order by whoever needs them (the next pass, the
+// walk), always by the same sequential loop, so every reader sees the same values.
+struct AcceptArgs {
+  SsdTree tree;
+  const float* P;
+  int64_t ldp;
+  const float* Q;
+  int64_t ldq;
+  int V;
+  int rows;      // verify rows in P and in the workspace
+  int max_kids;  // children considered per node (the launch runs this many rejection passes)
+  Rng rng;
+  SmpWs ws;
 };
 
-// p_j(y) for the state arrays above, evaluated at one column. `rej` holds the rejected
-// tokens x_1..x_{j} (only the first j entries are read); the walk and the state pass share
-// this code, so both see the same fp32 values.
+constexpr int SMP_MAXNODES = 63;  // verify nodes (rows = nodes + 1 <= 64)
+
+__device__ __forceinline__ int verify_nodes(const SsdTree& t) { return min(t.vmeta[0], SMP_MAXNODES); }
+
+struct NodeKids {
+  int n;
+  int kid[SMP_MAXK];
+  int tok[SMP_MAXK];
+};
+
+__device__ __forceinline__ const float* q_row(const AcceptArgs& a, int cur) {
+  return a.Q + (size_t)(cur < 0 ? 0 : 1 + a.tree.vorig[cur]) * a.ldq;
+}
+
+// Children of cur in rank order (ranks are distinct among siblings: they are draw order),
+// skipping those with q0(x) <= 0 (verify.py:77-78). One thread (the walk).
+__device__ __forceinline__ void node_kids(const AcceptArgs& a, int cur, NodeKids& k) {
+  const int vn = verify_nodes(a.tree);
+  const float* q0 = q_row(a, cur);
+  int cnt = 0, prev_rank = -1;
+  for (int s = 0; s < a.max_kids; ++s) {  // the next larger rank each time
+    int best = -1, best_rank = 0x7fffffff;
+    for (int v = 0; v < vn; ++v) {
+      const int rk = a.tree.vranks[v];
+      if (a.tree.vparents[v] == cur && rk > prev_rank && rk < best_rank) {
+        best = v;
+        best_rank = rk;
+      }
+    }
+    if (best < 0) break;
+    prev_rank = best_rank;
+    const int x = a.tree.vtokens[best];
+    if (q0[x] > 0.f) {
+      k.kid[cnt] = best;
+      k.tok[cnt] = x;
+      ++cnt;
+    }
+  }
+  k.n = cnt;
+}
+
+// The same list built by a whole workgroup (tree nodes staged in LDS; each child finds its
+// position by counting siblings of lower rank). Result in `k` (shared), valid after return.
+__device__ __forceinline__ void node_kids_block(const AcceptArgs& a, int cur, NodeKids& k, int* sh_par,
+                                                int* sh_rank, int* sh_pos) {
+  const int vn = verify_nodes(a.tree);
+  const int t = threadIdx.x;
+  if (t < vn) {
+    sh_par[t] = a.tree.vparents[t];
+    sh_rank[t] = a.tree.vranks[t];
+  }
+  if (t < SMP_MAXK) sh_pos[t] = -1;
+  __syncthreads();
+  if (t < vn && sh_par[t] == cur) {
+    int pos = 0;
+    for (int o = 0; o < vn; ++o) pos += sh_par[o] == cur && sh_rank[o] < sh_rank[t];
+    if (pos < SMP_MAXK) sh_pos[pos] = t;
+  }
+  __syncthreads();
+  if (t == 0) {
+    const float* q0 = q_row(a, cur);
+    int cnt = 0;
+    for (int i = 0; i < a.max_kids && sh_pos[i] >= 0; ++i) {
+      const int x = a.tree.vtokens[sh_pos[i]];
+      if (q0[x] > 0.f) {
+        k.kid[cnt] = sh_pos[i];
+        k.tok[cnt] = x;
+        ++cnt;
+      }
+    }
+    k.n = cnt;
+  }
+  __syncthreads();
+}
+
+struct StateScalars {
+  double s0;
+  int supp;
+  float zr[SMP_MAXK + 1];  // zr[j] for j >= 1 (0 when the residual had no mass)
+  float zq[SMP_MAXK + 1];  // zq[0] = 1
+};
+
+// Combine the chunk partials of row r: q0's mass and support, and states 1..upto. One thread;
+// the same sequential loops wherever the values are needed.
+__device__ __forceinline__ void combine_states(const AcceptArgs& a, int r, const float* q0, const NodeKids& k,
+                                               int upto, StateScalars& s) {
+  const int C = a.ws.C;
+  double s0 = 0.0;
+  int supp = 0;
+  for (int c = 0; c < C; ++c) {
+    s0 += a.ws.s0[(size_t)r * C + c];
+    supp += a.ws.supp[(size_t)r * C + c];
+  }
+  s.s0 = s0;
+  s.supp = supp;
+  s.zr[0] = 0.f;
+  s.zq[0] = 1.f;
+  double zq = s0;
+  for (int j = 1; j <= upto; ++j) {
+    double z = 0.0;
+    for (int c = 0; c < C; ++c) z += a.ws.zr[((size_t)r * (SMP_MAXK + 1) + j) * C + c];
+    s.zr[j] = z > 0.0 ? (float)z : 0.f;
+    zq -= (double)q0[k.tok[j - 1]];
+    s.zq[j] = (float)zq;
+  }
+}
+
+// p_j(y) for the state scalars, evaluated at one column. `rej` holds the rejected tokens
+// x_1..x_j (only the first j entries are read); the passes and the walk share this code.
 __device__ __forceinline__ float chain_p(float p0, float q0, int y, int j, const float* zr, const float* zq,
                                          const int* rej) {
   float pv = p0;
@@ -573,186 +824,137 @@ __device__ __forceinline__ float chain_p(float p0, float q0, int y, int j, const
   return pv;
 }
 
-struct AcceptArgs {
-  SsdTree tree;
-  const float* P;
-  int64_t ldp;
-  const float* Q;
-  int64_t ldq;
-  int V;
-  Rng rng;
-  SampleState* st;
-  int rows;
-};
-
-__global__ __launch_bounds__(SMP_THREADS) void sample_state_kernel(AcceptArgs a) {
+// Pass 0: bonus draw from p_0 per chunk; q0's mass and support per chunk.
+__global__ __launch_bounds__(SMP_THREADS) void state0_kernel(AcceptArgs a) {
   __shared__ KeyIdx red[16];
   __shared__ double red_d[16];
   __shared__ int red_i[16];
-  __shared__ int kid_sh[SMP_MAXK];
-  __shared__ int tok_sh[SMP_MAXK];
-  __shared__ int n_sh;
-  __shared__ float zr_sh[SMP_MAXK + 1], zq_sh[SMP_MAXK + 1];
-  __shared__ int bonus_sh[SMP_MAXK + 1];
-  const int r = blockIdx.x;
-  const int vn = a.tree.vmeta[0];
-  if (r > vn) return;
+  __shared__ int sh_par[64], sh_rank[64], sh_pos[SMP_MAXK];
+  __shared__ NodeKids kids;
+  const int r = blockIdx.y, c = blockIdx.x, t = threadIdx.x;
+  if (r > verify_nodes(a.tree)) return;
   const int cur = r - 1;
-  const int t = threadIdx.x;
-  // Children of cur in rank order (ranks are distinct among siblings: they are draw order).
-  if (t == 0) n_sh = 0;
-  __syncthreads();
-  int n_all = 0;
-  for (int v0 = 0; v0 < vn; v0 += SMP_THREADS) {
-    const int v = v0 + t;
-    const bool kid = v < vn && a.tree.vparents[v] == cur;
-    int pos = 0;
-    if (kid) {
-      const int rk = a.tree.vranks[v];
-      for (int o = 0; o < vn; ++o) pos += a.tree.vparents[o] == cur && a.tree.vranks[o] < rk;
-      if (pos < SMP_MAXK) kid_sh[pos] = v;
-    }
-    n_all += block_sum<int>(kid ? 1 : 0, red_i);
-  }
-  n_all = min(n_all, SMP_MAXK);
-  const float* p = a.P + (size_t)r * a.ldp;
-  const float* q0 = a.Q + (size_t)(cur < 0 ? 0 : 1 + a.tree.vorig[cur]) * a.ldq;
-  if (t == 0) {
-    int n = 0;
-    for (int i = 0; i < n_all; ++i) {
-      const int v = kid_sh[i];
-      const int x = a.tree.vtokens[v];
-      if (q0[x] > 0.f) {
-        kid_sh[n] = v;
-        tok_sh[n] = x;
-        ++n;
+  node_kids_block(a, cur, kids, sh_par, sh_rank, sh_pos);
+  const int i = c * SMP_CHUNK + t * 4;
+  float p[4];
+  load4_f32(a.P + (size_t)r * a.ldp, i, a.V, p);
+  const U4 rb = rng_block(a.rng, (uint32_t)(i >> 2), 0u, TAG_BONUS);
+  float best = -1.f;
+  int bi = NO_IDX;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if (i + e < a.V && p[e] > 0.f) {
+      const float key = p[e] / exp1_from_bits(u4_get(rb, e));
+      if (better(key, i + e, best, bi)) {
+        best = key;
+        bi = i + e;
       }
     }
-    n_sh = n;
   }
-  __syncthreads();
-  const int n = n_sh;
-  // Pass 0: draw from p_0; the support and mass of q0.
+  const KeyIdx w = block_argmax(best, bi, red);
   double s0 = 0.0;
   int supp = 0;
-  {
-    float best = -1.f;
-    int bi = 0x7fffffff;
-    for (int i = t * 4; i < a.V; i += 4 * SMP_THREADS) {
-      const U4 rb = rng_block(a.rng, (uint32_t)(i >> 2), 0u, TAG_BONUS);
+  if (kids.n > 0) {
+    float q[4];
+    load4_f32(q_row(a, cur), i, a.V, q);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int y = i + e;
-        if (y >= a.V) break;
-        const float pv = p[y];
-        if (pv > 0.f) {
-          const float key = pv / exp1_from_bits(u4_get(rb, e));
-          if (key > best) {
-            best = key;
-            bi = y;
-          }
-        }
-        if (n > 0) {
-          const float qv = q0[y];
-          s0 += qv;
-          supp += qv > 0.f;
-        }
-      }
+    for (int e = 0; e < 4; ++e) {
+      s0 += (double)q[e];
+      supp += q[e] > 0.f;
     }
-    const KeyIdx w = block_argmax(best, bi, red);
-    if (t == 0) {
-      bonus_sh[0] = w.idx == 0x7fffffff ? 0 : w.idx;
-      zr_sh[0] = 0.f;
-      zq_sh[0] = 1.f;
-    }
-  }
-  if (n > 0) {
     s0 = block_sum<double>(s0, red_d);
     supp = block_sum<int>(supp, red_i);
   }
-  if (t == 0 && n > 0) {
-    double zq = s0;
-    for (int j = 1; j <= n; ++j) {
-      zq -= (double)q0[tok_sh[j - 1]];
-      zq_sh[j] = (float)zq;
-    }
-  }
-  __syncthreads();
-  // Pass j: residual of state j-1 -> zr[j] and the draw from p_j.
-  for (int j = 1; j <= n; ++j) {
-    double zs = 0.0;
-    float best = -1.f;
-    int bi = 0x7fffffff;
-    for (int i = t * 4; i < a.V; i += 4 * SMP_THREADS) {
-      const U4 rb = rng_block(a.rng, (uint32_t)(i >> 2), 0u, TAG_BONUS);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int y = i + e;
-        if (y >= a.V) break;
-        const float qy = q0[y];
-        const float pprev = chain_p(p[y], qy, y, j - 1, zr_sh, zq_sh, tok_sh);
-        float qprev = qy;
-        if (j - 1 > 0) {
-          bool rj = false;
-          for (int u = 0; u < j - 1; ++u) rj |= tok_sh[u] == y;
-          qprev = rj ? 0.f : qy / zq_sh[j - 1];
-        }
-        const float res = fmaxf(pprev - qprev, 0.f);
-        zs += res;
-        if (res > 0.f) {
-          const float key = res / exp1_from_bits(u4_get(rb, e));
-          if (key > best) {
-            best = key;
-            bi = y;
-          }
-        }
-      }
-    }
-    zs = block_sum<double>(zs, red_d);
-    const KeyIdx w = block_argmax(best, bi, red);
-    if (t == 0) {
-      zr_sh[j] = zs > 0.0 ? (float)zs : 0.f;
-      bonus_sh[j] = zs > 0.0 && w.idx != 0x7fffffff ? w.idx : bonus_sh[j - 1];
-    }
-    __syncthreads();
-  }
   if (t == 0) {
-    SampleState* s = a.st + r;
-    s->n = n;
-    s->supp = n > 0 ? supp : 0;
-    for (int i = 0; i < SMP_MAXK; ++i) s->kid[i] = i < n ? kid_sh[i] : -1;
-    for (int j = 0; j <= SMP_MAXK; ++j) {
-      s->bonus[j] = j <= n ? bonus_sh[j] : 0;
-      s->zr[j] = j <= n ? zr_sh[j] : 0.f;
-      s->zq[j] = j <= n ? zq_sh[j] : 1.f;
-    }
+    const int C = a.ws.C;
+    a.ws.bon[((size_t)r * (SMP_MAXK + 1) + 0) * C + c] = w;
+    a.ws.s0[(size_t)r * C + c] = s0;
+    a.ws.supp[(size_t)r * C + c] = supp;
   }
 }
 
-// The walk of sample_verify over the precomputed states, then the same bookkeeping as the
-// greedy walk: result = [n_new, tokens...], compaction sources, next root token.
+// Pass j >= 1: residual of state j-1 -> chunk partials of zr[j] and of the draw from p_j.
+__global__ __launch_bounds__(SMP_THREADS) void statej_kernel(AcceptArgs a, int j) {
+  __shared__ KeyIdx red[16];
+  __shared__ double red_d[16];
+  __shared__ int sh_par[64], sh_rank[64], sh_pos[SMP_MAXK];
+  __shared__ NodeKids kids;
+  __shared__ StateScalars st;
+  const int r = blockIdx.y, c = blockIdx.x, t = threadIdx.x;
+  if (r > verify_nodes(a.tree)) return;
+  const int cur = r - 1;
+  node_kids_block(a, cur, kids, sh_par, sh_rank, sh_pos);
+  if (kids.n < j) return;  // uniform: this node has fewer children
+  const float* q0 = q_row(a, cur);
+  if (t == 0) combine_states(a, r, q0, kids, j - 1, st);
+  __syncthreads();
+  const int i = c * SMP_CHUNK + t * 4;
+  float p[4], q[4];
+  load4_f32(a.P + (size_t)r * a.ldp, i, a.V, p);
+  load4_f32(q0, i, a.V, q);
+  const U4 rb = rng_block(a.rng, (uint32_t)(i >> 2), 0u, TAG_BONUS);
+  double zs = 0.0;
+  float best = -1.f;
+  int bi = NO_IDX;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int y = i + e;
+    if (y >= a.V) continue;
+    const float pprev = chain_p(p[e], q[e], y, j - 1, st.zr, st.zq, kids.tok);
+    float qprev = q[e];
+    if (j - 1 > 0) {
+      bool rj = false;
+      for (int u = 0; u < j - 1; ++u) rj |= kids.tok[u] == y;
+      qprev = rj ? 0.f : q[e] / st.zq[j - 1];
+    }
+    const float res = fmaxf(pprev - qprev, 0.f);
+    zs += (double)res;
+    if (res > 0.f) {
+      const float key = res / exp1_from_bits(u4_get(rb, e));
+      if (better(key, y, best, bi)) {
+        best = key;
+        bi = y;
+      }
+    }
+  }
+  zs = block_sum<double>(zs, red_d);
+  const KeyIdx w = block_argmax(best, bi, red);
+  if (t == 0) {
+    const int C = a.ws.C;
+    a.ws.zr[((size_t)r * (SMP_MAXK + 1) + j) * C + c] = zs;
+    a.ws.bon[((size_t)r * (SMP_MAXK + 1) + j) * C + c] = w;
+  }
+}
+
+// The walk of sample_verify over the state scalars, then the same bookkeeping as the greedy
+// walk: result = [n_new, tokens...], compaction sources, next root token.
 __global__ void sample_walk_kernel(AcceptArgs a, int committed, int* result, int* keep_src, int* n_keep,
                                    int* root_token) {
   if (threadIdx.x != 0) return;
+  const int C = a.ws.C;
   int cur = -1, n_acc = 0, bonus = 0;
   int rej[SMP_MAXK];
+  NodeKids k;
+  StateScalars s;
   for (int step = 0; step <= SMP_MAXDEPTH; ++step) {
     const int r = cur + 1;
-    const SampleState& s = a.st[r];
+    if (r >= a.rows) break;  // a tree larger than the launch's rows (the engine never makes one)
+    node_kids(a, cur, k);
+    const float* q0 = q_row(a, cur);
     const float* p = a.P + (size_t)r * a.ldp;
-    const float* q0 = a.Q + (size_t)(cur < 0 ? 0 : 1 + a.tree.vorig[cur]) * a.ldq;
+    s.supp = 0;
+    s.zr[0] = 0.f;
+    s.zq[0] = 1.f;
+    if (k.n > 0) combine_states(a, r, q0, k, k.n, s);
     int chosen = -1, j = 0;
-    for (int i = 0; i < s.n; ++i) {
-      const int v = s.kid[i];
-      const int x = a.tree.vtokens[v];
+    for (int i = 0; i < k.n; ++i) {
+      const int x = k.tok[i];
       const float q0x = q0[x];
       const float pj = chain_p(p[x], q0x, x, j, s.zr, s.zq, rej);
       const float qj = j == 0 ? q0x : q0x / s.zq[j];
-      const U4 rb = rng_block(a.rng, (uint32_t)j, (uint32_t)r, TAG_ACCEPT);
-      const double u = uniform_from_bits(rb.x);
-      const float ratio = pj / qj;
-      if (u < (double)fminf(1.f, ratio)) {
-        chosen = v;
+      const double u = uniform_from_bits(rng_block(a.rng, (uint32_t)j, (uint32_t)r, TAG_ACCEPT).x);
+      if (u < (double)fminf(1.f, pj / qj)) {
+        chosen = k.kid[i];
         break;
       }
       rej[j] = x;
@@ -760,7 +962,10 @@ __global__ void sample_walk_kernel(AcceptArgs a, int committed, int* result, int
       if (j >= s.supp) break;  // no draft mass left
     }
     if (chosen < 0) {
-      bonus = s.bonus[j];
+      int jj = j;
+      while (jj > 0 && !(s.zr[jj] > 0.f)) --jj;  // p_j == p_{j-1} when the residual had no mass
+      const KeyIdx b = merge_chunks(a.ws.bon + ((size_t)r * (SMP_MAXK + 1) + jj) * C, C);
+      bonus = b.idx == NO_IDX ? 0 : b.idx;
       break;
     }
     result[1 + n_acc] = a.tree.vtokens[chosen];
@@ -782,78 +987,102 @@ using namespace ssd;
 SSD_API int ssd_sample_limits(int32_t* out2) {
   if (!out2) return set_error(SSD_EINVAL, "sample_limits: null");
   out2[0] = SMP_MAXK;
-  out2[1] = (int)sizeof(SampleState);
+  out2[1] = SMP_CHUNK * SMP_MAXC;
+  return SSD_OK;
+}
+
+SSD_API int64_t ssd_sample_ws_bytes(int rows, int n) {
+  if (rows < 0 || n <= 0 || chunks_of(n) > SMP_MAXC) return -1;
+  return smp_layout(rows, chunks_of(n), nullptr, nullptr);
+}
+
+static int carve(void* ws, int64_t ws_bytes, int rows, int n, SmpWs* out, const char* what) {
+  const int64_t need = ssd_sample_ws_bytes(rows, n);
+  if (need < 0) return set_error(SSD_ERANGE, "%s: %d columns > %d", what, n, SMP_CHUNK * SMP_MAXC);
+  if (!ws || ws_bytes < need)
+    return set_error(SSD_EINVAL, "%s: workspace %lld < %lld bytes", what, (long long)ws_bytes, (long long)need);
+  smp_layout(rows, chunks_of(n), (char*)ws, out);
   return SSD_OK;
 }
 
 SSD_API int ssd_warp_probs_bf16(const uint16_t* logits, int64_t ld, int rows, int n, const int32_t* vocab_ids,
                                 const int32_t* vocab_inv, int V, float temperature, float top_p,
-                                const int32_t* tree_meta, int level, float* probs, int64_t ldp, hipStream_t stream) {
+                                const int32_t* tree_meta, int level, float* probs, int64_t ldp, void* ws,
+                                int64_t ws_bytes, hipStream_t stream) {
   if (!logits || !probs || (vocab_ids && !vocab_inv)) return set_error(SSD_EINVAL, "warp_probs: null pointer");
-  if (rows < 0 || n <= 0 || V <= 0 || (!vocab_ids && n != V) || n > V || n > SMP_BINS * SMP_THREADS)
+  if (rows < 0 || n <= 0 || V <= 0 || (!vocab_ids && n != V) || n > V)
     return set_error(SSD_EINVAL, "warp_probs: bad shape rows=%d n=%d V=%d", rows, n, V);
   if (ld % 4 || ld < (n + 3) / 4 * 4 || ldp % 4 || ldp < V)
     return set_error(SSD_EINVAL, "warp_probs: ld %lld / ldp %lld must be multiples of 4 covering the row",
                      (long long)ld, (long long)ldp);
   if (!(temperature > 0.f)) return set_error(SSD_EINVAL, "warp_probs: temperature must be > 0");
   if (tree_meta && (level < 0 || level >= SMP_MAXDEPTH)) return set_error(SSD_ERANGE, "warp_probs: level %d", level);
+  if (rows > 65535) return set_error(SSD_ERANGE, "warp_probs: %d rows", rows);
   if (rows == 0) return SSD_OK;
-  WarpArgs a{logits, ld, rows, n, vocab_ids, vocab_inv, V, temperature, top_p, tree_meta, level, probs, ldp};
-  hipLaunchKernelGGL(warp_kernel, dim3(rows), dim3(SMP_THREADS), 0, stream, a);
+  SmpWs w;
+  if (int rc = carve(ws, ws_bytes, rows, V, &w, "warp_probs")) return rc;
+  const int C = chunks_of(n), CV = chunks_of(V);
+  w.C = C;  // stats / histograms are per logit chunk (the layout was sized for V >= n chunks)
+  const double tp = top_p < 0.f ? 0.0 : (double)top_p;
+  WarpArgs a{logits, ld, rows, n, vocab_ids, vocab_inv, V, temperature, top_p,
+             (uint64_t)fmin(tp * 0x1p52, 0x1p63), tree_meta, level, probs, ldp, w};
+  hipLaunchKernelGGL(warp_stats_kernel, dim3(C, rows), dim3(SMP_THREADS), 0, stream, a);
+  if (top_p < 1.f) {
+    hipLaunchKernelGGL(warp_coarse_kernel, dim3(C, rows), dim3(SMP_THREADS), 0, stream, a);
+    hipLaunchKernelGGL(warp_fine_kernel, dim3(C, rows), dim3(SMP_THREADS), 0, stream, a);
+  }
+  hipLaunchKernelGGL(warp_final_kernel, dim3(vocab_ids ? max(C, CV) : C, rows), dim3(SMP_THREADS), 0, stream, a);
   return check_launch("warp_probs");
 }
 
 SSD_API int ssd_gumbel_topk(const float* probs, int64_t ldp, int rows, int V, int k, const int32_t* tree_meta,
-                            int level, uint64_t seed, uint64_t counter, int32_t* out_tok, float* out_lp,
-                            hipStream_t stream) {
+                            int level, uint64_t seed, uint64_t counter, int32_t* out_tok, float* out_lp, void* ws,
+                            int64_t ws_bytes, hipStream_t stream) {
   if (!probs || !out_tok || !out_lp) return set_error(SSD_EINVAL, "gumbel_topk: null pointer");
   if (rows < 0 || V <= 0 || ldp % 4 || ldp < V) return set_error(SSD_EINVAL, "gumbel_topk: bad shape");
   if (k < 1 || k > SMP_MAXK) return set_error(SSD_ERANGE, "gumbel_topk: k=%d not in [1, %d]", k, SMP_MAXK);
   if (tree_meta && (level < 0 || level >= SMP_MAXDEPTH)) return set_error(SSD_ERANGE, "gumbel_topk: level %d", level);
   if (rows > 65535) return set_error(SSD_ERANGE, "gumbel_topk: %d rows", rows);
   if (rows == 0) return SSD_OK;
-  TopkArgs a{probs, ldp, rows, V, k, tree_meta, level, make_rng(seed, counter), out_tok, out_lp};
-  if (k <= 1)
-    hipLaunchKernelGGL(gumbel_topk_kernel<1>, dim3(rows), dim3(SMP_THREADS), 0, stream, a);
-  else if (k <= 2)
-    hipLaunchKernelGGL(gumbel_topk_kernel<2>, dim3(rows), dim3(SMP_THREADS), 0, stream, a);
-  else if (k <= 4)
-    hipLaunchKernelGGL(gumbel_topk_kernel<4>, dim3(rows), dim3(SMP_THREADS), 0, stream, a);
-  else if (k <= 8)
-    hipLaunchKernelGGL(gumbel_topk_kernel<8>, dim3(rows), dim3(SMP_THREADS), 0, stream, a);
-  else
-    hipLaunchKernelGGL(gumbel_topk_kernel<16>, dim3(rows), dim3(SMP_THREADS), 0, stream, a);
+  SmpWs w;
+  if (int rc = carve(ws, ws_bytes, rows, V, &w, "gumbel_topk")) return rc;
+  TopkArgs a{probs, ldp, rows, V, k, tree_meta, level, make_rng(seed, counter), out_tok, out_lp, w};
+  hipLaunchKernelGGL(gumbel_chunk_kernel, dim3(w.C, rows), dim3(SMP_THREADS), 0, stream, a);
+  hipLaunchKernelGGL(gumbel_merge_kernel, dim3(rows), dim3(SMP_THREADS), 0, stream, a);
   return check_launch("gumbel_topk");
 }
 
 SSD_API int ssd_sample_rows(const float* probs, int64_t ldp, int rows, int V, uint64_t seed, uint64_t counter,
-                            int32_t* out_tok, hipStream_t stream) {
+                            int32_t* out_tok, void* ws, int64_t ws_bytes, hipStream_t stream) {
   if (!probs || !out_tok) return set_error(SSD_EINVAL, "sample_rows: null pointer");
-  if (rows < 0 || V <= 0 || ldp < V) return set_error(SSD_EINVAL, "sample_rows: bad shape");
+  if (rows < 0 || V <= 0 || ldp % 4 || ldp < V) return set_error(SSD_EINVAL, "sample_rows: bad shape");
+  if (rows > 65535) return set_error(SSD_ERANGE, "sample_rows: %d rows", rows);
   if (rows == 0) return SSD_OK;
-  hipLaunchKernelGGL(sample_rows_kernel, dim3(rows), dim3(SMP_THREADS), 0, stream, probs, ldp, V,
-                     make_rng(seed, counter), out_tok);
+  SmpWs w;
+  if (int rc = carve(ws, ws_bytes, rows, V, &w, "sample_rows")) return rc;
+  hipLaunchKernelGGL(draw_chunk_kernel, dim3(w.C, rows), dim3(SMP_THREADS), 0, stream, probs, ldp, V,
+                     make_rng(seed, counter), w);
+  hipLaunchKernelGGL(draw_merge_kernel, dim3((rows + 63) / 64), dim3(64), 0, stream, rows, w, out_tok);
   return check_launch("sample_rows");
 }
 
-SSD_API int64_t ssd_sample_state_bytes(int rows) {
-  return rows < 0 ? -1 : (int64_t)rows * (int64_t)sizeof(SampleState);
-}
-
 SSD_API int ssd_accept_sample(const SsdTree* tree, const float* P, int64_t ldp, const float* Q, int64_t ldq, int V,
-                              int rows, uint64_t seed, uint64_t counter, void* state, int64_t state_bytes,
+                              int rows, int max_kids, uint64_t seed, uint64_t counter, void* ws, int64_t ws_bytes,
                               int committed, int32_t* result, int32_t* keep_src, int32_t* n_keep,
                               int32_t* root_token, hipStream_t stream) {
-  if (!tree || !P || !Q || !state || !result || !keep_src || !n_keep || !root_token)
+  if (!tree || !P || !Q || !result || !keep_src || !n_keep || !root_token)
     return set_error(SSD_EINVAL, "accept_sample: null pointer");
-  if (V <= 0 || ldp < V || ldq < V || rows < 1) return set_error(SSD_EINVAL, "accept_sample: bad shape");
-  if (state_bytes < ssd_sample_state_bytes(rows))
-    return set_error(SSD_EINVAL, "accept_sample: state workspace %lld < %lld bytes", (long long)state_bytes,
-                     (long long)ssd_sample_state_bytes(rows));
-  AcceptArgs a{*tree, P, ldp, Q, ldq, V, make_rng(seed, counter), (SampleState*)state, rows};
-  hipLaunchKernelGGL(sample_state_kernel, dim3(rows), dim3(SMP_THREADS), 0, stream, a);
-  if (int rc = check_launch("accept_sample/state")) return rc;
+  if (V <= 0 || ldp % 4 || ldq % 4 || ldp < V || ldq < V || rows < 1 || rows > 64)
+    return set_error(SSD_EINVAL, "accept_sample: bad shape (rows %d must be in [1, 64])", rows);
+  if (max_kids < 0 || max_kids > SMP_MAXK)
+    return set_error(SSD_ERANGE, "accept_sample: max_kids %d not in [0, %d]", max_kids, SMP_MAXK);
+  SmpWs w;
+  if (int rc = carve(ws, ws_bytes, rows, V, &w, "accept_sample")) return rc;
+  AcceptArgs a{*tree, P, ldp, Q, ldq, V, rows, max_kids, make_rng(seed, counter), w};
+  hipLaunchKernelGGL(state0_kernel, dim3(w.C, rows), dim3(SMP_THREADS), 0, stream, a);
+  for (int j = 1; j <= max_kids; ++j)
+    hipLaunchKernelGGL(statej_kernel, dim3(w.C, rows), dim3(SMP_THREADS), 0, stream, a, j);
   hipLaunchKernelGGL(sample_walk_kernel, dim3(1), dim3(64), 0, stream, a, committed, result, keep_src, n_keep,
                      root_token);
-  return check_launch("accept_sample/walk");
+  return check_launch("accept_sample");
 }

@@ -86,11 +86,12 @@ _PROTOS = {
     "ssd_qkv_rope_finalize_bf16": (I32, [P, I64, I64, I32, I32, I32, I32, I32, P, P, I64, P, P, P, I64, P, P, I64, P]),
     "ssd_add_rmsnorm_bf16": (I32, [P, I64, I64, I32, P, P, I64, I32, I32, P, F32, P, I64, P]),
     "ssd_sample_limits": (I32, [P]),
-    "ssd_warp_probs_bf16": (I32, [P, I64, I32, I32, P, P, I32, F32, F32, P, I32, P, I64, P]),
-    "ssd_gumbel_topk": (I32, [P, I64, I32, I32, I32, P, I32, U64, U64, P, P, P]),
-    "ssd_sample_rows": (I32, [P, I64, I32, I32, U64, U64, P, P]),
-    "ssd_sample_state_bytes": (I64, [I32]),
-    "ssd_accept_sample": (I32, [C.POINTER(SsdTree), P, I64, P, I64, I32, I32, U64, U64, P, I64, I32, P, P, P, P, P]),
+    "ssd_sample_ws_bytes": (I64, [I32, I32]),
+    "ssd_warp_probs_bf16": (I32, [P, I64, I32, I32, P, P, I32, F32, F32, P, I32, P, I64, P, I64, P]),
+    "ssd_gumbel_topk": (I32, [P, I64, I32, I32, I32, P, I32, U64, U64, P, P, P, I64, P]),
+    "ssd_sample_rows": (I32, [P, I64, I32, I32, U64, U64, P, P, I64, P]),
+    "ssd_accept_sample": (I32, [C.POINTER(SsdTree), P, I64, P, I64, I32, I32, I32, U64, U64, P, I64, I32, P, P, P, P,
+                                P]),
     "ssd_forward": (I32, [C.POINTER(SsdModel), C.POINTER(SsdPlan), C.POINTER(SsdBuffers), C.POINTER(SsdRows), I32,
                           I32, I32, I32, I32, P]),
 }

@@ -19,7 +19,7 @@ from typing import Optional
 
 import torch
 
-from ssd import _lib, ops
+from ssd import ops
 
 
 def new_seed() -> int:
@@ -39,7 +39,7 @@ class Sampler:
 
     ``Q`` [q_rows, V] fp32: warped draft distributions, row 0 for the root and 1 + i for tree
     node i (written while drafting, read by acceptance); ``P`` [p_rows, V] fp32: warped target
-    rows of the current verify pass; ``state``: per-row acceptance states.
+    rows of the current verify pass; ``ws``: the kernels' workspace (chunk partials, histograms).
     """
 
     def __init__(self, temperature: float, top_p: float, vocab: int, device, q_rows: int, p_rows: int,
@@ -53,7 +53,9 @@ class Sampler:
         f32 = dict(dtype=torch.float32, device=device)
         self.Q = torch.zeros(max(q_rows, 1), ld, **f32)
         self.P = torch.zeros(max(p_rows, 1), ld, **f32)
-        self.state = torch.zeros(ops.sample_state_bytes(max(p_rows, 1)), dtype=torch.uint8, device=device)
+        self.ws = torch.empty(ops.sample_ws_bytes(max(p_rows, q_rows, 1), self.vocab), dtype=torch.uint8,
+                              device=device)
+        self.max_kids = 1
 
     # ------------------------------------------------------------------ drafting
     def propose(self, draft, logits: torch.Tensor, rows: int, level: int, k: int, tree_meta: torch.Tensor,
@@ -63,23 +65,23 @@ class Sampler:
         children by Gumbel top-k."""
         n = logits.shape[1]
         ops.warp_probs(logits, rows, n, self.temperature, self.top_p, self.Q, V=self.vocab,
-                       vocab_ids=draft._vocab_ids_i32, vocab_inv=draft._vocab_inv, tree_meta=tree_meta, level=level)
+                       vocab_ids=draft._vocab_ids_i32, vocab_inv=draft._vocab_inv, tree_meta=tree_meta, level=level,
+                       ws=self.ws)
         ops.gumbel_topk(self.Q, rows, self.vocab, k, self.seed, self.counter, cand_tok, cand_lp,
-                        tree_meta=tree_meta, level=level)
+                        tree_meta=tree_meta, level=level, ws=self.ws)
 
     # --------------------------------------------------------------- verification
     def accept(self, tree, logits: torch.Tensor, m: int, committed: int, result: torch.Tensor,
                keep_src: torch.Tensor, n_keep: torch.Tensor, root_token: torch.Tensor) -> None:
         """sample_verify on the device: warp the m target rows into P, then the acceptance walk
         (writes the round record like ssd_accept_greedy)."""
-        ops.warp_probs(logits, m, self.vocab, self.temperature, self.top_p, self.P)
-        _lib.call("ssd_accept_sample", tree.struct, self.P.data_ptr(), self.P.stride(0), self.Q.data_ptr(),
-                  self.Q.stride(0), self.vocab, m, self.seed, self.counter, self.state.data_ptr(), self.state.numel(),
-                  committed, result.data_ptr(), keep_src.data_ptr(), n_keep.data_ptr(), root_token.data_ptr(),
-                  ops.stream())
+        ops.warp_probs(logits, m, self.vocab, self.temperature, self.top_p, self.P, ws=self.ws)
+        ops.accept_sample(tree.struct, self.P, self.Q, self.vocab, m, self.max_kids, self.seed, self.counter,
+                          committed, result, keep_src, n_keep, root_token, ws=self.ws)
 
     # ------------------------------------------------------------------ one draw
     def draw(self, logits: torch.Tensor, out_tok: torch.Tensor, counter: Optional[int] = None) -> None:
         """torch.multinomial(warp_probs(logits)) for one row of logits into out_tok[0]."""
-        ops.warp_probs(logits, 1, self.vocab, self.temperature, self.top_p, self.P)
-        ops.sample_rows(self.P, 1, self.vocab, self.seed, self.counter if counter is None else counter, out_tok)
+        ops.warp_probs(logits, 1, self.vocab, self.temperature, self.top_p, self.P, ws=self.ws)
+        ops.sample_rows(self.P, 1, self.vocab, self.seed, self.counter if counter is None else counter, out_tok,
+                        ws=self.ws)

@@ -173,6 +173,7 @@ class DecodeSession:
         if cfg.temperature != 0:
             self.sampler = Sampler(cfg.temperature, cfg.top_p, target.model.shape.vocab, dev,
                                    1 + drafter.max_tree_cache(), ROW_CAP_VERIFY, seed)
+            self.sampler.max_kids = max(drafter.branch)
         self.cache = target.new_cache(capacity)
         self.ws = draft.workspace(CHUNK)
         self.root_rows, self.level_rows, self.verify_rows = Rows(CHUNK, dev), Rows(CHUNK, dev), Rows(CHUNK, dev)

@@ -73,6 +73,7 @@ def sample_verify(tree: DraftTree, target_logits: torch.Tensor, temperature: flo
         raise ValueError(f"target_logits has {lg.shape[0]} rows, the tree needs {n + 1}")
     dev = lg.device
     sampler = Sampler(temperature, top_p, V, dev, 1 + n, n + 1, seed_from_generator(generator))
+    sampler.max_kids = max([tree.parents.count(p) for p in set(tree.parents)] + [1])
     for p in set(tree.parents):
         sampler.Q[0 if p == ROOT else 1 + p, :V] = torch.as_tensor(tree.child_q[p], device=dev).float()
     dt = DeviceTree(dev, cap=max(n, 1))

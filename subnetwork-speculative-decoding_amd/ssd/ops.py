@@ -275,8 +275,28 @@ def add_rmsnorm(part, s, ld, h, m, w, eps, out, bias=None):
 
 
 # ------------------------------------------------------------------------ sampling
+def sample_ws_bytes(rows: int, n: int) -> int:
+    b = int(_lib.load().ssd_sample_ws_bytes(rows, n))
+    if b < 0:
+        raise ValueError(f"sampling workspace: {n} columns beyond the compiled limit")
+    return b
+
+
+_SMP_WS: dict = {}
+
+
+def sample_ws(device, rows: int, n: int) -> torch.Tensor:
+    """A reusable workspace for the sampling kernels on ``device`` (grown on demand)."""
+    need = sample_ws_bytes(rows, n)
+    buf = _SMP_WS.get(str(device))
+    if buf is None or buf.numel() < need:
+        buf = torch.empty(need, dtype=torch.uint8, device=device)
+        _SMP_WS[str(device)] = buf
+    return buf
+
+
 def warp_probs(logits, rows, n, temperature, top_p, out, V=None, vocab_ids=None, vocab_inv=None, tree_meta=None,
-               level=0):
+               level=0, ws=None):
     """softmax(logits / T) + nucleus cut per row into fp32 ``out`` [*, V] (ssd_warp_probs_bf16)."""
     _check(logits, "logits"); _check(out, "probs", torch.float32)
     V = n if V is None else V
@@ -287,29 +307,43 @@ def warp_probs(logits, rows, n, temperature, top_p, out, V=None, vocab_ids=None,
         _check(tree_meta, "tree_meta", torch.int32)
     elif out.shape[0] < rows:
         raise ValueError(f"probs has {out.shape[0]} rows < {rows}")
+    ws = sample_ws(logits.device, rows, V) if ws is None else ws
     _lib.call("ssd_warp_probs_bf16", logits.data_ptr(), _rows(logits, "logits", n, rows), rows, n, _p(vocab_ids),
               _p(vocab_inv), V, float(temperature), float(top_p), _p(tree_meta), level, out.data_ptr(),
-              _rows(out, "probs", V), stream())
+              _rows(out, "probs", V), ws.data_ptr(), ws.numel(), stream())
     return out
 
 
-def gumbel_topk(probs, rows, V, k, seed, counter, out_tok, out_lp, tree_meta=None, level=0):
+def gumbel_topk(probs, rows, V, k, seed, counter, out_tok, out_lp, tree_meta=None, level=0, ws=None):
     _check(probs, "probs", torch.float32); _check(out_tok, "out_tok", torch.int32)
     _check(out_lp, "out_lp", torch.float32)
     _len(out_tok, "out_tok", rows * k); _len(out_lp, "out_lp", rows * k)
     if tree_meta is not None:
         _check(tree_meta, "tree_meta", torch.int32)
+    ws = sample_ws(probs.device, rows, V) if ws is None else ws
     _lib.call("ssd_gumbel_topk", probs.data_ptr(), _rows(probs, "probs", V), rows, V, k, _p(tree_meta), level,
-              seed & (2**64 - 1), counter & (2**64 - 1), out_tok.data_ptr(), out_lp.data_ptr(), stream())
+              seed & (2**64 - 1), counter & (2**64 - 1), out_tok.data_ptr(), out_lp.data_ptr(), ws.data_ptr(),
+              ws.numel(), stream())
 
 
-def sample_rows(probs, rows, V, seed, counter, out_tok):
+def sample_rows(probs, rows, V, seed, counter, out_tok, ws=None):
     _check(probs, "probs", torch.float32); _check(out_tok, "out_tok", torch.int32)
     _len(out_tok, "out_tok", rows)
+    ws = sample_ws(probs.device, rows, V) if ws is None else ws
     _lib.call("ssd_sample_rows", probs.data_ptr(), _rows(probs, "probs", V, rows), rows, V, seed & (2**64 - 1),
-              counter & (2**64 - 1), out_tok.data_ptr(), stream())
+              counter & (2**64 - 1), out_tok.data_ptr(), ws.data_ptr(), ws.numel(), stream())
     return out_tok
 
 
-def sample_state_bytes(rows: int) -> int:
-    return int(_lib.load().ssd_sample_state_bytes(rows))
+def accept_sample(tree_struct, P, Q, V, rows, max_kids, seed, counter, committed, result, keep_src, n_keep,
+                  root_token, ws=None):
+    """ssd_accept_sample: speculative-sampling walk over the finalized tree (P: warped target rows,
+    Q: warped draft rows at 1 + draft node index, row 0 the root)."""
+    _check(P, "P", torch.float32); _check(Q, "Q", torch.float32)
+    for t, name in ((result, "result"), (keep_src, "keep_src"), (n_keep, "n_keep"), (root_token, "root_token")):
+        _check(t, name, torch.int32)
+    ws = sample_ws(P.device, rows, V) if ws is None else ws
+    _lib.call("ssd_accept_sample", tree_struct, P.data_ptr(), _rows(P, "P", V, rows), Q.data_ptr(),
+              _rows(Q, "Q", V), V, rows, max_kids, seed & (2**64 - 1), counter & (2**64 - 1), ws.data_ptr(),
+              ws.numel(), committed, result.data_ptr(), keep_src.data_ptr(), n_keep.data_ptr(), root_token.data_ptr(),
+              stream())

@@ -93,6 +93,25 @@ def test_warp_ties_at_the_cut_keep_lower_columns():
     check_warp_rows(got, lg, 4000, 1.0, 0.6)
 
 
+def test_warp_tie_ranks_cross_chunks():
+    """A tie group spread over every 4096-column chunk of a 128256 row: the kept ties are the
+    lowest columns across chunks (per-chunk tie counts give the prefix)."""
+    V = 128256
+    g = torch.Generator().manual_seed(6)
+    x = torch.full((1, V), -3.0)
+    x[0, torch.randperm(V, generator=g)[:20]] = 2.0  # 20 leaders
+    ld = (V + 7) // 8 * 8
+    lg = torch.zeros(1, ld, dtype=torch.bfloat16)
+    lg[:, :V] = x.to(torch.bfloat16)
+    # leaders hold 20 e^5 / (20 e^5 + 128236) ~ 0.0225 of the mass; top_p 0.5 cuts deep into the
+    # -3 tie group, which spans all chunks
+    got = run_warp(lg, V, 1.0, 0.5)
+    check_warp_rows(got, lg, V, 1.0, 0.5)
+    kept_low = (got[0] > 0) & (x[0] < 0)
+    idx = kept_low.nonzero().flatten()
+    assert len(idx) > 4096 and torch.equal(idx, (x[0] < 0).nonzero().flatten()[:len(idx)])
+
+
 @pytest.mark.parametrize("top_p", [1.0, 0.9])
 def test_warp_vocab_subset_scatters_to_full_vocabulary(top_p):
     V, n = 5000, 1200
@@ -203,9 +222,8 @@ def device_tree(tokens, parents, ranks):
     return t
 
 
-def accept_on_gpu(tree, P, child_q, V, seed, ctr, rows_pad=0):
+def accept_on_gpu(tree, P, child_q, V, seed, ctr, rows_pad=0, max_kids=16):
     """ssd_accept_sample with Q rows at 1 + node (row 0 the root)."""
-    from ssd import _lib
     from ssd import ops as o
 
     ld = (V + 3) // 4 * 4
@@ -215,14 +233,10 @@ def accept_on_gpu(tree, P, child_q, V, seed, ctr, rows_pad=0):
     Qd = torch.zeros(m, ld, device=DEV)
     for p, q in child_q.items():
         Qd[0 if p == -1 else 1 + p, :V] = q.to(DEV)
-    state = torch.zeros(o.sample_state_bytes(m), dtype=torch.uint8, device=DEV)
-    result = torch.zeros(40, dtype=torch.int32, device=DEV)
-    keep = torch.zeros(40, dtype=torch.int32, device=DEV)
-    nk = torch.zeros(1, dtype=torch.int32, device=DEV)
-    root = torch.zeros(1, dtype=torch.int32, device=DEV)
-    _lib.call("ssd_accept_sample", tree.struct, Pd.data_ptr(), ld, Qd.data_ptr(), ld, V, m, seed, ctr,
-              state.data_ptr(), state.numel(), 0, result.data_ptr(), keep.data_ptr(), nk.data_ptr(),
-              root.data_ptr(), o.stream())
+    i32 = dict(dtype=torch.int32, device=DEV)
+    result, keep = torch.zeros(40, **i32), torch.zeros(40, **i32)
+    nk, root = torch.zeros(1, **i32), torch.zeros(1, **i32)
+    o.accept_sample(tree.struct, Pd, Qd, V, m, max_kids, seed, ctr, 0, result, keep, nk, root)
     r = result.tolist()
     n_new = r[0]
     accepted = [x - 1 for x in keep[1:n_new].tolist()]
@@ -285,7 +299,6 @@ def test_first_committed_token_is_target_distributed(top_p):
     target + N(0, 1), T = 0.7; the root proposes 4 children by ssd_gumbel_topk, then
     ssd_accept_sample. Over 4000 rounds (fresh counters) the first committed token must follow
     warp(target) (chi-square, bins with expected count >= 5, the rest pooled)."""
-    from ssd import _lib
     from ssd import ops as o
 
     V, T, k, N = 128256, 0.7, 4, 4000
@@ -308,18 +321,14 @@ def test_first_committed_token_is_target_distributed(top_p):
     t = device_tree([0] * k, [-1] * k, list(range(k)))
     tok = torch.zeros(k, dtype=torch.int32, device=DEV)
     lp = torch.zeros(k, device=DEV)
-    state = torch.zeros(o.sample_state_bytes(k + 1), dtype=torch.uint8, device=DEV)
-    result = torch.zeros(8, dtype=torch.int32, device=DEV)
-    keep = torch.zeros(8, dtype=torch.int32, device=DEV)
-    nk = torch.zeros(1, dtype=torch.int32, device=DEV)
-    root = torch.zeros(1, dtype=torch.int32, device=DEV)
+    i32 = dict(dtype=torch.int32, device=DEV)
+    result, keep = torch.zeros(8, **i32), torch.zeros(8, **i32)
+    nk, root = torch.zeros(1, **i32), torch.zeros(1, **i32)
     first = torch.zeros(N, dtype=torch.int32, device=DEV)
     for n in range(N):
         o.gumbel_topk(Q, 1, V, k, 2024, n, tok, lp)
         t.vtokens[:k].copy_(tok)
-        _lib.call("ssd_accept_sample", t.struct, P.data_ptr(), ldp, Q.data_ptr(), ldp, V, k + 1, 2024, n,
-                  state.data_ptr(), state.numel(), 0, result.data_ptr(), keep.data_ptr(), nk.data_ptr(),
-                  root.data_ptr(), o.stream())
+        o.accept_sample(t.struct, P, Q, V, k + 1, k, 2024, n, 0, result, keep, nk, root)
         first[n:n + 1].copy_(result[1:2])
     first = first.cpu().numpy()
     p = P[0, :V].double().cpu().numpy()

@@ -164,3 +164,20 @@ def test_first_token_is_target_distributed(top_p, residual):
     assert len(ex) >= 4  # several tokens survive the warp, so the test has power
     pv = stats.chisquare(obs, ex).pvalue
     assert pv > 1e-3 if residual else pv < 1e-6
+
+
+def test_warp64_checker_agrees_with_fp32_rule():
+    """The float64 statement used to check the kernel: same kept set as the fp32 restatement away
+    from the boundary band, same values to fp32 precision, and the hand-derived tie case."""
+    g = torch.Generator().manual_seed(1)
+    for top_p in (1.0, 0.9, 0.3):
+        lg = (torch.randn(6, 3000, generator=g) * 2).to(torch.bfloat16).float()
+        for row in lg:
+            p32, _ = osm.warp_probs(row, 0.8, top_p)
+            p64, kept, band = osm.warp_probs64(row, 0.8, top_p)
+            assert not ((p32 > 0) != kept)[~band].any()
+            if not band.any():
+                torch.testing.assert_close(p64[kept] / (p64[kept].sum() if top_p < 1 else 1.0),
+                                           p32[kept].double(), rtol=1e-5, atol=0)
+    p64, kept, band = osm.warp_probs64(torch.zeros(4), 1.0, 0.3)
+    assert kept.tolist() == [True, True, False, False] and not band.any()
