@@ -118,27 +118,29 @@ def kernel_figures(gen, sess) -> dict:
 
     def qkv(i):
         kc, vt = cache.layer(i)
-        ops.qkv_rope(ws.x, m, L[i].wqkv, s.hidden, s.heads, s.kv_heads, s.head_dim, cos, sin, rows.pos, rows.slot,
-                     ws.q, kc, vt, cache.capacity)
+        ops.qkv_rope(ws.h, m, L[i].wqkv, s.hidden, s.heads, s.kv_heads, s.head_dim, cos, sin, rows.pos, rows.slot,
+                     ws.q, kc, vt, cache.capacity, norm_eps=s.eps)
 
     fig("gemm_qkv_rope", time_launches(qkv, nl), n_qkv * s.hidden * 2 + m * s.hidden * 2 + m * n_qkv * 2)
 
     def gateup(i):
-        ops.gemm_swiglu(ws.x, m, L[i].wgu, s.inter, s.hidden, ws.mlp)
+        ops.gemm_swiglu(ws.h, m, L[i].wgu, s.inter, s.hidden, ws.mlp, norm_eps=s.eps)
 
     fig("gemm_gate_up", time_launches(gateup, nl), 2 * s.inter * s.hidden * 2 + m * s.hidden * 2 + m * s.inter * 2,
         flops=2 * m * 2 * s.inter * s.hidden)
 
+    h_scratch = ws.h.clone()  # the residual projection updates h in place
+
     def down(i):
-        ops.gemm_partial(ws.mlp, m, L[i].wd, s.hidden, s.inter, part)
+        ops.gemm_residual(ws.mlp, m, L[i].wd, s.hidden, s.inter, h_scratch, part)
 
     sp = ops.gemm_splits(s.hidden, s.inter)
-    fig("gemm_down_partial", time_launches(down, nl),
-        s.hidden * s.inter * 2 + m * s.inter * 2 + sp * m * s.hidden * 4, splits=sp)
+    fig("gemm_down_residual", time_launches(down, nl),
+        s.hidden * s.inter * 2 + m * s.inter * 2 + 2 * m * s.hidden * 2, splits=sp)
     logits = ws.logits_buf(m, s.vocab)
 
     def head(i):
-        ops.gemm(ws.x, m, model.lm_head, s.vocab, s.hidden, logits)
+        ops.gemm(ws.h, m, model.lm_head, s.vocab, s.hidden, logits, norm_eps=s.eps)
 
     fig("lm_head", time_launches(head, 4), s.vocab * s.hidden * 2 + m * s.hidden * 2 + m * s.vocab * 2)
     n = gen.cfg.depth + 1

@@ -44,31 +44,39 @@ int ssd_device_arch(char* buf, int len); /* host buffer; gcnArchName of the curr
  * modules). */
 int64_t ssd_packed_weight_elems(int N, int K);
 int ssd_gemm_weight_group(int N, int K); /* 1, 2, 4 or 8; 0 on a bad shape */
+/* col_scale [K] (may be NULL): each column k is multiplied by col_scale[k] and rounded once to
+ * bf16 -- the RMSNorm weight folded into the projection that consumes the norm
+ * (modeling_llama RMSNorm `weight * hidden` at :66-67; bridge RMSNorm ssd/models/bridges.py:33-37). */
 int ssd_pack_weight_bf16(const uint16_t* src, int64_t ld, int N_src, int K, const int32_t* row_map, int N_packed,
-                         int group, uint16_t* dst, hipStream_t stream);
+                         int group, const uint16_t* col_scale, uint16_t* dst, hipStream_t stream);
 
 /* ---------------------------------------------------------------- GEMMs
  * Y = act(X W^T + bias) [+ residual] with bf16 rounding after each step; Y may alias residual.
  * Replaces F.linear / nn.Linear at ssd/models/subnetwork_draft.py:243 (o_proj + residual),
  * :349 (lm_head and vocab-subset head) and the bridge linears ssd/models/bridges.py:53-54,131-135.
- * act: 0 none, 1 silu, 2 gelu, 3 relu. Batch-invariant: a row's result does not depend on M. */
-int ssd_gemm_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int N, int K, uint16_t* Y,
-                  int64_t ldy, const uint16_t* bias, int act, const uint16_t* residual, int64_t ldr,
+ * act: 0 none, 1 silu, 2 gelu, 3 relu. Batch-invariant: a row's result does not depend on M.
+ * norm_eps > 0 folds the RMSNorm that precedes the projection (modeling_llama.py:53-67,
+ * ssd/models/bridges.py:27-37): X is the un-normalised residual stream h, W was packed with the
+ * norm weight as col_scale, and every output of row m is scaled by rsqrt(mean(h_m^2) + norm_eps)
+ * (the row's sum of squares is accumulated from the X fragments the GEMM streams anyway).
+ * norm_eps = 0: plain GEMM. The same flag exists on the SwiGLU and q/k/v GEMMs. */
+int ssd_gemm_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int N, int K, float norm_eps,
+                  uint16_t* Y, int64_t ldy, const uint16_t* bias, int act, const uint16_t* residual, int64_t ldr,
                   hipStream_t stream);
 
 /* Y[M, I] = silu(X Wg^T + bg) * (X Wu^T + bu), gate/up interleaved per 16-row tile.
  * Replaces LlamaMLP's gate/up/act (modeling_llama MLP called at ssd/models/subnetwork_draft.py:245)
  * and the swiglu bridge (ssd/models/bridges.py:57-65). */
 int ssd_gemm_swiglu_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int I, int K,
-                         uint16_t* Y, int64_t ldy, const uint16_t* bias_gate, const uint16_t* bias_up,
-                         hipStream_t stream);
+                         float norm_eps, uint16_t* Y, int64_t ldy, const uint16_t* bias_gate,
+                         const uint16_t* bias_up, hipStream_t stream);
 
 /* q/k/v projection + RoPE + KV-cache write, fused. Replaces ssd/models/subnetwork_draft.py:209-222
  * (q/k/v_proj, rotate_half RoPE, KVCache.update at ssd/engine/kv_cache.py:32-43). Row m is at
  * rotary position row_pos[m] (cos/sin tables [rope_rows, hd/2]) and writes cache slot row_slot[m]
  * (rows whose slot is outside [0, max_len) are not written); V is stored transposed. */
-int ssd_gemm_qkv_rope_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int K, int heads,
-                           int kv_heads, int head_dim, const uint16_t* cos_tab, const uint16_t* sin_tab,
+int ssd_gemm_qkv_rope_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int K, float norm_eps,
+                           int heads, int kv_heads, int head_dim, const uint16_t* cos_tab, const uint16_t* sin_tab,
                            int64_t rope_rows, const int32_t* row_pos, const int32_t* row_slot, uint16_t* Q, int64_t ldq,
                            uint16_t* k_cache, uint16_t* vt_cache, int64_t max_len, hipStream_t stream);
 
@@ -98,6 +106,16 @@ int ssd_qkv_rope_finalize_bf16(const float* P, int64_t ldp, int64_t split_stride
 int ssd_add_rmsnorm_bf16(const float* P, int64_t ldp, int64_t split_stride, int S, const uint16_t* bias, uint16_t* h,
                          int64_t ldh, int M, int D, const uint16_t* w, float eps, uint16_t* y, int64_t ldy,
                          hipStream_t stream);
+/* Projection + residual add (ssd/models/subnetwork_draft.py:243, :245 residual adds;
+ * ssd/models/bridges.py:131-135 bridge residual): h[:M] <- bf16(h + bf16(X W^T + bias)). By shape:
+ * one direct GEMM with the add in its epilogue, or (long K) split-K partials plus a finalize that
+ * adds -- W packed with group = ssd_gemm_residual_group(N, K); part: fp32 scratch of
+ * ssd_gemm_residual_floats(M, N, K) floats (0 when the direct form is used). */
+int ssd_gemm_residual_group(int N, int K);
+int64_t ssd_gemm_residual_floats(int M, int N, int K);
+int ssd_gemm_residual_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int N, int K,
+                           const uint16_t* bias, uint16_t* h, int64_t ldh, float* part, int64_t part_floats,
+                           hipStream_t stream);
 
 /* ------------------------------------------------------------ tree attention
  * Row t attends cache slots [0, prefix[t]) then anc[t][0..depth[t]) (ancestors in depth order,
@@ -232,9 +250,9 @@ int ssd_accept_sample(const SsdTree* tree, const float* P, int64_t ldp, const fl
  * Descriptors of one model forward; every pointer is device memory in the formats above
  * (weights packed by ssd_pack_weight_bf16). Host structs, read during the call only. */
 typedef struct SsdLayerW {    /* one decoder layer */
-  const uint16_t* wqkv;       /* q/k/v fused, rotary-paired rows */
+  const uint16_t* wqkv;       /* q/k/v fused, rotary-paired rows, ln1 folded in (col_scale) */
   const uint16_t* wo;
-  const uint16_t* wgu;        /* gate/up interleaved per 16-row tile */
+  const uint16_t* wgu;        /* gate/up interleaved per 16-row tile, ln2 folded in */
   const uint16_t* wd;
   const uint16_t* ln1;        /* input RMSNorm weight [hidden] */
   const uint16_t* ln2;        /* post-attention RMSNorm weight [hidden] */
@@ -255,7 +273,8 @@ typedef struct SsdBridgeW {   /* x + MLP(RMSNorm(x)) */
   const uint16_t* norm;
   float eps;
   int32_t hidden, swiglu, n_body;
-  const uint16_t* body_w[2];  /* plain MLP: n_body linears with bias + activation */
+  const uint16_t* body_w[2];  /* plain MLP: n_body linears with bias + activation; the norm is
+                                 folded into body_w[0] (or into gu for swiglu) */
   const uint16_t* body_b[2];
   int32_t body_n[2], body_act[2];
   const uint16_t* gu;         /* swiglu: packed gate/up and biases */
@@ -270,7 +289,8 @@ typedef struct SsdPlan {      /* which layers run, with which bridges, and which
   const int32_t* layer_ids;          /* host [n_steps] */
   const SsdBridgeW* const* pre_bridge; /* host [n_steps], NULL entries = none; NULL = no bridges */
   const SsdBridgeW* pre_norm;        /* bridge before the final norm, or NULL */
-  const uint16_t* head_w;            /* packed lm_head (full or vocabulary subset), or NULL */
+  const uint16_t* head_w;            /* packed lm_head (full or vocabulary subset) with the final
+                                        norm folded in, or NULL */
   int32_t head_n;
 } SsdPlan;
 

@@ -3,30 +3,17 @@
 // host calls instead of one per kernel.
 //
 // Order per selected layer (ssd/models/subnetwork_draft.py:193-246 and :315-351 in the
-// reference), with each residual add fused with the RMSNorm that follows it:
-//   [bridge: body GEMMs -> out_proj partials -> h += out, x = ln1(h)]
-//   q/k/v GEMM with RoPE + KV write in its epilogue -> tree attention (+ combine)
-//   -> o partials -> h += o, x = ln2(h) -> gate/up GEMM + SwiGLU
-//   -> down partials -> h += down, x = <next norm>(h)
-// where <next norm> is the next bridge's norm, the next layer's ln1, the pre-norm bridge's norm
-// or the final norm; then the head over the final-normed rows.
+// reference). Every RMSNorm is folded into the projection that consumes it (its weight is in the
+// packed columns, the row scale is computed inside the GEMM from the rows it streams), and every
+// residual add is fused into the projection that produces it, so h is the only activation that
+// moves between sub-layers (a long-K projection runs as split-K partials plus a finalize that adds):
+//   [bridge: body GEMMs (bridge norm folded) -> out_proj, h += out]
+//   q/k/v GEMM (ln1 folded) with RoPE + KV write in its epilogue -> tree attention (+ combine)
+//   -> o_proj, h += o -> gate/up GEMM (ln2 folded) + SwiGLU -> down_proj, h += down
+// then the head over h (final norm folded).
 #include "common.h"
 
 namespace ssd {
-
-struct NormRef {
-  const uint16_t* w;
-  float eps;
-};
-
-// The RMSNorm applied to h before plan step `st` (st == n_steps: before the head).
-static NormRef norm_before(const SsdModel* md, const SsdPlan* plan, int st) {
-  if (st < plan->n_steps) {
-    if (plan->pre_bridge && plan->pre_bridge[st]) return {plan->pre_bridge[st]->norm, plan->pre_bridge[st]->eps};
-    return {md->layers[plan->layer_ids[st]].ln1, md->eps};
-  }
-  return {md->norm, md->eps};
-}
 
 struct Fwd {
   const SsdModel* md;
@@ -34,40 +21,25 @@ struct Fwd {
   int m, d;
   hipStream_t s;
 
-  // Split-K partials of X W^T into buf->part; returns the split count (or a negative error).
-  int partials(const uint16_t* X, int64_t ldx, const uint16_t* W, int N, int K, int64_t* ldp) {
-    const int S = ssd_gemm_splits(N, K);
-    if (S < 1) return -1;
-    *ldp = (N + 63) / 64 * 64;
-    if ((int64_t)S * m * *ldp > buf->part_floats)
-      return -set_error(SSD_EINVAL, "forward: partial buffer of %lld floats < %lld", (long long)buf->part_floats,
-                        (long long)S * m * *ldp);
-    const int rc = ssd_gemm_partial_bf16(X, ldx, m, W, N, K, buf->part, *ldp, (int64_t)m * *ldp, s);
-    return rc ? -rc : S;
+  // h += X W^T (+ bias), one launch.
+  int residual(const uint16_t* X, int64_t ldx, const uint16_t* W, int K, const uint16_t* bias) {
+    return ssd_gemm_residual_bf16(X, ldx, m, W, d, K, bias, buf->h, d, buf->part, buf->part_floats, s);
   }
 
-  // h += X W^T (+ bias), then x = RMSNorm(h) with `next`.
-  int residual(const uint16_t* X, int64_t ldx, const uint16_t* W, int K, const uint16_t* bias, NormRef next) {
-    int64_t ldp;
-    const int S = partials(X, ldx, W, d, K, &ldp);
-    if (S < 0) return -S;
-    return ssd_add_rmsnorm_bf16(buf->part, ldp, (int64_t)m * ldp, S, bias, buf->h, d, m, d, next.w, next.eps, buf->x,
-                                d, s);
-  }
-
-  // Bridge on x = its norm(h): body, then h += out_proj(...), x = next(h).
-  int bridge(const SsdBridgeW* b, NormRef next) {
+  // Bridge: body on RMSNorm(h) (folded into its first GEMM), then h += out_proj(...).
+  int bridge(const SsdBridgeW* b) {
     const int widest = b->swiglu ? b->hidden : (b->n_body > 0 ? b->body_n[b->n_body - 1] : 0);
     if (b->n_body < 0 || b->n_body > 2 || (!b->swiglu && b->n_body == 0))
       return set_error(SSD_EINVAL, "forward: bridge with %d body linears", b->n_body);
+    if (!(b->eps > 0.f)) return set_error(SSD_EINVAL, "forward: bridge norm eps must be > 0");
     for (int i = 0; i < (b->swiglu ? 0 : b->n_body); ++i)
       if (b->body_n[i] > buf->mid_cols) return set_error(SSD_EINVAL, "forward: bridge width %d > %d", b->body_n[i], buf->mid_cols);
     if (widest > buf->mid_cols) return set_error(SSD_EINVAL, "forward: bridge width %d > %d", widest, buf->mid_cols);
-    const uint16_t* cur = buf->x;
+    const uint16_t* cur = buf->h;
     int64_t ldc = d;
     int kin = d, rc;
     if (b->swiglu) {
-      rc = ssd_gemm_swiglu_bf16(buf->x, d, m, b->gu, b->hidden, d, buf->mid0, buf->mid_cols, b->bg, b->bu, s);
+      rc = ssd_gemm_swiglu_bf16(buf->h, d, m, b->gu, b->hidden, d, b->eps, buf->mid0, buf->mid_cols, b->bg, b->bu, s);
       if (rc) return rc;
       cur = buf->mid0;
       ldc = buf->mid_cols;
@@ -75,15 +47,15 @@ struct Fwd {
     } else {
       for (int i = 0; i < b->n_body; ++i) {
         uint16_t* dst = (i % 2) ? buf->mid1 : buf->mid0;
-        rc = ssd_gemm_bf16(cur, ldc, m, b->body_w[i], b->body_n[i], kin, dst, buf->mid_cols, b->body_b[i],
-                           b->body_act[i], nullptr, 0, s);
+        rc = ssd_gemm_bf16(cur, ldc, m, b->body_w[i], b->body_n[i], kin, i == 0 ? b->eps : 0.f, dst, buf->mid_cols,
+                           b->body_b[i], b->body_act[i], nullptr, 0, s);
         if (rc) return rc;
         cur = dst;
         ldc = buf->mid_cols;
         kin = b->body_n[i];
       }
     }
-    return residual(cur, ldc, b->out, kin, b->out_b, next);
+    return residual(cur, ldc, b->out, kin, b->out_b);
   }
 };
 
@@ -102,6 +74,7 @@ SSD_API int ssd_forward(const SsdModel* md, const SsdPlan* plan, const SsdBuffer
     return set_error(SSD_EINVAL, "forward: head of %d columns into logits rows of %lld", plan->head_n,
                      (long long)buf->ld_logits);
   if (!md->layers || (plan->n_steps > 0 && !plan->layer_ids)) return set_error(SSD_EINVAL, "forward: null layer table");
+  if (!(md->eps > 0.f)) return set_error(SSD_EINVAL, "forward: norm eps must be > 0");
   for (int st = 0; st < plan->n_steps; ++st)
     if (plan->layer_ids[st] < 0 || plan->layer_ids[st] >= md->n_layers)
       return set_error(SSD_EINVAL, "forward: layer %d", plan->layer_ids[st]);
@@ -111,36 +84,29 @@ SSD_API int ssd_forward(const SsdModel* md, const SsdPlan* plan, const SsdBuffer
   Fwd f{md, buf, m, d, s};
   int rc = ssd_embed_bf16(rows->ids, m, md->embed, md->vocab, d, buf->h, d, s);
   if (rc) return rc;
-  // x = the first norm of h (first bridge's, first layer's ln1, or the final one)
-  const NormRef first = plan->n_steps ? norm_before(md, plan, 0)
-                                      : (plan->pre_norm ? NormRef{plan->pre_norm->norm, plan->pre_norm->eps}
-                                                        : NormRef{md->norm, md->eps});
-  if ((rc = ssd_add_rmsnorm_bf16(nullptr, 0, 0, 0, nullptr, buf->h, d, m, d, first.w, first.eps, buf->x, d, s)))
-    return rc;
   for (int st = 0; st < plan->n_steps; ++st) {
     const int li = plan->layer_ids[st];
     const SsdLayerW& L = md->layers[li];
-    if (plan->pre_bridge && plan->pre_bridge[st] && (rc = f.bridge(plan->pre_bridge[st], {L.ln1, md->eps})))
-      return rc;
+    if (plan->pre_bridge && plan->pre_bridge[st] && (rc = f.bridge(plan->pre_bridge[st]))) return rc;
     uint16_t* kc = buf->k_arena + li * layer_elems;
     uint16_t* vt = buf->vt_arena + li * layer_elems;
-    if ((rc = ssd_gemm_qkv_rope_bf16(buf->x, d, m, L.wqkv, d, H, KV, hd, md->cos, md->sin, md->rope_rows, rows->pos,
-                                     rows->slot, buf->q, qdim, kc, vt, buf->cache_cap, s)))
+    if ((rc = ssd_gemm_qkv_rope_bf16(buf->h, d, m, L.wqkv, d, md->eps, H, KV, hd, md->cos, md->sin, md->rope_rows,
+                                     rows->pos, rows->slot, buf->q, qdim, kc, vt, buf->cache_cap, s)))
       return rc;
     if ((rc = ssd_tree_attention_bf16(buf->q, qdim, m, H, KV, hd, kc, vt, buf->cache_cap, rows->prefix, rows->depth,
                                       rows->anc, p_min, l_max, md->attn_scale, buf->attn_ws, buf->attn_ws_floats,
                                       buf->attn, qdim, s)))
       return rc;
-    if ((rc = f.residual(buf->attn, qdim, L.wo, (int)qdim, nullptr, {L.ln2, md->eps}))) return rc;
-    if ((rc = ssd_gemm_swiglu_bf16(buf->x, d, m, L.wgu, md->inter, d, buf->mlp, md->inter, nullptr, nullptr, s))) return rc;
-    NormRef next = norm_before(md, plan, st + 1);
-    if (st + 1 == plan->n_steps && plan->pre_norm) next = {plan->pre_norm->norm, plan->pre_norm->eps};
-    if ((rc = f.residual(buf->mlp, md->inter, L.wd, md->inter, nullptr, next))) return rc;
+    if ((rc = f.residual(buf->attn, qdim, L.wo, (int)qdim, nullptr))) return rc;
+    if ((rc = ssd_gemm_swiglu_bf16(buf->h, d, m, L.wgu, md->inter, d, md->eps, buf->mlp, md->inter, nullptr, nullptr,
+                                   s)))
+      return rc;
+    if ((rc = f.residual(buf->mlp, md->inter, L.wd, md->inter, nullptr))) return rc;
   }
-  if (plan->pre_norm && (rc = f.bridge(plan->pre_norm, {md->norm, md->eps}))) return rc;
+  if (plan->pre_norm && (rc = f.bridge(plan->pre_norm))) return rc;
   if (head_rows > 0 && plan->head_w) {
-    rc = ssd_gemm_bf16(buf->x + (size_t)head_first * d, d, head_rows, plan->head_w, plan->head_n, d, buf->logits,
-                       buf->ld_logits, nullptr, 0, nullptr, 0, s);
+    rc = ssd_gemm_bf16(buf->h + (size_t)head_first * d, d, head_rows, plan->head_w, plan->head_n, d, md->eps,
+                       buf->logits, buf->ld_logits, nullptr, 0, nullptr, 0, s);
     if (rc) return rc;
   }
   return SSD_OK;

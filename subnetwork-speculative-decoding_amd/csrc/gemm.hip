@@ -60,6 +60,9 @@ struct GemmArgs {
   bf16_t* k_cache;        // this layer: [kv_heads, max_len, head_dim]
   bf16_t* vt_cache;       // this layer: [kv_heads, head_dim, max_len]
   int64_t max_len;
+  // RMSNorm of the rows of X folded into the GEMM (> 0: X is the residual stream h; the norm's
+  // weight is already folded into W's columns; each output is scaled by rsqrt(mean(h^2) + eps))
+  float norm_eps;
 };
 
 
@@ -120,6 +123,47 @@ __device__ __forceinline__ void epi_qkv(const GemmArgs& a, int nb, int m, int r,
   }
 }
 
+// Where tile nb of the fused q/k/v weight lands: region 0 q / 1 k / 2 v, its head, and the
+// rotary pair block p (tile rows r and r + 8 are dims p*8 + r and hd/2 + p*8 + r).
+struct QkvTile {
+  int region, head, p;
+};
+__device__ __forceinline__ QkvTile qkv_tile(const GemmArgs& a, int nb) {
+  const int tph = a.head_dim >> 4;  // tiles per head (head_dim is a power of two)
+  const int sh = __ffs(tph) - 1;
+  const int q_tiles = a.heads * tph, k_tiles = a.kv_heads * tph;
+  const int region = nb < q_tiles ? 0 : nb < q_tiles + k_tiles ? 1 : 2;
+  const int rel = nb - (region == 0 ? 0 : region == 1 ? q_tiles : q_tiles + k_tiles);
+  return QkvTile{region, rel >> sh, rel & (tph - 1)};
+}
+
+// epi_qkv with the row's cache slot and rotary cos/sin already loaded (prefetched before the
+// main loop, so the epilogue issues no dependent loads).
+__device__ __forceinline__ void epi_qkv_pre(const GemmArgs& a, const QkvTile& q, int m, int r, float vlo,
+                                            float vhi, int slot, float cs, float sn) {
+  const int hd = a.head_dim, half = hd >> 1;
+  const int dlo = q.p * 8 + r, dhi = dlo + half;
+  const float xlo = rbf(vlo), xhi = rbf(vhi);
+  if (q.region != 0 && (slot < 0 || slot >= a.max_len)) return;  // never write outside the cache
+  if (q.region == 2) {
+    bf16_t* vt = a.vt_cache + (size_t)q.head * hd * a.max_len;
+    vt[(size_t)dlo * a.max_len + slot] = f2bf(xlo);
+    vt[(size_t)dhi * a.max_len + slot] = f2bf(xhi);
+    return;
+  }
+  const float olo = rbf(rbf(xlo * cs) - rbf(xhi * sn));
+  const float ohi = rbf(rbf(xhi * cs) + rbf(xlo * sn));
+  if (q.region == 0) {
+    bf16_t* qo = a.Y + (size_t)m * a.ldy + (size_t)q.head * hd;
+    qo[dlo] = f2bf(olo);
+    qo[dhi] = f2bf(ohi);
+  } else {
+    bf16_t* kr = a.k_cache + ((size_t)q.head * a.max_len + slot) * hd;
+    kr[dlo] = f2bf(olo);
+    kr[dhi] = f2bf(ohi);
+  }
+}
+
 // Epilogue of one 16-row tile `nb` for rows m < Mv; val(r, m) is the fp32 dot product of tile
 // row r and token m. Threads tid, tid + NTHREADS, ... of the caller share the work.
 template <int EPI, int NTHREADS, class Val>
@@ -148,9 +192,23 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, int nb, int Mv,
 template <int KS, int NSUB, int CT>
 struct GemmLds {
   float4 red[KS][NSUB][CT][64];
+  float ss[KS][CT][16];  // per-wave sums of x^2 per row (folded RMSNorm)
+  float rn[CT * 16];     // per-row rsqrt(mean(x^2) + eps)
 };
 
-template <int CT, int NSUB, int KS, int U, int EPI>
+// Sum of squares of the 8 bf16 values in a 16-byte fragment.
+__device__ __forceinline__ float sumsq8(u32x4_t v) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float lo = __uint_as_float(v[i] << 16), hi = __uint_as_float(v[i] & 0xffff0000u);
+    s = fmaf(lo, lo, s);
+    s = fmaf(hi, hi, s);
+  }
+  return s;
+}
+
+template <int CT, int NSUB, int KS, int U, int EPI, int NORM>
 __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
@@ -165,6 +223,9 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
   for (int s = 0; s < NSUB; ++s)
 #pragma unroll
     for (int c = 0; c < CT; ++c) acc[s][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float ss[CT];  // folded RMSNorm: this lane's sum of x^2 for row c*16 + j
+#pragma unroll
+  for (int c = 0; c < CT; ++c) ss[c] = 0.f;
 
   const u32x4_t* wp[NSUB];
 #pragma unroll
@@ -173,6 +234,19 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
   const bf16_t* xp[CT];
 #pragma unroll
   for (int c = 0; c < CT; ++c) xp[c] = a.X + (size_t)min(c * 16 + j, a.M - 1) * a.ldx + g * 8;
+
+  // q/k/v: thread t owns pair t (token t / 8, pair row t % 8) of every sub-tile when the
+  // workgroup has enough threads; its cache slot and position are loaded now (clamped, so the
+  // loads are unconditional) and arrive while the weights stream.
+  const int Mv = a.M < CT * 16 ? a.M : CT * 16;
+  const bool qkv_pre = EPI == EPI_QKV && 8 * Mv <= 64 * KS;
+  int pre_m = 0, pre_r = 0, pre_slot = 0, pre_pos = 0;
+  if constexpr (EPI == EPI_QKV) {
+    pre_m = min((int)threadIdx.x >> 3, Mv - 1);
+    pre_r = threadIdx.x & 7;
+    pre_slot = a.row_slot[pre_m];
+    pre_pos = min(max(a.row_pos[pre_m], 0), (int)a.rope_rows - 1);
+  }
 
   int kb = kb_lo;
   for (; kb + U - 1 < kb_hi; kb += U) {
@@ -195,6 +269,12 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
       for (int s = 0; s < NSUB; ++s)
 #pragma unroll
         for (int c = 0; c < CT; ++c) acc[s][c] = mfma16x16x32(bits_bf16x8(wr[u][s]), bits_bf16x8(xr[u][c]), acc[s][c]);
+    if constexpr (NORM) {
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int c = 0; c < CT; ++c) ss[c] += sumsq8(xr[u][c]);
+    }
   }
   for (; kb < kb_hi; ++kb) {
     u32x4_t wr[NSUB], xr[CT];
@@ -206,6 +286,23 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
     for (int s = 0; s < NSUB; ++s)
 #pragma unroll
       for (int c = 0; c < CT; ++c) acc[s][c] = mfma16x16x32(bits_bf16x8(wr[s]), bits_bf16x8(xr[c]), acc[s][c]);
+    if constexpr (NORM) {
+#pragma unroll
+      for (int c = 0; c < CT; ++c) ss[c] += sumsq8(xr[c]);
+    }
+  }
+
+  // rotary cos/sin of this thread's pairs (issued before the reduction so they overlap it)
+  float pre_cs[NSUB], pre_sn[NSUB];
+  if constexpr (EPI == EPI_QKV) {
+    const int half = a.head_dim >> 1;
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s) {
+      const QkvTile q = qkv_tile(a, min(tile * NSUB + s, (a.N >> 4) - 1));
+      const size_t at = (size_t)pre_pos * half + min(q.p * 8 + pre_r, half - 1);
+      pre_cs[s] = bf2f(a.cos_tab[at]);
+      pre_sn[s] = bf2f(a.sin_tab[at]);
+    }
   }
 
   __shared__ GemmLds<KS, NSUB, CT> lds;
@@ -214,13 +311,33 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int c = 0; c < CT; ++c)
       lds.red[w][s][c][lane] = make_float4(acc[s][c][0], acc[s][c][1], acc[s][c][2], acc[s][c][3]);
-  __syncthreads();
-
-  // Tile row r (0..15) of sub-tile s, token m, summed over the waves in wave order.
-  const int Mv = a.M < CT * 16 ? a.M : CT * 16;
+  if constexpr (NORM) {
+    // row sums: the 4 k-groups of the wave (lanes j, j+16, j+32, j+48), then the waves in order
 #pragma unroll
-  for (int s = 0; s < NSUB; ++s)
-    gemm_epilogue<EPI, 64 * KS>(a, tile * NSUB + s, Mv, [&](int r, int m) -> float {
+    for (int c = 0; c < CT; ++c) {
+      float v = ss[c];
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      if (g == 0) lds.ss[w][c][j] = v;
+    }
+  }
+  __syncthreads();
+  if constexpr (NORM) {
+    if ((int)threadIdx.x < CT * 16) {
+      const int c = threadIdx.x >> 4, jj = threadIdx.x & 15;
+      float v = lds.ss[0][c][jj];
+#pragma unroll
+      for (int ww = 1; ww < KS; ++ww) v += lds.ss[ww][c][jj];
+      lds.rn[threadIdx.x] = rsqrtf(v / (float)(kbt * 32) + a.norm_eps);
+    }
+    __syncthreads();
+  }
+
+  // Tile row r (0..15) of sub-tile s, token m, summed over the waves in wave order (then scaled
+  // by the row's folded RMSNorm factor).
+#pragma unroll
+  for (int s = 0; s < NSUB; ++s) {
+    auto val = [&](int r, int m) -> float {
       const int c = m >> 4;
       const int ln = (m & 15) + 16 * (r >> 2);
       const int e = r & 3;
@@ -231,8 +348,20 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
         const float x = e == 0 ? q.x : e == 1 ? q.y : e == 2 ? q.z : q.w;
         v = ww == 0 ? x : v + x;
       }
+      if constexpr (NORM) v *= lds.rn[m];
       return v;
-    }, threadIdx.x);
+    };
+    if constexpr (EPI == EPI_QKV) {
+      if (qkv_pre) {
+        const int nb = tile * NSUB + s;
+        if (nb * 16 < a.N && (int)threadIdx.x < 8 * Mv)
+          epi_qkv_pre(a, qkv_tile(a, nb), pre_m, pre_r, val(pre_r, pre_m), val(pre_r + 8, pre_m), pre_slot,
+                      pre_cs[s], pre_sn[s]);
+        continue;
+      }
+    }
+    gemm_epilogue<EPI, 64 * KS>(a, tile * NSUB + s, Mv, val, threadIdx.x);
+  }
 }
 
 // ------------------------------------------------------------ split-K partials
@@ -435,7 +564,8 @@ static int launch_part(const GemmArgs& a, float* P, int64_t ldp, int64_t sstride
 // nb = g*group .. g*group+group-1 of one k-block sit next to each other ([g][kb][nb % group]), so
 // a workgroup that owns a group streams one contiguous region.
 __global__ void pack_kernel(const bf16_t* __restrict__ src, int64_t ld, int K, const int* __restrict__ row_map,
-                            int n_tiles_n, int kb_total, int group, uint4* __restrict__ dst) {
+                            int n_tiles_n, int kb_total, int group, const bf16_t* __restrict__ col_scale,
+                            uint4* __restrict__ dst) {
   const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (tile >= (int64_t)n_tiles_n * kb_total) return;
@@ -444,7 +574,11 @@ __global__ void pack_kernel(const bf16_t* __restrict__ src, int64_t ld, int K, c
   const int k0 = kb * 32 + (lane >> 4) * 8;
   Pack8 p;
 #pragma unroll
-  for (int t = 0; t < 8; ++t) p.h[t] = (row >= 0 && k0 + t < K) ? src[(size_t)row * ld + k0 + t] : (bf16_t)0;
+  for (int t = 0; t < 8; ++t) {
+    const bf16_t v = (row >= 0 && k0 + t < K) ? src[(size_t)row * ld + k0 + t] : (bf16_t)0;
+    // folded RMSNorm weight: column k scaled by col_scale[k], rounded once to bf16
+    p.h[t] = (col_scale && k0 + t < K) ? f2bf(bf2f(v) * bf2f(col_scale[k0 + t])) : v;
+  }
   const int64_t dst_tile = ((int64_t)(nb / group) * kb_total + kb) * group + nb % group;
   dst[dst_tile * 64 + lane] = p.u;
 }
@@ -492,8 +626,11 @@ static int launch_gemm(GemmArgs a, hipStream_t s) {
     const int ct = (b.M + 15) / 16;
     dim3 grid(p.tiles);
 #define SSD_GEMM_CASE(CT_, NS_, KS_) \
-  if (ct == CT_ && p.nsub == NS_ && p.ks == KS_) {                                                            \
-    hipLaunchKernelGGL((gemm_kernel<CT_, NS_, KS_, (CT_ == 1 ? 4 : 2), EPI>), grid, dim3(64 * KS_), 0, s, b);   \
+  if (ct == CT_ && p.nsub == NS_ && p.ks == KS_) {                                                             \
+    if (b.norm_eps > 0.f)                                                                                      \
+      hipLaunchKernelGGL((gemm_kernel<CT_, NS_, KS_, (CT_ == 1 ? 4 : 2), EPI, 1>), grid, dim3(64 * KS_), 0, s, b); \
+    else                                                                                                       \
+      hipLaunchKernelGGL((gemm_kernel<CT_, NS_, KS_, (CT_ == 1 ? 4 : 2), EPI, 0>), grid, dim3(64 * KS_), 0, s, b); \
   }
 #define SSD_GEMM_PLANS(CT_)                                                                                \
   SSD_GEMM_CASE(CT_, 8, 2) SSD_GEMM_CASE(CT_, 8, 1) SSD_GEMM_CASE(CT_, 4, 2) SSD_GEMM_CASE(CT_, 4, 1)     \
@@ -536,7 +673,8 @@ SSD_API int ssd_gemm_weight_group(int N, int K) {
 
 
 SSD_API int ssd_pack_weight_bf16(const uint16_t* src, int64_t ld, int N_src, int K, const int32_t* row_map,
-                                 int N_packed, int group, uint16_t* dst, hipStream_t stream) {
+                                 int N_packed, int group, const uint16_t* col_scale, uint16_t* dst,
+                                 hipStream_t stream) {
   if (!src || !dst || !row_map) return set_error(SSD_EINVAL, "pack: null pointer");
   if (N_packed <= 0 || N_packed % 128 || K <= 0 || N_src <= 0)
     return set_error(SSD_EINVAL, "pack: N_packed=%d must be a positive multiple of 128 (K=%d)", N_packed, K);
@@ -545,14 +683,16 @@ SSD_API int ssd_pack_weight_bf16(const uint16_t* src, int64_t ld, int N_src, int
   const int n_tiles_n = N_packed / 16, kb_total = (K + 31) / 32;
   const int64_t tiles = (int64_t)n_tiles_n * kb_total;
   hipLaunchKernelGGL(pack_kernel, dim3((unsigned)((tiles + 3) / 4)), dim3(256), 0, stream, src, ld, K, row_map,
-                     n_tiles_n, kb_total, group, (uint4*)dst);
+                     n_tiles_n, kb_total, group, col_scale, (uint4*)dst);
   return check_launch("pack");
 }
 
 // Y = act(X W^T + bias) [+ residual], bf16 rounding after each step. Y may alias residual.
+// norm_eps > 0: X is the residual stream h and W was packed with the RMSNorm weight as col_scale;
+// each row's outputs are scaled by rsqrt(mean(h^2) + norm_eps) (RMSNorm folded into the GEMM).
 SSD_API int ssd_gemm_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int N, int K,
-                          uint16_t* Y, int64_t ldy, const uint16_t* bias, int act, const uint16_t* residual,
-                          int64_t ldr, hipStream_t stream) {
+                          float norm_eps, uint16_t* Y, int64_t ldy, const uint16_t* bias, int act,
+                          const uint16_t* residual, int64_t ldr, hipStream_t stream) {
   int rc = check_common(X, ldx, M, W_packed, N, K);
   if (rc) return rc;
   if (!Y) return set_error(SSD_EINVAL, "gemm: null Y");
@@ -562,14 +702,15 @@ SSD_API int ssd_gemm_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t*
   GemmArgs a{};
   a.X = X; a.ldx = ldx; a.M = M; a.W = (const uint4*)W_packed; a.N = N; a.kb_total = K / 32;
   a.Y = Y; a.ldy = ldy; a.bias = bias; a.act = act; a.residual = residual; a.ldr = ldr;
+  a.norm_eps = norm_eps > 0.f ? norm_eps : 0.f;
   return launch_gemm<EPI_STORE>(a, stream);
 }
 
 // Y[M, I] = silu(X Wg^T + bg) * (X Wu^T + bu); W_packed holds, per 16-row tile i, gate rows
 // [8i, 8i+8) then up rows [8i, 8i+8). N = 2 I.
 SSD_API int ssd_gemm_swiglu_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int I, int K,
-                                 uint16_t* Y, int64_t ldy, const uint16_t* bias_gate, const uint16_t* bias_up,
-                                 hipStream_t stream) {
+                                 float norm_eps, uint16_t* Y, int64_t ldy, const uint16_t* bias_gate,
+                                 const uint16_t* bias_up, hipStream_t stream) {
   int rc = check_common(X, ldx, M, W_packed, 2 * I, K);
   if (rc) return rc;
   if (!Y || I % 8) return set_error(SSD_EINVAL, "gemm_swiglu: null Y or I=%d not a multiple of 8", I);
@@ -577,6 +718,7 @@ SSD_API int ssd_gemm_swiglu_bf16(const uint16_t* X, int64_t ldx, int M, const ui
   GemmArgs a{};
   a.X = X; a.ldx = ldx; a.M = M; a.W = (const uint4*)W_packed; a.N = 2 * I; a.kb_total = K / 32;
   a.Y = Y; a.ldy = ldy; a.bias = bias_gate; a.bias2 = bias_up;
+  a.norm_eps = norm_eps > 0.f ? norm_eps : 0.f;
   return launch_gemm<EPI_SWIGLU>(a, stream);
 }
 
@@ -585,7 +727,7 @@ SSD_API int ssd_gemm_swiglu_bf16(const uint16_t* X, int64_t ldx, int M, const ui
 // [hd/2 + 8p, hd/2 + 8p + 8). q -> Q[m, heads*hd]; k -> k_cache[kvh, slot, :];
 // v -> vt_cache[kvh, :, slot] (V is kept transposed).
 SSD_API int ssd_gemm_qkv_rope_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int K,
-                                   int heads, int kv_heads, int head_dim, const uint16_t* cos_tab,
+                                   float norm_eps, int heads, int kv_heads, int head_dim, const uint16_t* cos_tab,
                                    const uint16_t* sin_tab, int64_t rope_rows, const int32_t* row_pos,
                                    const int32_t* row_slot,
                                    uint16_t* Q, int64_t ldq, uint16_t* k_cache, uint16_t* vt_cache,
@@ -603,6 +745,7 @@ SSD_API int ssd_gemm_qkv_rope_bf16(const uint16_t* X, int64_t ldx, int M, const 
   if (rope_rows <= 0) return set_error(SSD_EINVAL, "qkv: empty rope table");
   a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.rope_rows = rope_rows; a.row_pos = row_pos; a.row_slot = row_slot;
   a.k_cache = k_cache; a.vt_cache = vt_cache; a.max_len = max_len;
+  a.norm_eps = norm_eps > 0.f ? norm_eps : 0.f;
   return launch_gemm<EPI_QKV>(a, stream);
 }
 
@@ -670,3 +813,45 @@ SSD_API int ssd_qkv_rope_finalize_bf16(const float* P, int64_t ldp, int64_t spli
   return rc ? rc : check_launch("qkv_finalize");
 }
 
+
+// ------------------------------------------------------- residual projection
+// Measured on MI355X at decode shapes (M = 25, weights streamed from HBM): a K <= 4096 projection
+// (o_proj, bridge out_proj) is fastest as one direct GEMM with the residual add in its epilogue;
+// a long-K projection (down_proj, K = intermediate) as split-K partials plus a finalize that only
+// adds (the direct GEMM would re-read the long activation rows in every workgroup).
+static bool residual_split(int N, int K) { return K > 4096; }
+
+SSD_API int ssd_gemm_residual_group(int N, int K) {
+  if (N <= 0 || K <= 0 || K % 32) {
+    set_error(SSD_EINVAL, "residual_group: bad shape N=%d K=%d", N, K);
+    return 0;
+  }
+  return residual_split(N, K) ? 1 : plan_for(N, K).nsub;
+}
+
+SSD_API int64_t ssd_gemm_residual_floats(int M, int N, int K) {
+  if (M < 0 || N <= 0 || K <= 0 || K % 32) return -1;
+  return residual_split(N, K) ? (int64_t)part_plan(N, K).S * M * ((N + 63) / 64 * 64) : 0;
+}
+
+SSD_API int ssd_gemm_residual_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int N, int K,
+                                   const uint16_t* bias, uint16_t* h, int64_t ldh, float* part, int64_t part_floats,
+                                   hipStream_t stream) {
+  int rc = check_common(X, ldx, M, W_packed, N, K);
+  if (rc) return rc;
+  if (!h) return set_error(SSD_EINVAL, "gemm_residual: null h");
+  if (M == 0) return SSD_OK;
+  GemmArgs a{};
+  a.X = X; a.ldx = ldx; a.M = M; a.W = (const uint4*)W_packed; a.N = N; a.kb_total = K / 32;
+  a.Y = h; a.ldy = ldh; a.bias = bias; a.residual = h; a.ldr = ldh;
+  if (!residual_split(N, K)) return launch_gemm<EPI_STORE>(a, stream);
+  const int64_t ldp = (N + 63) / 64 * 64;
+  const int S = part_plan(N, K).S;
+  if (part_floats < (int64_t)S * M * ldp)
+    return set_error(SSD_EINVAL, "gemm_residual: scratch of %lld floats < %lld", (long long)part_floats,
+                     (long long)S * M * ldp);
+  if ((rc = check_partials(part, ldp, (int64_t)M * ldp, M, N))) return rc;
+  if ((rc = launch_part(a, part, ldp, (int64_t)M * ldp, stream))) return rc;
+  rc = launch_finalize<EPI_STORE>(a, part, ldp, (int64_t)M * ldp, S, stream);
+  return rc ? rc : check_launch("gemm_residual");
+}

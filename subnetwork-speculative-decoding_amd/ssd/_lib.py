@@ -62,10 +62,10 @@ _PROTOS = {
     "ssd_device_arch": (I32, [C.c_char_p, I32]),
     "ssd_packed_weight_elems": (I64, [I32, I32]),
     "ssd_gemm_weight_group": (I32, [I32, I32]),
-    "ssd_pack_weight_bf16": (I32, [P, I64, I32, I32, P, I32, I32, P, P]),
-    "ssd_gemm_bf16": (I32, [P, I64, I32, P, I32, I32, P, I64, P, I32, P, I64, P]),
-    "ssd_gemm_swiglu_bf16": (I32, [P, I64, I32, P, I32, I32, P, I64, P, P, P]),
-    "ssd_gemm_qkv_rope_bf16": (I32, [P, I64, I32, P, I32, I32, I32, I32, P, P, I64, P, P, P, I64, P, P, I64, P]),
+    "ssd_pack_weight_bf16": (I32, [P, I64, I32, I32, P, I32, I32, P, P, P]),
+    "ssd_gemm_bf16": (I32, [P, I64, I32, P, I32, I32, F32, P, I64, P, I32, P, I64, P]),
+    "ssd_gemm_swiglu_bf16": (I32, [P, I64, I32, P, I32, I32, F32, P, I64, P, P, P]),
+    "ssd_gemm_qkv_rope_bf16": (I32, [P, I64, I32, P, I32, F32, I32, I32, I32, P, P, I64, P, P, P, I64, P, P, I64, P]),
     "ssd_attn_workspace_floats": (I32, [I32, I32, I32, I64]),
     "ssd_attn_max_depth": (I32, []),
     "ssd_tree_attention_bf16": (I32, [P, I64, I32, I32, I32, I32, P, P, I64, P, P, P, I32, I32, F32, P, I64, P,
@@ -85,6 +85,9 @@ _PROTOS = {
     "ssd_gemm_finalize_bf16": (I32, [P, I64, I64, I32, I32, I32, P, I64, P, I32, P, I64, P]),
     "ssd_qkv_rope_finalize_bf16": (I32, [P, I64, I64, I32, I32, I32, I32, I32, P, P, I64, P, P, P, I64, P, P, I64, P]),
     "ssd_add_rmsnorm_bf16": (I32, [P, I64, I64, I32, P, P, I64, I32, I32, P, F32, P, I64, P]),
+    "ssd_gemm_residual_group": (I32, [I32, I32]),
+    "ssd_gemm_residual_floats": (I64, [I32, I32, I32]),
+    "ssd_gemm_residual_bf16": (I32, [P, I64, I32, P, I32, I32, P, P, I64, P, I64, P]),
     "ssd_sample_limits": (I32, [P]),
     "ssd_sample_ws_bytes": (I64, [I32, I32]),
     "ssd_warp_probs_bf16": (I32, [P, I64, I32, I32, P, P, I32, F32, F32, P, I32, P, I64, P, I64, P]),

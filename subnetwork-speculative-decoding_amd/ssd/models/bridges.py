@@ -79,19 +79,19 @@ class PackedBridge:
 
             m = bridge.mlp
             w = torch.cat([bf(m.gate_proj.weight), bf(m.up_proj.weight)], 0)
-            self.gu = ops.pack_weight(w, gate_up_row_map(self.hidden))
+            self.gu = ops.pack_weight(w, gate_up_row_map(self.hidden), col_scale=self.norm)  # norm folded
             self.bg, self.bu = bf(m.gate_proj.bias), bf(m.up_proj.bias)
             self.body = []
         else:
             self.body = []
             lins = [mod for mod in bridge.mlp.body if isinstance(mod, nn.Linear)]
             acts = [mod for mod in bridge.mlp.body if not isinstance(mod, nn.Linear)]
-            for lin, act in zip(lins, acts):
+            for i, (lin, act) in enumerate(zip(lins, acts)):
                 name = {nn.SiLU: "silu", nn.GELU: "gelu", nn.ReLU: "relu"}[type(act)]
-                self.body.append((ops.pack_weight(bf(lin.weight)), bf(lin.bias), lin.out_features,
-                                  lin.in_features, name))
+                w = ops.pack_weight(bf(lin.weight), col_scale=self.norm if i == 0 else None)  # norm folded in first
+                self.body.append((w, bf(lin.bias), lin.out_features, lin.in_features, name))
         out = bridge.mlp.out_proj
-        self.out = ops.pack_weight(bf(out.weight), split=True)
+        self.out = ops.pack_weight(bf(out.weight), residual=True)
         self.out_bias = bf(out.bias)
         self._native: Optional[_lib.SsdBridgeW] = None
 
@@ -112,25 +112,24 @@ class PackedBridge:
             self._native = st
         return self._native
 
-    def body_(self, x: torch.Tensor, m: int, mids: list) -> tuple:
-        """MLP body over x[:m] (x = RMSNorm(h) already); returns (output, its width)."""
+    def body_(self, h: torch.Tensor, m: int, mids: list) -> tuple:
+        """MLP body over RMSNorm(h[:m]) (the norm folded into the first GEMM); returns (output,
+        its width)."""
         if self.swiglu:
-            ops.gemm_swiglu(x, m, self.gu, self.hidden, self.d, mids[0], self.bg, self.bu)
+            ops.gemm_swiglu(h, m, self.gu, self.hidden, self.d, mids[0], self.bg, self.bu, norm_eps=self.eps)
             return mids[0], self.hidden
-        cur, k = x, self.d
+        cur, k = h, self.d
         for i, (w, b, n, kin, act) in enumerate(self.body):
             dst = mids[i % 2]
-            ops.gemm(cur, m, w, n, kin, dst, bias=b, act=act)
+            ops.gemm(cur, m, w, n, kin, dst, bias=b, act=act, norm_eps=self.eps if i == 0 else 0.0)
             cur, k = dst, n
         return cur, k
 
-    def apply_(self, h: torch.Tensor, m: int, x: torch.Tensor, mids: list, part: torch.Tensor, next_w: torch.Tensor,
-               next_eps: float) -> None:
-        """x[:m] = RMSNorm_bridge(h) on entry. h[:m] <- h + MLP(x) (out_proj as split-K partials, residual
-        add fused with the next RMSNorm), then x[:m] <- next RMSNorm(h): the kernel order of ssd_forward."""
-        cur, k = self.body_(x, m, mids)
-        s, ld = ops.gemm_partial(cur, m, self.out, self.d, k, part)
-        ops.add_rmsnorm(part, s, ld, h, m, next_w, next_eps, x, bias=self.out_bias)
+    def apply_(self, h: torch.Tensor, m: int, mids: list, part: torch.Tensor) -> None:
+        """h[:m] <- h + MLP(RMSNorm(h)) with the kernels of ssd_forward (body GEMMs, then the
+        out_proj with the residual add in its epilogue)."""
+        cur, k = self.body_(h, m, mids)
+        ops.gemm_residual(cur, m, self.out, self.d, k, h, part, bias=self.out_bias)
 
 
 class TransitionBridge(nn.Module):

@@ -7,7 +7,10 @@ the layout the gfx950 kernels stream:
 * per layer: q/k/v fused into one packed matrix whose 16-row tiles pair rotary dims d and
   d + hd/2 (so RoPE and the KV-cache write run in the GEMM epilogue); gate/up fused with 8
   gate rows + the matching 8 up rows per tile (SwiGLU in the epilogue); o and down packed
-  as-is; RMSNorm weights as plain bf16 vectors;
+  as-is. Each RMSNorm weight is folded into the columns of the projection that consumes it
+  (ln1 into q/k/v, ln2 into gate/up, the final norm into the lm_head): those GEMMs take the
+  residual stream itself and scale each row by its rsqrt(mean(h^2) + eps), so no separate
+  norm kernel runs (the weights are also kept as plain bf16 vectors);
 * the embedding table row-major (a gather), the lm_head packed (a weight-streaming GEMM);
 * RoPE cos/sin tables [positions, hd/2] computed in fp32 and rounded to bf16 exactly as HF's
   rotary embedding does.
@@ -133,17 +136,18 @@ class MI355XLlama:
     def _set_layer(self, get) -> None:
         s = self.shape
         L = Layer()
-        qkv = torch.cat([self._put(get("self_attn.q_proj.weight")), self._put(get("self_attn.k_proj.weight")),
-                         self._put(get("self_attn.v_proj.weight"))], 0)
-        L.wqkv = ops.pack_weight(qkv, qkv_row_map(s.heads, s.kv_heads, s.head_dim))
-        del qkv
-        L.wo = ops.pack_weight(self._put(get("self_attn.o_proj.weight")), split=True)
-        gu = torch.cat([self._put(get("mlp.gate_proj.weight")), self._put(get("mlp.up_proj.weight"))], 0)
-        L.wgu = ops.pack_weight(gu, gate_up_row_map(s.inter))
-        del gu
-        L.wd = ops.pack_weight(self._put(get("mlp.down_proj.weight")), split=True)
         L.ln1 = self._put(get("input_layernorm.weight"))
         L.ln2 = self._put(get("post_attention_layernorm.weight"))
+        # each RMSNorm weight is folded into the columns of the projection that consumes it
+        qkv = torch.cat([self._put(get("self_attn.q_proj.weight")), self._put(get("self_attn.k_proj.weight")),
+                         self._put(get("self_attn.v_proj.weight"))], 0)
+        L.wqkv = ops.pack_weight(qkv, qkv_row_map(s.heads, s.kv_heads, s.head_dim), col_scale=L.ln1)
+        del qkv
+        L.wo = ops.pack_weight(self._put(get("self_attn.o_proj.weight")), residual=True)
+        gu = torch.cat([self._put(get("mlp.gate_proj.weight")), self._put(get("mlp.up_proj.weight"))], 0)
+        L.wgu = ops.pack_weight(gu, gate_up_row_map(s.inter), col_scale=L.ln2)
+        del gu
+        L.wd = ops.pack_weight(self._put(get("mlp.down_proj.weight")), residual=True)
         self.layers.append(L)
 
     @classmethod
@@ -155,7 +159,7 @@ class MI355XLlama:
         m.norm = m._put(sd["model.norm.weight"])
         head = sd.get("lm_head.weight", sd["model.embed_tokens.weight"])
         head = m._put(head)
-        m.lm_head = ops.pack_weight(head)
+        m.lm_head = ops.pack_weight(head, col_scale=m.norm)  # final norm folded
         if keep_lm_head_rows:
             m._lm_head_rows = head
         torch.cuda.synchronize(m.device)
@@ -198,7 +202,7 @@ class MI355XLlama:
             m._set_layer(w.__getitem__)
             del w
         m.norm = ones.clone()
-        m.lm_head = ops.pack_weight(rnd(s.vocab, s.hidden))
+        m.lm_head = ops.pack_weight(rnd(s.vocab, s.hidden), col_scale=m.norm)
         torch.cuda.synchronize(m.device)
         return m
 
@@ -232,10 +236,12 @@ class MI355XLlama:
         return 2 * (b + self.lm_head.numel())
 
     def lm_head_rows(self, ids: torch.Tensor) -> torch.Tensor:
-        """Row-major lm_head rows ``ids`` (for a vocabulary-subset head). Unpacks from the
-        packed tiles when the row-major copy was not kept."""
+        """Row-major lm_head rows ``ids`` as the packed head applies them (final-norm weight folded
+        into the columns), for a vocabulary-subset head. Unpacks from the packed tiles when the
+        row-major copy was not kept."""
         if self._lm_head_rows is not None:
-            return self._lm_head_rows.index_select(0, ids.to(self.device))
+            rows = self._lm_head_rows.index_select(0, ids.to(self.device))
+            return (rows.float() * self.norm.float()).to(BF16)  # the fold of ssd_pack_weight_bf16
         return unpack_rows(self.lm_head, self.shape.vocab, self.shape.hidden, ids.to(self.device),
                            ops.weight_group(self.shape.vocab, self.shape.hidden))
 

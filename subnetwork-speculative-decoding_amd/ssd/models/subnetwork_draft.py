@@ -162,7 +162,8 @@ class Workspace:
         # split-K partials of the largest GEMM that writes them (q/k/v, o, down, bridge out_proj)
         n_qkv = (s.heads + 2 * s.kv_heads) * s.head_dim
         shapes = [(n_qkv, s.hidden), (s.hidden, s.heads * s.head_dim), (s.hidden, s.inter), (s.hidden, bh)]
-        self.part = torch.zeros(max(ops.partial_floats(m_cap, n, k) for n, k in shapes), dtype=torch.float32,
+        self.part = torch.zeros(max([ops.partial_floats(m_cap, n, k) for n, k in shapes]
+                                    + [ops.residual_floats(m_cap, n, k) for n, k in shapes]), dtype=torch.float32,
                                 device=dev)
         self.ws = torch.zeros(0, dtype=torch.float32, device=dev)
         self.logits = torch.zeros(0, **bf)
@@ -307,8 +308,9 @@ class SubnetworkDraftModel(nn.Module):
     def forward_rows(self, rows, m: int, p_min: int, l_max: int, cache: KVCache, ws: Workspace,
                      head_first: int = 0, head_rows: Optional[int] = None) -> Optional[torch.Tensor]:
         """One ssd_forward call over rows [0, m) on the device: embedding, the selected layers and
-        bridges, the final norm (into ws.x) and the head over rows [head_first, head_first +
-        head_rows) (default all). Returns the bf16 logits view [head_rows, n] (None if no rows)."""
+        bridges (final residual stream in ws.h) and the head, with the final norm folded, over rows
+        [head_first, head_first + head_rows) (default all). Returns the bf16 logits view
+        [head_rows, n] (None if no rows)."""
         if head_rows is None:
             head_rows = m
         n = self._head_n()
@@ -317,25 +319,10 @@ class SubnetworkDraftModel(nn.Module):
                   int(p_min), int(l_max), head_first, head_rows, ops.stream())
         return logits[:head_rows, :n] if head_rows else None
 
-    def _norm_before(self, st: int):
-        """(weight, eps) of the RMSNorm applied to h before plan step st (st == #layers: the head)."""
-        s = self.model.shape
-        if st < len(self.layer_indices):
-            name = self._pre_layer_bridge[st]
-            if name is not None:
-                b = self._packed_bridge(name)
-                return b.norm, b.eps
-            return self.base.layers[st].ln1, s.eps
-        if self._pre_norm_bridge is not None:
-            b = self._packed_bridge(self._pre_norm_bridge)
-            return b.norm, b.eps
-        return self.model.norm, s.eps
-
     def run_rows(self, rows: Rows, m: int, p_min: int, l_max: int, cache: KVCache, ws: Workspace,
                  bridge_states: Optional[dict] = None, ids_ready: bool = True) -> torch.Tensor:
         """The kernels of ssd_forward called one by one from Python, in the same order (used when
-        bridge states are requested). Leaves the residual stream in ws.h[:m] and the final-normed
-        rows in ws.x[:m]; returns ws.h."""
+        bridge states are requested). Leaves the final residual stream in ws.h[:m] and returns it."""
         if m > ws.m_cap:
             raise ValueError(f"{m} rows > workspace {ws.m_cap}")
         model, s = self.model, self.model.shape
@@ -343,38 +330,34 @@ class SubnetworkDraftModel(nn.Module):
         aws = ws.attn_ws(model, cache.capacity)
         part = ws.part
         ops.embed(rows.ids, m, model.embed, ws.h)
-        w0, e0 = self._norm_before(0)
-        ops.add_rmsnorm(None, 0, 0, ws.h, m, w0, e0, ws.x)
         for slot, layer in enumerate(self.base.layers):
             li = self.layer_indices[slot]
             name = self._pre_layer_bridge[slot]
             if name is not None:
-                self._packed_bridge(name).apply_(ws.h, m, ws.x, ws.mids, part, layer.ln1, s.eps)
+                self._packed_bridge(name).apply_(ws.h, m, ws.mids, part)
                 if bridge_states is not None:
                     bridge_states[name] = ws.h[:m].clone()
             kc, vt = cache.layer(li)
-            ops.qkv_rope(ws.x, m, layer.wqkv, s.hidden, s.heads, s.kv_heads, s.head_dim, cos, sin, rows.pos, rows.slot,
-                         ws.q, kc, vt, cache.capacity)
+            ops.qkv_rope(ws.h, m, layer.wqkv, s.hidden, s.heads, s.kv_heads, s.head_dim, cos, sin, rows.pos, rows.slot,
+                         ws.q, kc, vt, cache.capacity, norm_eps=s.eps)
             ops.tree_attention(ws.q, m, s.heads, s.kv_heads, s.head_dim, kc, vt, cache.capacity, rows.prefix,
                                rows.depth, rows.anc, p_min, l_max, aws, ws.attn)
-            sp, ld = ops.gemm_partial(ws.attn, m, layer.wo, s.hidden, s.heads * s.head_dim, part)
-            ops.add_rmsnorm(part, sp, ld, ws.h, m, layer.ln2, s.eps, ws.x)
-            ops.gemm_swiglu(ws.x, m, layer.wgu, s.inter, s.hidden, ws.mlp)
-            wn, en = self._norm_before(slot + 1)
-            sp, ld = ops.gemm_partial(ws.mlp, m, layer.wd, s.hidden, s.inter, part)
-            ops.add_rmsnorm(part, sp, ld, ws.h, m, wn, en, ws.x)
+            ops.gemm_residual(ws.attn, m, layer.wo, s.hidden, s.heads * s.head_dim, ws.h, part)
+            ops.gemm_swiglu(ws.h, m, layer.wgu, s.inter, s.hidden, ws.mlp, norm_eps=s.eps)
+            ops.gemm_residual(ws.mlp, m, layer.wd, s.hidden, s.inter, ws.h, part)
         if self._pre_norm_bridge is not None:
-            self._packed_bridge(self._pre_norm_bridge).apply_(ws.h, m, ws.x, ws.mids, part, model.norm, s.eps)
+            self._packed_bridge(self._pre_norm_bridge).apply_(ws.h, m, ws.mids, part)
             if bridge_states is not None:
                 bridge_states[self._pre_norm_bridge] = ws.h[:m].clone()
         return ws.h
 
-    def head(self, hn: torch.Tensor, m: int, ws: Workspace) -> torch.Tensor:
-        """lm_head (or the vocab-subset head) over hn[:m] -> bf16 logits view [m, V]."""
+    def head(self, h: torch.Tensor, m: int, ws: Workspace) -> torch.Tensor:
+        """lm_head (or the vocab-subset head) over the final residual stream h[:m], final norm
+        folded -> bf16 logits view [m, V]."""
         n = self._head_n()
         w = self._sub_head if self._sub_head is not None else self.model.lm_head
         out = ws.logits_buf(m, n)
-        ops.gemm(hn, m, w, n, self.d_model, out)
+        ops.gemm(h, m, w, n, self.d_model, out, norm_eps=self.model.shape.eps)
         return out[:, :n]
 
     def final_norm(self, h: torch.Tensor, m: int, out: torch.Tensor) -> torch.Tensor:
@@ -439,7 +422,7 @@ class SubnetworkDraftModel(nn.Module):
         prefix, anc = self.mask_to_rows(q, past, tree_attention_mask)
         ws = self.workspace(CHUNK)
         rows = Rows(CHUNK, self.model.device)
-        hidden = torch.empty(q, self.d_model, dtype=torch.bfloat16, device=self.model.device)
+        hraw = torch.empty(q, self.d_model, dtype=torch.bfloat16, device=self.model.device)
         states: dict = {} if output_bridge_states else None
         for c0 in range(0, q, CHUNK):
             c1 = min(q, c0 + CHUNK)
@@ -453,15 +436,19 @@ class SubnetworkDraftModel(nn.Module):
             l_max = max(p + len(a) for p, a in zip(prefix[c0:c1], anc[c0:c1]))
             if states is None:
                 self.forward_rows(rows, m, p_min, l_max, cache, ws, head_rows=0)
-                hidden[c0:c1].copy_(ws.x[:m])
             else:
                 self.run_rows(rows, m, p_min, l_max, cache, ws, states)
-                hidden[c0:c1].copy_(ws.x[:m])
+            hraw[c0:c1].copy_(ws.h[:m])
             torch.cuda.current_stream().synchronize()  # the pinned staging buffer is reused next chunk
         cache.advance(q)
+        # hidden_states = the final-normed rows (reference :343); the decode path never needs
+        # them (its head folds the norm), so they are computed here only
+        hidden = torch.empty_like(hraw)
+        for c0 in range(0, q, CHUNK):
+            self.final_norm(hraw[c0:c0 + CHUNK], min(CHUNK, q - c0), hidden[c0:c0 + CHUNK])
         logits = None
         if compute_logits:
-            keep = hidden[-logits_to_keep:] if logits_to_keep > 0 else hidden
+            keep = hraw[-logits_to_keep:] if logits_to_keep > 0 else hraw
             outs = []
             for c0 in range(0, keep.shape[0], CHUNK):
                 part = keep[c0:c0 + CHUNK]

@@ -59,11 +59,14 @@ def weight_group(n: int, k: int) -> int:
 
 
 def pack_weight(w: torch.Tensor, row_map: Optional[torch.Tensor] = None, split: bool = False,
-                n_logical: Optional[int] = None) -> torch.Tensor:
+                n_logical: Optional[int] = None, col_scale: Optional[torch.Tensor] = None,
+                residual: bool = False) -> torch.Tensor:
     """Row-major bf16 W[N, K] -> MFMA tile layout. row_map picks the source row of each packed
     row (-1 = zeros); default = identity. Rows are padded with zeros to a multiple of 128. Tiles
     are grouped for the single-pass GEMMs (group = weight_group(N_logical, K), N_logical = the
-    GEMM's output width, default the row_map length); split=True packs for gemm_partial (group 1)."""
+    GEMM's output width, default the row_map length); split=True packs for gemm_partial (group 1),
+    residual=True for gemm_residual (group = residual_group(N, K)). col_scale [K] folds an RMSNorm
+    weight into the columns (W * s, rounded once to bf16), for GEMMs called with norm_eps."""
     _check(w, "w")
     n, k = w.shape
     ld = _rows(w, "w", k)
@@ -75,14 +78,20 @@ def pack_weight(w: torch.Tensor, row_map: Optional[torch.Tensor] = None, split: 
     if n_packed != row_map.numel():
         row_map = torch.cat([row_map, torch.full((n_packed - row_map.numel(),), -1, dtype=torch.int32)])
     rm = row_map.to(device=w.device)
-    group = 1 if split else weight_group(n_log, k)
+    group = 1 if split else residual_group(n_log, k) if residual else weight_group(n_log, k)
+    if col_scale is not None:
+        _check(col_scale, "col_scale")
+        _len(col_scale, "col_scale", k)
     out = torch.empty(packed_elems(n_packed, k), dtype=BF16, device=w.device)
-    _lib.call("ssd_pack_weight_bf16", w.data_ptr(), ld, n, k, rm.data_ptr(), n_packed, group, out.data_ptr(), stream())
+    _lib.call("ssd_pack_weight_bf16", w.data_ptr(), ld, n, k, rm.data_ptr(), n_packed, group, _p(col_scale),
+              out.data_ptr(), stream())
     return out
 
 
 def gemm(x: torch.Tensor, m: int, wp: torch.Tensor, n: int, k: int, out: torch.Tensor, bias=None, act=None,
-         residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+         residual: Optional[torch.Tensor] = None, norm_eps: float = 0.0) -> torch.Tensor:
+    """Y = act(X W^T + b) [+ residual]; norm_eps > 0: X is h and W was packed with the RMSNorm
+    weight as col_scale (RMSNorm folded into the GEMM)."""
     _check(x, "x"); _check(wp, "w_packed"); _check(out, "out")
     if bias is not None:
         _check(bias, "bias")
@@ -94,22 +103,23 @@ def gemm(x: torch.Tensor, m: int, wp: torch.Tensor, n: int, k: int, out: torch.T
     if residual is not None:
         _check(residual, "residual")
         ldr = _rows(residual, "residual", n, m)
-    _lib.call("ssd_gemm_bf16", x.data_ptr(), ldx, m, wp.data_ptr(), n, k, out.data_ptr(), ldy, _p(bias),
-              ACT[act], _p(residual), ldr, stream())
+    _lib.call("ssd_gemm_bf16", x.data_ptr(), ldx, m, wp.data_ptr(), n, k, float(norm_eps), out.data_ptr(), ldy,
+              _p(bias), ACT[act], _p(residual), ldr, stream())
     return out
 
 
 def gemm_swiglu(x: torch.Tensor, m: int, wp: torch.Tensor, inter: int, k: int, out: torch.Tensor, bias_gate=None,
-                bias_up=None) -> torch.Tensor:
+                bias_up=None, norm_eps: float = 0.0) -> torch.Tensor:
     _check(x, "x"); _check(wp, "w_packed"); _check(out, "out")
     _len(bias_gate, "bias_gate", inter); _len(bias_up, "bias_up", inter)
     _len(wp, "w_packed", packed_elems(2 * inter, k))
-    _lib.call("ssd_gemm_swiglu_bf16", x.data_ptr(), _rows(x, "x", k, m), m, wp.data_ptr(), inter, k, out.data_ptr(),
-              _rows(out, "out", inter, m), _p(bias_gate), _p(bias_up), stream())
+    _lib.call("ssd_gemm_swiglu_bf16", x.data_ptr(), _rows(x, "x", k, m), m, wp.data_ptr(), inter, k, float(norm_eps),
+              out.data_ptr(), _rows(out, "out", inter, m), _p(bias_gate), _p(bias_up), stream())
     return out
 
 
-def qkv_rope(x, m, wp, k, heads, kv_heads, head_dim, cos, sin, pos, slot, q_out, k_cache, vt_cache, max_len):
+def qkv_rope(x, m, wp, k, heads, kv_heads, head_dim, cos, sin, pos, slot, q_out, k_cache, vt_cache, max_len,
+             norm_eps: float = 0.0):
     _check(x, "x"); _check(wp, "w_packed"); _check(q_out, "q"); _check(k_cache, "k_cache"); _check(vt_cache, "vt")
     for t, nm in ((pos, "pos"), (slot, "slot")):
         _check(t, nm, torch.int32)
@@ -119,9 +129,10 @@ def qkv_rope(x, m, wp, k, heads, kv_heads, head_dim, cos, sin, pos, slot, q_out,
         raise ValueError("qkv_rope: cache smaller than kv_heads * max_len * head_dim")
     if cos.shape != sin.shape or cos.dim() != 2 or cos.shape[1] != head_dim // 2:
         raise ValueError("qkv_rope: cos/sin must be [rows, head_dim/2]")
-    _lib.call("ssd_gemm_qkv_rope_bf16", x.data_ptr(), _rows(x, "x", k, m), m, wp.data_ptr(), k, heads, kv_heads,
-              head_dim, cos.data_ptr(), sin.data_ptr(), cos.shape[0], pos.data_ptr(), slot.data_ptr(), q_out.data_ptr(),
-              _rows(q_out, "q", heads * head_dim, m), k_cache.data_ptr(), vt_cache.data_ptr(), max_len, stream())
+    _lib.call("ssd_gemm_qkv_rope_bf16", x.data_ptr(), _rows(x, "x", k, m), m, wp.data_ptr(), k, float(norm_eps), heads,
+              kv_heads, head_dim, cos.data_ptr(), sin.data_ptr(), cos.shape[0], pos.data_ptr(), slot.data_ptr(),
+              q_out.data_ptr(), _rows(q_out, "q", heads * head_dim, m), k_cache.data_ptr(), vt_cache.data_ptr(),
+              max_len, stream())
 
 
 def attn_workspace_floats(m: int, heads: int, head_dim: int, max_len: int) -> int:
@@ -255,6 +266,33 @@ def qkv_rope_finalize(part, s, ld, m, heads, kv_heads, head_dim, cos, sin, pos, 
     _lib.call("ssd_qkv_rope_finalize_bf16", part.data_ptr(), ld, m * ld, s, m, heads, kv_heads, head_dim,
               cos.data_ptr(), sin.data_ptr(), cos.shape[0], pos.data_ptr(), slot.data_ptr(), q_out.data_ptr(),
               _rows(q_out, "q", heads * head_dim, m), k_cache.data_ptr(), vt_cache.data_ptr(), max_len, stream())
+
+
+def residual_group(n: int, k: int) -> int:
+    g = int(_lib.load().ssd_gemm_residual_group(n, k))
+    if g < 1:
+        raise ValueError(f"residual_group: bad shape N={n} K={k}")
+    return g
+
+
+def residual_floats(m: int, n: int, k: int) -> int:
+    """fp32 scratch of gemm_residual for m rows of an [n, k] projection (0: none needed)."""
+    return int(_lib.load().ssd_gemm_residual_floats(m, n, k))
+
+
+def gemm_residual(x, m, wp, n, k, h, part, bias=None):
+    """h[:m] <- bf16(h + bf16(x W^T + bias)) (W packed with residual=True)."""
+    _check(x, "x"); _check(wp, "w_packed"); _check(h, "h")
+    if bias is not None:
+        _check(bias, "bias"); _len(bias, "bias", n)
+    need = residual_floats(m, n, k)
+    if need:
+        _check(part, "part", torch.float32)
+        _len(part, "part", need)
+    _len(wp, "w_packed", packed_elems(n, k))
+    _lib.call("ssd_gemm_residual_bf16", x.data_ptr(), _rows(x, "x", k, m), m, wp.data_ptr(), n, k, _p(bias),
+              h.data_ptr(), _rows(h, "h", n, m), _p(part) if need else None, part.numel() if need else 0, stream())
+    return h
 
 
 def add_rmsnorm(part, s, ld, h, m, w, eps, out, bias=None):

@@ -50,7 +50,7 @@ def test_host_only_entry_points():
     assert lib.ssd_tree_limits(lim) == 0 and list(lim) == [1024, 32, 32]
     assert lib.ssd_attn_max_depth() == 32
     # argument validation happens on the host, before any launch
-    rc = lib.ssd_gemm_bf16(None, 0, 1, None, 16, 32, None, 0, None, 0, None, 0, None)
+    rc = lib.ssd_gemm_bf16(None, 0, 1, None, 16, 32, 0.0, None, 0, None, 0, None, 0, None)
     assert rc == 1 and b"null" in lib.ssd_last_error()
 
 

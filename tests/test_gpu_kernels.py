@@ -453,3 +453,94 @@ def test_accept_greedy_matches_oracle(seed):
     assert nn_ == len(acc_ref) + 1
     assert result[1:1 + nn_].tolist() == [t.tokens[i] for i in acc_ref] + [bonus_ref]
     assert keep[:nn_].tolist() == [30] + [31 + i for i in acc_ref] and int(nkeep) == nn_ and int(root) == bonus_ref
+
+
+# ---------------------------------------------- folded RMSNorm / fused residual projection
+def _exact_norm_linear(h, g, eps, w):
+    """fp64 RMSNorm(h) * g then x W^T: the exact value both the reference chain and the folded
+    kernel approximate."""
+    hd = h.double()
+    xn = hd * torch.rsqrt(hd.pow(2).mean(-1, keepdim=True) + eps) * g.double()
+    return xn @ w.double().T
+
+
+@pytest.mark.parametrize("m", [1, 25, 64, 70])
+@pytest.mark.parametrize("n,k", [(1040, 2048), (16384, 4096), (128256, 512)])
+def test_gemm_folded_rmsnorm(m, n, k):
+    """RMSNorm folded into the GEMM (norm weight in the packed columns, row scale computed in the
+    kernel) against the exact norm + linear (abs/rel 2e-2, the per-node logit tolerance) and
+    against the reference's bf16 chain (oracle rmsnorm then linear) for >= 99% of outputs;
+    batch-invariant bitwise."""
+    ops = _ops()
+    h = bf(rand(m, k, std=3.0, seed=60))
+    g = bf(1 + rand(k, std=0.2, seed=61))
+    w = bf(rand(n, k, std=0.02, seed=62))
+    wp = ops.pack_weight(w.to(DEV), col_scale=g.to(DEV))
+    y = torch.zeros(m, n, dtype=torch.bfloat16, device=DEV)
+    ops.gemm(h.to(DEV), m, wp, n, k, y, norm_eps=1e-5)
+    got = y.float().cpu()
+    torch.testing.assert_close(got.double(), _exact_norm_linear(h, g, 1e-5, w), atol=2e-2, rtol=2e-2)
+    chain = ok.linear(ok.rmsnorm(h.float(), g, 1e-5), w)
+    lim = 1e-2 + 2e-2 * chain.abs()
+    assert ((got - chain).abs() <= lim).float().mean() >= 0.99
+    one = torch.zeros(1, n, dtype=torch.bfloat16, device=DEV)
+    for r in {0, m // 2, m - 1}:
+        ops.gemm(h[r:r + 1].contiguous().to(DEV), 1, wp, n, k, one, norm_eps=1e-5)
+        assert torch.equal(one[0], y[r]), f"row {r}"
+
+
+def test_swiglu_and_qkv_folded_rmsnorm():
+    ops = _ops()
+    from ssd.models.llama import gate_up_row_map, qkv_row_map, rope_tables
+
+    m, inter, k = 25, 320, 512
+    h = bf(rand(m, k, std=2.0, seed=63))
+    g = bf(1 + rand(k, std=0.2, seed=64))
+    wg, wu = bf(rand(inter, k, std=0.05, seed=65)), bf(rand(inter, k, std=0.05, seed=66))
+    wp = ops.pack_weight(torch.cat([wg, wu]).to(DEV), gate_up_row_map(inter), col_scale=g.to(DEV))
+    y = torch.zeros(m, inter, dtype=torch.bfloat16, device=DEV)
+    ops.gemm_swiglu(h.to(DEV), m, wp, inter, k, y, norm_eps=1e-6)
+    xn = ok.rmsnorm(h.float(), g, 1e-6)
+    ref = ok.swiglu(xn, wg, wu)
+    torch.testing.assert_close(y.float().cpu(), ref, atol=2e-2, rtol=2e-2)
+
+    heads, kvh, hd, d, max_len = 4, 2, 64, 256, 64
+    h = bf(rand(6, d, std=2.0, seed=67))
+    g = bf(1 + rand(d, std=0.2, seed=68))
+    wq, wk, wv = (bf(rand(hh * hd, d, std=0.05, seed=69 + i)) for i, hh in enumerate((heads, kvh, kvh)))
+    wp = ops.pack_weight(torch.cat([wq, wk, wv]).to(DEV), qkv_row_map(heads, kvh, hd), col_scale=g.to(DEV))
+    cos, sin = rope_tables(max_len, hd, 500000.0, DEV)
+    pos = torch.tensor([3, 3, 9, 40, 0, 63], dtype=torch.int32)
+    slot = torch.tensor([10, 11, 12, 13, 20, 63], dtype=torch.int32)
+    q = torch.zeros(6, heads * hd, dtype=torch.bfloat16, device=DEV)
+    kc = torch.zeros(kvh, max_len, hd, dtype=torch.bfloat16, device=DEV)
+    vt = torch.zeros(kvh, hd, max_len, dtype=torch.bfloat16, device=DEV)
+    ops.qkv_rope(h.to(DEV), 6, wp, d, heads, kvh, hd, cos, sin, pos.to(DEV), slot.to(DEV), q, kc, vt, max_len,
+                 norm_eps=1e-6)
+    rq, rk, rv = ok.qkv_rope(ok.rmsnorm(h.float(), g, 1e-6), wq, wk, wv, heads, kvh, hd, pos.long(), 500000.0)
+    torch.testing.assert_close(q.view(6, heads, hd).float().cpu(), rq.float(), atol=2e-2, rtol=2e-2)
+    torch.testing.assert_close(kc[:, slot.long()].transpose(0, 1).float().cpu(), rk.float(), atol=2e-2, rtol=2e-2)
+    torch.testing.assert_close(vt[:, :, slot.long()].permute(2, 0, 1).float().cpu(), rv.float(), atol=2e-2, rtol=2e-2)
+
+
+@pytest.mark.parametrize("m", [1, 7, 25, 64, 100])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (4096, 14336), (320, 512), (2048, 8192)])
+def test_gemm_residual(m, n, k):
+    """The residual projection (direct GEMM with the add in its epilogue, or split-K partials plus
+    a finalize that adds, chosen by shape) is bit-identical to the same arithmetic composed from
+    the plain entry points, and matches the oracle's bf16 chain."""
+    ops = _ops()
+    x, w = bf(rand(m, k, seed=70)).to(DEV), bf(rand(n, k, std=0.02, seed=71)).to(DEV)
+    b, h0 = bf(rand(n, std=0.1, seed=72)).to(DEV), bf(rand(m, n, seed=73)).to(DEV)
+    wp = ops.pack_weight(w, residual=True)
+    part = torch.zeros(max(1, ops.residual_floats(m, n, k)), dtype=torch.float32, device=DEV)
+    h = h0.clone()
+    ops.gemm_residual(x, m, wp, n, k, h, part, bias=b)
+    ref = h0.clone()
+    if ops.residual_floats(m, n, k):
+        p2, s, ld = _partial(ops, x, m, ops.pack_weight(w, split=True), n, k)
+        ops.gemm_finalize(p2, s, ld, m, n, ref, bias=b, residual=ref)
+    else:
+        ops.gemm(x, m, ops.pack_weight(w), n, k, ref, bias=b, residual=ref)
+    assert torch.equal(h, ref)
+    close_bf16(h, ok.linear(x.cpu(), w.cpu(), b.cpu(), residual=h0.cpu()))
