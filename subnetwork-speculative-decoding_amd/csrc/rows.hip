@@ -168,104 +168,101 @@ __global__ __launch_bounds__(256) void kv_compact_kernel(bf16_t* __restrict__ kc
 }
 
 constexpr int TOPK_MAX = 16;
+constexpr int TOPK_CHUNK = 4096;  // columns per partial workgroup: 256 threads x 16 columns
+constexpr int TOPK_PER = TOPK_CHUNK / 256;
 
-struct Cand {
-  float v;
-  int i;
-};
-
-// a ranks before b: larger value, then lower column (the oracle's stable-sort order).
-__device__ __forceinline__ bool better(float av, int ai, float bv, int bi) { return av > bv || (av == bv && ai < bi); }
-
-__device__ __forceinline__ void topk_insert(Cand (&c)[TOPK_MAX], int k, float v, int i) {
-  if (!better(v, i, c[k - 1].v, c[k - 1].i)) return;
-  int p = k - 1;
-  while (p > 0 && better(v, i, c[p - 1].v, c[p - 1].i)) {
-    c[p] = c[p - 1];
-    --p;
-  }
-  c[p] = Cand{v, i};
+// Ranking key of a (value, column) pair: a larger key ranks first, i.e. larger value, then
+// lower column (the oracle's stable-sort order). The value maps to its order-preserving
+// unsigned image; NaN ranks below every number; key 0 is "no candidate".
+__device__ __forceinline__ uint64_t rank_key(float v, int col) {
+  uint32_t b = __float_as_uint(v);
+  b = (v != v) ? 0u : ((b & 0x80000000u) ? ~b : (b | 0x80000000u));
+  return ((uint64_t)b << 32) | (uint32_t)(~(uint32_t)col);
 }
+__device__ __forceinline__ float key_value(uint64_t key) {
+  const uint32_t b = (uint32_t)(key >> 32);
+  return __uint_as_float((b & 0x80000000u) ? (b & 0x7fffffffu) : ~b);
+}
+__device__ __forceinline__ int key_col(uint64_t key) { return (int)~(uint32_t)key; }
 
-constexpr int TOPK_CHUNK = 4096;  // columns per partial workgroup
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, off), hi = __shfl_xor((uint32_t)(v >> 32), off);
+    const uint64_t o = ((uint64_t)hi << 32) | lo;
+    v = o > v ? o : v;
+  }
+  return v;
+}
 
 struct TopkPart {
   float mx;  // chunk maximum
   float se;  // sum of exp(x - mx) over the chunk (mode 1)
-  float v[TOPK_MAX];
-  int i[TOPK_MAX];
+  uint64_t key[TOPK_MAX];  // the chunk's k best, best first
 };
 
-// Partial pass: workgroup (s, row) scans columns [s*chunk, (s+1)*chunk) of one row of bf16
-// logits and writes its k best (value, column) pairs -- larger value first, lower column on
-// ties -- its maximum and (mode 1) its sum of exp(x - max).
+// Partial pass: workgroup (s, row) holds columns [s*4096, (s+1)*4096) of one row of bf16 logits
+// in registers (thread t: columns t*8 + [0, 8) and 2048 + t*8 + [0, 8) of the chunk) and takes
+// its k best keys in k rounds of a block-wide maximum, each round retiring the winner; it also
+// writes the chunk maximum and (mode 1) the sum of exp(x - max).
 __global__ __launch_bounds__(256) void row_topk_partial_kernel(const bf16_t* __restrict__ logits, int64_t ld, int N,
                                                                int k, int mode, TopkPart* __restrict__ parts) {
-  __shared__ float sv[256 * TOPK_MAX];
-  __shared__ int si[256 * TOPK_MAX];
+  __shared__ uint64_t wbest[2][4];
   __shared__ float sh[4];
   const int s = blockIdx.x, row = blockIdx.y, S = gridDim.x;
-  const int c0 = s * TOPK_CHUNK, c1 = min(N, c0 + TOPK_CHUNK);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const bf16_t* x = logits + (size_t)row * ld;
-  Cand c[TOPK_MAX];
+  float val[TOPK_PER];
+  uint64_t key[TOPK_PER];
 #pragma unroll
-  for (int q = 0; q < TOPK_MAX; ++q) c[q] = Cand{-INFINITY, 0x7fffffff};
-  const int v1 = c0 + ((c1 - c0) / 8) * 8;
-  for (int col = c0 + threadIdx.x * 8; col < v1; col += 256 * 8) {
+  for (int h = 0; h < 2; ++h) {
+    const int col = s * TOPK_CHUNK + h * 2048 + threadIdx.x * 8;
     Pack8 p;
-    p.u = *(const uint4*)(x + col);
+    if (col + 8 <= N) {
+      p.u = *(const uint4*)(x + col);
+    } else {
 #pragma unroll
-    for (int t = 0; t < 8; ++t) topk_insert(c, k, bf2f(p.h[t]), col + t);
+      for (int t = 0; t < 8; ++t) p.h[t] = col + t < N ? x[col + t] : (bf16_t)0;
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const bool ok = col + t < N;
+      val[h * 8 + t] = ok ? bf2f(p.h[t]) : -INFINITY;
+      key[h * 8 + t] = ok ? rank_key(val[h * 8 + t], col + t) : 0ull;
+    }
   }
-  for (int col = v1 + threadIdx.x; col < c1; col += 256) topk_insert(c, k, bf2f(x[col]), col);
+  TopkPart* out = parts + (size_t)row * S + s;
+  uint32_t taken = 0;
+  float mx = -INFINITY;
   for (int q = 0; q < k; ++q) {
-    sv[threadIdx.x * TOPK_MAX + q] = c[q].v;
-    si[threadIdx.x * TOPK_MAX + q] = c[q].i;
+    uint64_t b = 0;
+    int bj = -1;
+#pragma unroll
+    for (int j = 0; j < TOPK_PER; ++j)
+      if (!((taken >> j) & 1u) && key[j] > b) { b = key[j]; bj = j; }
+    const uint64_t wm = wave_max_u64(b);
+    if (lane == 0) wbest[q & 1][wave] = wm;
+    __syncthreads();  // one barrier per round: rounds alternate between the two slots
+    uint64_t m = wbest[q & 1][0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) m = wbest[q & 1][w] > m ? wbest[q & 1][w] : m;
+    if (bj >= 0 && b == m) taken |= 1u << bj;  // keys are distinct: one thread retires it
+    if (threadIdx.x == 0) out->key[q] = m;
+    if (q == 0) mx = m ? key_value(m) : -INFINITY;
   }
-  __syncthreads();
-  for (int stride = 128; stride >= 1; stride >>= 1) {
-    Cand mrg[TOPK_MAX];
-    const bool act = threadIdx.x < stride;
-    if (act) {
-      const float* av = sv + threadIdx.x * TOPK_MAX;
-      const int* ai = si + threadIdx.x * TOPK_MAX;
-      const float* bv = sv + (threadIdx.x + stride) * TOPK_MAX;
-      const int* bi = si + (threadIdx.x + stride) * TOPK_MAX;
-      int pa = 0, pb = 0;
-      for (int q = 0; q < k; ++q) {
-        if (better(av[pa], ai[pa], bv[pb], bi[pb])) { mrg[q] = Cand{av[pa], ai[pa]}; ++pa; }
-        else { mrg[q] = Cand{bv[pb], bi[pb]}; ++pb; }
-      }
-    }
-    __syncthreads();
-    if (act) {
-      for (int q = 0; q < k; ++q) {
-        sv[threadIdx.x * TOPK_MAX + q] = mrg[q].v;
-        si[threadIdx.x * TOPK_MAX + q] = mrg[q].i;
-      }
-    }
-    __syncthreads();
-  }
-  const float mx = sv[0];
   float se = 0.f;
   if (mode == 1) {
     float acc = 0.f;
-    for (int col = c0 + threadIdx.x * 8; col < v1; col += 256 * 8) {
-      Pack8 p;
-      p.u = *(const uint4*)(x + col);
 #pragma unroll
-      for (int t = 0; t < 8; ++t) acc += __expf(bf2f(p.h[t]) - mx);
-    }
-    for (int col = v1 + threadIdx.x; col < c1; col += 256) acc += __expf(bf2f(x[col]) - mx);
+    for (int j = 0; j < TOPK_PER; ++j) acc += __expf(val[j] - mx);
     se = block_sum_256(acc, sh);
   }
-  TopkPart* out = parts + (size_t)row * S + s;
   if (threadIdx.x == 0) { out->mx = mx; out->se = se; }
-  if (threadIdx.x < k) { out->v[threadIdx.x] = sv[threadIdx.x]; out->i[threadIdx.x] = si[threadIdx.x]; }
 }
 
 // Merge pass, one wave per row: global max M; logsumexp = M + log(sum_s se_s * exp(mx_s - M))
-// (lanes own chunks; fixed butterfly order); the k best of the chunks' sorted lists.
+// (lanes own chunks; fixed butterfly order); the k best of the S*k chunk keys, held in
+// registers (lane l: candidates l + 64*j), in k rounds of a wave maximum.
 // mode 0 writes raw values, mode 1 log-softmax values (x - M) - log(sum).
 __global__ __launch_bounds__(64) void row_topk_merge_kernel(const TopkPart* __restrict__ parts, int S, int k, int mode,
                                                             const int* __restrict__ vocab_ids, int* __restrict__ out_tok,
@@ -282,25 +279,30 @@ __global__ __launch_bounds__(64) void row_topk_merge_kernel(const TopkPart* __re
     for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
     lse = logf(acc);
   }
-  if (lane == 0) {
-    int head[64];
-    for (int s = 0; s < S && s < 64; ++s) head[s] = 0;
-    for (int q = 0; q < k; ++q) {
-      int best = -1;
-      float bv = -INFINITY;
-      int bi = 0x7fffffff;
-      for (int s = 0; s < S && s < 64; ++s) {
-        if (head[s] >= k) continue;
-        const float v = p[s].v[head[s]];
-        const int ix = p[s].i[head[s]];
-        if (best < 0 || better(v, ix, bv, bi)) { best = s; bv = v; bi = ix; }
-      }
-      ++head[best];
-      out_tok[row * k + q] = vocab_ids ? vocab_ids[bi] : bi;
-      if (out_val) out_val[row * k + q] = mode == 1 ? (bv - mx) - lse : bv;
-    }
-    if (mode == 1 && out_lse) out_lse[row] = mx + lse;
+  const int total = S * k;  // <= 64 * TOPK_MAX
+  uint64_t key[TOPK_MAX];
+#pragma unroll
+  for (int j = 0; j < TOPK_MAX; ++j) {
+    const int c = lane + 64 * j;
+    key[j] = c < total ? p[c / k].key[c % k] : 0ull;
   }
+  uint32_t taken = 0;
+  for (int q = 0; q < k; ++q) {
+    uint64_t b = 0;
+    int bj = -1;
+#pragma unroll
+    for (int j = 0; j < TOPK_MAX; ++j)
+      if (!((taken >> j) & 1u) && key[j] > b) { b = key[j]; bj = j; }
+    const uint64_t m = wave_max_u64(b);
+    if (bj >= 0 && b == m) taken |= 1u << bj;
+    if (lane == 0) {
+      const int col = key_col(m);
+      const float v = key_value(m);
+      out_tok[row * k + q] = vocab_ids ? vocab_ids[col] : col;
+      if (out_val) out_val[row * k + q] = mode == 1 ? (v - mx) - lse : v;
+    }
+  }
+  if (lane == 0 && mode == 1 && out_lse) out_lse[row] = mx + lse;
 }
 
 }  // namespace ssd

@@ -267,6 +267,32 @@ def test_row_topk_argmax_and_logsoftmax():
     assert tk.view(m, k).cpu().tolist() == (ri * 3 + 1).tolist()
 
 
+@pytest.mark.parametrize("m,n,k", [(3, 7, 7), (2, 4101, 16), (25, 128256, 1), (24, 128256, 3), (4, 262144, 16)])
+def test_row_topk_shapes(m, n, k):
+    """Ragged tails (n not a multiple of 8 or of a chunk), k up to 16, a full vocabulary and the
+    64-chunk maximum; rows with many equal values and -inf entries."""
+    ops = _ops()
+    x = bf(rand(m, n, seed=26 + n) * 4)
+    x[0, :] = 0.0  # all equal: the k lowest columns, in order
+    if m > 1:
+        x[1, ::2] = float("-inf")
+        x[1, n - 1] = x[1].max() + 2  # the winner in the last (ragged) chunk
+    ld = (n + 7) // 8 * 8
+    xd = torch.zeros(m, ld, dtype=torch.bfloat16, device=DEV)
+    xd[:, :n] = x.to(DEV)
+    tk = torch.zeros(m * k, dtype=torch.int32, device=DEV)
+    lp = torch.zeros(m * k, dtype=torch.float32, device=DEV)
+    lse = torch.zeros(m, dtype=torch.float32, device=DEV)
+    ops.row_topk(xd, m, n, k, 1, None, tk, lp, lse)
+    rv, ri, rlse = ok.log_softmax_topk(x, k)
+    assert tk.view(m, k).cpu().tolist() == ri.tolist()
+    torch.testing.assert_close(lp.view(m, k).cpu(), rv, atol=2e-5, rtol=1e-5)
+    torch.testing.assert_close(lse.cpu(), rlse, atol=2e-5, rtol=1e-5)
+    ops.row_topk(xd, m, n, k, 0, None, tk, lp)
+    assert tk.view(m, k).cpu().tolist() == ri.tolist()
+    torch.testing.assert_close(lp.view(m, k).cpu(), torch.sort(x.float(), dim=1, descending=True, stable=True)[0][:, :k])
+
+
 # ------------------------------------------------------------------ attention
 def _attn_case(m, heads, kvh, hd, S, prefix, anc, seed):
     q = bf(rand(m, heads, hd, seed=seed))
