@@ -76,6 +76,16 @@ __device__ __forceinline__ void epi_store(const GemmArgs& a, int n, int m, float
   a.Y[(size_t)m * a.ldy + n] = f2bf(t);
 }
 
+// epi_store with the bias and residual values already loaded (bias_v / res_v are read only when
+// the corresponding pointer is set).
+__device__ __forceinline__ void epi_store_pre(const GemmArgs& a, int n, int m, float t, float bias_v, float res_v) {
+  if (a.bias) t += bias_v;
+  t = rbf(t);
+  if (a.act) t = rbf(apply_act(a.act, t));
+  if (a.residual) t = rbf(res_v + t);
+  a.Y[(size_t)m * a.ldy + n] = f2bf(t);
+}
+
 // SwiGLU: intermediate column col of row m from its gate and up dot products.
 __device__ __forceinline__ void epi_swiglu(const GemmArgs& a, int col, int m, float gt, float up) {
   if (a.bias) gt += bf2f(a.bias[col]);
@@ -191,7 +201,9 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, int nb, int Mv,
 
 template <int KS, int NSUB, int CT>
 struct GemmLds {
-  float4 red[KS][NSUB][CT][64];
+  // [wave][sub-tile][column tile][element e][lane]; the e stride of 68 words puts the 64 values
+  // one wave reads in the epilogue (4 rows m x 16 tile rows r) in 64 different banks
+  float red[KS][NSUB][CT][4][68];
   float ss[KS][CT][16];  // per-wave sums of x^2 per row (folded RMSNorm)
   float rn[CT * 16];     // per-row rsqrt(mean(x^2) + eps)
 };
@@ -246,6 +258,21 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
     pre_r = threadIdx.x & 7;
     pre_slot = a.row_slot[pre_m];
     pre_pos = min(max(a.row_pos[pre_m], 0), (int)a.rope_rows - 1);
+  }
+
+  // plain store: thread t owns output (token t / 16, tile row t % 16) of every sub-tile when the
+  // workgroup has enough threads; its residual and bias values are loaded now (clamped
+  // addresses) and arrive while the weights stream.
+  const bool st_pre = EPI == EPI_STORE && 16 * Mv <= 64 * KS;
+  float pre_res[NSUB], pre_bias[NSUB];
+  if constexpr (EPI == EPI_STORE) {
+    const int pm = min((int)threadIdx.x >> 4, Mv - 1);
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s) {
+      const int n = min((tile * NSUB + s) * 16 + ((int)threadIdx.x & 15), a.N - 1);
+      pre_res[s] = a.residual ? bf2f(a.residual[(size_t)pm * a.ldr + n]) : 0.f;
+      pre_bias[s] = a.bias ? bf2f(a.bias[n]) : 0.f;
+    }
   }
 
   int kb = kb_lo;
@@ -310,7 +337,8 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
   for (int s = 0; s < NSUB; ++s)
 #pragma unroll
     for (int c = 0; c < CT; ++c)
-      lds.red[w][s][c][lane] = make_float4(acc[s][c][0], acc[s][c][1], acc[s][c][2], acc[s][c][3]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) lds.red[w][s][c][e][lane] = acc[s][c][e];
   if constexpr (NORM) {
     // row sums: the 4 k-groups of the wave (lanes j, j+16, j+32, j+48), then the waves in order
 #pragma unroll
@@ -341,16 +369,20 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
       const int c = m >> 4;
       const int ln = (m & 15) + 16 * (r >> 2);
       const int e = r & 3;
-      float v = 0.f;
+      float v = lds.red[0][s][c][e][ln];
 #pragma unroll
-      for (int ww = 0; ww < KS; ++ww) {
-        const float4 q = lds.red[ww][s][c][ln];
-        const float x = e == 0 ? q.x : e == 1 ? q.y : e == 2 ? q.z : q.w;
-        v = ww == 0 ? x : v + x;
-      }
+      for (int ww = 1; ww < KS; ++ww) v += lds.red[ww][s][c][e][ln];
       if constexpr (NORM) v *= lds.rn[m];
       return v;
     };
+    if constexpr (EPI == EPI_STORE) {
+      if (st_pre) {
+        const int m = threadIdx.x >> 4, r = threadIdx.x & 15;
+        const int n = (tile * NSUB + s) * 16 + r;
+        if (m < Mv && n < a.N) epi_store_pre(a, n, m, val(r, m), pre_bias[s], pre_res[s]);
+        continue;
+      }
+    }
     if constexpr (EPI == EPI_QKV) {
       if (qkv_pre) {
         const int nb = tile * NSUB + s;

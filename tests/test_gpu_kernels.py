@@ -570,3 +570,8 @@ def test_gemm_residual(m, n, k):
         ops.gemm(x, m, ops.pack_weight(w), n, k, ref, bias=b, residual=ref)
     assert torch.equal(h, ref)
     close_bf16(h, ok.linear(x.cpu(), w.cpu(), b.cpu(), residual=h0.cpu()))
+    # reusing the scratch: a second call and a smaller one agree too, rows past m untouched
+    for mm in (m, max(1, m // 3)):
+        h2 = h0.clone()
+        ops.gemm_residual(x, mm, wp, n, k, h2, part, bias=b)
+        assert torch.equal(h2[:mm], ref[:mm]) and torch.equal(h2[mm:], h0[mm:])
