@@ -94,11 +94,10 @@ def kernel_figures(gen, sess) -> dict:
     L = model.layers
     nl = s.layers
     m = gen.drafter.max_verify_nodes() + 1
-    committed = cache.get_seq_length()
     aws = ws.attn_ws(model, cache.capacity)
-    p = committed + 1
-    rows = sess.verify_rows
-    gen.drafter.finalize_device(sess.tree, committed, sess.root_rows, rows)
+    rows = sess.verify_rows  # the last round's verify rows (the next round's draft only touches the root row)
+    p = int(rows.prefix[0])  # that round's committed length + 1
+    committed = p - 1
     part = ws.part
     out = {}
 

@@ -188,6 +188,13 @@ typedef struct SsdRows {
 
 int ssd_tree_limits(int32_t* out3); /* host: {node capacity, max depth, max ancestors per row} */
 
+/* Start of a draft phase (ssd/engine/tree_drafter.py:147-160: a fresh DraftTree and the root fed
+ * at root_pos): tree level counts to zero and root row 0 = position/slot root_pos, prefix
+ * root_pos + 1, depth 0, on the device (no host copy). root_pos = base + n_new[0], read on the
+ * device (n_new: the committed count of the previous round's record; NULL: root_pos = base), so
+ * a round can start before the host has read the previous one. */
+int ssd_round_begin(const SsdTree* tree, const SsdRows* root, int base, const int32_t* n_new, hipStream_t stream);
+
 /* One level of TreeDrafter.build (ssd/engine/tree_drafter.py:165-200): candidates of the current
  * frontier (cand_tok/cand_lp [F, k]; tok < 0 = none) -> score = parent score + lp, stable sort,
  * width cut, append; if feed, write the next draft forward's rows (positions root_pos+d+1, slots

@@ -208,9 +208,32 @@ __global__ void accept_greedy_kernel(SsdTree t, const int* __restrict__ argmax, 
   *root_token = want;
 }
 
+// Start of a round: empty tree (level counts zero) and the root's draft row (position and slot
+// root_pos = base + n_new[0] (n_new null: base), prefix root_pos + 1, no ancestors); the root
+// token stays as the last round left it.
+__global__ void round_begin_kernel(SsdTree t, SsdRows r, int base, const int32_t* n_new) {
+  const int i = threadIdx.x;
+  if (i < 1 + 2 * TREE_MAXDEPTH) t.meta[i] = 0;
+  if (i == 0) {
+    const int root_pos = base + (n_new ? n_new[0] : 0);
+    r.pos[0] = root_pos;
+    r.slot[0] = root_pos;
+    r.prefix[0] = root_pos + 1;
+    r.depth[0] = 0;
+  }
+}
+
 }  // namespace ssd
 
 using namespace ssd;
+
+SSD_API int ssd_round_begin(const SsdTree* tree, const SsdRows* root, int base, const int32_t* n_new,
+                            hipStream_t stream) {
+  if (!tree || !root || !tree->meta || !root->pos || root->cap < 1) return set_error(SSD_EINVAL, "round_begin: null");
+  if (base < 0) return set_error(SSD_EINVAL, "round_begin: base %d < 0", base);
+  hipLaunchKernelGGL(round_begin_kernel, dim3(1), dim3(128), 0, stream, *tree, *root, base, n_new);
+  return check_launch("round_begin");
+}
 
 SSD_API int ssd_tree_limits(int32_t* out) {
   if (!out) return set_error(SSD_EINVAL, "tree_limits: null");

@@ -80,10 +80,11 @@ class _Phases:
         self._pending.append((name, ev))
 
     def resolve(self) -> None:
+        """Adds up every closed phase; a phase still open (the last mark, when named) stays pending."""
         for (name, a), (_, b) in zip(self._pending, self._pending[1:]):
             if name is not None:
                 self.totals[name] = self.totals.get(name, 0.0) + a.elapsed_time(b) / 1000.0
-        self._pending = []
+        self._pending = self._pending[-1:] if self._pending and self._pending[-1][0] is not None else []
 
 
 def _prefill(target: SubnetworkDraftModel, ids: list, cache: KVCache, ws, out_dev: torch.Tensor,
@@ -188,20 +189,34 @@ class DecodeSession:
         self.phases = _Phases()
         self.accepted_per_round: list = []
         self.tree_sizes: list = []
+        self._begun = False  # the next round's first draft forward is already enqueued
 
     def prefill(self, ids: list) -> int:
         _prefill(self.target, ids, self.cache, self.ws, self.root_rows.ids[0:1], self.sampler)
         return int(self.root_rows.ids[0])
 
+    def _begin(self, base: int, n_new_dev: Optional[torch.Tensor], counter: int) -> None:
+        if self.sampler is not None:
+            self.sampler.counter = counter
+        self.phases.mark("draft")
+        self.drafter.begin_device(self.cache, self.root_rows, base, self.tree, self.cand_tok, self.cand_lp, self.ws,
+                                  self.sampler, n_new_dev)
+
     def step(self) -> list:
+        """One round. The round's first draft forward (root at the new committed length, read on
+        the device) is enqueued for the next round before this one's result is read, so the GPU
+        keeps working while the host reads the result and enqueues the rest."""
         cfg, drafter, target, cache, ws = self.cfg, self.drafter, self.target, self.cache, self.ws
         committed = cache.get_seq_length()
         ph = self.phases
+        counter = len(self.accepted_per_round) + 1
+        if not self._begun:
+            self._begin(committed, None, counter)
+        self._begun = False
         if self.sampler is not None:
-            self.sampler.counter = len(self.accepted_per_round) + 1
-        ph.mark("draft")
-        drafter.build_device(cache, self.root_rows, committed, self.tree, self.level_rows, self.cand_tok,
-                             self.cand_lp, ws, self.sampler)
+            self.sampler.counter = counter
+        drafter.levels_device(cache, committed, self.tree, self.level_rows, self.cand_tok, self.cand_lp, ws,
+                              self.sampler)
         cache.crop(committed)
         ph.mark("verify")
         m = drafter.finalize_device(self.tree, committed, self.root_rows, self.verify_rows)
@@ -219,7 +234,13 @@ class DecodeSession:
         cache.compact_device(committed, self.keep_src, self.n_keep, cfg.depth + 1)
         self.record_host.copy_(self.record, non_blocking=True)
         ph.mark(None)
-        torch.cuda.current_stream().synchronize()
+        done = torch.cuda.Event()
+        done.record()
+        hi = committed + cfg.depth + 1  # the next root position is at most this
+        if hi + 1 + drafter.max_tree_cache() <= cache.max_length:
+            self._begin(committed, self.record[2:3], counter + 1)
+            self._begun = True
+        done.synchronize()
         ph.resolve()
         n_new = int(self.record_host[2])
         new = self.record_host[3:3 + n_new].tolist()

@@ -160,29 +160,35 @@ class TreeDrafter:
         return min(total, self.cfg.max_nodes) if self.cfg.max_nodes else total
 
     # ------------------------------------------------------------------ device
-    def build_device(self, cache: KVCache, root_rows, root_pos: int, tree: DeviceTree, level_rows, cand_tok,
-                     cand_lp, ws, sampler=None) -> None:
-        """Enqueue the whole draft phase for the root held in ``root_rows.ids[0]``; leaves the
-        unpruned tree in ``tree`` (no host synchronisation). Sampled drafting (temperature > 0)
-        needs ``sampler`` (ssd.engine.sampling.Sampler): proposals are Gumbel top-k draws from
-        the warped draft distribution, which is kept per node in ``sampler.Q``."""
+    def _propose(self, logits, rows: int, d: int, tree: DeviceTree, cand_tok, cand_lp, sampler) -> None:
+        if self.greedy:
+            ops.row_topk(logits, rows, logits.shape[1], self.branch[d], 1, self.draft._vocab_ids_i32, cand_tok,
+                         cand_lp)
+        else:
+            sampler.propose(self.draft, logits, rows, d, self.branch[d], tree.meta, cand_tok, cand_lp)
+
+    def begin_device(self, cache: KVCache, root_rows, base_pos: int, tree: DeviceTree, cand_tok, cand_lp, ws,
+                     sampler=None, n_new_dev: Optional[torch.Tensor] = None) -> None:
+        """First part of the draft phase: empty tree, the root (token in ``root_rows.ids[0]``) fed
+        at root_pos = base_pos + n_new_dev[0] (``n_new_dev`` None: base_pos), and the root's
+        proposals. With ``n_new_dev`` the position is only read on the device, so this can be
+        enqueued before the host has read the previous round; the root forward then gets bounds
+        (root_pos is at most depth + 1 past base_pos) instead of the exact position."""
         if not self.greedy and sampler is None:
             raise ValueError("sampled drafting needs a Sampler")
-        draft = self.draft
-        tree.reset()
+        hi = base_pos + (self.cfg.depth + 1 if n_new_dev is not None else 0)
+        cache.check_room(hi + 1 + self.max_tree_cache())
+        _lib.call("ssd_round_begin", tree.struct, root_rows.struct, base_pos,
+                  None if n_new_dev is None else n_new_dev.data_ptr(), ops.stream())
+        logits = self.draft.forward_rows(root_rows, 1, base_pos + 1, hi + 1, cache, ws)
+        self._propose(logits, 1, 0, tree, cand_tok, cand_lp, sampler)
+
+    def levels_device(self, cache: KVCache, root_pos: int, tree: DeviceTree, level_rows, cand_tok, cand_lp, ws,
+                      sampler=None) -> None:
+        """Rest of the draft phase once root_pos is known on the host: every level's expansion /
+        width cut and the forwards of the fed levels; leaves the unpruned tree in ``tree``."""
         tree_start = root_pos + 1
         cache.check_room(tree_start + self.max_tree_cache())
-        root_rows.upload(None, [root_pos], [root_pos], [root_pos + 1], [0])
-        logits = draft.forward_rows(root_rows, 1, root_pos + 1, root_pos + 1, cache, ws)
-        n = logits.shape[1]
-
-        def propose(logits, rows, d):
-            if self.greedy:
-                ops.row_topk(logits, rows, n, self.branch[d], 1, draft._vocab_ids_i32, cand_tok, cand_lp)
-            else:
-                sampler.propose(draft, logits, rows, d, self.branch[d], tree.meta, cand_tok, cand_lp)
-
-        propose(logits, 1, 0)
         past = tree_start
         for d in range(self.cfg.depth):
             feed = d < self.cfg.depth - 1
@@ -193,10 +199,19 @@ class TreeDrafter:
                       level_rows.struct, m if feed else 0, ops.stream())
             if not feed:
                 break
-            logits = draft.forward_rows(level_rows, m, tree_start, tree_start + d + 1, cache, ws)
-            propose(logits, m, d + 1)
+            logits = self.draft.forward_rows(level_rows, m, tree_start, tree_start + d + 1, cache, ws)
+            self._propose(logits, m, d + 1, tree, cand_tok, cand_lp, sampler)
             past += m
         cache.seq_len = past
+
+    def build_device(self, cache: KVCache, root_rows, root_pos: int, tree: DeviceTree, level_rows, cand_tok,
+                     cand_lp, ws, sampler=None) -> None:
+        """Enqueue the whole draft phase for the root held in ``root_rows.ids[0]``; leaves the
+        unpruned tree in ``tree`` (no host synchronisation). Sampled drafting (temperature > 0)
+        needs ``sampler`` (ssd.engine.sampling.Sampler): proposals are Gumbel top-k draws from
+        the warped draft distribution, which is kept per node in ``sampler.Q``."""
+        self.begin_device(cache, root_rows, root_pos, tree, cand_tok, cand_lp, ws, sampler)
+        self.levels_device(cache, root_pos, tree, level_rows, cand_tok, cand_lp, ws, sampler)
 
     def finalize_device(self, tree: DeviceTree, committed: int, root_rows, verify_rows) -> int:
         """max_nodes cut + verify rows; returns the verify row count used for the launch."""
