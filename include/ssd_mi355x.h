@@ -74,7 +74,8 @@ int ssd_gemm_swiglu_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* 
 /* q/k/v projection + RoPE + KV-cache write, fused. Replaces ssd/models/subnetwork_draft.py:209-222
  * (q/k/v_proj, rotate_half RoPE, KVCache.update at ssd/engine/kv_cache.py:32-43). Row m is at
  * rotary position row_pos[m] (cos/sin tables [rope_rows, hd/2]) and writes cache slot row_slot[m]
- * (rows whose slot is outside [0, max_len) are not written); V is stored transposed. */
+ * (rows whose slot is outside [0, max_len) are not written); K and V go to the cache block layout
+ * below. */
 int ssd_gemm_qkv_rope_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int K, float norm_eps,
                            int heads, int kv_heads, int head_dim, const uint16_t* cos_tab, const uint16_t* sin_tab,
                            int64_t rope_rows, const int32_t* row_pos, const int32_t* row_slot, uint16_t* Q, int64_t ldq,
@@ -116,6 +117,18 @@ int64_t ssd_gemm_residual_floats(int M, int N, int K);
 int ssd_gemm_residual_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int N, int K,
                            const uint16_t* bias, uint16_t* h, int64_t ldh, float* part, int64_t part_floats,
                            hipStream_t stream);
+
+/* ------------------------------------------------------------ KV-cache layout
+ * k_cache / vt_cache (one layer, as passed to the q/k/v GEMM and the attention; the compaction
+ * takes all layers back to back) are kv_heads regions of max_len * head_dim bf16 each, max_len a
+ * multiple of 64 and head_dim a multiple of 32. A region is a sequence of 64-slot blocks, each
+ * stored as the tree-attention MFMA operands in lane order (64 lanes x 8 bf16 per 1 KiB tile):
+ *   K[s][d] at ((((s/64)*4 + kt)*(hd/32) + d/32)*64 + ((d/8)%4)*16 + i)*8 + d%8, with o = s%64,
+ *     kt = (o/32)*2 + (o/4)%2, i = ((o/8)%4)*4 + o%4;
+ *   V[s][d] at ((((s/64)*(hd/16) + d/16)*2 + o/32)*64 + ((o/8)%4)*16 + d%16)*8 + o%8.
+ * (Python: ssd.ops.kv_block_index / kv_tile / kv_untile.) The attention reads every tile of a
+ * block as one contiguous 1 KiB load; the reference's cache is [1, kv_heads, max_len, hd] per
+ * layer (ssd/engine/kv_cache.py:38-43). */
 
 /* ------------------------------------------------------------ tree attention
  * Row t attends cache slots [0, prefix[t]) then anc[t][0..depth[t]) (ancestors in depth order,

@@ -38,8 +38,8 @@ constexpr int ATT_MAXD = 32;     // gathered tree slots per row
 struct AttnArgs {
   const bf16_t* Q;  // [M, heads*hd] (row stride ldq)
   int64_t ldq;
-  const bf16_t* K;   // this layer: [kv_heads, max_len, hd]
-  const bf16_t* Vt;  // this layer: [kv_heads, hd, max_len]
+  const bf16_t* K;   // this layer: kv_heads x (max_len x hd), 64-slot block layout (k_off in common.h)
+  const bf16_t* Vt;  // this layer: kv_heads x (max_len x hd), 64-slot block layout (v_off in common.h)
   int64_t max_len;
   int M, heads, kv_heads;
   const int* prefix;  // [M]
@@ -70,22 +70,21 @@ struct Frags {
   u32x4_t v[DT][2];
 };
 
+// The block's operand tiles are stored in lane order (cache block layout), so each tile is one
+// contiguous 1 KiB load: lane l gets elements [8l, 8l + 8) of the tile.
 template <int HD>
 __device__ __forceinline__ void load_shared_frags(Frags<HD>& f, const AttnArgs& a, int kvh, int key0, int lane) {
-  const int i = lane & 15, g = lane >> 4;
-  const bf16_t* kb = a.K + (size_t)kvh * a.max_len * HD;
+  constexpr int KS = Frags<HD>::KS, DT = Frags<HD>::DT;
+  const bf16_t* kb = a.K + (size_t)kvh * a.max_len * HD + (size_t)(key0 >> 6) * 64 * HD + lane * 8;
 #pragma unroll
-  for (int kt = 0; kt < 4; ++kt) {
-    const bf16_t* row = kb + (size_t)(key0 + perm_key(kt, i)) * HD + g * 8;
+  for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-    for (int ks = 0; ks < Frags<HD>::KS; ++ks) f.k[kt][ks] = *(const u32x4_t*)(row + ks * 32);
-  }
-  const bf16_t* vb = a.Vt + (size_t)kvh * HD * a.max_len;
+    for (int ks = 0; ks < KS; ++ks) f.k[kt][ks] = *(const u32x4_t*)(kb + (kt * KS + ks) * 512);
+  const bf16_t* vb = a.Vt + (size_t)kvh * HD * a.max_len + (size_t)(key0 >> 6) * 64 * HD + lane * 8;
 #pragma unroll
-  for (int dt = 0; dt < Frags<HD>::DT; ++dt) {
-    const bf16_t* row = vb + (size_t)(dt * 16 + i) * a.max_len + key0 + g * 8;
-    f.v[dt][0] = *(const u32x4_t*)(row);
-    f.v[dt][1] = *(const u32x4_t*)(row + 32);
+  for (int dt = 0; dt < DT; ++dt) {
+    f.v[dt][0] = *(const u32x4_t*)(vb + (dt * 2) * 512);
+    f.v[dt][1] = *(const u32x4_t*)(vb + (dt * 2 + 1) * 512);
   }
 }
 
@@ -112,10 +111,10 @@ __device__ __forceinline__ void load_virtual_frags(Frags<HD>& f, const AttnArgs&
 #pragma unroll
   for (int kt = 0; kt < 4; ++kt) {
     const int slot = logical_slot(key0 + perm_key(kt, i), P, L, anc_t, a.max_len);
-    const bf16_t* row = kb + (size_t)(slot < 0 ? 0 : slot) * HD + g * 8;
+    const int sl = slot < 0 ? 0 : slot;
     const uint32_t keep = slot >= 0 ? 0xffffffffu : 0u;
 #pragma unroll
-    for (int ks = 0; ks < Frags<HD>::KS; ++ks) f.k[kt][ks] = *(const u32x4_t*)(row + ks * 32) & keep;
+    for (int ks = 0; ks < Frags<HD>::KS; ++ks) f.k[kt][ks] = *(const u32x4_t*)(kb + k_off(sl, ks * 32 + g * 8, HD)) & keep;
   }
   const bf16_t* vb = a.Vt + (size_t)kvh * HD * a.max_len;
   const int lim = P < a.max_len ? P : (int)a.max_len;  // prefix positions that exist
@@ -129,7 +128,7 @@ __device__ __forceinline__ void load_virtual_frags(Frags<HD>& f, const AttnArgs&
       keep[w2] = (pos0 + 2 * w2 < lim ? 0x0000ffffu : 0u) | (pos0 + 2 * w2 + 1 < lim ? 0xffff0000u : 0u);
 #pragma unroll
     for (int dt = 0; dt < Frags<HD>::DT; ++dt)
-      f.v[dt][c] = *(const u32x4_t*)(vb + (size_t)(dt * 16 + i) * a.max_len + base) & keep;
+      f.v[dt][c] = *(const u32x4_t*)(vb + v_off(base, dt * 16 + i, HD)) & keep;
   }
 }
 
@@ -343,7 +342,7 @@ __global__ __launch_bounds__(256, 2) void attn_partial_kernel(AttnArgs a) {
         const int an = min(idx / HD, L - P - 1), d = idx % HD;
         const int slot = s_anc[an];
         const bool ok = slot >= 0 && slot < a.max_len;
-        const uint32_t h = vb[(size_t)d * a.max_len + (ok ? slot : 0)];
+        const uint32_t h = vb[v_off(ok ? slot : 0, d, HD)];
         av[it] = ok ? h : 0u;
       }
     }
@@ -543,7 +542,8 @@ SSD_API int ssd_attn_workspace_floats(int M, int heads, int head_dim, int64_t ma
 SSD_API int ssd_attn_max_depth(void) { return ATT_MAXD; }
 
 // out[t, h*hd:(h+1)*hd] = softmax over row t's logical keys (see header) of q.k/sqrt(hd), times v.
-// q: [M, heads*hd] bf16 (post-RoPE); k_cache: [kv_heads, max_len, hd]; vt_cache: [kv_heads, hd, max_len].
+// q: [M, heads*hd] bf16 (post-RoPE); k_cache / vt_cache: kv_heads x (max_len x hd) each, in the
+// 64-slot block layout (k_off / v_off in common.h).
 // prefix/depth: [M] int32; anc: [M, 32] int32 slots; p_min <= min(prefix); l_max >= max(prefix+depth).
 // ws: fp32 workspace of ssd_attn_workspace_floats(M, heads, hd, max_len) floats.
 SSD_API int ssd_tree_attention_bf16(const uint16_t* q, int64_t ldq, int M, int heads, int kv_heads, int head_dim,
@@ -555,8 +555,8 @@ SSD_API int ssd_tree_attention_bf16(const uint16_t* q, int64_t ldq, int M, int h
     return set_error(SSD_EINVAL, "attention: null pointer");
   if (M <= 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads)
     return set_error(SSD_EINVAL, "attention: bad M=%d heads=%d kv_heads=%d", M, heads, kv_heads);
-  if (max_len % 8 || ((uintptr_t)vt_cache & 15) || ((uintptr_t)k_cache & 15) || ((uintptr_t)q & 15) || ldq % 8)
-    return set_error(SSD_EINVAL, "attention: caches/q must be 16-byte aligned, max_len %% 8 == 0");
+  if (max_len % 64 || ((uintptr_t)vt_cache & 15) || ((uintptr_t)k_cache & 15) || ((uintptr_t)q & 15) || ldq % 8)
+    return set_error(SSD_EINVAL, "attention: caches/q must be 16-byte aligned, max_len %% 64 == 0");
   if (l_max > max_len || p_min < 0 || l_max < 1 || p_min > l_max)
     return set_error(SSD_EINVAL, "attention: bad bounds p_min=%d l_max=%d max_len=%lld", p_min, l_max,
                      (long long)max_len);

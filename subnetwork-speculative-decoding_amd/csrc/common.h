@@ -69,6 +69,30 @@ __device__ __forceinline__ uint4 ld_stream(const uint4* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// ---- KV-cache layout: 64-slot blocks stored as the attention kernel's MFMA operands.
+// One (layer, kv head) holds max_len slots (a multiple of 64) of K and of V, max_len * hd
+// elements each. Slot s sits in block s / 64 at offset o = s % 64.
+//  K: block b is 4 * hd/32 operand tiles (kt, ks) of 64 lanes x 8 bf16, tile (kt, ks) lane
+//     (g * 16 + i) = K[slot 64b + key(kt, i)][32 ks + 8 g .. + 8], key(kt, i) =
+//     (kt / 2) * 32 + (i / 4) * 8 + (kt % 2) * 4 + i % 4: the A operand of S^T = K Q^T for key
+//     tile kt and k-step ks, so the attention kernel loads each tile as one contiguous 1 KiB.
+//  V: block b is hd/16 x 2 tiles (dt, c), tile (dt, c) lane (g * 16 + i) = V[slots 64b + 32c +
+//     8g .. + 8][dim 16 dt + i]: the A operand of O^T = V^T P^T for dim tile dt and key half c.
+__device__ __forceinline__ int kv_key_tile(int o) { return ((o >> 5) << 1) | ((o >> 2) & 1); }
+__device__ __forceinline__ int kv_key_lane(int o) { return (((o >> 3) & 3) << 2) | (o & 3); }
+// element offset of K[s][d] (d and the 8 following dims of the same 8-group are contiguous)
+__device__ __forceinline__ size_t k_off(int s, int d, int hd) {
+  const int o = s & 63;
+  return ((((size_t)(s >> 6) * 4 + kv_key_tile(o)) * (hd >> 5) + (d >> 5)) * 64 + ((d >> 3) & 3) * 16 +
+          kv_key_lane(o)) * 8 + (d & 7);
+}
+// element offset of V[s][d] (slots s .. s + 7 of the same 8-group are contiguous)
+__device__ __forceinline__ size_t v_off(int s, int d, int hd) {
+  const int o = s & 63;
+  return ((((size_t)(s >> 6) * (hd >> 4) + (d >> 4)) * 2 + (o >> 5)) * 64 + ((o >> 3) & 3) * 16 + (d & 15)) * 8 +
+         (o & 7);
+}
+
 __device__ __forceinline__ f32x4_t mfma16x16x32(bf16x8_t a, bf16x8_t b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }

@@ -57,8 +57,8 @@ struct GemmArgs {
   const int* row_pos;     // [M]
   const int* row_slot;    // [M]
   int64_t rope_rows;
-  bf16_t* k_cache;        // this layer: [kv_heads, max_len, head_dim]
-  bf16_t* vt_cache;       // this layer: [kv_heads, head_dim, max_len]
+  bf16_t* k_cache;        // this layer: kv_heads x (max_len x head_dim) in the block layout (k_off)
+  bf16_t* vt_cache;       // this layer: kv_heads x (max_len x head_dim) in the block layout (v_off)
   int64_t max_len;
   // RMSNorm of the rows of X folded into the GEMM (> 0: X is the residual stream h; the norm's
   // weight is already folded into W's columns; each output is scaled by rsqrt(mean(h^2) + eps))
@@ -95,7 +95,7 @@ __device__ __forceinline__ void epi_swiglu(const GemmArgs& a, int col, int m, fl
 }
 
 // q/k/v tile nb, pair r (rows r and r + 8 = rotary dims p*8 + r and hd/2 + p*8 + r) of row m:
-// RoPE for q/k, then Q store or KV-cache write (V transposed).
+// RoPE for q/k, then Q store or KV-cache write (block layout, k_off / v_off).
 __device__ __forceinline__ void epi_qkv(const GemmArgs& a, int nb, int m, int r, float vlo, float vhi) {
   const int hd = a.head_dim, half = hd >> 1, tiles_per_head = hd >> 4;
   const int q_tiles = a.heads * tiles_per_head, k_tiles = a.kv_heads * tiles_per_head;
@@ -113,8 +113,8 @@ __device__ __forceinline__ void epi_qkv(const GemmArgs& a, int nb, int m, int r,
   if (region != 0 && (slot < 0 || slot >= a.max_len)) return;  // never write outside the cache
   if (region == 2) {
     bf16_t* vt = a.vt_cache + (size_t)head * hd * a.max_len;
-    vt[(size_t)dlo * a.max_len + slot] = f2bf(xlo);
-    vt[(size_t)dhi * a.max_len + slot] = f2bf(xhi);
+    vt[v_off(slot, dlo, hd)] = f2bf(xlo);
+    vt[v_off(slot, dhi, hd)] = f2bf(xhi);
     return;
   }
   const int pos = min(max(a.row_pos[m], 0), (int)a.rope_rows - 1);
@@ -127,9 +127,9 @@ __device__ __forceinline__ void epi_qkv(const GemmArgs& a, int nb, int m, int r,
     q[dlo] = f2bf(olo);
     q[dhi] = f2bf(ohi);
   } else {
-    bf16_t* kr = a.k_cache + ((size_t)head * a.max_len + slot) * hd;
-    kr[dlo] = f2bf(olo);
-    kr[dhi] = f2bf(ohi);
+    bf16_t* kc = a.k_cache + (size_t)head * a.max_len * hd;
+    kc[k_off(slot, dlo, hd)] = f2bf(olo);
+    kc[k_off(slot, dhi, hd)] = f2bf(ohi);
   }
 }
 
@@ -157,8 +157,8 @@ __device__ __forceinline__ void epi_qkv_pre(const GemmArgs& a, const QkvTile& q,
   if (q.region != 0 && (slot < 0 || slot >= a.max_len)) return;  // never write outside the cache
   if (q.region == 2) {
     bf16_t* vt = a.vt_cache + (size_t)q.head * hd * a.max_len;
-    vt[(size_t)dlo * a.max_len + slot] = f2bf(xlo);
-    vt[(size_t)dhi * a.max_len + slot] = f2bf(xhi);
+    vt[v_off(slot, dlo, hd)] = f2bf(xlo);
+    vt[v_off(slot, dhi, hd)] = f2bf(xhi);
     return;
   }
   const float olo = rbf(rbf(xlo * cs) - rbf(xhi * sn));
@@ -168,9 +168,9 @@ __device__ __forceinline__ void epi_qkv_pre(const GemmArgs& a, const QkvTile& q,
     qo[dlo] = f2bf(olo);
     qo[dhi] = f2bf(ohi);
   } else {
-    bf16_t* kr = a.k_cache + ((size_t)q.head * a.max_len + slot) * hd;
-    kr[dlo] = f2bf(olo);
-    kr[dhi] = f2bf(ohi);
+    bf16_t* kc = a.k_cache + (size_t)q.head * a.max_len * hd;
+    kc[k_off(slot, dlo, hd)] = f2bf(olo);
+    kc[k_off(slot, dhi, hd)] = f2bf(ohi);
   }
 }
 
@@ -756,8 +756,8 @@ SSD_API int ssd_gemm_swiglu_bf16(const uint16_t* X, int64_t ldx, int M, const ui
 
 // Fused q/k/v projection + RoPE + KV-cache write. W_packed: q heads, k heads, v heads; each
 // head as head_dim/16 tiles whose rows 0-7 are dims [8p, 8p+8) and rows 8-15 dims
-// [hd/2 + 8p, hd/2 + 8p + 8). q -> Q[m, heads*hd]; k -> k_cache[kvh, slot, :];
-// v -> vt_cache[kvh, :, slot] (V is kept transposed).
+// [hd/2 + 8p, hd/2 + 8p + 8). q -> Q[m, heads*hd]; k and v -> slot row_slot[m] of the cache in
+// its 64-slot block layout (k_off / v_off).
 SSD_API int ssd_gemm_qkv_rope_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int K,
                                    float norm_eps, int heads, int kv_heads, int head_dim, const uint16_t* cos_tab,
                                    const uint16_t* sin_tab, int64_t rope_rows, const int32_t* row_pos,
@@ -767,9 +767,10 @@ SSD_API int ssd_gemm_qkv_rope_bf16(const uint16_t* X, int64_t ldx, int M, const 
   const int N = (heads + 2 * kv_heads) * head_dim;
   int rc = check_common(X, ldx, M, W_packed, N, K);
   if (rc) return rc;
-  if (head_dim % 16 || head_dim > 256) return set_error(SSD_EINVAL, "qkv: head_dim=%d unsupported", head_dim);
+  if (head_dim % 32 || head_dim > 256) return set_error(SSD_EINVAL, "qkv: head_dim=%d unsupported", head_dim);
   if (!Q || !k_cache || !vt_cache || !cos_tab || !sin_tab || !row_pos || !row_slot)
     return set_error(SSD_EINVAL, "qkv: null pointer");
+  if (max_len <= 0 || max_len % 64) return set_error(SSD_EINVAL, "qkv: max_len %lld not a multiple of 64", (long long)max_len);
   if (M == 0) return SSD_OK;
   GemmArgs a{};
   a.X = X; a.ldx = ldx; a.M = M; a.W = (const uint4*)W_packed; a.N = N; a.kb_total = K / 32;
@@ -833,7 +834,9 @@ SSD_API int ssd_qkv_rope_finalize_bf16(const float* P, int64_t ldp, int64_t spli
   int rc = check_partials(P, ldp, split_stride, M, N);
   if (rc) return rc;
   if (S < 1 || M < 0 || heads <= 0 || kv_heads <= 0) return set_error(SSD_EINVAL, "qkv_finalize: bad S/M/heads");
-  if (head_dim % 16 || head_dim > 256) return set_error(SSD_EINVAL, "qkv_finalize: head_dim=%d unsupported", head_dim);
+  if (head_dim % 32 || head_dim > 256) return set_error(SSD_EINVAL, "qkv_finalize: head_dim=%d unsupported", head_dim);
+  if (max_len <= 0 || max_len % 64)
+    return set_error(SSD_EINVAL, "qkv_finalize: max_len %lld not a multiple of 64", (long long)max_len);
   if (!Q || !k_cache || !vt_cache || !cos_tab || !sin_tab || !row_pos || !row_slot || rope_rows <= 0)
     return set_error(SSD_EINVAL, "qkv_finalize: null pointer or empty rope table");
   if (M == 0) return SSD_OK;

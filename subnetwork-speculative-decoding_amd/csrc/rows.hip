@@ -141,8 +141,9 @@ __global__ __launch_bounds__(256) void embed_kernel(const int* __restrict__ ids,
 // Move cache entries src[0..n) to [start, start+n) in every layer and kv head
 // (ssd/engine/kv_cache.py:54-70). All sources are read before any destination is
 // written: a destination may be the source of a later entry (start=10, src=[10,12,13]).
-// K is [L][kvh][max_len][hd]; V is transposed, [L][kvh][hd][max_len]. n is read from
-// device memory (n_ptr) so the launch needs no host round trip; n <= n_max.
+// Every (layer, kv head) holds max_len slots of K and of V in the 64-slot block layout (k_off,
+// v_off in common.h). n is read from device memory (n_ptr) so the launch needs no host round
+// trip; n <= n_max.
 __global__ __launch_bounds__(256) void kv_compact_kernel(bf16_t* __restrict__ kc, bf16_t* __restrict__ vt, int kv_heads,
                                                          int hd, int64_t max_len, int start, const int* __restrict__ src,
                                                          const int* __restrict__ n_ptr, int n_max) {
@@ -156,14 +157,14 @@ __global__ __launch_bounds__(256) void kv_compact_kernel(bf16_t* __restrict__ kc
     const int i = e / hd, d = e % hd;
     int s = src[i];
     s = (s >= 0 && s < max_len) ? s : start + i;  // out-of-range source: leave the slot as is
-    stage[e] = kbase[(size_t)s * hd + d];
-    stage[n_max * hd + e] = vbase[(size_t)d * max_len + s];
+    stage[e] = kbase[k_off(s, d, hd)];
+    stage[n_max * hd + e] = vbase[v_off(s, d, hd)];
   }
   __syncthreads();
   for (int e = threadIdx.x; e < tot; e += 256) {
     const int i = e / hd, d = e % hd;
-    kbase[(size_t)(start + i) * hd + d] = stage[e];
-    vbase[(size_t)d * max_len + start + i] = stage[n_max * hd + e];
+    kbase[k_off(start + i, d, hd)] = stage[e];
+    vbase[v_off(start + i, d, hd)] = stage[n_max * hd + e];
   }
 }
 
@@ -331,6 +332,9 @@ SSD_API int ssd_kv_compact_bf16(uint16_t* k_arena, uint16_t* vt_arena, int layer
                                 hipStream_t stream) {
   if (!k_arena || !vt_arena || !src || !n_dev || layers <= 0 || kv_heads <= 0 || head_dim <= 0 || n_max < 0)
     return set_error(SSD_EINVAL, "kv_compact: bad arguments");
+  if (head_dim % 32 || max_len % 64)
+    return set_error(SSD_EINVAL, "kv_compact: head_dim %d / max_len %lld must be multiples of 32 / 64", head_dim,
+                     (long long)max_len);
   if (start < 0 || start + n_max > max_len) return set_error(SSD_EINVAL, "kv_compact: start %d + %d > max_len", start, n_max);
   if (n_max == 0) return SSD_OK;
   const size_t lds = (size_t)2 * n_max * head_dim * sizeof(bf16_t);

@@ -1,10 +1,11 @@
 """Shared KV cache for target and draft (reference ssd/engine/kv_cache.py).
 
 One arena per cache in HBM, keyed by *base* layer index like the reference's slots:
-
-* ``k``  [layers, kv_heads, max_len, head_dim]  bf16 -- rows are keys (QK^T operand);
-* ``vt`` [layers, kv_heads, head_dim, max_len]  bf16 -- V transposed, so the P.V operand of
-  the tree-attention MFMA is a contiguous 16-byte run of 8 keys.
+``k`` and ``vt`` are each [layers, kv_heads, max_len * head_dim] bf16, max_len a multiple of 64,
+in the 64-slot block layout of csrc/common.h (k_off / v_off): every 64-slot block of K is stored
+as the tree-attention kernel's S = K Q^T operand tiles and every block of V as its O = V^T P^T
+operand tiles, each tile in lane order, so the kernel reads a block as contiguous 1 KiB loads.
+``read`` / ``ops.kv_untile`` give the plain [kv_heads, slots, head_dim] view.
 
 Writes happen inside the fused q/k/v + RoPE GEMM epilogue; ``keep_positions`` (the
 accepted-path compaction) is one kernel launch over every layer. ``seq_len`` bookkeeping,
@@ -26,8 +27,8 @@ class KVCache:
                  head_dim: Optional[int] = None, device=None):
         self.num_slots = num_slots
         self.max_length = max_length
-        # Slot capacity rounded up so every V^T row is 16-byte aligned for the vector loads.
-        self.capacity = (max_length + 7) // 8 * 8
+        # Slot capacity in whole 64-slot blocks (the block layout's unit).
+        self.capacity = (max_length + 63) // 64 * 64
         self.seq_len = 0
         self.kv_heads, self.head_dim, self.device = kv_heads, head_dim, device
         self.k: Optional[torch.Tensor] = None
@@ -36,10 +37,9 @@ class KVCache:
             self._alloc()
 
     def _alloc(self) -> None:
-        shape_k = (self.num_slots, self.kv_heads, self.capacity, self.head_dim)
-        shape_v = (self.num_slots, self.kv_heads, self.head_dim, self.capacity)
-        self.k = torch.zeros(shape_k, dtype=torch.bfloat16, device=self.device)
-        self.vt = torch.zeros(shape_v, dtype=torch.bfloat16, device=self.device)
+        shape = (self.num_slots, self.kv_heads, self.capacity * self.head_dim)
+        self.k = torch.zeros(shape, dtype=torch.bfloat16, device=self.device)
+        self.vt = torch.zeros(shape, dtype=torch.bfloat16, device=self.device)
 
     def ensure(self, kv_heads: int, head_dim: int, device) -> None:
         if self.k is None:
@@ -58,14 +58,22 @@ class KVCache:
 
     def update(self, slot: int, k: torch.Tensor, v: torch.Tensor):
         """Write k/v [1, kv_heads, q, hd] at [seq_len, seq_len+q) of base layer ``slot`` and return
-        views of [0, seq_len+q) (API form of the reference's update; decoding writes in-kernel)."""
+        plain copies [1, kv_heads, seq_len+q, hd] of K and V (API form of the reference's update;
+        decoding writes in-kernel)."""
         q = k.shape[2]
         end = self.seq_len + q
         self.check_room(end)
         self.ensure(k.shape[1], k.shape[3], k.device)
-        self.k[slot, :, self.seq_len:end] = k[0].to(torch.bfloat16)
-        self.vt[slot, :, :, self.seq_len:end] = v[0].to(torch.bfloat16).transpose(1, 2)
-        return self.k[slot, None, :, :end], self.vt[slot, None, :, :, :end].transpose(-1, -2)
+        k_idx, v_idx = ops.kv_block_index(self.capacity, self.head_dim, self.k.device)
+        self.k[slot][:, k_idx[self.seq_len:end]] = k[0].to(torch.bfloat16)
+        self.vt[slot][:, v_idx[self.seq_len:end]] = v[0].to(torch.bfloat16)
+        kk, vv = self.read(slot, end)
+        return kk[None], vv[None]
+
+    def read(self, slot: int, end: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """Plain copies K, V [kv_heads, end, head_dim] of slots [0, end) of base layer ``slot``."""
+        k_idx, v_idx = ops.kv_block_index(self.capacity, self.head_dim, self.k.device)
+        return self.k[slot][:, k_idx[:end]], self.vt[slot][:, v_idx[:end]]
 
     def advance(self, n: int) -> None:
         self.seq_len += n

@@ -172,6 +172,45 @@ def embed(ids, m, table, out):
     return out
 
 
+# ------------------------------------------------------------------ KV-cache block layout
+_KV_INDEX: dict = {}
+
+
+def kv_block_index(cap: int, hd: int, device) -> tuple:
+    """Element offsets (k_idx, v_idx), each [cap, hd] int64, of K[s][d] and V[s][d] inside one
+    (layer, kv head) region of the cache's 64-slot block layout (csrc/common.h k_off / v_off):
+    a 64-slot block of K is stored as the attention kernel's S = K Q^T operand tiles, one of V as
+    its O = V^T P^T operand tiles, each tile in lane order. cap % 64 == 0, hd % 32 == 0."""
+    if cap % 64 or hd % 32:
+        raise ValueError(f"kv_block_index: cap {cap} / head_dim {hd} must be multiples of 64 / 32")
+    key = (cap, hd, str(device))
+    if key not in _KV_INDEX:
+        s = torch.arange(cap, dtype=torch.int64, device=device)[:, None]
+        d = torch.arange(hd, dtype=torch.int64, device=device)[None, :]
+        o = s & 63
+        kt = ((o >> 5) << 1) | ((o >> 2) & 1)
+        i = (((o >> 3) & 3) << 2) | (o & 3)
+        k_idx = ((((s >> 6) * 4 + kt) * (hd >> 5) + (d >> 5)) * 64 + ((d >> 3) & 3) * 16 + i) * 8 + (d & 7)
+        v_idx = ((((s >> 6) * (hd >> 4) + (d >> 4)) * 2 + (o >> 5)) * 64 + ((o >> 3) & 3) * 16 + (d & 15)) * 8 + (o & 7)
+        _KV_INDEX[key] = (k_idx, v_idx)
+    return _KV_INDEX[key]
+
+
+def kv_tile(x: torch.Tensor, which: str) -> torch.Tensor:
+    """[..., cap, hd] K or V (``which`` = "k" / "v") -> [..., cap * hd] in the block layout."""
+    cap, hd = x.shape[-2:]
+    idx = kv_block_index(cap, hd, x.device)[0 if which == "k" else 1].reshape(-1)
+    out = torch.empty(*x.shape[:-2], cap * hd, dtype=x.dtype, device=x.device)
+    out[..., idx] = x.reshape(*x.shape[:-2], cap * hd)
+    return out
+
+
+def kv_untile(flat: torch.Tensor, cap: int, hd: int, which: str) -> torch.Tensor:
+    """Inverse of kv_tile: [..., cap * hd] in the block layout -> [..., cap, hd]."""
+    idx = kv_block_index(cap, hd, flat.device)[0 if which == "k" else 1]
+    return flat[..., idx]
+
+
 def kv_compact(k_arena, vt_arena, layers, kv_heads, head_dim, max_len, start, src, n_dev, n_max):
     _check(k_arena, "k_arena"); _check(vt_arena, "vt_arena")
     _check(src, "src", torch.int32); _check(n_dev, "n", torch.int32)

@@ -115,16 +115,17 @@ def test_qkv_rope_and_cache_write(hd):
     pos = torch.tensor([3, 3, 9, 40, 0, 63], dtype=torch.int32)
     slot = torch.tensor([10, 11, 12, 13, 20, 63], dtype=torch.int32)
     q = torch.zeros(m, heads * hd, dtype=torch.bfloat16, device=DEV)
-    kc = torch.zeros(kvh, max_len, hd, dtype=torch.bfloat16, device=DEV)
-    vt = torch.zeros(kvh, hd, max_len, dtype=torch.bfloat16, device=DEV)
+    kc = torch.zeros(kvh, max_len * hd, dtype=torch.bfloat16, device=DEV)
+    vt = torch.zeros(kvh, max_len * hd, dtype=torch.bfloat16, device=DEV)
     ops.qkv_rope(x.to(DEV), m, wp, d, heads, kvh, hd, cos, sin, pos.to(DEV), slot.to(DEV), q, kc, vt, max_len)
     rq, rk, rv = ok.qkv_rope(x, wq, wk, wv, heads, kvh, hd, pos.long(), 500000.0)
     close_bf16(q.view(m, heads, hd), rq, frac=0.95)
+    kc, vv = ops.kv_untile(kc, max_len, hd, "k"), ops.kv_untile(vt, max_len, hd, "v")  # [kvh, slots, hd]
     close_bf16(kc[:, slot.long()].transpose(0, 1), rk, frac=0.95)
-    close_bf16(vt[:, :, slot.long()].permute(2, 0, 1), rv, frac=0.97)
+    close_bf16(vv[:, slot.long()].transpose(0, 1), rv, frac=0.97)
     untouched = torch.ones(max_len, dtype=torch.bool)
     untouched[slot.long()] = False
-    assert kc[:, untouched].abs().sum() == 0 and vt[:, :, untouched].abs().sum() == 0
+    assert kc[:, untouched].abs().sum() == 0 and vv[:, untouched].abs().sum() == 0
 
 
 # --------------------------------------------------------------- split-K GEMMs
@@ -203,17 +204,18 @@ def test_qkv_rope_finalize_matches_oracle(hd):
     pos = torch.tensor([3, 3, 9, 40, 0, 63], dtype=torch.int32)
     slot = torch.tensor([10, 11, 12, 13, 20, 63], dtype=torch.int32)
     q = torch.zeros(m, heads * hd, dtype=torch.bfloat16, device=DEV)
-    kc = torch.zeros(kvh, max_len, hd, dtype=torch.bfloat16, device=DEV)
-    vt = torch.zeros(kvh, hd, max_len, dtype=torch.bfloat16, device=DEV)
+    kc = torch.zeros(kvh, max_len * hd, dtype=torch.bfloat16, device=DEV)
+    vt = torch.zeros(kvh, max_len * hd, dtype=torch.bfloat16, device=DEV)
     part, s, ld = _partial(ops, x.to(DEV), m, wp, n, d)
     ops.qkv_rope_finalize(part, s, ld, m, heads, kvh, hd, cos, sin, pos.to(DEV), slot.to(DEV), q, kc, vt, max_len)
     rq, rk, rv = ok.qkv_rope(x, wq, wk, wv, heads, kvh, hd, pos.long(), 500000.0)
     close_bf16(q.view(m, heads, hd), rq, frac=0.95)
+    kc, vv = ops.kv_untile(kc, max_len, hd, "k"), ops.kv_untile(vt, max_len, hd, "v")  # [kvh, slots, hd]
     close_bf16(kc[:, slot.long()].transpose(0, 1), rk, frac=0.95)
-    close_bf16(vt[:, :, slot.long()].permute(2, 0, 1), rv, frac=0.97)
+    close_bf16(vv[:, slot.long()].transpose(0, 1), rv, frac=0.97)
     untouched = torch.ones(max_len, dtype=torch.bool)
     untouched[slot.long()] = False
-    assert kc[:, untouched].abs().sum() == 0 and vt[:, :, untouched].abs().sum() == 0
+    assert kc[:, untouched].abs().sum() == 0 and vv[:, untouched].abs().sum() == 0
 
 
 # ----------------------------------------------------------------------- rows
@@ -232,15 +234,16 @@ def test_rmsnorm_and_embed():
 
 def test_kv_compact_overlapping_and_all_layers():
     ops = _ops()
-    L, kvh, hd, S = 3, 2, 64, 40
-    k = bf(rand(L, kvh, S, hd, seed=23)).to(DEV)
-    vt = bf(rand(L, kvh, hd, S, seed=24)).to(DEV)
-    k0, vt0 = k.clone().cpu(), vt.clone().cpu()
-    src = [10, 12, 13, 17]
-    buf = torch.tensor(src + [33], dtype=torch.int32, device=DEV)  # capacity 5, device count 4
-    ops.kv_compact(k, vt, L, kvh, hd, S, 10, buf, torch.tensor([4], dtype=torch.int32, device=DEV), 5)
-    assert torch.equal(k.cpu(), ok.kv_compact(k0, 10, src))
-    assert torch.equal(vt.cpu().transpose(-1, -2), ok.kv_compact(vt0.transpose(-1, -2), 10, src))
+    L, kvh, hd, S = 3, 2, 64, 128
+    k0 = bf(rand(L, kvh, S, hd, seed=23))
+    v0 = bf(rand(L, kvh, S, hd, seed=24))
+    k, vt = ops.kv_tile(k0.to(DEV), "k"), ops.kv_tile(v0.to(DEV), "v")
+    assert torch.equal(ops.kv_untile(k, S, hd, "k").cpu(), k0)  # the layout helpers invert each other
+    src = [10, 12, 13, 17, 70]
+    buf = torch.tensor(src + [33], dtype=torch.int32, device=DEV)  # capacity 6, device count 5
+    ops.kv_compact(k, vt, L, kvh, hd, S, 10, buf, torch.tensor([5], dtype=torch.int32, device=DEV), 6)
+    assert torch.equal(ops.kv_untile(k, S, hd, "k").cpu(), ok.kv_compact(k0, 10, src))
+    assert torch.equal(ops.kv_untile(vt, S, hd, "v").cpu(), ok.kv_compact(v0, 10, src))
 
 
 def test_row_topk_argmax_and_logsoftmax():
@@ -306,8 +309,12 @@ def _run_attn(q, k, v, prefix, anc, S, m_cap=None):
     m, heads, hd = q.shape
     kvh = k.shape[0]
     qd = q.reshape(m, heads * hd).to(DEV).contiguous()
-    kd = k.to(DEV).contiguous()
-    vtd = v.transpose(1, 2).to(DEV).contiguous()
+    S64 = (S + 63) // 64 * 64  # the cache holds whole 64-slot blocks
+    kp = torch.zeros(kvh, S64, hd, dtype=k.dtype)
+    vp = torch.zeros(kvh, S64, hd, dtype=v.dtype)
+    kp[:, :S], vp[:, :S] = k, v
+    kd, vtd = ops.kv_tile(kp.to(DEV), "k"), ops.kv_tile(vp.to(DEV), "v")
+    S = S64
     pre = torch.tensor(prefix, dtype=torch.int32, device=DEV)
     dep = torch.tensor([len(a) for a in anc], dtype=torch.int32, device=DEV)
     an = torch.zeros(m, 32, dtype=torch.int32)
@@ -539,14 +546,15 @@ def test_swiglu_and_qkv_folded_rmsnorm():
     pos = torch.tensor([3, 3, 9, 40, 0, 63], dtype=torch.int32)
     slot = torch.tensor([10, 11, 12, 13, 20, 63], dtype=torch.int32)
     q = torch.zeros(6, heads * hd, dtype=torch.bfloat16, device=DEV)
-    kc = torch.zeros(kvh, max_len, hd, dtype=torch.bfloat16, device=DEV)
-    vt = torch.zeros(kvh, hd, max_len, dtype=torch.bfloat16, device=DEV)
+    kc = torch.zeros(kvh, max_len * hd, dtype=torch.bfloat16, device=DEV)
+    vt = torch.zeros(kvh, max_len * hd, dtype=torch.bfloat16, device=DEV)
     ops.qkv_rope(h.to(DEV), 6, wp, d, heads, kvh, hd, cos, sin, pos.to(DEV), slot.to(DEV), q, kc, vt, max_len,
                  norm_eps=1e-6)
     rq, rk, rv = ok.qkv_rope(ok.rmsnorm(h.float(), g, 1e-6), wq, wk, wv, heads, kvh, hd, pos.long(), 500000.0)
     torch.testing.assert_close(q.view(6, heads, hd).float().cpu(), rq.float(), atol=2e-2, rtol=2e-2)
+    kc, vv = ops.kv_untile(kc, max_len, hd, "k"), ops.kv_untile(vt, max_len, hd, "v")
     torch.testing.assert_close(kc[:, slot.long()].transpose(0, 1).float().cpu(), rk.float(), atol=2e-2, rtol=2e-2)
-    torch.testing.assert_close(vt[:, :, slot.long()].permute(2, 0, 1).float().cpu(), rv.float(), atol=2e-2, rtol=2e-2)
+    torch.testing.assert_close(vv[:, slot.long()].transpose(0, 1).float().cpu(), rv.float(), atol=2e-2, rtol=2e-2)
 
 
 @pytest.mark.parametrize("m", [1, 7, 25, 64, 100])
