@@ -158,6 +158,26 @@ __device__ __forceinline__ void patch_ancestors(Frags<HD>& f, const bf16_t (*avt
   }
 }
 
+// Reductions over lanes j, j ^ 16 (and j ^ 32) with gfx950's v_permlane16/32_swap (VALU, no LDS
+// round trip): swapping a value with itself leaves {own, partner} in the pair, in the same order
+// on both lanes, so both get the same result.
+__device__ __forceinline__ float pair_max16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_max32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float pair_sum32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // One 64-key block for a 16-row tile. valid_bits: bit (kt*4+e) says whether key perm_key(kt, 4g+e)
 // is attended (same for every row of the pass). Outputs per lane (row j = lane%16): m (log2 units,
 // -inf if nothing attended), l, and O[row j][dt*16 + 4g + e] in o[dt][e].
@@ -188,8 +208,8 @@ __device__ __forceinline__ void block_attend(const Frags<HD>& f, const u32x4_t (
       sv[kt * 4 + e] = v;
       mx = fmaxf(mx, v);
     }
-  mx = fmaxf(mx, __shfl_xor(mx, 16));
-  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  mx = pair_max16(mx);
+  mx = pair_max32(mx);
   m_out = mx;
   // A row with nothing attended gets p = 0 everywhere (m stays -inf and marks it absent).
   // No early exit: every lane must stay active for the MFMAs below.
@@ -206,8 +226,8 @@ __device__ __forceinline__ void block_attend(const Frags<HD>& f, const u32x4_t (
       l += p1;
       pw[kt >> 1][(kt & 1) * 2 + e / 2] = pack_bf16x2(p0, p1);
     }
-  l += __shfl_xor(l, 16);
-  l += __shfl_xor(l, 32);
+  l = pair_sum16(l);
+  l = pair_sum32(l);
   l_out = l;
   const u32x4_t pb0 = {pw[0][0], pw[0][1], pw[0][2], pw[0][3]};
   const u32x4_t pb1 = {pw[1][0], pw[1][1], pw[1][2], pw[1][3]};
