@@ -250,7 +250,7 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="llama3_8b_tree", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-rounds", type=int, default=4)
+    ap.add_argument("--cpu-rounds", type=int, default=40)
     ap.add_argument("--cpu-prompt", type=int, default=128)
     ap.add_argument("--ar-tokens", type=int, default=128)
     ap.add_argument("--sampled-rounds", type=int, default=30,
