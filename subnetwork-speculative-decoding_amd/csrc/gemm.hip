@@ -625,7 +625,7 @@ struct GemmPlan {
 // per-trip unroll U may follow M: it does not change the order. Measured on MI355X with every
 // launch streaming its weights from HBM: vocabulary-wide heads stream best as 8 tiles x 2 waves,
 // gate/up-wide outputs as 4 tiles x 2 waves, q/k/v-wide outputs as 2 tiles x 8 waves, narrow
-// outputs as 1 tile x 16 waves.
+// outputs as 1 tile x 8 waves (16 waves left the workgroup waiting ≈ 3 us for its slowest wave).
 static GemmPlan plan_for(int N, int K) {
   const int kbt = K / 32;
   GemmPlan p;
@@ -636,7 +636,7 @@ static GemmPlan plan_for(int N, int K) {
   } else if (N >= 6144) {
     p.nsub = 2; p.ks = 8;
   } else {
-    p.nsub = 1; p.ks = 16;
+    p.nsub = 1; p.ks = 8;
   }
   while (p.ks > 1 && kbt / p.ks < 4) p.ks >>= 1;  // at least 4 k-blocks per wave
   p.tiles = (N + 16 * p.nsub - 1) / (16 * p.nsub);
