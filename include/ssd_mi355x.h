@@ -118,6 +118,22 @@ int ssd_gemm_residual_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t
                            const uint16_t* bias, uint16_t* h, int64_t ldh, float* part, int64_t part_floats,
                            hipStream_t stream);
 
+/* Decoder MLP with its RMSNorm and residual add, fused into one cooperative launch of 256
+ * workgroups: h[:M] <- bf16(h + bf16(down(act))), act = bf16(silu(bf16(g))) * bf16(u) rounded to
+ * bf16, [g | u] = RMSNorm(h) . Wgu^T. Replaces the post-attention half of the decoder layer
+ * (ssd/models/subnetwork_draft.py:244-246: post_attention_layernorm, LlamaMLP, residual add).
+ * ssd_mlp_group(I, H) = the packing group of Wgu for this path (gate/up interleaved per 16-row
+ * tile, ln2 folded in as col_scale), 0 when the shape has no fused plan; Wd is packed with
+ * group ssd_gemm_residual_group(H, I). act: [M][lda] bf16 scratch (lda >= I); part: fp32 scratch
+ * of ssd_gemm_residual_floats(min(M, 64), H, I) floats; sync: ssd_mlp_sync_words() uint32 words,
+ * zero before the first call and then left to the kernel (word 257 counts grid-barrier
+ * timeouts, 0 when every barrier completed). Calls sharing sync must run in stream order. */
+int ssd_mlp_group(int I, int H);
+int64_t ssd_mlp_sync_words(void);
+int ssd_mlp_bf16(uint16_t* h, int64_t ldh, int M, const uint16_t* Wgu_packed, const uint16_t* Wd_packed, int I, int H,
+                 float eps, uint16_t* act, int64_t lda, float* part, int64_t part_floats, uint32_t* sync,
+                 hipStream_t stream);
+
 /* ------------------------------------------------------------ KV-cache layout
  * k_cache / vt_cache (one layer, as passed to the q/k/v GEMM and the attention; the compaction
  * takes all layers back to back) are kv_heads regions of max_len * head_dim bf16 each, max_len a
@@ -287,6 +303,7 @@ typedef struct SsdModel {     /* base model shared by target and draft */
   const uint16_t* sin;
   int64_t rope_rows;
   const SsdLayerW* layers;    /* host array [n_layers] */
+  int32_t mlp_fused;          /* 1: wgu packed with group ssd_mlp_group(inter, hidden) -> ssd_mlp_bf16 */
 } SsdModel;
 
 typedef struct SsdBridgeW {   /* x + MLP(RMSNorm(x)) */
@@ -317,8 +334,8 @@ typedef struct SsdPlan {      /* which layers run, with which bridges, and which
 typedef struct SsdBuffers {   /* activations [m_cap][...] and the layer-major KV arena */
   uint16_t *h, *x, *q, *attn, *mlp, *mid0, *mid1;
   int32_t m_cap, mid_cols;
-  uint16_t* k_arena;          /* [n_layers][kv_heads][cache_cap][head_dim] */
-  uint16_t* vt_arena;         /* [n_layers][kv_heads][head_dim][cache_cap] */
+  uint16_t* k_arena;          /* [n_layers][kv_heads][cache_cap * head_dim], 64-slot block layout */
+  uint16_t* vt_arena;         /* [n_layers][kv_heads][cache_cap * head_dim], 64-slot block layout */
   int64_t cache_cap;
   float* attn_ws;
   int64_t attn_ws_floats;
@@ -326,6 +343,7 @@ typedef struct SsdBuffers {   /* activations [m_cap][...] and the layer-major KV
   int64_t ld_logits;
   float* part;                /* split-K partials of one GEMM (fp32) */
   int64_t part_floats;
+  uint32_t* sync;             /* ssd_mlp_sync_words() words, zeroed once (used when mlp_fused) */
 } SsdBuffers;
 
 /* Embedding, the plan's decoder layers with their bridges, final norm and the head over rows

@@ -26,7 +26,7 @@ int check_launch(const char* what) {
 
 SSD_API const char* ssd_last_error(void) { return ssd::g_err; }
 
-SSD_API int ssd_abi_version(void) { return 1; }
+SSD_API int ssd_abi_version(void) { return 2; }
 
 SSD_API int ssd_device_arch(char* buf, int len) {
   int dev = 0;

@@ -10,6 +10,8 @@
 //   [bridge: body GEMMs (bridge norm folded) -> out_proj, h += out]
 //   q/k/v GEMM (ln1 folded) with RoPE + KV write in its epilogue -> tree attention (+ combine)
 //   -> o_proj, h += o -> gate/up GEMM (ln2 folded) + SwiGLU -> down_proj, h += down
+//   (the last three as one cooperative launch, ssd_mlp_bf16, when the model's gate/up weights
+//   are packed for it)
 // then the head over h (final norm folded).
 #include "common.h"
 
@@ -98,6 +100,12 @@ SSD_API int ssd_forward(const SsdModel* md, const SsdPlan* plan, const SsdBuffer
                                       buf->attn, qdim, s)))
       return rc;
     if ((rc = f.residual(buf->attn, qdim, L.wo, (int)qdim, nullptr))) return rc;
+    if (md->mlp_fused) {
+      if ((rc = ssd_mlp_bf16(buf->h, d, m, L.wgu, L.wd, md->inter, d, md->eps, buf->mlp, md->inter, buf->part,
+                             buf->part_floats, buf->sync, s)))
+        return rc;
+      continue;
+    }
     if ((rc = ssd_gemm_swiglu_bf16(buf->h, d, m, L.wgu, md->inter, d, md->eps, buf->mlp, md->inter, nullptr, nullptr,
                                    s)))
       return rc;

@@ -710,9 +710,9 @@ SSD_API int ssd_pack_weight_bf16(const uint16_t* src, int64_t ld, int N_src, int
   if (!src || !dst || !row_map) return set_error(SSD_EINVAL, "pack: null pointer");
   if (N_packed <= 0 || N_packed % 128 || K <= 0 || N_src <= 0)
     return set_error(SSD_EINVAL, "pack: N_packed=%d must be a positive multiple of 128 (K=%d)", N_packed, K);
-  if (group != 1 && group != 2 && group != 4 && group != 8)
-    return set_error(SSD_EINVAL, "pack: group %d not in {1, 2, 4, 8}", group);
   const int n_tiles_n = N_packed / 16, kb_total = (K + 31) / 32;
+  if (group < 1 || group > 16 || n_tiles_n % group)
+    return set_error(SSD_EINVAL, "pack: group %d must be in [1, 16] and divide the %d row tiles", group, n_tiles_n);
   const int64_t tiles = (int64_t)n_tiles_n * kb_total;
   hipLaunchKernelGGL(pack_kernel, dim3((unsigned)((tiles + 3) / 4)), dim3(256), 0, stream, src, ld, K, row_map,
                      n_tiles_n, kb_total, group, col_scale, (uint4*)dst);

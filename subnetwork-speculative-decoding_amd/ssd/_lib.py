@@ -35,7 +35,7 @@ class SsdLayerW(C.Structure):
 class SsdModel(C.Structure):
     _fields_ = [(n, C.c_int32) for n in ("hidden", "heads", "kv_heads", "head_dim", "inter", "vocab", "n_layers")] + [
         ("eps", F32), ("attn_scale", F32), ("embed", P), ("norm", P), ("cos", P), ("sin", P), ("rope_rows", I64),
-        ("layers", C.POINTER(SsdLayerW))]
+        ("layers", C.POINTER(SsdLayerW)), ("mlp_fused", C.c_int32)]
 
 
 class SsdBridgeW(C.Structure):
@@ -53,7 +53,8 @@ class SsdPlan(C.Structure):
 class SsdBuffers(C.Structure):
     _fields_ = [(n, P) for n in ("h", "x", "q", "attn", "mlp", "mid0", "mid1")] + [
         ("m_cap", C.c_int32), ("mid_cols", C.c_int32), ("k_arena", P), ("vt_arena", P), ("cache_cap", I64),
-        ("attn_ws", P), ("attn_ws_floats", I64), ("logits", P), ("ld_logits", I64), ("part", P), ("part_floats", I64)]
+        ("attn_ws", P), ("attn_ws_floats", I64), ("logits", P), ("ld_logits", I64), ("part", P), ("part_floats", I64),
+        ("sync", P)]
 
 
 _PROTOS = {
@@ -62,6 +63,9 @@ _PROTOS = {
     "ssd_device_arch": (I32, [C.c_char_p, I32]),
     "ssd_packed_weight_elems": (I64, [I32, I32]),
     "ssd_gemm_weight_group": (I32, [I32, I32]),
+    "ssd_mlp_group": (I32, [I32, I32]),
+    "ssd_mlp_sync_words": (I64, []),
+    "ssd_mlp_bf16": (I32, [P, I64, I32, P, P, I32, I32, F32, P, I64, P, I64, P, P]),
     "ssd_pack_weight_bf16": (I32, [P, I64, I32, I32, P, I32, I32, P, P, P]),
     "ssd_gemm_bf16": (I32, [P, I64, I32, P, I32, I32, F32, P, I64, P, I32, P, I64, P]),
     "ssd_gemm_swiglu_bf16": (I32, [P, I64, I32, P, I32, I32, F32, P, I64, P, P, P]),
@@ -101,6 +105,7 @@ _PROTOS = {
 }
 
 EXPORTED = tuple(_PROTOS)
+ABI_VERSION = 2  # descriptor struct layouts (SsdModel.mlp_fused, SsdBuffers.sync)
 
 _lib = None
 
@@ -121,6 +126,8 @@ def load(path: str = LIB_PATH):
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
+    if lib.ssd_abi_version() != ABI_VERSION:
+        raise ImportError(f"{path} has ABI {lib.ssd_abi_version()}, this package needs {ABI_VERSION}: rebuild it")
     _lib = lib
     return lib
 

@@ -106,15 +106,16 @@ def rope_tables(positions: int, hd: int, theta: float, device) -> tuple[torch.Te
 
 
 class Layer:
-    __slots__ = ("wqkv", "wo", "wgu", "wd", "ln1", "ln2")
+    __slots__ = ("wqkv", "wo", "wgu", "wd", "ln1", "ln2", "mlp_fused")
 
 
 class MI355XLlama:
     """A Llama target resident in HBM in the kernels' layout. ``config`` mimics the HF config."""
 
-    def __init__(self, shape: LlamaShape, device="cuda"):
+    def __init__(self, shape: LlamaShape, device="cuda", fused_mlp: bool = True):
         shape.validate()
         self.shape = shape
+        self.fused_mlp = fused_mlp  # pack gate/up for the one-launch MLP where the shape allows
         self.config = _Cfg(shape)
         self.generation_config = types.SimpleNamespace(eos_token_id=None)
         dev = torch.device(device)
@@ -145,14 +146,23 @@ class MI355XLlama:
         del qkv
         L.wo = ops.pack_weight(self._put(get("self_attn.o_proj.weight")), residual=True)
         gu = torch.cat([self._put(get("mlp.gate_proj.weight")), self._put(get("mlp.up_proj.weight"))], 0)
-        L.wgu = ops.pack_weight(gu, gate_up_row_map(s.inter), col_scale=L.ln2)
+        # grouped for the fused MLP (one cooperative launch) where the shape has a plan for it
+        g = ops.mlp_group(s.inter, s.hidden) if self.fused_mlp else 0
+        L.wgu = ops.pack_weight(gu, gate_up_row_map(s.inter), col_scale=L.ln2, group=g or None)
+        L.mlp_fused = g > 0
         del gu
         L.wd = ops.pack_weight(self._put(get("mlp.down_proj.weight")), residual=True)
         self.layers.append(L)
 
+    @property
+    def mlp_fused(self) -> bool:
+        """Every layer's MLP runs as one cooperative launch (ops.mlp)."""
+        return bool(self.layers) and all(L.mlp_fused for L in self.layers)
+
     @classmethod
-    def from_state_dict(cls, sd: dict, shape: LlamaShape, device="cuda", keep_lm_head_rows: bool = False):
-        m = cls(shape, device)
+    def from_state_dict(cls, sd: dict, shape: LlamaShape, device="cuda", keep_lm_head_rows: bool = False,
+                        fused_mlp: bool = True):
+        m = cls(shape, device, fused_mlp)
         m.embed = m._put(sd["model.embed_tokens.weight"])
         for i in range(shape.layers):
             m._set_layer(lambda n, i=i: sd[f"model.layers.{i}.{n}"])
@@ -166,17 +176,18 @@ class MI355XLlama:
         return m
 
     @classmethod
-    def from_hf(cls, model, device="cuda", keep_lm_head_rows: bool = False) -> "MI355XLlama":
+    def from_hf(cls, model, device="cuda", keep_lm_head_rows: bool = False, fused_mlp: bool = True) -> "MI355XLlama":
         m = cls.from_state_dict(model.state_dict(), LlamaShape.from_hf_config(model.config), device,
-                                keep_lm_head_rows)
+                                keep_lm_head_rows, fused_mlp)
         m.generation_config.eos_token_id = getattr(getattr(model, "generation_config", None), "eos_token_id", None)
         return m
 
     @classmethod
-    def synthetic(cls, shape: LlamaShape, seed: int = 0, std: float = 0.02, device="cuda") -> "MI355XLlama":
+    def synthetic(cls, shape: LlamaShape, seed: int = 0, std: float = 0.02, device="cuda",
+                  fused_mlp: bool = True) -> "MI355XLlama":
         """Random-init weights N(0, std) (norms = 1) generated on the GPU, one seeded generator
         per tensor (seed * 1000 + tensor index), so the model is reproducible on one torch build."""
-        m = cls(shape, device)
+        m = cls(shape, device, fused_mlp)
         counter = [0]
 
         def rnd(*size):
@@ -224,7 +235,7 @@ class MI355XLlama:
                                L.ln2.data_ptr()) for L in self.layers])
             st = _lib.SsdModel(s.hidden, s.heads, s.kv_heads, s.head_dim, s.inter, s.vocab, s.layers, s.eps,
                                s.head_dim ** -0.5, self.embed.data_ptr(), self.norm.data_ptr(), cos.data_ptr(),
-                               sin.data_ptr(), cos.shape[0], arr)
+                               sin.data_ptr(), cos.shape[0], arr, int(self.mlp_fused))
             self._native = (cos.data_ptr(), st, arr)
         return self._native[1]
 

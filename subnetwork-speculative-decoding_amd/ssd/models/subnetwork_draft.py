@@ -167,6 +167,7 @@ class Workspace:
                                 device=dev)
         self.ws = torch.zeros(0, dtype=torch.float32, device=dev)
         self.logits = torch.zeros(0, **bf)
+        self.sync = ops.mlp_sync(dev)  # grid-barrier words of the fused MLP (this workspace's stream)
         self._native: dict = {}
 
     def attn_ws(self, model: MI355XLlama, max_len: int) -> torch.Tensor:
@@ -198,7 +199,7 @@ class Workspace:
                                  self.mlp.data_ptr(), self.mids[0].data_ptr(), self.mids[1].data_ptr(), self.m_cap,
                                  self.mids[0].shape[1], cache.k.data_ptr(), cache.vt.data_ptr(), cache.capacity,
                                  aws.data_ptr(), aws.numel(), self.logits.data_ptr(), ld, self.part.data_ptr(),
-                                 self.part.numel())
+                                 self.part.numel(), self.sync.data_ptr())
             self._native[key] = st
         return st, self.logits[: self.m_cap * ld].view(self.m_cap, ld)
 
@@ -343,6 +344,9 @@ class SubnetworkDraftModel(nn.Module):
             ops.tree_attention(ws.q, m, s.heads, s.kv_heads, s.head_dim, kc, vt, cache.capacity, rows.prefix,
                                rows.depth, rows.anc, p_min, l_max, aws, ws.attn)
             ops.gemm_residual(ws.attn, m, layer.wo, s.hidden, s.heads * s.head_dim, ws.h, part)
+            if layer.mlp_fused:
+                ops.mlp(ws.h, m, layer.wgu, layer.wd, s.inter, s.hidden, s.eps, ws.mlp, part, ws.sync)
+                continue
             ops.gemm_swiglu(ws.h, m, layer.wgu, s.inter, s.hidden, ws.mlp, norm_eps=s.eps)
             ops.gemm_residual(ws.mlp, m, layer.wd, s.hidden, s.inter, ws.h, part)
         if self._pre_norm_bridge is not None:

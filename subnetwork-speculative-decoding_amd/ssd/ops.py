@@ -60,13 +60,14 @@ def weight_group(n: int, k: int) -> int:
 
 def pack_weight(w: torch.Tensor, row_map: Optional[torch.Tensor] = None, split: bool = False,
                 n_logical: Optional[int] = None, col_scale: Optional[torch.Tensor] = None,
-                residual: bool = False) -> torch.Tensor:
+                residual: bool = False, group: Optional[int] = None) -> torch.Tensor:
     """Row-major bf16 W[N, K] -> MFMA tile layout. row_map picks the source row of each packed
     row (-1 = zeros); default = identity. Rows are padded with zeros to a multiple of 128. Tiles
     are grouped for the single-pass GEMMs (group = weight_group(N_logical, K), N_logical = the
     GEMM's output width, default the row_map length); split=True packs for gemm_partial (group 1),
-    residual=True for gemm_residual (group = residual_group(N, K)). col_scale [K] folds an RMSNorm
-    weight into the columns (W * s, rounded once to bf16), for GEMMs called with norm_eps."""
+    residual=True for gemm_residual (group = residual_group(N, K)); group overrides all of these
+    (mlp: gate/up packed with mlp_group(I, H)). col_scale [K] folds an RMSNorm weight into the
+    columns (W * s, rounded once to bf16), for GEMMs called with norm_eps."""
     _check(w, "w")
     n, k = w.shape
     ld = _rows(w, "w", k)
@@ -78,7 +79,8 @@ def pack_weight(w: torch.Tensor, row_map: Optional[torch.Tensor] = None, split: 
     if n_packed != row_map.numel():
         row_map = torch.cat([row_map, torch.full((n_packed - row_map.numel(),), -1, dtype=torch.int32)])
     rm = row_map.to(device=w.device)
-    group = 1 if split else residual_group(n_log, k) if residual else weight_group(n_log, k)
+    if group is None:
+        group = 1 if split else residual_group(n_log, k) if residual else weight_group(n_log, k)
     if col_scale is not None:
         _check(col_scale, "col_scale")
         _len(col_scale, "col_scale", k)
@@ -331,6 +333,32 @@ def gemm_residual(x, m, wp, n, k, h, part, bias=None):
     _len(wp, "w_packed", packed_elems(n, k))
     _lib.call("ssd_gemm_residual_bf16", x.data_ptr(), _rows(x, "x", k, m), m, wp.data_ptr(), n, k, _p(bias),
               h.data_ptr(), _rows(h, "h", n, m), _p(part) if need else None, part.numel() if need else 0, stream())
+    return h
+
+
+def mlp_group(inter: int, hidden: int) -> int:
+    """Packing group of the gate/up weight for the fused MLP (0: no fused plan for this shape)."""
+    return int(_lib.load().ssd_mlp_group(inter, hidden))
+
+
+def mlp_sync(device) -> torch.Tensor:
+    """Zeroed grid-barrier words for mlp (one buffer per stream; word 257 counts timeouts)."""
+    return torch.zeros(int(_lib.load().ssd_mlp_sync_words()), dtype=torch.int32, device=device)
+
+
+def mlp(h, m, wgu, wd, inter, hidden, eps, act, part, sync):
+    """h[:m] <- h + down(SwiGLU(RMSNorm(h))) in one cooperative launch (wgu packed with
+    group=mlp_group(inter, hidden) and the ln2 weight as col_scale, wd with residual=True)."""
+    _check(h, "h"); _check(wgu, "wgu"); _check(wd, "wd"); _check(act, "act")
+    _check(part, "part", torch.float32); _check(sync, "sync", torch.int32)
+    need = residual_floats(min(m, 64), hidden, inter)
+    _len(part, "part", need)
+    _len(sync, "sync", int(_lib.load().ssd_mlp_sync_words()))
+    _len(wgu, "wgu", packed_elems(2 * inter, hidden))
+    _len(wd, "wd", packed_elems(hidden, inter))
+    _lib.call("ssd_mlp_bf16", h.data_ptr(), _rows(h, "h", hidden, m), m, wgu.data_ptr(), wd.data_ptr(), inter, hidden,
+              float(eps), act.data_ptr(), _rows(act, "act", inter, m), part.data_ptr(), part.numel(), sync.data_ptr(),
+              stream())
     return h
 
 

@@ -42,10 +42,14 @@ def test_host_only_entry_points():
     from ssd import _lib
 
     lib = _lib.load()
-    assert lib.ssd_abi_version() == 1
+    assert lib.ssd_abi_version() == _lib.ABI_VERSION == 2
     assert lib.ssd_packed_weight_elems(17, 40) == 128 * 64  # rows padded to 128, K to 32
     assert [lib.ssd_gemm_weight_group(n, 4096) for n in (4096, 8192, 28672, 128256)] == [1, 2, 4, 8]
     assert lib.ssd_gemm_weight_group(4096, 100) == 0
+    # fused MLP plans: Llama-3.2-1B, -3-8B, -3-70B shapes; none for a small MLP
+    assert [lib.ssd_mlp_group(i, h) for i, h in ((8192, 2048), (14336, 4096), (28672, 8192), (1024, 256))] == [
+        4, 7, 14, 0]
+    assert lib.ssd_mlp_sync_words() >= 258
     lim = (ctypes.c_int32 * 3)()
     assert lib.ssd_tree_limits(lim) == 0 and list(lim) == [1024, 32, 32]
     assert lib.ssd_attn_max_depth() == 32
