@@ -258,7 +258,9 @@ def test_greedy_tokens_match_oracle_up_to_near_ties(hf, oracle_base):
 @pytest.mark.parametrize("shape", ["llama32_1b", "llama3_8b"])
 def test_realistic_shapes_sd_equals_ar(shape):
     """Two layers at the real per-layer shapes (1B: hd 64, 32/8 heads; 8B: hd 128, 32/8 heads;
-    vocab 128256), synthetic weights, ~600-token context crossing superblock boundaries."""
+    vocab 128256), synthetic weights, ~600-token context crossing superblock boundaries. Both
+    shapes run their MLPs as the fused one-launch kernel (ssd_mlp_bf16) in draft, verify and the
+    autoregressive baseline."""
     sp, BridgeConfig, DraftingConfig, SDM = ssd()
     from ssd.models.llama import LlamaShape, MI355XLlama
 
@@ -266,6 +268,7 @@ def test_realistic_shapes_sd_equals_ar(shape):
     s = LlamaShape(hidden=dims[0], layers=2, heads=dims[1], kv_heads=dims[2], head_dim=dims[3], inter=dims[4],
                    vocab=128256, eps=1e-5)
     model = MI355XLlama.synthetic(s, seed=1)
+    assert model.mlp_fused
     target = sp.TargetRunner(model)
     torch.manual_seed(0)
     draft = SDM(model, [1], BridgeConfig(init_std=0.02))
