@@ -91,8 +91,8 @@ TREES = {
     "tree": dict(depth=3, branch=[3, 2, 2]),
     "pruned": dict(depth=5, branch=[4, 3, 2, 2, 1], width=[4, 6, 6, 4, 4], max_nodes=12),
     "deep_chain": dict(depth=8, branch=1),
-    "north_star": dict(depth=4, branch=[3, 2, 2, 1], max_nodes=24),
-    "config_b": dict(depth=4, branch=[3, 2, 2, 1], width=8, max_nodes=24),
+    "d4_3221_max24": dict(depth=4, branch=[3, 2, 2, 1], max_nodes=24),
+    "d4_3221_w8_max24": dict(depth=4, branch=[3, 2, 2, 1], width=8, max_nodes=24),
 }
 
 
