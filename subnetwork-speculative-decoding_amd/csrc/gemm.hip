@@ -396,6 +396,155 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
   }
 }
 
+// ------------------------------------------------------------ wide outputs (vocabulary heads)
+// One 8-wave workgroup per CU streams whole 8-tile groups g = blockIdx.x, + gridDim.x, ... (the
+// NSUB = 8 packing); the waves take each group's k-block pairs round-robin (pair i to wave i % 8),
+// so all eight walk one contiguous weight region together and finish together, and their
+// partial sums meet in LDS in wave order. The folded RMSNorm scale comes from the first group's
+// X fragments. Order of every sum: a function of (N, K) only.
+constexpr int WIDE_WAVES = 8, WIDE_DEAL = 2;
+
+template <int CT>
+struct WideCfg {
+  static constexpr int SC0 = 17408 / (WIDE_WAVES * CT * 4 * 68);
+  static constexpr int SC = SC0 < 8 ? SC0 : 8;  // sub-tiles reduced per LDS pass
+};
+
+template <int CT, int U, int NORM>
+__global__ __launch_bounds__(64 * WIDE_WAVES) void gemm_wide_kernel(GemmArgs a, int n_groups) {
+  constexpr int SC = WideCfg<CT>::SC;
+  __shared__ float red[WIDE_WAVES][SC][CT][4][68];
+  __shared__ float ssw[WIDE_WAVES][CT][16];
+  __shared__ float rn[CT * 16];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int kbt = a.kb_total;
+  const int Mv = a.M < CT * 16 ? a.M : CT * 16;
+  const bf16_t* xp[CT];
+#pragma unroll
+  for (int c = 0; c < CT; ++c) xp[c] = a.X + (size_t)min(c * 16 + j, a.M - 1) * a.ldx + g * 8;
+  const int n_full = (kbt / (WIDE_WAVES * WIDE_DEAL)) * WIDE_DEAL;  // this wave's k-blocks in whole rounds
+  auto kb_at = [&](int t) { return ((t / WIDE_DEAL) * WIDE_WAVES + w) * WIDE_DEAL + t % WIDE_DEAL; };
+  const int kb_rest = (kbt / (WIDE_WAVES * WIDE_DEAL)) * WIDE_WAVES * WIDE_DEAL + w;
+  // plain logits: two adjacent outputs per 4-byte store
+  const bool pair_store = !a.bias && !a.act && !a.residual && a.ldy % 2 == 0 && ((uintptr_t)a.Y & 3) == 0;
+  bool first = true;
+  for (int grp = blockIdx.x; grp < n_groups; grp += gridDim.x, first = false) {
+    f32x4_t acc[8][CT];
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+      for (int c = 0; c < CT; ++c) acc[s][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float ss[CT];
+#pragma unroll
+    for (int c = 0; c < CT; ++c) ss[c] = 0.f;
+    const u32x4_t* wp = (const u32x4_t*)a.W + (size_t)grp * kbt * 8 * 64 + lane;
+    int t = 0;
+    for (; t + U <= n_full; t += U) {
+      u32x4_t wr[U][8], xr[U][CT];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int kb = kb_at(t + u);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) wr[u][s] = __builtin_nontemporal_load(wp + ((size_t)kb * 8 + s) * 64);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int kb = kb_at(t + u);
+#pragma unroll
+        for (int c = 0; c < CT; ++c) xr[u][c] = *(const u32x4_t*)(xp[c] + kb * 32);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // every load of the trip ahead of its MFMAs
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+#pragma unroll
+          for (int c = 0; c < CT; ++c)
+            acc[s][c] = mfma16x16x32(bits_bf16x8(wr[u][s]), bits_bf16x8(xr[u][c]), acc[s][c]);
+      if (NORM && first) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int c = 0; c < CT; ++c) ss[c] += sumsq8(xr[u][c]);
+      }
+    }
+    for (int tt = t;; ++tt) {  // the rest of the whole rounds, then the leftover k-blocks
+      const int kb = tt < n_full ? kb_at(tt) : kb_rest + (tt - n_full) * WIDE_WAVES;
+      if (kb >= kbt) break;
+      u32x4_t wr[8], xr[CT];
+#pragma unroll
+      for (int s = 0; s < 8; ++s) wr[s] = __builtin_nontemporal_load(wp + ((size_t)kb * 8 + s) * 64);
+#pragma unroll
+      for (int c = 0; c < CT; ++c) xr[c] = *(const u32x4_t*)(xp[c] + kb * 32);
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+#pragma unroll
+        for (int c = 0; c < CT; ++c) acc[s][c] = mfma16x16x32(bits_bf16x8(wr[s]), bits_bf16x8(xr[c]), acc[s][c]);
+      if (NORM && first) {
+#pragma unroll
+        for (int c = 0; c < CT; ++c) ss[c] += sumsq8(xr[c]);
+      }
+    }
+    if (NORM && first) {
+#pragma unroll
+      for (int c = 0; c < CT; ++c) {
+        float v = ss[c];
+        v += __shfl_xor(v, 16);
+        v += __shfl_xor(v, 32);
+        if (g == 0) ssw[w][c][j] = v;
+      }
+    }
+    // sub-tiles in passes of SC through LDS; item (sub-tile, row m, column pair q): outputs
+    // 16 (8 grp + s) + 2q and + 2q + 1
+#pragma unroll
+    for (int s0 = 0; s0 < 8; s0 += SC) {
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+        if (s >= s0 && s < s0 + SC)
+#pragma unroll
+          for (int c = 0; c < CT; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) red[w][s - s0][c][e][lane] = acc[s][c][e];
+      __syncthreads();
+      if (NORM && first && s0 == 0) {
+        if ((int)threadIdx.x < CT * 16) {
+          const int c = threadIdx.x >> 4, jj = threadIdx.x & 15;
+          float v = ssw[0][c][jj];
+#pragma unroll
+          for (int ww = 1; ww < WIDE_WAVES; ++ww) v += ssw[ww][c][jj];
+          rn[threadIdx.x] = rsqrtf(v / (float)(kbt * 32) + a.norm_eps);
+        }
+        __syncthreads();
+      }
+      const int nsc = 8 - s0 < SC ? 8 - s0 : SC;
+      for (int o = threadIdx.x; o < nsc * 8 * Mv; o += 64 * WIDE_WAVES) {
+        const int q = o & 7;
+        const int m = (o >> 3) % Mv, sl = (o >> 3) / Mv;
+        const int c = m >> 4;
+        auto val = [&](int r) -> float {
+          const int ln = (m & 15) + 16 * (r >> 2), e = r & 3;
+          float v = red[0][sl][c][e][ln];
+#pragma unroll
+          for (int ww = 1; ww < WIDE_WAVES; ++ww) v += red[ww][sl][c][e][ln];
+          if constexpr (NORM) v *= rn[m];
+          return v;
+        };
+        const int n = (grp * 8 + s0 + sl) * 16 + 2 * q;
+        if (n >= a.N) continue;
+        const float v0 = val(2 * q), v1 = val(2 * q + 1);
+        if (pair_store && n + 1 < a.N) {
+          *(uint32_t*)(a.Y + (size_t)m * a.ldy + n) = pack_bf16x2(rbf(v0), rbf(v1));
+        } else {
+          epi_store(a, n, m, v0);
+          if (n + 1 < a.N) epi_store(a, n + 1, m, v1);
+        }
+      }
+      __syncthreads();  // the next pass (or group) overwrites red
+    }
+  }
+}
+
 // ------------------------------------------------------------ split-K partials
 // P[s][m][n] = sum over the s-th K range of X[m, k] W[n, k], fp32 (s < S). Workgroup = (NW*NSUB
 // 16-row tiles of N, one K range); wave w streams its NSUB weight tiles over the whole range,
@@ -623,7 +772,8 @@ struct GemmPlan {
 // arithmetic identical for any batch size (a row's sum runs over the k-blocks of each of the ks
 // waves in order, then over the waves in order; the tile grouping nsub does not enter it). The
 // per-trip unroll U may follow M: it does not change the order. Measured on MI355X with every
-// launch streaming its weights from HBM: vocabulary-wide heads stream best as 8 tiles x 2 waves,
+// launch streaming its weights from HBM: vocabulary-wide heads stream best as 8-tile groups (run by
+// gemm_wide_kernel for plain stores, else by gemm_kernel as 8 tiles x 2 waves),
 // gate/up-wide outputs as 4 tiles x 2 waves, q/k/v-wide outputs as 2 tiles x 8 waves, narrow
 // outputs as 1 tile x 8 waves (16 waves left the workgroup waiting ≈ 3 us for its slowest wave).
 static GemmPlan plan_for(int N, int K) {
@@ -643,6 +793,30 @@ static GemmPlan plan_for(int N, int K) {
   return p;
 }
 
+// Wide plain-store GEMMs (N >= 65536: vocabulary heads) use gemm_wide_kernel on the same 8-tile
+// packing (a function of the shape only).
+static bool use_wide(const GemmPlan& p) { return p.nsub == 8; }
+
+template <int EPI>
+static int launch_wide(GemmArgs a, int n_groups, hipStream_t s) {
+  int cus = 256;
+  int dev = 0;
+  if (hipGetDevice(&dev) == hipSuccess) hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  const dim3 grid((unsigned)std::min(n_groups, std::max(cus, 1))), block(64 * WIDE_WAVES);
+  const int ct = (a.M + 15) / 16;
+#define SSD_WIDE(CT_, U_)                                                                          \
+  if (a.norm_eps > 0.f) hipLaunchKernelGGL((gemm_wide_kernel<CT_, U_, 1>), grid, block, 0, s, a, n_groups); \
+  else hipLaunchKernelGGL((gemm_wide_kernel<CT_, U_, 0>), grid, block, 0, s, a, n_groups);
+  switch (ct) {
+    case 1: SSD_WIDE(1, 4) break;
+    case 2: SSD_WIDE(2, 2) break;
+    case 3: SSD_WIDE(3, 2) break;
+    default: SSD_WIDE(4, 1) break;
+  }
+#undef SSD_WIDE
+  return check_launch("gemm_wide");
+}
+
 template <int EPI>
 static int launch_gemm(GemmArgs a, hipStream_t s) {
   const GemmPlan p = plan_for(a.N, a.kb_total * 32);
@@ -655,6 +829,13 @@ static int launch_gemm(GemmArgs a, hipStream_t s) {
     if (a.residual) b.residual = a.residual + (size_t)m0 * a.ldr;
     if (a.row_pos) b.row_pos = a.row_pos + m0;
     if (a.row_slot) b.row_slot = a.row_slot + m0;
+    if constexpr (EPI == EPI_STORE) {
+      if (use_wide(p)) {
+        const int rc = launch_wide<EPI>(b, p.tiles, s);
+        if (rc) return rc;
+        continue;
+      }
+    }
     const int ct = (b.M + 15) / 16;
     dim3 grid(p.tiles);
 #define SSD_GEMM_CASE(CT_, NS_, KS_) \

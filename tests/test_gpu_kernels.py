@@ -55,6 +55,33 @@ def test_gemm_matches_oracle(m, n, k):
     close_bf16(y, ok.linear(x, w))
 
 
+@pytest.mark.parametrize("m", [1, 17, 33, 64])
+def test_gemm_wide_outputs(m):
+    """Vocabulary-wide outputs (N >= 65536) take the 8-wave one-workgroup-per-CU kernel: plain store
+    with N not a multiple of 16 and an odd output stride (single stores), bias + activation, and
+    the residual add, against the oracle; rows alone equal rows in the batch."""
+    ops = _ops()
+    n, k = 65560, 320
+    x, w = bf(rand(m, k, seed=11)), bf(rand(n, k, std=0.05, seed=12))
+    b, r = bf(rand(n, std=0.1, seed=13)), bf(rand(m, n, seed=14))
+    wp = ops.pack_weight(w.to(DEV))
+    y = torch.zeros(m, n + 1, dtype=torch.bfloat16, device=DEV)[:, :n]  # row stride n + 1 (odd)
+    ops.gemm(x.to(DEV), m, wp, n, k, y)
+    close_bf16(y, ok.linear(x, w))
+    y2 = torch.zeros(m, n + 8, dtype=torch.bfloat16, device=DEV)[:, :n]
+    ops.gemm(x.to(DEV), m, wp, n, k, y2)
+    assert torch.equal(y2, y)
+    one = torch.zeros(1, n + 8, dtype=torch.bfloat16, device=DEV)[:, :n]
+    for row in sorted({0, m // 2, m - 1}):
+        ops.gemm(x[row:row + 1].contiguous().to(DEV), 1, wp, n, k, one)
+        assert torch.equal(one[0], y2[row]), f"row {row}"
+    ops.gemm(x.to(DEV), m, wp, n, k, y2, bias=b.to(DEV), act="silu")
+    close_bf16(y2, ok.linear(x, w, b, act="silu"))
+    h = r.to(DEV).clone()
+    ops.gemm(x.to(DEV), m, wp, n, k, h, bias=b.to(DEV), residual=h)
+    close_bf16(h, ok.linear(x, w, b, residual=r))
+
+
 @pytest.mark.parametrize("n,k", [(1040, 4096), (16384, 2048)])
 def test_gemm_batch_invariance_bitwise(n, k):
     """A row's output is identical whether it is computed alone or at any position of a
