@@ -799,10 +799,16 @@ static bool use_wide(const GemmPlan& p) { return p.nsub == 8; }
 
 template <int EPI>
 static int launch_wide(GemmArgs a, int n_groups, hipStream_t s) {
-  int cus = 256;
+  // one workgroup per CU (the CU count is read once per device)
+  static int cus_of[64] = {0};
   int dev = 0;
-  if (hipGetDevice(&dev) == hipSuccess) hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  const dim3 grid((unsigned)std::min(n_groups, std::max(cus, 1))), block(64 * WIDE_WAVES);
+  if (hipGetDevice(&dev) != hipSuccess) return set_error(SSD_EHIP, "gemm_wide: no current device");
+  int cus = dev >= 0 && dev < 64 ? cus_of[dev] : 0;
+  if (cus <= 0) {
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    if (dev >= 0 && dev < 64) cus_of[dev] = cus;
+  }
+  const dim3 grid((unsigned)std::min(n_groups, cus)), block(64 * WIDE_WAVES);
   const int ct = (a.M + 15) / 16;
 #define SSD_WIDE(CT_, U_)                                                                          \
   if (a.norm_eps > 0.f) hipLaunchKernelGGL((gemm_wide_kernel<CT_, U_, 1>), grid, block, 0, s, a, n_groups); \
