@@ -8,7 +8,7 @@
 //   v_mfma_f32_16x16x32_bf16 A operand wants it. A wave's load of one tile is
 //   one fully contiguous 1 KiB request (16 B per lane). Rows are padded to 64.
 // * A workgroup owns NSUB 16-row tiles of N and the whole K; its KS waves split
-//   K into fixed contiguous ranges and are summed through LDS in wave order. Each
+//   K (k-block pairs dealt round-robin) and are summed through LDS in wave order. Each
 //   wave streams its NSUB weight tiles against one X fragment per k-block, so
 //   activation traffic from L2 is CT/NSUB of the weight traffic (CT = 16-row
 //   column tiles of M), and issues 4 k-blocks of loads (4*NSUB KiB of weights)
@@ -226,8 +226,6 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
   const int w = threadIdx.x >> 6;
   const int tile = blockIdx.x;
   const int kbt = a.kb_total;
-  const int kb_lo = (kbt * w) / KS;
-  const int kb_hi = (kbt * (w + 1)) / KS;
   const int j = lane & 15, g = lane >> 4;
 
   f32x4_t acc[NSUB][CT];
@@ -275,18 +273,24 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
     }
   }
 
-  int kb = kb_lo;
-  for (; kb + U - 1 < kb_hi; kb += U) {
+  // The wave's k-blocks: pairs dealt round-robin to the KS waves (pair i to wave i % KS), so the
+  // waves stream neighbouring weight regions at the same time and finish together; the k-blocks
+  // left after whole rounds go one by one. The sequence depends on (N, K) only.
+  const int n_full = (kbt / (KS * 2)) * 2;
+  auto kb_at = [&](int t) { return ((t >> 1) * KS + w) * 2 + (t & 1); };
+  const int kb_rest = (kbt / (KS * 2)) * KS * 2 + w;
+  int t = 0;
+  for (; t + U <= n_full; t += U) {
     u32x4_t wr[U][NSUB], xr[U][CT];
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int s = 0; s < NSUB; ++s) wr[u][s] = __builtin_nontemporal_load(wp[s] + (size_t)(kb + u) * NSUB * 64);
+      for (int s = 0; s < NSUB; ++s) wr[u][s] = __builtin_nontemporal_load(wp[s] + (size_t)kb_at(t + u) * NSUB * 64);
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int c = 0; c < CT; ++c)
-        xr[u][c] = *(const u32x4_t*)(xp[c] + (kb + u) * 32);
+        xr[u][c] = *(const u32x4_t*)(xp[c] + kb_at(t + u) * 32);
     // Keep every load of the trip ahead of its MFMAs: left alone, the scheduler sinks the later
     // k-blocks' loads below the first MFMAs to save registers, leaving one k-block in flight.
     __builtin_amdgcn_sched_barrier(0);
@@ -303,7 +307,9 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
         for (int c = 0; c < CT; ++c) ss[c] += sumsq8(xr[u][c]);
     }
   }
-  for (; kb < kb_hi; ++kb) {
+  for (int tt = t;; ++tt) {  // the rest of the whole rounds, then the leftover k-blocks
+    const int kb = tt < n_full ? kb_at(tt) : kb_rest + (tt - n_full) * KS;
+    if (kb >= kbt) break;
     u32x4_t wr[NSUB], xr[CT];
 #pragma unroll
     for (int s = 0; s < NSUB; ++s) wr[s] = __builtin_nontemporal_load(wp[s] + (size_t)kb * NSUB * 64);
