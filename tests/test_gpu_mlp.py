@@ -2,7 +2,8 @@
 cooperative launch with grid barriers) against the separate-launch path and the CPU oracle.
 
 * act (the SwiGLU output the kernel leaves in its scratch) matches gemm_swiglu over the same
-  weights at the GEMM tolerance (the gate/up K split differs, so a bf16 rounding step may too);
+  weights for >= 97% of outputs exactly and for all within abs/rel 2e-2 (the two sum K in
+  different orders, so gate and up may each round one bf16 step apart and their product a few);
 * h is bit-identical to the split-K residual projection (gemm_residual) applied to that act: the
   down phase and the final add are the same arithmetic in the same order;
 * h matches the oracle's bf16 chain (rmsnorm, swiglu, linear + residual) at abs 2e-2 + rel 2e-2
@@ -75,7 +76,7 @@ def test_mlp_matches_composed_path_and_oracle(inter, hidden, ms):
         act_u = torch.zeros(m, inter, dtype=torch.bfloat16, device=DEV)
         ops.gemm_swiglu(h0, m, wgu_u, inter, hidden, act_u, norm_eps=eps)
         a, b = act.float().cpu(), act_u.float().cpu()
-        torch.testing.assert_close(a, b, atol=1e-2, rtol=1e-2)
+        torch.testing.assert_close(a, b, atol=2e-2, rtol=2e-2)
         assert (a == b).float().mean().item() >= 0.97
         # h: bitwise the split-K residual projection of that act
         ref = h0.clone()
@@ -119,7 +120,7 @@ def test_mlp_70b_shape():
     act_u = torch.zeros(m, inter, dtype=torch.bfloat16, device=DEV)
     ops.gemm_swiglu(h0, m, wgu_u, inter, hidden, act_u, norm_eps=eps)
     a, b = act.float().cpu(), act_u.float().cpu()
-    torch.testing.assert_close(a, b, atol=1e-2, rtol=1e-2)
+    torch.testing.assert_close(a, b, atol=2e-2, rtol=2e-2)
     assert (a == b).float().mean().item() >= 0.97
     ref = h0.clone()
     part = torch.zeros(ops.residual_floats(m, hidden, inter), dtype=torch.float32, device=DEV)
