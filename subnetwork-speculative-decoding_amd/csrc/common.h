@@ -112,4 +112,20 @@ __device__ __forceinline__ float apply_act(int act, float x) {
   }
 }
 
+// Device-scope (agent) loads and stores: how workgroups of one launch hand data to each other
+// across CUs and XCDs (a plain store may sit in the writer's L2; a plain load may hit a line the
+// reader's L2 cached earlier in the launch).
+__device__ __forceinline__ uint32_t ld_agent_u32(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent_u32(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent_u64(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait until every global load and store this wave issued has completed; also a compiler barrier
+// (no memory access moves across it).
+__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 }  // namespace ssd

@@ -69,19 +69,6 @@ struct MlpArgs {
   uint32_t epoch;      // calls made on this sync buffer before this one
 };
 
-__device__ __forceinline__ uint32_t ld_agent_u32(const uint32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_agent_u32(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_agent_u64(uint64_t* p, uint64_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// Wait until every global load and store this wave issued has completed; also a compiler barrier
-// (no memory access moves across it).
-__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
 // Publish this workgroup's flag: every wave has waited for its own cross-phase stores
 // (wait_vmem) before the workgroup barrier, so the data is visible device-wide before the flag.
 __device__ __forceinline__ void publish_flag(uint32_t* sync, uint32_t value) {
