@@ -93,6 +93,7 @@ TREES = {
     "deep_chain": dict(depth=8, branch=1),
     "d4_3221_max24": dict(depth=4, branch=[3, 2, 2, 1], max_nodes=24),
     "d4_3221_w8_max24": dict(depth=4, branch=[3, 2, 2, 1], width=8, max_nodes=24),
+    "d6_422111_max32": dict(depth=6, branch=[4, 2, 2, 1, 1, 1], max_nodes=32),  # 76 drafted, 33 verify rows
 }
 
 
