@@ -14,7 +14,7 @@ the timed rounds: verify M = 25 rows at the reached context). ``cpu_baseline`` t
 oracle (this repo's PyTorch restatement of the reference path) on the host cores for a few
 rounds of the same model shape and tree after a shortened prompt.
 
-Prints one JSON line. More than one GPU is not part of this build: --gpus > 1 exits.
+Prints one JSON line. More than one GPU is not supported: --gpus > 1 exits.
 """
 
 from __future__ import annotations
@@ -269,7 +269,7 @@ def main() -> None:
                     help="also run one plain device copy of this many MiB (calibrates rocprofv3 byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build runs on exactly one GPU (got --gpus {args.gpus}); multi-GPU is not part of it",
+        print(f"bench.py: bench.py runs on exactly one GPU (got --gpus {args.gpus}); multi-GPU runs are not supported",
               file=sys.stderr)
         sys.exit(3)
 

@@ -2,7 +2,7 @@
 
 ``top_vocab`` picks the N most frequent token ids (forced ids included), sorted ascending;
 the draft's lm_head then scores only those rows. Counting frequencies over a text dataset
-is training-side and stays out of this build; ``zipf_counts`` gives the seeded synthetic
+is training-side and stays out of this package; ``zipf_counts`` gives the seeded synthetic
 frequencies used by the benchmarks (Zipf(s) expected counts over a seeded permutation).
 """
 

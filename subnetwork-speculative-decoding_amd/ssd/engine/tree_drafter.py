@@ -137,9 +137,9 @@ class TreeDrafter:
         self.greedy = cfg.temperature == 0
         self.levels = self.max_nodes_per_level()
         if max(self.branch) > TOPK_MAX:
-            raise ValueError(f"drafting.branch entries must be <= {TOPK_MAX} on this build")
+            raise ValueError(f"drafting.branch entries must be <= {TOPK_MAX} (per-node top-k kernel limit)")
         if cfg.depth > 32:
-            raise ValueError("drafting.depth must be <= 32 on this build")
+            raise ValueError("drafting.depth must be <= 32 (ancestor lists hold 32 slots)")
         fed = self.levels[:-1]
         if fed and max(fed) > ROW_CAP:
             raise ValueError(f"a fed level has {max(fed)} nodes > {ROW_CAP}; set drafting.width")

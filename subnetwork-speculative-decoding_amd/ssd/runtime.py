@@ -43,7 +43,7 @@ def resolve_device(name: str = "auto") -> torch.device:
     if name != "auto":
         return torch.device(name)
     if not torch.cuda.is_available():
-        raise RuntimeError("no HIP device: this build runs on MI355X (gfx950) only")
+        raise RuntimeError("no HIP device: this package runs on MI355X (gfx950) only")
     return torch.device("cuda", torch.cuda.current_device())
 
 
@@ -55,7 +55,7 @@ def load_base_model(cfg: SSDConfig, device: Optional[torch.device] = None, seed:
     name = cfg.model.base_model
     dev = device or resolve_device(cfg.model.device)
     if cfg.model.torch_dtype != "bfloat16":
-        raise ValueError("this build runs bf16 models (model.torch_dtype: bfloat16)")
+        raise ValueError("this package runs bf16 models (model.torch_dtype: bfloat16)")
     if name.startswith("synthetic:"):
         shape = SHAPES[name.split(":", 1)[1]]
         base = MI355XLlama.synthetic(shape, seed=seed, device=dev)

@@ -1,8 +1,9 @@
 """End-to-end parity of the HIP decode path (the reference's own invariants, on the GPU).
 
 * Greedy speculative output is bit-identical to greedy autoregressive decoding with the
-  same kernels, for chain / tree / pruned / deep-chain / north-star trees, untrained and
-  perfect drafts, draft-vocab subsets and EOS (reference tests/test_engine.py:44-92).
+  same kernels, for chain / tree / pruned / deep-chain / d4 [3,2,2,1] max 24 (with and without
+  width 8) / d6 [4,2,2,1,1,1] max 32 trees, untrained and perfect drafts, draft-vocab subsets and
+  EOS (reference tests/test_engine.py:44-92).
 * Tree rows are bit-identical to decoding each root->node path alone, before and after KV
   compaction (reference tests/test_forward_pass.py:146-180) -- stronger than the reference,
   which checks them to 1e-5 in fp32.
