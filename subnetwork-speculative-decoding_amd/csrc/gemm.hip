@@ -276,8 +276,13 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
   // The wave's k-blocks: pairs dealt round-robin to the KS waves (pair i to wave i % KS), so the
   // waves stream neighbouring weight regions at the same time and finish together; the k-blocks
   // left after whole rounds go one by one. The sequence depends on (N, K) only.
+  // Every workgroup reads all of X: the sequence is rotated by a tile-dependent, even number of
+  // k-blocks ((tile / 8) % 8 eighths of K) so that the workgroups of one XCD (tiles 8 apart) read
+  // different X lines at any moment instead of all the same ones.
   const int n_full = (kbt / (KS * 2)) * 2;
-  auto kb_at = [&](int t) { return ((t >> 1) * KS + w) * 2 + (t & 1); };
+  const int rot = ((((tile >> 3) & 7) * kbt) >> 3) & ~1;
+  auto wrap = [&](int kb) { return kb >= kbt ? kb - kbt : kb; };
+  auto kb_at = [&](int t) { return wrap(((t >> 1) * KS + w) * 2 + (t & 1) + rot); };
   const int kb_rest = (kbt / (KS * 2)) * KS * 2 + w;
   int t = 0;
   for (; t + U <= n_full; t += U) {
@@ -308,8 +313,9 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
     }
   }
   for (int tt = t;; ++tt) {  // the rest of the whole rounds, then the leftover k-blocks
-    const int kb = tt < n_full ? kb_at(tt) : kb_rest + (tt - n_full) * KS;
-    if (kb >= kbt) break;
+    const int kb0 = tt < n_full ? ((tt >> 1) * KS + w) * 2 + (tt & 1) : kb_rest + (tt - n_full) * KS;
+    if (kb0 >= kbt) break;
+    const int kb = wrap(kb0 + rot);
     u32x4_t wr[NSUB], xr[CT];
 #pragma unroll
     for (int s = 0; s < NSUB; ++s) wr[s] = __builtin_nontemporal_load(wp[s] + (size_t)kb * NSUB * 64);
