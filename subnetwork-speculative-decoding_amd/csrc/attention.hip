@@ -464,7 +464,8 @@ __global__ __launch_bounds__(256, 2) void attn_partial_kernel(AttnArgs a) {
 // Cross-superblock combine, one wave per (token, q head). Canonical arithmetic for a row with
 // superblocks s = 0..n-1: M = max_s m_s; w_s = 2^(m_s - M) (0 where m_s = -inf); l = sum_s l_s w_s
 // and O = sum_s O_s w_s, both summed in increasing s; out = O / l. The partials of up to 32
-// superblocks are loaded in one batch, issued before the max is reduced.
+// superblocks (a batch divides the 64-superblock window) are loaded in one batch, issued before
+// the max is reduced.
 template <int HD>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ ws, int n_sb_cap, int M,
                                                            int heads, int kv_heads, bf16_t* __restrict__ out,
@@ -479,21 +480,22 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
   const size_t row = (size_t)kvh * n_rows + tok * rep + hq % rep;
   const float* O = ws + row * n_sb_cap * HD;
   const float2* ml = (const float2*)(ws + (size_t)kv_heads * n_rows * n_sb_cap * HD) + row * n_sb_cap;
-  float v[CH][PER], mc[CH], lc[CH];
+  // Lane s of a 64-superblock window holds record (m, l) of superblock window + s; the fold reads
+  // it back with readlane (no registers per superblock).
+  float v[CH][PER];
   // Unconditional loads from clamped indices (a per-lane conditional load would be waited for
   // one by one); entries past n are masked where they are used.
   auto load_chunk = [&](int s0) {
 #pragma unroll
     for (int q = 0; q < CH; ++q) {
       const int sq = min(s0 + q, n - 1);
-      mc[q] = ml[sq].x;
-      lc[q] = ml[sq].y;
 #pragma unroll
       for (int i = 0; i < PER; ++i) v[q][i] = O[(size_t)sq * HD + min(lane + 64 * i, HD - 1)];
     }
   };
+  float2 win = ml[min(lane, n - 1)];
   load_chunk(0);
-  float mx = ml[min(lane, n - 1)].x;
+  float mx = win.x;
   for (int s = lane + 64; s < n; s += 64) mx = fmaxf(mx, ml[s].x);
   for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
   float l = 0.f, o[PER];
@@ -502,15 +504,19 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
   for (int s0 = 0;;) {
 #pragma unroll
     for (int q = 0; q < CH; ++q) {
-      const float wq = (s0 + q >= n || mc[q] == -INFINITY) ? 0.f : fast_exp2(mc[q] - mx);
+      const int ln = (s0 & 63) + q;
+      const float mq = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(win.x), ln));
+      const float lq = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(win.y), ln));
+      const float wq = (s0 + q >= n || mq == -INFINITY) ? 0.f : fast_exp2(mq - mx);
       if (wq != 0.f) {
-        l += lc[q] * wq;
+        l += lq * wq;
 #pragma unroll
         for (int i = 0; i < PER; ++i) o[i] += v[q][i] * wq;
       }
     }
     s0 += CH;
     if (s0 >= n) break;
+    if ((s0 & 63) == 0) win = ml[min(s0 + lane, n - 1)];
     load_chunk(s0);
   }
   bf16_t* dst = out + (size_t)tok * ldo + (size_t)hq * HD;
