@@ -18,7 +18,12 @@ How each part is pinned (so that a plausible mistake fails a check):
   pruned and deep-chain drafts; draft-vocab subsets and EOS; tree-shape
   limits; the V=8 brute-force joint for sampling (tests/test_engine.py).
   Tree pruning order and ``warp_probs`` boundaries are also pinned by small
-  hand-derived known-answer cases (tests/test_oracle_engine.py).
+  hand-derived known-answer cases (tests/test_oracle_engine.py). The per-level
+  expansion ``expand_level`` (stable sort on -score, width cut) is pinned by a
+  hand-derived case with ties across parents and ranks, a brute-force ranking by
+  the explicit key (-score, frontier index, rank), and mutation guards (sign flip,
+  other tie orders, dropped or shifted width cut) that must fail
+  (tests/test_oracle_expand.py).
 * ``sampling``: the sampling path with the kernels' Philox4x32-10 streams: the
   generator against its published known-answer vectors, the nucleus warp against
   hand-derived cases (ties included) and the fp32 rule, the verify.py:60-95 loop
