@@ -190,7 +190,8 @@ def cpu_baseline(model, layers: list, dcfg: dict, rounds: int, prompt_len: int) 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     s = model.shape
-    shape = om.LlamaShape(s.hidden, s.layers, s.heads, s.kv_heads, s.head_dim, s.inter, s.vocab, s.eps, s.theta)
+    shape = om.LlamaShape(s.hidden, s.layers, s.heads, s.kv_heads, s.head_dim, s.inter, s.vocab, s.eps, s.theta,
+                          s.rope_scaling)
     t0 = time.perf_counter()
     host = lambda t, n, k: t[: n * k].view(n, k).cpu()
     sd = {"model.embed_tokens.weight": model.embed.cpu(), "model.norm.weight": model.norm.cpu(),

@@ -29,6 +29,9 @@ typedef struct ihipStream_t* hipStream_t;
 /* ------------------------------------------------------------------ library */
 const char* ssd_last_error(void);
 int ssd_abi_version(void);
+/* Hash of the csrc/ and include/ sources the library was built from (16 hex digits; "unknown" for a
+ * build without it); the Python package refuses a library whose hash differs from its sources. */
+const char* ssd_build_hash(void);
 int ssd_device_arch(char* buf, int len); /* host buffer; gcnArchName of the current device */
 
 /* ------------------------------------------------------------ weight format
@@ -118,18 +121,25 @@ int ssd_gemm_residual_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t
                            const uint16_t* bias, uint16_t* h, int64_t ldh, float* part, int64_t part_floats,
                            hipStream_t stream);
 
-/* Decoder MLP with its RMSNorm and residual add, fused into one cooperative launch of 256
- * workgroups: h[:M] <- bf16(h + bf16(down(act))), act = bf16(silu(bf16(g))) * bf16(u) rounded to
+/* Decoder MLP with its RMSNorm and residual add, fused into one launch of 256 workgroups (one per
+ * CU; the workgroups wait on each other's flags, so the device must hold all of them at once,
+ * which is checked per kernel instantiation before the first launch):
+ * h[:M] <- bf16(h + bf16(down(act))), act = bf16(silu(bf16(g))) * bf16(u) rounded to
  * bf16, [g | u] = RMSNorm(h) . Wgu^T. Replaces the post-attention half of the decoder layer
  * (ssd/models/subnetwork_draft.py:244-246: post_attention_layernorm, LlamaMLP, residual add).
  * ssd_mlp_group(I, H) = the packing group of Wgu for this path (gate/up interleaved per 16-row
  * tile, ln2 folded in as col_scale), 0 when the shape has no fused plan; Wd is packed with
  * group ssd_gemm_residual_group(H, I). act: [M][lda] bf16 scratch (lda >= I); part: fp32 scratch
  * of ssd_gemm_residual_floats(min(M, 64), H, I) floats; sync: ssd_mlp_sync_words() uint32 words,
- * zero before the first call and then left to the kernel (word 257 counts grid-barrier
- * timeouts, 0 when every barrier completed). Calls sharing sync must run in stream order. */
+ * zero before the first call and then left to the kernel. Word ssd_mlp_timeout_word() counts
+ * flag waits that gave up (a workgroup another process kept off the GPU): nonzero means the
+ * results of every call since it was last zero are invalid, and the caller must check it (the
+ * waits are bounded, so a failure never hangs). Calls sharing sync must run in stream order; the
+ * call count is kept in the flags themselves, so a launch captured in a HIP graph replays
+ * correctly. */
 int ssd_mlp_group(int I, int H);
 int64_t ssd_mlp_sync_words(void);
+int ssd_mlp_timeout_word(void); /* index of the timeout count in sync */
 int ssd_mlp_bf16(uint16_t* h, int64_t ldh, int M, const uint16_t* Wgu_packed, const uint16_t* Wd_packed, int I, int H,
                  float eps, uint16_t* act, int64_t lda, float* part, int64_t part_floats, uint32_t* sync,
                  hipStream_t stream);

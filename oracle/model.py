@@ -44,14 +44,21 @@ class LlamaShape:
     vocab: int
     eps: float = 1e-6
     theta: float = 500000.0
+    rope_scaling: Optional[tuple] = None  # llama3: (factor, low_freq_factor, high_freq_factor, original ctx)
 
     @classmethod
     def from_hf_config(cls, c) -> "LlamaShape":
         hd = getattr(c, "head_dim", None) or c.hidden_size // c.num_attention_heads
         rp = getattr(c, "rope_parameters", None) or {}
         theta = rp.get("rope_theta", getattr(c, "rope_theta", 10000.0))
+        scaling = None
+        if rp.get("rope_type", "default") == "llama3":
+            scaling = (rp["factor"], rp["low_freq_factor"], rp["high_freq_factor"],
+                       rp.get("original_max_position_embeddings") or c.max_position_embeddings)
+        elif rp.get("rope_type", "default") != "default":
+            raise ValueError(f"rope_type {rp['rope_type']!r}")
         return cls(c.hidden_size, c.num_hidden_layers, c.num_attention_heads, c.num_key_value_heads, hd,
-                   c.intermediate_size, c.vocab_size, c.rms_norm_eps, float(theta))
+                   c.intermediate_size, c.vocab_size, c.rms_norm_eps, float(theta), scaling)
 
 
 def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
@@ -66,9 +73,28 @@ def bridge_rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tenso
     return rms_norm(x, w, eps)
 
 
-def rope_cos_sin(positions: torch.Tensor, head_dim: int, theta: float, dtype) -> tuple[torch.Tensor, torch.Tensor]:
+def llama3_inv_freq(inv: torch.Tensor, factor, low, high, ctx) -> torch.Tensor:
+    """Llama 3.1 frequency scaling (transformers modeling_rope_utils._compute_llama3_parameters):
+    frequencies whose wavelength exceeds ctx/low are divided by factor, those below ctx/high kept,
+    the band between blended: (1 - s) w / factor + s w with s = (ctx / wavelength - low) / (high - low)."""
+    out = inv.clone()
+    for i in range(inv.numel()):
+        w = inv[i:i + 1]
+        wl = 2 * math.pi / w
+        if wl.item() > ctx / low:
+            out[i:i + 1] = w / factor
+        elif wl.item() >= ctx / high:
+            s = (ctx / wl - low) / (high - low)
+            out[i:i + 1] = (1 - s) * w / factor + s * w
+    return out
+
+
+def rope_cos_sin(positions: torch.Tensor, head_dim: int, theta: float, dtype,
+                 scaling: Optional[tuple] = None) -> tuple[torch.Tensor, torch.Tensor]:
     """cos/sin [n, head_dim] for integer positions, computed in fp32 and cast."""
     inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float) / head_dim))
+    if scaling is not None:
+        inv = llama3_inv_freq(inv, *scaling)
     freqs = positions.float()[:, None] * inv[None, :]
     emb = torch.cat([freqs, freqs], -1)
     return emb.cos().to(dtype), emb.sin().to(dtype)
@@ -286,7 +312,7 @@ class Subnetwork:
         pos = (torch.arange(past, past + m) if position_ids is None
                else torch.as_tensor(position_ids).reshape(-1).long())
         s = self.base.shape
-        cos, sin = rope_cos_sin(pos, s.head_dim, s.theta, self.base.dtype)
+        cos, sin = rope_cos_sin(pos, s.head_dim, s.theta, self.base.dtype, s.rope_scaling)
         mask = None if (cache is None and tree_attention_mask is None) else build_attn_mask(m, past, tree_attention_mask)
         h = self.base.w("model.embed_tokens.weight")[ids]
         for slot, li in enumerate(self.layer_indices):

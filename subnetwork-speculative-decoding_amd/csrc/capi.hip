@@ -28,6 +28,13 @@ SSD_API const char* ssd_last_error(void) { return ssd::g_err; }
 
 SSD_API int ssd_abi_version(void) { return 2; }
 
+#ifndef SSD_BUILD_HASH
+#define SSD_BUILD_HASH "unknown"
+#endif
+// Hash of the sources this library was built from (set by the build script); the Python loader
+// compares it with the sources beside it and refuses a stale build.
+SSD_API const char* ssd_build_hash(void) { return SSD_BUILD_HASH; }
+
 SSD_API int ssd_device_arch(char* buf, int len) {
   int dev = 0;
   hipDeviceProp_t p;

@@ -29,11 +29,17 @@
 // the first read of a line in an XCD fetches the written data and later reads share it. No
 // agent-scope fence is used (that would write back and invalidate every L2).
 //
-// Flags: sync[b] = 2 E + 1 once workgroup b finished phase 1 of call E, 2 E + 2 after phase 2
-// (E counts the calls on this sync buffer modulo 2^31 - 1, kept by the host; waits compare for
-// equality, so neither a flag left by the previous call (2 E) nor a zeroed one matches). Every wait is bounded; one that gives up counts a timeout in
-// sync[MLP_WGS + 1] and lets the workgroup go on (its results are then wrong, and the count says
-// so). The waits need all 256 workgroups resident at once: one per CU (123 KiB of LDS each).
+// Flags: every call advances each workgroup's flag by 2: sync[b] = F + 1 once workgroup b finished
+// phase 1, F + 2 after phase 2, where F is the value sync[b] held when the call started (2 E for the
+// E-th call on a zeroed buffer, modulo 2^32). Only workgroup b writes sync[b], so it reads F at
+// its start without a race, and since every call leaves all flags equal, F is every producer's
+// start value too. Waits compare for equality, so a flag left by the previous call (F) never
+// matches. The call count lives in the flags themselves, not in a host counter baked into the
+// kernel arguments, so a launch captured in a HIP graph stays correct on every replay. Every wait
+// is bounded; one that gives up counts a timeout in sync[MLP_WGS + 1] and lets the workgroup go
+// on (its results are then wrong, and the count says so; the host reads the count and fails the
+// call's results). The waits need all 256 workgroups resident at once: one per CU (123 KiB of LDS
+// each).
 //
 // The order of every sum depends only on (I, H): results are batch-invariant (a row computed
 // alone equals the same row inside a 64-row batch).
@@ -66,7 +72,6 @@ struct MlpArgs {
   int64_t ldp, sstride;
   int groups;          // down: hidden / 128 tile groups; groups * S == MLP_WGS
   uint32_t* sync;
-  uint32_t epoch;      // calls made on this sync buffer before this one
 };
 
 // Publish this workgroup's flag: every wave has waited for its own cross-phase stores
@@ -157,7 +162,8 @@ __global__ __launch_bounds__(MLP_THREADS) void mlp_kernel(MlpArgs a) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int Mv = a.M < CT * 16 ? a.M : CT * 16;
-  const uint32_t flag1 = 2u * a.epoch + 1u, flag2 = 2u * a.epoch + 2u;
+  const uint32_t flag0 = ld_agent_u32(&a.sync[blockIdx.x]);  // all flags hold this value now
+  const uint32_t flag1 = flag0 + 1u, flag2 = flag0 + 2u;
 
   // ---------------------------------------------------------------- phase 1: gate/up + SwiGLU
   {
@@ -451,37 +457,41 @@ static hipError_t launch_mlp_ct(int ct, const MlpArgs& a, hipStream_t s) {
 }
 
 // The waits between workgroups need all MLP_WGS workgroups resident at once (one per CU): checked
-// once per device from its CU count and the kernel's occupancy. (A cooperative launch would
-// guarantee it too, but costs ~17 us more per launch on this runtime.)
-static int check_residency(int dev) {
+// once per (device, kernel instantiation) from the CU count and that instantiation's occupancy.
+// (A cooperative launch would guarantee it too, but costs ~17 us more per launch on this runtime.)
+static int check_residency(int dev, const void* fn) {
   static std::mutex mu;
-  static std::unordered_map<int, int> ok;
+  static std::unordered_map<uint64_t, int> ok;
   std::lock_guard<std::mutex> lock(mu);
-  auto it = ok.find(dev);
+  const uint64_t key = ((uint64_t)(uint32_t)dev << 48) ^ (uint64_t)(uintptr_t)fn;
+  auto it = ok.find(key);
   if (it != ok.end()) return it->second;
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)mlp_kernel<2, 7, 1, 8>, MLP_THREADS, 0) !=
-          hipSuccess)
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, MLP_THREADS, 0) != hipSuccess)
     return set_error(SSD_EHIP, "mlp: cannot query device %d", dev);
   const int rc = (int64_t)cus * per_cu >= MLP_WGS
                      ? SSD_OK
                      : set_error(SSD_ERANGE, "mlp: device %d holds %d x %d workgroups at once, needs %d", dev, cus,
                                  per_cu, MLP_WGS);
-  ok[dev] = rc;
+  ok[key] = rc;
   return rc;
 }
 
-// Calls made so far on each sync buffer, modulo 2^31 - 1 (the flags of a call are 2 E + 1 and
-// 2 E + 2, never 0 or the previous call's).
-static uint32_t next_epoch(const void* sync) {
-  static std::mutex mu;
-  static std::unordered_map<const void*, uint32_t> calls;
-  std::lock_guard<std::mutex> lock(mu);
-  uint32_t& c = calls[sync];
-  const uint32_t e = c;
-  c = (c + 1) % 0x7fffffffu;
-  return e;
+template <int NS1, int TG1, int S>
+static const void* mlp_fn(int ct) {
+  switch (ct) {
+    case 1: return (const void*)mlp_kernel<1, NS1, TG1, S>;
+    case 2: return (const void*)mlp_kernel<2, NS1, TG1, S>;
+    case 3: return (const void*)mlp_kernel<3, NS1, TG1, S>;
+    default: return (const void*)mlp_kernel<4, NS1, TG1, S>;
+  }
+}
+
+static const void* mlp_fn_for(const MlpPlan& p, int ct) {
+  if (p.ns1 == 4) return mlp_fn<4, 1, 16>(ct);
+  if (p.tg1 == 1) return mlp_fn<7, 1, 8>(ct);
+  return mlp_fn<7, 2, 4>(ct);
 }
 
 }  // namespace ssd
@@ -494,6 +504,8 @@ SSD_API int ssd_mlp_group(int inter, int hidden) {
 }
 
 SSD_API int64_t ssd_mlp_sync_words(void) { return MLP_SYNC_WORDS; }
+
+SSD_API int ssd_mlp_timeout_word(void) { return MLP_WGS + 1; }
 
 SSD_API int ssd_mlp_bf16(uint16_t* h, int64_t ldh, int M, const uint16_t* wgu, const uint16_t* wd, int inter,
                          int hidden, float eps, uint16_t* act, int64_t lda, float* part, int64_t part_floats,
@@ -521,7 +533,10 @@ SSD_API int ssd_mlp_bf16(uint16_t* h, int64_t ldh, int M, const uint16_t* wgu, c
   if (M == 0) return SSD_OK;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return set_error(SSD_EHIP, "mlp: no current device");
-  if (int rc = check_residency(dev)) return rc;
+  for (int m0 = 0; m0 < M; m0 += 64) {
+    const int mc0 = M - m0 < 64 ? M - m0 : 64;
+    if (int rc = check_residency(dev, mlp_fn_for(p, (mc0 + 15) / 16))) return rc;
+  }
   for (int m0 = 0; m0 < M; m0 += 64) {
     MlpArgs a{};
     a.M = M - m0 < 64 ? M - m0 : 64;
@@ -540,7 +555,6 @@ SSD_API int ssd_mlp_bf16(uint16_t* h, int64_t ldh, int M, const uint16_t* wgu, c
     a.sstride = (int64_t)a.M * ldp;
     a.groups = p.groups;
     a.sync = sync;
-    a.epoch = next_epoch(sync);
     const int ct = (a.M + 15) / 16;
     hipError_t e;
     if (p.ns1 == 4) e = launch_mlp_ct<4, 1, 16>(ct, a, stream);

@@ -7,10 +7,28 @@ raises. Build it with ``python subnetwork-speculative-decoding_amd/build.py``.
 from __future__ import annotations
 
 import ctypes as C
+import hashlib
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libssd_mi355x.so")
+_PKG = os.path.dirname(_HERE)
+SOURCE_DIRS = (os.path.join(_PKG, "csrc"), os.path.join(os.path.dirname(_PKG), "include"))
+
+
+def source_hash() -> str:
+    """First 16 hex digits of a sha256 over the HIP sources and C headers the library is built
+    from (file names and contents, sorted); build.py compiles it into the library, and load()
+    refuses a library whose hash differs from the sources beside it (a stale build)."""
+    h = hashlib.sha256()
+    for d in SOURCE_DIRS:
+        for f in sorted(os.listdir(d)):
+            if f.endswith((".hip", ".h")):
+                h.update(f.encode() + b"\0")
+                with open(os.path.join(d, f), "rb") as fh:
+                    h.update(fh.read())
+                h.update(b"\0")
+    return h.hexdigest()[:16]
 
 P = C.c_void_p
 I32 = C.c_int
@@ -60,11 +78,13 @@ class SsdBuffers(C.Structure):
 _PROTOS = {
     "ssd_last_error": (C.c_char_p, []),
     "ssd_abi_version": (I32, []),
+    "ssd_build_hash": (C.c_char_p, []),
     "ssd_device_arch": (I32, [C.c_char_p, I32]),
     "ssd_packed_weight_elems": (I64, [I32, I32]),
     "ssd_gemm_weight_group": (I32, [I32, I32]),
     "ssd_mlp_group": (I32, [I32, I32]),
     "ssd_mlp_sync_words": (I64, []),
+    "ssd_mlp_timeout_word": (I32, []),
     "ssd_mlp_bf16": (I32, [P, I64, I32, P, P, I32, I32, F32, P, I64, P, I64, P, P]),
     "ssd_pack_weight_bf16": (I32, [P, I64, I32, I32, P, I32, I32, P, P, P]),
     "ssd_gemm_bf16": (I32, [P, I64, I32, P, I32, I32, F32, P, I64, P, I32, P, I64, P]),
@@ -128,6 +148,11 @@ def load(path: str = LIB_PATH):
         fn.argtypes = args
     if lib.ssd_abi_version() != ABI_VERSION:
         raise ImportError(f"{path} has ABI {lib.ssd_abi_version()}, this package needs {ABI_VERSION}: rebuild it")
+    if all(os.path.isdir(d) for d in SOURCE_DIRS):
+        built, now = lib.ssd_build_hash().decode(), source_hash()
+        if built != now:
+            raise ImportError(f"{path} was built from other sources (hash {built}, sources {now}): rebuild it with "
+                              "`python subnetwork-speculative-decoding_amd/build.py`")
     _lib = lib
     return lib
 

@@ -106,6 +106,7 @@ def _prefill(target: SubnetworkDraftModel, ids: list, cache: KVCache, ws, out_de
         last = c1 == q
         logits = target.forward_rows(rows, m, past + c0 + 1, past + c1, cache, ws, m - 1 if last else 0, int(last))
         torch.cuda.current_stream().synchronize()  # the pinned staging buffer is reused next chunk
+    ws.check_faults()
     cache.advance(q)
     if sampler is not None:
         sampler.draw(logits, out_dev, counter=0)
@@ -154,6 +155,7 @@ def autoregressive_generate(target: TargetRunner, input_ids: torch.Tensor, max_n
             s += 1
         cache.seq_len = n_prompt + s
         out = rows.ids[: s + 1].tolist()
+        ws.check_faults()
     times["decode"] = time.perf_counter() - t0
     return GenerationResult(tokens=_finish(out, eos_ids, max_new_tokens)[0], times=times)
 
@@ -178,8 +180,13 @@ class DecodeSession:
         self.cache = target.new_cache(capacity)
         self.ws = draft.workspace(CHUNK)
         self.root_rows, self.level_rows, self.verify_rows = Rows(CHUNK, dev), Rows(CHUNK, dev), Rows(CHUNK, dev)
-        self.record = torch.zeros(4 + cfg.depth + 2, dtype=torch.int32, device=dev)  # [_, vn, n_new, tokens...]
-        self.record_host = torch.zeros_like(self.record, device="cpu").pin_memory()
+        # [_, vn, n_new, tokens...], placed after the workspace's fused-MLP sync words so that the one
+        # read-back per round also returns the MLP's timeout count (status_host[0])
+        n_rec = 4 + cfg.depth + 2
+        self.record = self.ws.record(n_rec)
+        self.status = self.ws.status_span(n_rec)
+        self.status_host = torch.zeros(self.status.numel(), dtype=torch.int32).pin_memory()
+        self.record_host = self.status_host[self.status.numel() - n_rec:]
         self.tree = DeviceTree(dev, vmeta=self.record[1:2])
         self.cand_tok = torch.zeros(TREE_CAP, dtype=torch.int32, device=dev)
         self.cand_lp = torch.zeros(TREE_CAP, dtype=torch.float32, device=dev)
@@ -232,7 +239,7 @@ class DecodeSession:
                       self.root_rows.ids.data_ptr(), ops.stream())
         ph.mark("bookkeeping")
         cache.compact_device(committed, self.keep_src, self.n_keep, cfg.depth + 1)
-        self.record_host.copy_(self.record, non_blocking=True)
+        self.status_host.copy_(self.status, non_blocking=True)
         ph.mark(None)
         done = torch.cuda.Event()
         done.record()
@@ -242,6 +249,7 @@ class DecodeSession:
             self._begun = True
         done.synchronize()
         ph.resolve()
+        ops.check_mlp_timeouts(int(self.status_host[0]))
         n_new = int(self.record_host[2])
         new = self.record_host[3:3 + n_new].tolist()
         cache.seq_len = committed + n_new

@@ -43,17 +43,16 @@ class LlamaShape:
     vocab: int
     eps: float = 1e-6
     theta: float = 500000.0
+    # Llama 3.1 frequency scaling (HF rope_type "llama3", used by Llama-3.1/3.2 checkpoints):
+    # (factor, low_freq_factor, high_freq_factor, original_max_position_embeddings); None = plain RoPE
+    rope_scaling: Optional[tuple] = None
 
     @classmethod
     def from_hf_config(cls, c) -> "LlamaShape":
         hd = getattr(c, "head_dim", None) or c.hidden_size // c.num_attention_heads
-        rp = getattr(c, "rope_parameters", None) or {}
-        theta = rp.get("rope_theta", getattr(c, "rope_theta", 10000.0))
-        rtype = rp.get("rope_type", "default")
-        if rtype != "default":
-            raise ValueError(f"rope_type {rtype!r} is not supported (default RoPE only)")
+        theta, scaling = rope_config(c)
         return cls(c.hidden_size, c.num_hidden_layers, c.num_attention_heads, c.num_key_value_heads, hd,
-                   c.intermediate_size, c.vocab_size, float(c.rms_norm_eps), float(theta))
+                   c.intermediate_size, c.vocab_size, float(c.rms_norm_eps), theta, scaling)
 
     def validate(self) -> None:
         if self.heads % self.kv_heads:
@@ -78,6 +77,11 @@ class _Cfg:
         self.vocab_size = s.vocab
         self.rms_norm_eps = s.eps
         self.rope_theta = s.theta
+        self.rope_parameters = {"rope_type": "default", "rope_theta": s.theta}
+        if s.rope_scaling is not None:
+            f, lo, hi, ctx = s.rope_scaling
+            self.rope_parameters.update(rope_type="llama3", factor=f, low_freq_factor=lo, high_freq_factor=hi,
+                                        original_max_position_embeddings=ctx)
 
 
 def qkv_row_map(heads: int, kv_heads: int, hd: int) -> torch.Tensor:
@@ -98,9 +102,45 @@ def gate_up_row_map(inter: int) -> torch.Tensor:
     return torch.cat([i, i + inter], 1).reshape(-1)
 
 
-def rope_tables(positions: int, hd: int, theta: float, device) -> tuple[torch.Tensor, torch.Tensor]:
-    """cos/sin [positions, hd/2] as HF computes them (fp32 inv_freq and angles, then bf16)."""
+def rope_config(c) -> tuple:
+    """(theta, llama3 scaling tuple or None) from an HF config: ``rope_parameters`` (transformers
+    5) or ``rope_theta`` + ``rope_scaling`` (4.x). Other rope types raise ValueError."""
+    rp = dict(getattr(c, "rope_parameters", None) or {})
+    legacy = getattr(c, "rope_scaling", None)
+    if legacy and not rp.get("rope_type"):
+        rp.update(legacy)
+    theta = float(rp.get("rope_theta", getattr(c, "rope_theta", None) or 10000.0))
+    rtype = rp.get("rope_type", rp.get("type", "default"))
+    if rtype == "default":
+        return theta, None
+    if rtype == "llama3":
+        old = rp.get("original_max_position_embeddings") or getattr(c, "max_position_embeddings")
+        return theta, (float(rp["factor"]), float(rp["low_freq_factor"]), float(rp["high_freq_factor"]), int(old))
+    raise ValueError(f"rope_type {rtype!r} is not supported (default and llama3 RoPE)")
+
+
+def rope_inv_freq(hd: int, theta: float, scaling: Optional[tuple] = None) -> torch.Tensor:
+    """fp32 inverse frequencies theta^(-2i/hd); with Llama 3.1 scaling (factor f, low/high
+    frequency factors l/h, original context C) the wavelength 2 pi / w decides per frequency:
+    above C / l divide by f, below C / h keep, in between blend w / f and w linearly by
+    s = (C / wavelength - l) / (h - l), all in fp32 as HF's rope init does."""
     inv = 1.0 / (theta ** (torch.arange(0, hd, 2, dtype=torch.int64).float() / hd))
+    if scaling is None:
+        return inv
+    f, lo, hi, ctx = scaling
+    wavelen = 2 * torch.pi / inv
+    low_cut, high_cut = ctx / lo, ctx / hi  # long wavelengths are scaled, short ones kept
+    scaled = torch.where(wavelen > low_cut, inv / f, inv)
+    s = (ctx / wavelen - lo) / (hi - lo)
+    blend = (1 - s) * scaled / f + s * scaled
+    mid = (wavelen >= high_cut) & (wavelen <= low_cut)
+    return torch.where(mid, blend, scaled)
+
+
+def rope_tables(positions: int, hd: int, theta: float, device,
+                scaling: Optional[tuple] = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """cos/sin [positions, hd/2] as HF computes them (fp32 inv_freq and angles, then bf16)."""
+    inv = rope_inv_freq(hd, theta, scaling)
     ang = torch.arange(positions, dtype=torch.float32)[:, None] * inv[None, :]
     return ang.cos().to(BF16).to(device).contiguous(), ang.sin().to(BF16).to(device).contiguous()
 
@@ -221,7 +261,8 @@ class MI355XLlama:
     def rope(self, max_pos: int) -> tuple[torch.Tensor, torch.Tensor]:
         if self._cos is None or self._cos.shape[0] < max_pos:
             n = max(max_pos, 4096)
-            self._cos, self._sin = rope_tables(n, self.shape.head_dim, self.shape.theta, self.device)
+            self._cos, self._sin = rope_tables(n, self.shape.head_dim, self.shape.theta, self.device,
+                                               self.shape.rope_scaling)
         return self._cos, self._sin
 
     def native(self, max_pos: int) -> "_lib.SsdModel":

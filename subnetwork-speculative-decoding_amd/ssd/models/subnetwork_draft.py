@@ -167,8 +167,34 @@ class Workspace:
                                 device=dev)
         self.ws = torch.zeros(0, dtype=torch.float32, device=dev)
         self.logits = torch.zeros(0, **bf)
-        self.sync = ops.mlp_sync(dev)  # grid-barrier words of the fused MLP (this workspace's stream)
+        # The fused MLP's flag words, followed by RECORD_WORDS words for the decode loop's per-round
+        # record, so that one device->host copy returns the record and the MLP's timeout count.
+        n_sync = ops.mlp_sync_words()
+        self.status = torch.zeros(n_sync + self.RECORD_WORDS, dtype=torch.int32, device=dev)
+        self.sync = self.status[:n_sync]
+        self.timeout_word = ops.mlp_timeout_word()
         self._native: dict = {}
+
+    RECORD_WORDS = 64
+
+    def record(self, n: int) -> torch.Tensor:
+        """The n-word round record (n <= RECORD_WORDS) that follows the sync words, zeroed."""
+        if n > self.RECORD_WORDS:
+            raise ValueError(f"record of {n} words > {self.RECORD_WORDS}")
+        r = self.status[self.sync.numel():self.sync.numel() + n]
+        r.zero_()
+        return r
+
+    def status_span(self, n: int) -> torch.Tensor:
+        """Words [timeout word, end of an n-word record): what the decode loop copies back."""
+        return self.status[self.timeout_word:self.sync.numel() + n]
+
+    def check_faults(self) -> None:
+        """Raises SsdError when a fused-MLP flag wait gave up on this workspace (synchronises)."""
+        ops.check_mlp_timeouts(int(self.status[self.timeout_word]))
+
+    def clear_faults(self) -> None:
+        self.status[self.timeout_word] = 0
 
     def attn_ws(self, model: MI355XLlama, max_len: int) -> torch.Tensor:
         s = model.shape
@@ -444,6 +470,7 @@ class SubnetworkDraftModel(nn.Module):
                 self.run_rows(rows, m, p_min, l_max, cache, ws, states)
             hraw[c0:c1].copy_(ws.h[:m])
             torch.cuda.current_stream().synchronize()  # the pinned staging buffer is reused next chunk
+        ws.check_faults()
         cache.advance(q)
         # hidden_states = the final-normed rows (reference :343); the decode path never needs
         # them (its head folds the norm), so they are computed here only

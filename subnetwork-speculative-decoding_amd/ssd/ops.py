@@ -341,9 +341,26 @@ def mlp_group(inter: int, hidden: int) -> int:
     return int(_lib.load().ssd_mlp_group(inter, hidden))
 
 
+def mlp_sync_words() -> int:
+    return int(_lib.load().ssd_mlp_sync_words())
+
+
+def mlp_timeout_word() -> int:
+    """Index of the word in an mlp sync buffer that counts flag waits that gave up."""
+    return int(_lib.load().ssd_mlp_timeout_word())
+
+
 def mlp_sync(device) -> torch.Tensor:
-    """Zeroed grid-barrier words for mlp (one buffer per stream; word 257 counts timeouts)."""
-    return torch.zeros(int(_lib.load().ssd_mlp_sync_words()), dtype=torch.int32, device=device)
+    """Zeroed flag words for mlp (one buffer per stream; word mlp_timeout_word() counts timeouts)."""
+    return torch.zeros(mlp_sync_words(), dtype=torch.int32, device=device)
+
+
+def check_mlp_timeouts(count: int) -> None:
+    """Raises SsdError for a nonzero timeout count read from an mlp sync buffer."""
+    if count:
+        raise _lib.SsdError(
+            f"fused MLP: {count} flag waits gave up (the device did not run all 256 workgroups at once: "
+            "another stream or process held compute units); results computed since the count was zero are invalid")
 
 
 def mlp(h, m, wgu, wd, inter, hidden, eps, act, part, sync):

@@ -49,7 +49,8 @@ def test_host_only_entry_points():
     # fused MLP plans: Llama-3.2-1B, -3-8B, -3-70B shapes; none for a small MLP
     assert [lib.ssd_mlp_group(i, h) for i, h in ((8192, 2048), (14336, 4096), (28672, 8192), (1024, 256))] == [
         4, 7, 14, 0]
-    assert lib.ssd_mlp_sync_words() >= 258
+    assert lib.ssd_mlp_sync_words() >= 258 and 0 <= lib.ssd_mlp_timeout_word() < lib.ssd_mlp_sync_words()
+    assert lib.ssd_build_hash().decode() == _lib.source_hash()  # built from the sources beside it
     lim = (ctypes.c_int32 * 3)()
     assert lib.ssd_tree_limits(lim) == 0 and list(lim) == [1024, 32, 32]
     assert lib.ssd_attn_max_depth() == 32

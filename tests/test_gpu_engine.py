@@ -109,6 +109,30 @@ def test_target_logits_match_oracle(hf, oracle_base):
     assert_logits_close(got, ref, exact)
 
 
+def test_llama3_rope_target_logits_match_oracle():
+    """A model with Llama 3.1 frequency scaling (rope_type "llama3", original context 64 so that the
+    scaled and blended bands reach the positions used): logits vs the oracle, and greedy SD == AR."""
+    sp, _, DraftingConfig, _ = ssd()
+    torch.manual_seed(5)
+    cfg = LlamaConfig(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=4,
+                      num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=4096,
+                      rope_parameters={"rope_type": "llama3", "rope_theta": 500000.0, "factor": 8.0,
+                                       "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+                                       "original_max_position_embeddings": 64})
+    hf3 = LlamaForCausalLM(cfg).eval().to(torch.bfloat16)
+    base = om.Llama.from_hf(hf3)
+    assert base.shape.rope_scaling is not None
+    target = sp.TargetRunner(hf3)
+    assert target.model.shape.rope_scaling == (8.0, 1.0, 4.0, 64)
+    ids = prompt(48, 7)
+    got = target(ids).logits[0].float().cpu()
+    assert_logits_close(got, om.Target(base)(ids[0])[0].float(), om.Target(fp32_view(base))(ids[0])[0])
+    draft = make_draft(hf3, "untrained", layers=(0, 3))
+    ar = sp.autoregressive_generate(target, ids, 24, {-1}).tokens
+    sd = sp.SpeculativeGenerator(hf3, draft, DraftingConfig(depth=3, branch=[2, 2, 1]), target).generate(ids, 24, {-1})
+    assert sd.tokens == ar
+
+
 def test_draft_logits_match_oracle(hf, oracle_base):
     draft = make_draft(hf, "untrained")
     ids = prompt(30, 2)
@@ -282,3 +306,32 @@ def test_realistic_shapes_sd_equals_ar(shape):
     perfect = SDM(model, [0, 1])
     res = sp.SpeculativeGenerator(model, perfect, cfg, target).generate(ids, 40, {-1})
     assert res.tokens == ref and res.mean_accepted > 3.0
+
+
+def test_mlp_timeout_count_fails_the_round(hf):
+    """A nonzero fused-MLP timeout count (preset from the host: no kernel is made to stall) makes
+    the round, greedy decoding and the generic forward raise instead of returning tokens."""
+    from ssd import _lib
+    sp, _, DraftingConfig, _ = ssd()
+    target = sp.TargetRunner(hf)
+    draft = make_draft(hf, "untrained")
+    gen = sp.SpeculativeGenerator(hf, draft, DraftingConfig(depth=3, branch=[2, 2, 1]), target)
+    ids = torch.randint(0, 512, (1, 12), generator=torch.Generator().manual_seed(3))
+    sess = gen.session(gen.capacity(12, 16))
+    sess.prefill(ids[0].tolist())
+    sess.step()
+    sess.ws.status[sess.ws.timeout_word] = 1
+    try:
+        with pytest.raises(_lib.SsdError, match="flag waits gave up"):
+            sess.step()
+        ws = target.workspace()
+        ws.status[ws.timeout_word] = 1
+        with pytest.raises(_lib.SsdError, match="flag waits gave up"):
+            sp.autoregressive_generate(target, ids, 4, {-1})
+        with pytest.raises(_lib.SsdError, match="flag waits gave up"):
+            target(ids)
+    finally:
+        for w in (sess.ws, target.workspace()):
+            w.clear_faults()
+    torch.cuda.synchronize()
+    assert sp.autoregressive_generate(target, ids, 4, {-1}).tokens

@@ -1,5 +1,6 @@
 """The fused decoder MLP (ssd_mlp_bf16: RMSNorm -> gate/up + SwiGLU -> down -> residual add in one
-cooperative launch with grid barriers) against the separate-launch path and the CPU oracle.
+launch of 256 workgroups that wait on each other's per-call flags instead of separate launches)
+against the separate-launch path and the CPU oracle.
 
 * act (the SwiGLU output the kernel leaves in its scratch) matches gemm_swiglu over the same
   weights for >= 97% of outputs exactly and for all within abs/rel 2e-2 (the two sum K in
@@ -10,7 +11,9 @@ cooperative launch with grid barriers) against the separate-launch path and the 
   (of the larger of |h| and the residual |h0|) for >= 99% of outputs, every output within
   abs 6e-2 + rel 2e-2, and the largest deviation is no larger than the separate-launch path's;
 * each row computed alone equals the same row inside the batch, bitwise (batch invariance);
-* no grid barrier timed out (sync word 257 stays 0), over repeated and shrinking calls.
+* no flag wait gave up (the sync buffer's timeout word stays 0), over repeated and shrinking calls;
+* a single launch captured in a HIP graph gives the eager result on every replay (the call count
+  lives in the flags, not in the captured kernel arguments).
 """
 
 import pytest
@@ -71,7 +74,7 @@ def test_mlp_matches_composed_path_and_oracle(inter, hidden, ms):
         h0 = bf(rand(m, hidden, std=2.0, seed=90 + m)).to(DEV)
         h, act = _run(ops, h0, m, wgu_f, wdp, inter, hidden, eps, sync)
         torch.cuda.synchronize()
-        assert int(sync[257]) == 0, "grid barrier timed out"
+        assert int(sync[ops.mlp_timeout_word()]) == 0, "a flag wait timed out"
         # act against the separate gate/up launch over the same weights
         act_u = torch.zeros(m, inter, dtype=torch.bfloat16, device=DEV)
         ops.gemm_swiglu(h0, m, wgu_u, inter, hidden, act_u, norm_eps=eps)
@@ -105,7 +108,7 @@ def test_mlp_matches_composed_path_and_oracle(inter, hidden, ms):
             h1, _ = _run(ops, h0[r:r + 1].contiguous(), 1, wgu_f, wdp, inter, hidden, eps, sync)
             assert torch.equal(h1[0], h[r]), f"m={m} row {r}"
     torch.cuda.synchronize()
-    assert int(sync[257]) == 0
+    assert int(sync[ops.mlp_timeout_word()]) == 0
 
 
 def test_mlp_70b_shape():
@@ -129,7 +132,7 @@ def test_mlp_70b_shape():
     h1, _ = _run(ops, h0[3:4].contiguous(), 1, wgu_f, wdp, inter, hidden, eps, sync)
     assert torch.equal(h1[0], h[3])
     torch.cuda.synchronize()
-    assert int(sync[257]) == 0
+    assert int(sync[ops.mlp_timeout_word()]) == 0
 
 
 def test_mlp_rejects_bad_arguments():
@@ -146,3 +149,34 @@ def test_mlp_rejects_bad_arguments():
     w = torch.zeros(1 << 20, dtype=torch.bfloat16, device=DEV)
     with pytest.raises(ValueError):
         ops.mlp(h, 4, w, w, 1024, 256, 1e-5, act, part, sync)
+
+
+def test_mlp_single_launch_graph_replays():
+    """One fused-MLP launch captured alone in a HIP graph and replayed several times, with eager
+    launches on the same sync buffer in between: every replay equals the eager result bitwise."""
+    ops = _ops()
+    inter, hidden, eps, m = 8192, 2048, 1e-5, 25
+    g, wg, wu, wd, wgu_f, wgu_u, wdp = _setup(ops, inter, hidden, seed=140)
+    sync = ops.mlp_sync(DEV)
+    h0 = bf(rand(m, hidden, std=2.0, seed=150)).to(DEV)
+    want, _ = _run(ops, h0, m, wgu_f, wdp, inter, hidden, eps, sync)
+    h = h0.clone()
+    act = torch.zeros(m, inter, dtype=torch.bfloat16, device=DEV)
+    part = torch.zeros(ops.residual_floats(m, hidden, inter), dtype=torch.float32, device=DEV)
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        ops.mlp(h, m, wgu_f, wdp, inter, hidden, eps, act, part, sync)  # warm-up outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        ops.mlp(h, m, wgu_f, wdp, inter, hidden, eps, act, part, sync)
+    for rep in range(4):
+        h.copy_(h0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(h, want), f"replay {rep}"
+        eager, _ = _run(ops, h0, m, wgu_f, wdp, inter, hidden, eps, sync)  # advances the flags eagerly
+        assert torch.equal(eager, want)
+    assert int(sync[ops.mlp_timeout_word()]) == 0

@@ -144,3 +144,60 @@ def test_bf16_forward_close_to_hf_bf16(hf):
         ref = hfb(ids[None]).logits[0].float()
     got = om.Target(base)(ids)[0].float()
     torch.testing.assert_close(got, ref, atol=1e-2, rtol=2e-2)
+
+
+LLAMA3_ROPE = {"rope_type": "llama3", "rope_theta": 500000.0, "factor": 8.0, "low_freq_factor": 1.0,
+               "high_freq_factor": 4.0, "original_max_position_embeddings": 8192}
+
+
+def test_llama3_rope_tables_match_hf():
+    """Llama 3.1 frequency scaling (rope_type "llama3", the Llama-3.1/3.2 checkpoints' setting): the
+    oracle's and the package's cos/sin tables equal transformers' LlamaRotaryEmbedding exactly, at
+    head_dim 128 and 64 where all three wavelength bands (kept, blended, scaled) occur."""
+    from transformers.models.llama.modeling_llama import LlamaRotaryEmbedding
+
+    from ssd.models.llama import LlamaShape, rope_tables
+
+    for hd in (128, 64):
+        cfg = LlamaConfig(hidden_size=hd * 4, num_attention_heads=4, head_dim=hd, max_position_embeddings=131072,
+                          rope_parameters=dict(LLAMA3_ROPE))
+        rot = LlamaRotaryEmbedding(cfg)
+        pos = torch.arange(0, 5000, 7)
+        cos_hf, sin_hf = rot(torch.zeros(1, dtype=torch.float32), pos[None])
+        cos_o, sin_o = om.rope_cos_sin(pos, hd, 500000.0, torch.float32, om.LlamaShape.from_hf_config(cfg).rope_scaling)
+        assert torch.equal(cos_o, cos_hf[0]) and torch.equal(sin_o, sin_hf[0])
+        shape = LlamaShape.from_hf_config(cfg)
+        assert shape.rope_scaling == (8.0, 1.0, 4.0, 8192)
+        cos_p, sin_p = rope_tables(5000, hd, shape.theta, "cpu", shape.rope_scaling)
+        half = hd // 2
+        assert torch.equal(cos_p[pos], cos_hf[0, :, :half].to(torch.bfloat16))
+        assert torch.equal(sin_p[pos], sin_hf[0, :, :half].to(torch.bfloat16))
+        # the scaling matters: plain tables differ
+        cos_plain, _ = om.rope_cos_sin(pos, hd, 500000.0, torch.float32)
+        assert (cos_plain - cos_hf[0]).abs().max() > 1e-2
+
+
+def test_llama3_rope_forward_matches_hf():
+    torch.manual_seed(4)
+    cfg = LlamaConfig(vocab_size=128, hidden_size=64, intermediate_size=128, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=131072,
+                      rope_parameters=dict(LLAMA3_ROPE, original_max_position_embeddings=64),
+                      attn_implementation="eager")
+    hf = LlamaForCausalLM(cfg).eval()
+    base = om.Llama.from_hf(hf)
+    assert base.shape.rope_scaling == (8.0, 1.0, 4.0, 64)
+    ids = torch.randint(0, 128, (40,), generator=torch.Generator().manual_seed(2))
+    with torch.no_grad():
+        ref = hf(ids[None]).logits[0]
+    torch.testing.assert_close(om.Target(base)(ids)[0], ref, atol=1e-5, rtol=1e-4)
+    plain = om.Llama(base.sd, om.LlamaShape(**{**vars(base.shape), "rope_scaling": None}), torch.float32)
+    assert (om.Target(plain)(ids)[0] - ref).abs().max() > 1e-3
+
+
+def test_unsupported_rope_type_is_rejected():
+    from ssd.models.llama import LlamaShape
+
+    cfg = LlamaConfig(hidden_size=64, num_attention_heads=4,
+                      rope_parameters={"rope_type": "linear", "rope_theta": 10000.0, "factor": 2.0})
+    with pytest.raises(ValueError, match="rope_type"):
+        LlamaShape.from_hf_config(cfg)
