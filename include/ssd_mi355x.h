@@ -192,6 +192,17 @@ int64_t ssd_row_topk_ws_bytes(int M, int N);
 int ssd_row_topk_bf16(const uint16_t* logits, int64_t ld, int M, int N, int k, int mode, const int32_t* vocab_ids,
                       int32_t* out_tok, float* out_val, float* out_lse, void* ws, int64_t ws_bytes,
                       hipStream_t stream);
+/* ssd_row_topk_bf16 without the workspace argument: no counterpart in the reference; for callers
+ * that cannot allocate device memory (code under HIP graph capture, serving loops or harnesses
+ * that forbid hipMalloc). The chunk partials live in a static device array of the library, one
+ * per GPU (544 KiB, held until the process ends): M * ceil(N / 4096) must be <= 4096 (e.g. 64
+ * rows of a 128256-column vocabulary), larger calls fail with code 2. The call allocates nothing
+ * and needs nothing cleared. All calls on one GPU share that array: calls that overlap in time on
+ * one GPU (other streams or threads) race and must be serialised by the caller. Results are
+ * bit-identical to ssd_row_topk_bf16. */
+int ssd_row_topk_bf16_noalloc(const uint16_t* logits, int64_t ld, int M, int N, int k, int mode,
+                              const int32_t* vocab_ids, int32_t* out_tok, float* out_val, float* out_lse,
+                              hipStream_t stream);
 
 /* ------------------------------------------------------------------ tree
  * Device-resident DraftTree (ssd/engine/tree_drafter.py:48-95). All members are device

@@ -7,6 +7,8 @@
 
 #include <math.h>
 
+#include <mutex>
+
 namespace ssd {
 
 // Deterministic 256-thread sum: butterfly inside each wave, then waves in order.
@@ -349,23 +351,80 @@ SSD_API int64_t ssd_row_topk_ws_bytes(int M, int N) {
   return (int64_t)M * S * (int64_t)sizeof(TopkPart);
 }
 
+static int row_topk_launch(const uint16_t* logits, int64_t ld, int M, int N, int k, int mode,
+                           const int32_t* vocab_ids, int32_t* out_tok, float* out_val, float* out_lse, TopkPart* parts,
+                           hipStream_t stream) {
+  const int S = (N + TOPK_CHUNK - 1) / TOPK_CHUNK;
+  hipLaunchKernelGGL(row_topk_partial_kernel, dim3(S, M), dim3(256), 0, stream, logits, ld, N, k, mode, parts);
+  int rc = check_launch("row_topk_partial");
+  if (rc) return rc;
+  hipLaunchKernelGGL(row_topk_merge_kernel, dim3(M), dim3(64), 0, stream, (const TopkPart*)parts, S, k, mode,
+                     vocab_ids, out_tok, out_val, out_lse);
+  return check_launch("row_topk_merge");
+}
+
+static int row_topk_check(const uint16_t* logits, int64_t ld, int N, int k, int mode, const int32_t* out_tok) {
+  if (!logits || !out_tok || N <= 0 || k < 1 || k > TOPK_MAX || k > N || (mode != 0 && mode != 1))
+    return set_error(SSD_EINVAL, "row_topk: bad arguments (k=%d, N=%d, mode=%d)", k, N, mode);
+  if (ld % 8 || ((uintptr_t)logits & 15)) return set_error(SSD_EINVAL, "row_topk: logits must be 16-byte aligned");
+  if ((N + TOPK_CHUNK - 1) / TOPK_CHUNK > 64)
+    return set_error(SSD_ERANGE, "row_topk: N=%d above %d columns", N, 64 * TOPK_CHUNK);
+  return SSD_OK;
+}
+
 SSD_API int ssd_row_topk_bf16(const uint16_t* logits, int64_t ld, int M, int N, int k, int mode,
                               const int32_t* vocab_ids, int32_t* out_tok, float* out_val, float* out_lse, void* ws,
                               int64_t ws_bytes, hipStream_t stream) {
-  if (!logits || !out_tok || !ws || M < 0 || N <= 0 || k < 1 || k > TOPK_MAX || k > N || (mode != 0 && mode != 1))
-    return set_error(SSD_EINVAL, "row_topk: bad arguments (k=%d, N=%d, mode=%d)", k, N, mode);
-  if (ld % 8 || ((uintptr_t)logits & 15)) return set_error(SSD_EINVAL, "row_topk: logits must be 16-byte aligned");
-  const int S = (N + TOPK_CHUNK - 1) / TOPK_CHUNK;
-  if (S > 64) return set_error(SSD_ERANGE, "row_topk: N=%d above %d columns", N, 64 * TOPK_CHUNK);
+  if (M < 0 || !ws) return set_error(SSD_EINVAL, "row_topk: bad arguments (M=%d, workspace %p)", M, ws);
+  if (int rc = row_topk_check(logits, ld, N, k, mode, out_tok)) return rc;
   if (ws_bytes < ssd_row_topk_ws_bytes(M, N)) return set_error(SSD_EINVAL, "row_topk: workspace too small");
   if (M == 0) return SSD_OK;
-  hipLaunchKernelGGL(row_topk_partial_kernel, dim3(S, M), dim3(256), 0, stream, logits, ld, N, k, mode,
-                     (TopkPart*)ws);
-  int rc = check_launch("row_topk_partial");
-  if (rc) return rc;
-  hipLaunchKernelGGL(row_topk_merge_kernel, dim3(M), dim3(64), 0, stream, (const TopkPart*)ws, S, k, mode, vocab_ids,
-                     out_tok, out_val, out_lse);
-  return check_launch("row_topk_merge");
+  return row_topk_launch(logits, ld, M, N, k, mode, vocab_ids, out_tok, out_val, out_lse, (TopkPart*)ws, stream);
+}
+
+// ---- the same reduction without a caller workspace: the chunk partials live in a file-scope
+// device array (one copy per GPU, held until the process ends). Host code never passes the
+// array's name to a kernel (on the host it is only a stand-in symbol): its device address is
+// looked up once per device with hipGetSymbolAddress, with that device current, and kept.
+constexpr int TOPK_STATIC_PARTS = 64 * 64;  // rows x 4096-column chunks: 64 rows of up to 262144 columns
+static __device__ __align__(256) TopkPart scratch[TOPK_STATIC_PARTS];  // 544 KiB per GPU
+
+constexpr int MAX_DEVICES = 64;
+static TopkPart* scratch_ptr[MAX_DEVICES];
+static std::mutex scratch_mu;
+
+static int topk_scratch(TopkPart** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return set_error(SSD_EHIP, "row_topk_noalloc: no current device");
+  if (dev < 0 || dev >= MAX_DEVICES) return set_error(SSD_ERANGE, "row_topk_noalloc: device %d", dev);
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(SSD_EHIP, "row_topk_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                       hipGetErrorString(e));
+    scratch_ptr[dev] = (TopkPart*)p;
+  }
+  *out = scratch_ptr[dev];
+  return SSD_OK;
+}
+
+SSD_API int ssd_row_topk_bf16_noalloc(const uint16_t* logits, int64_t ld, int M, int N, int k, int mode,
+                                      const int32_t* vocab_ids, int32_t* out_tok, float* out_val, float* out_lse,
+                                      hipStream_t stream) {
+  if (M < 0) return set_error(SSD_EINVAL, "row_topk_noalloc: M=%d", M);
+  if (int rc = row_topk_check(logits, ld, N, k, mode, out_tok)) return rc;
+  const int64_t parts = (int64_t)M * ((N + TOPK_CHUNK - 1) / TOPK_CHUNK);
+  if (parts > TOPK_STATIC_PARTS)
+    return set_error(SSD_ERANGE,
+                     "row_topk_noalloc: M=%d rows x %d-column chunks of N=%d need %lld partials, the static "
+                     "scratch holds %d (use ssd_row_topk_bf16 with a workspace)",
+                     M, TOPK_CHUNK, N, (long long)parts, TOPK_STATIC_PARTS);
+  if (M == 0) return SSD_OK;
+  TopkPart* ws = nullptr;
+  if (int rc = topk_scratch(&ws)) return rc;
+  return row_topk_launch(logits, ld, M, N, k, mode, vocab_ids, out_tok, out_val, out_lse, ws, stream);
 }
 
 SSD_API int ssd_add_rmsnorm_bf16(const float* P, int64_t ldp, int64_t split_stride, int S, const uint16_t* bias,
