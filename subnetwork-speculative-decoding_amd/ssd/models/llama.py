@@ -225,35 +225,18 @@ class MI355XLlama:
     @classmethod
     def synthetic(cls, shape: LlamaShape, seed: int = 0, std: float = 0.02, device="cuda",
                   fused_mlp: bool = True) -> "MI355XLlama":
-        """Random-init weights N(0, std) (norms = 1) generated on the GPU, one seeded generator
-        per tensor (seed * 1000 + tensor index), so the model is reproducible on one torch build."""
+        """Random-init weights N(0, std) (norms = 1) generated on the GPU by ``synthetic_tensors``
+        (one seeded generator per tensor), so the model is reproducible on one torch build."""
         m = cls(shape, device, fused_mlp)
-        counter = [0]
-
-        def rnd(*size):
-            g = torch.Generator(device=m.device).manual_seed(seed * 1000 + counter[0])
-            counter[0] += 1
-            return (torch.randn(*size, generator=g, device=m.device, dtype=torch.float32) * std).to(BF16)
-
         s = shape
-        m.embed = rnd(s.vocab, s.hidden)
-        ones = torch.ones(s.hidden, dtype=BF16, device=m.device)
+        gen = synthetic_tensors(shape, seed, std, m.device)
+        m.embed = next(gen)[1]
         for _ in range(s.layers):
-            w = {
-                "self_attn.q_proj.weight": rnd(s.heads * s.head_dim, s.hidden),
-                "self_attn.k_proj.weight": rnd(s.kv_heads * s.head_dim, s.hidden),
-                "self_attn.v_proj.weight": rnd(s.kv_heads * s.head_dim, s.hidden),
-                "self_attn.o_proj.weight": rnd(s.hidden, s.heads * s.head_dim),
-                "mlp.gate_proj.weight": rnd(s.inter, s.hidden),
-                "mlp.up_proj.weight": rnd(s.inter, s.hidden),
-                "mlp.down_proj.weight": rnd(s.hidden, s.inter),
-                "input_layernorm.weight": ones,
-                "post_attention_layernorm.weight": ones,
-            }
+            w = {n.split(".", 3)[3]: t for n, t in (next(gen) for _ in range(9))}
             m._set_layer(w.__getitem__)
             del w
-        m.norm = ones.clone()
-        m.lm_head = ops.pack_weight(rnd(s.vocab, s.hidden), col_scale=m.norm)
+        m.norm = next(gen)[1]
+        m.lm_head = ops.pack_weight(next(gen)[1], col_scale=m.norm)
         torch.cuda.synchronize(m.device)
         return m
 
@@ -296,6 +279,36 @@ class MI355XLlama:
             return (rows.float() * self.norm.float()).to(BF16)  # the fold of ssd_pack_weight_bf16
         return unpack_rows(self.lm_head, self.shape.vocab, self.shape.hidden, ids.to(self.device),
                            ops.weight_group(self.shape.vocab, self.shape.hidden))
+
+
+def synthetic_tensors(shape: LlamaShape, seed: int = 0, std: float = 0.02, device="cuda"):
+    """The synthetic model's tensors in HF state-dict naming, generated one at a time on
+    ``device``: linear weights and the embedding N(0, std) in fp32 rounded to bf16, each from its
+    own generator seeded seed * 1000 + index (index = order of generation), norm weights 1. Yields
+    (name, tensor) in the order embed, per layer (q, k, v, o, gate, up, down, ln1, ln2), norm,
+    lm_head, so a caller can rebuild any tensor of a model ``MI355XLlama.synthetic`` made."""
+    counter = [0]
+
+    def rnd(*size):
+        g = torch.Generator(device=device).manual_seed(seed * 1000 + counter[0])
+        counter[0] += 1
+        return (torch.randn(*size, generator=g, device=device, dtype=torch.float32) * std).to(BF16)
+
+    s = shape
+    yield "model.embed_tokens.weight", rnd(s.vocab, s.hidden)
+    for i in range(s.layers):
+        p = f"model.layers.{i}."
+        yield p + "self_attn.q_proj.weight", rnd(s.heads * s.head_dim, s.hidden)
+        yield p + "self_attn.k_proj.weight", rnd(s.kv_heads * s.head_dim, s.hidden)
+        yield p + "self_attn.v_proj.weight", rnd(s.kv_heads * s.head_dim, s.hidden)
+        yield p + "self_attn.o_proj.weight", rnd(s.hidden, s.heads * s.head_dim)
+        yield p + "mlp.gate_proj.weight", rnd(s.inter, s.hidden)
+        yield p + "mlp.up_proj.weight", rnd(s.inter, s.hidden)
+        yield p + "mlp.down_proj.weight", rnd(s.hidden, s.inter)
+        yield p + "input_layernorm.weight", torch.ones(s.hidden, dtype=BF16, device=device)
+        yield p + "post_attention_layernorm.weight", torch.ones(s.hidden, dtype=BF16, device=device)
+    yield "model.norm.weight", torch.ones(s.hidden, dtype=BF16, device=device)
+    yield "lm_head.weight", rnd(s.vocab, s.hidden)
 
 
 def unpack_rows(packed: torch.Tensor, n: int, k: int, ids: torch.Tensor, group: int = 1) -> torch.Tensor:
