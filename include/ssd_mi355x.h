@@ -374,6 +374,55 @@ typedef struct SsdBuffers {   /* activations [m_cap][...] and the layer-major KV
 int ssd_forward(const SsdModel* model, const SsdPlan* plan, const SsdBuffers* buf, const SsdRows* rows, int m,
                 int p_min, int l_max, int head_first, int head_rows, hipStream_t stream);
 
+/* ---- Prefill: the target's forward over a long prompt chunk (reference
+ * ssd/engine/speculative.py:149-151, the target called on the prompt; its layers
+ * ssd/models/subnetwork_draft.py:193-246). Compute-bound MFMA GEMMs tiled 128 x 128 through LDS
+ * and causal flash attention; rows are prompt positions pos0 .. pos0 + m - 1 written to cache
+ * slots of the same index. Results match the decode kernels within bf16 rounding (not bit for
+ * bit); greedy speculative and greedy autoregressive decoding share one prefill. */
+#define SSD_EPI_STORE 0   /* Y = XW^T (+ residual) */
+#define SSD_EPI_SWIGLU 1  /* Y[:, i] = silu(gate_i) * up_i, gate/up interleaved 8 + 8 rows per tile */
+#define SSD_EPI_QKV 2     /* q -> Y with RoPE; k (RoPE), v -> the cache at slot pos0 + row */
+
+typedef struct SsdQkvEpilogue {
+  int32_t heads, kv_heads, head_dim;
+  const uint16_t* cos;        /* bf16 rotary tables [rope_rows][head_dim/2] */
+  const uint16_t* sin;
+  int64_t rope_rows;
+  int32_t pos0;               /* position (= cache slot) of row 0 */
+  uint16_t* k_cache;          /* this layer: kv_heads x (max_len x head_dim), 64-slot block layout */
+  uint16_t* vt_cache;
+  int64_t max_len;
+} SsdQkvEpilogue;
+
+/* Y = epilogue(X[M, K] W^T) for any M (W packed by ssd_pack_weight_bf16 with `group`, K % 64 == 0);
+ * norm_eps > 0 folds the RMSNorm of X's rows as the decode GEMMs do. Replaces the prompt-length
+ * F.linear / nn.Linear calls of the target layers (ssd/models/subnetwork_draft.py:209-212, :243-245). */
+int ssd_prefill_gemm_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int group, int N, int K,
+                          float norm_eps, int epi, uint16_t* Y, int64_t ldy, const uint16_t* residual, int64_t ldr,
+                          const SsdQkvEpilogue* qkv, hipStream_t stream);
+
+/* Causal attention of prompt rows: row t (position pos0 + t) attends cache slots [0, pos0 + t],
+ * scale * q.k, GQA (heads / kv_heads q heads per kv head). Replaces the causal SDPA of the prompt
+ * forward (ssd/models/subnetwork_draft.py:236-241 with no tree mask). head_dim 64 or 128. */
+int ssd_prefill_attention_bf16(const uint16_t* q, int64_t ldq, int M, int pos0, int heads, int kv_heads,
+                               int head_dim, const uint16_t* k_cache, const uint16_t* vt_cache, int64_t max_len,
+                               float scale, uint16_t* out, int64_t ldo, hipStream_t stream);
+
+typedef struct SsdPrefillBuffers {  /* activations [m_cap][...] and the KV arena */
+  int32_t m_cap;
+  uint16_t *h, *q, *attn, *act;     /* [m_cap][hidden], [m_cap][heads*hd] x 2, [m_cap][inter] */
+  uint16_t* k_arena;                /* as SsdBuffers */
+  uint16_t* vt_arena;
+  int64_t cache_cap;
+  uint16_t* logits;                 /* [vocab]: the last row's logits */
+} SsdPrefillBuffers;
+
+/* The whole target forward over rows [pos0, pos0 + m), m <= m_cap, in one call; head_w (the packed
+ * full lm_head with the final norm folded, NULL = no head) gives the last row's logits. */
+int ssd_prefill(const SsdModel* model, const uint16_t* head_w, const SsdPrefillBuffers* buf, const int32_t* ids,
+                int m, int pos0, hipStream_t stream);
+
 #if defined(__GNUC__) || defined(__clang__)
 #pragma GCC visibility pop
 #endif

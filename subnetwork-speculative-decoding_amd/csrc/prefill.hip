@@ -1,0 +1,508 @@
+// Prefill on gfx950: the target forward over a long prompt chunk (hundreds to thousands of rows),
+// where every projection is a compute-bound GEMM and attention is causal.
+//
+// The decode kernels stream each weight once per call and suit M <= 64 rows; a 4096-token prompt
+// through them re-reads every weight 64 times. Here (reference ssd/engine/speculative.py:149-151,
+// the target's forward over the prompt):
+//
+// * prefill_gemm_kernel: Y = X W^T over the same packed weights as the decode GEMMs (16 x 32
+//   MFMA A-operand tiles, any tile grouping), as an LDS-tiled MFMA GEMM: a workgroup of 4 waves
+//   owns a 128 (N) x 128 (M) output tile, stages 128 x 64 of W and of X per step in LDS (double
+//   buffered, the next step's global loads in flight while the MFMAs run), and each wave computes a
+//   64 x 64 sub-tile with v_mfma_f32_16x16x32_bf16. X is staged in the MFMA B-operand lane order so
+//   every LDS read is one contiguous 1 KiB per wave. The decode epilogues run on the accumulators:
+//   the folded RMSNorm scale (sum of x^2 accumulated by the threads that stage X), RoPE + KV-cache
+//   write for q/k/v, SwiGLU for gate/up (rotary / gate-up row pairs r and r + 8 meet through one
+//   v_permlane32_swap), residual add for o and down. Workgroup ids are mapped XCD-aware: each XCD
+//   (ids b, b + 8, ...) takes a contiguous run of output tiles ordered M-fastest within a band of
+//   N tiles, so the weight and activation tiles it reads stay in its L2.
+// * prefill_attention_kernel: causal flash attention, one wave per (q head, 32 tokens), K/V read
+//   in the cache's 64-slot MFMA-operand blocks; S^T = K Q^T and O^T = V^T P^T on MFMA with the
+//   running max / sum rescaled per 64-key block.
+// * ssd_prefill: the whole target forward for one chunk of prompt rows in one C call.
+//
+// Prefill rows are not required to be bit-identical to the same rows decoded one by one: greedy
+// speculative decoding and greedy autoregressive decoding both start from the same prefill, and
+// the decode kernels keep their batch invariance among themselves.
+#include "gemm_epi.h"
+
+#include <math.h>
+
+namespace ssd {
+
+constexpr int PF_BN = 128;  // output rows of W per workgroup
+constexpr int PF_BM = 128;  // tokens per workgroup
+constexpr int PF_KB = 2;    // 32-wide k-blocks per pipeline step
+
+// Tile (nb, kb) of a packed weight with `group` row tiles per k-block group: 64 lanes x 16 B.
+__device__ __forceinline__ size_t packed_tile(int nb, int kb, int kbt, int group) {
+  return ((size_t)(nb / group) * kbt + kb) * group + nb % group;
+}
+
+template <int EPI, int NORM>
+__global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(GemmArgs a, int group, int n_mt, int n_nt, int pos0) {
+  __shared__ u32x4_t As[2][PF_KB][8][64];
+  __shared__ u32x4_t Bs[2][PF_KB][8][64];
+  __shared__ float rn_s[PF_BM];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int wn = w & 1, wm = w >> 1;
+  const int kbt = a.kb_total;
+
+  // XCD-aware tile order: XCD x = id % 8 owns logical tiles [x * per, (x + 1) * per); within it,
+  // tiles go M-fastest inside bands of 8 N tiles (the band's weights and all of X cycle through
+  // that XCD's L2).
+  const int n_tiles = n_mt * n_nt;
+  const int per = (n_tiles + 7) / 8;
+  const int lt = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+  if (lt >= n_tiles) return;
+  constexpr int BAND = 8;
+  const int band = lt / (BAND * n_mt), in_band = lt % (BAND * n_mt);
+  const int band_w = min(BAND, n_nt - band * BAND);
+  const int bn = band * BAND + in_band % band_w, bm = in_band / band_w;
+  const int nb0 = bn * 8, m0 = bm * PF_BM;
+
+  // Staging assignment: 1024 16-byte chunks of W and of X per step, 4 of each per thread.
+  // W chunk i: k-block i >> 9 of the step, row tile (i >> 6) & 7, lane i & 63 (one tile = 1 KiB).
+  // X chunk i: row i >> 3 of the tile (t >> 3, + 32, + 64, + 96), 16-byte column c = t & 7 of the
+  // step's 64 k (k-block c >> 2, B-operand lane group c & 3).
+  const u32x4_t* W = (const u32x4_t*)a.W;
+  size_t wbase[4];
+  int wkb[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int i = t + 256 * r;
+    wkb[r] = i >> 9;
+    const int nb = nb0 + ((i >> 6) & 7);
+    wbase[r] = packed_tile(nb, 0, kbt, group) * 64 + (i & 63);
+  }
+  const int xc = t & 7;
+  const bf16_t* xrow[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) xrow[r] = a.X + (size_t)min(m0 + (t >> 3) + 32 * r, a.M - 1) * a.ldx + xc * 8;
+  const int xkb = xc >> 2, xg = xc & 3;
+
+  u32x4_t ra[4], rb[4];
+  float ss[4] = {0.f, 0.f, 0.f, 0.f};
+  auto gload = [&](int st) {
+    const int k0 = st * PF_KB;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ra[r] = __builtin_nontemporal_load(W + wbase[r] + (size_t)(k0 + wkb[r]) * group * 64);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) rb[r] = *(const u32x4_t*)(xrow[r] + (size_t)k0 * 32);
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) (&As[buf][0][0][0])[t + 256 * r] = ra[r];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = (t >> 3) + 32 * r;
+      Bs[buf][xkb][row >> 4][xg * 16 + (row & 15)] = rb[r];
+    }
+    if constexpr (NORM) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ss[r] += sumsq8(rb[r]);
+    }
+  };
+
+  f32x4_t acc[4][4];
+#pragma unroll
+  for (int x = 0; x < 4; ++x)
+#pragma unroll
+    for (int y = 0; y < 4; ++y) acc[x][y] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int n_st = kbt / PF_KB;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int st = 0; st < n_st; ++st) {
+    const int buf = st & 1;
+    const bool more = st + 1 < n_st;
+    if (more) gload(st + 1);
+#pragma unroll
+    for (int kb = 0; kb < PF_KB; ++kb) {
+      u32x4_t af[4], bf[4];
+#pragma unroll
+      for (int x = 0; x < 4; ++x) af[x] = As[buf][kb][wn * 4 + x][lane];
+#pragma unroll
+      for (int y = 0; y < 4; ++y) bf[y] = Bs[buf][kb][wm * 4 + y][lane];
+#pragma unroll
+      for (int x = 0; x < 4; ++x)
+#pragma unroll
+        for (int y = 0; y < 4; ++y) acc[x][y] = mfma16x16x32(bits_bf16x8(af[x]), bits_bf16x8(bf[y]), acc[x][y]);
+    }
+    if (more) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  if constexpr (NORM) {
+    // the 8 threads that staged one row hold its partial sums (consecutive lanes t, t ^ 1, ...)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v = ss[r];
+      v += __shfl_xor(v, 1);
+      v += __shfl_xor(v, 2);
+      v += __shfl_xor(v, 4);
+      if (xc == 0) rn_s[(t >> 3) + 32 * r] = rsqrtf(v / (float)(kbt * 32) + a.norm_eps);
+    }
+    __syncthreads();
+  }
+
+  // Lane (g, j) of acc[x][y] holds rows n = 16 (nb0 + 4 wn + x) + 4 g + e of token m = m0 + 64 wm
+  // + 16 y + j.
+#pragma unroll
+  for (int y = 0; y < 4; ++y) {
+    const int mr = wm * 64 + y * 16 + j;
+    const int m = m0 + mr;
+    const float sc = NORM ? rn_s[mr] : 1.f;
+    const bool mv = m < a.M;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      const int nb = nb0 + wn * 4 + x;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = acc[x][y][e] * sc;
+      if constexpr (EPI == EPI_STORE) {
+        const int n = nb * 16 + 4 * g;
+        if (mv) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < a.N) {
+              float r = rbf(v[e]);
+              if (a.residual) r = rbf(bf2f(a.residual[(size_t)m * a.ldr + n + e]) + r);
+              a.Y[(size_t)m * a.ldy + n + e] = f2bf(r);
+            }
+        }
+      } else {
+        // rows r (lanes g < 2) and r + 8 (lanes g >= 2) of the tile meet: r[0] = the lower
+        // half's value, r[1] = the upper half's, on every lane
+        float lo[4], hi[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[e]), __float_as_uint(v[e]), false, false);
+          lo[e] = __uint_as_float(p[0]);
+          hi[e] = __uint_as_float(p[1]);
+        }
+        if (mv && g < 2 && nb * 16 < a.N) {
+          if constexpr (EPI == EPI_SWIGLU) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) epi_swiglu(a, nb * 8 + 4 * g + e, m, lo[e], hi[e]);
+          } else {
+            const QkvTile q = qkv_tile(a, nb);
+            const int pos = min(max(pos0 + m, 0), (int)a.rope_rows - 1), half = a.head_dim >> 1;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int pr = 4 * g + e;
+              const size_t at = (size_t)pos * half + q.p * 8 + pr;
+              epi_qkv_pre(a, q, m, pr, lo[e], hi[e], pos0 + m, bf2f(a.cos_tab[at]), bf2f(a.sin_tab[at]));
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ causal flash attention
+// Row (token t, q head h) at position pos0 + t attends cache slots [0, pos0 + t] (the prompt rows
+// before it and itself, whose K/V the q/k/v GEMM of this chunk already wrote).
+__device__ __forceinline__ int pf_perm_key(int kt, int i) {
+  return (kt >> 1) * 32 + (i >> 2) * 8 + (kt & 1) * 4 + (i & 3);
+}
+
+__device__ __forceinline__ float pf_max_lanes(float v) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pf_sum_lanes(float v) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+constexpr int PF_TOK = 32;  // tokens per wave (two 16-row tiles)
+
+template <int HD>
+__global__ __launch_bounds__(256, 2) void prefill_attention_kernel(const bf16_t* __restrict__ Q, int64_t ldq, int M,
+                                                                   int pos0, int heads, int kv_heads,
+                                                                   const bf16_t* __restrict__ Kc,
+                                                                   const bf16_t* __restrict__ Vt, int64_t max_len,
+                                                                   float scale_log2, bf16_t* __restrict__ out,
+                                                                   int64_t ldo, int n_tt) {
+  constexpr int KS = HD / 32, DT = HD / 16, NT = PF_TOK / 16;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int n_hg = (heads + 3) / 4;
+  // the longest token tiles first (their rows attend the most keys)
+  const int tt = n_tt - 1 - (int)blockIdx.x / n_hg;
+  const int h = ((int)blockIdx.x % n_hg) * 4 + w;
+  if (h >= heads) return;
+  const int kvh = h / (heads / kv_heads);
+  const int t0 = tt * PF_TOK;
+  const bf16_t* kb = Kc + (size_t)kvh * max_len * HD + lane * 8;
+  const bf16_t* vb = Vt + (size_t)kvh * max_len * HD + lane * 8;
+
+  u32x4_t qf[NT][KS];
+  int lim[NT];  // last attended key of this lane's row in tile rt
+#pragma unroll
+  for (int rt = 0; rt < NT; ++rt) {
+    const int tok = min(t0 + rt * 16 + j, M - 1);
+    lim[rt] = pos0 + t0 + rt * 16 + j;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[rt][ks] = *(const u32x4_t*)(Q + (size_t)tok * ldq + (size_t)h * HD + ks * 32 + g * 8);
+  }
+  float m_run[NT], l_run[NT];
+  f32x4_t o[NT][DT];
+#pragma unroll
+  for (int rt = 0; rt < NT; ++rt) {
+    m_run[rt] = -INFINITY;
+    l_run[rt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[rt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  const int last = pos0 + min(t0 + PF_TOK, M) - 1;  // the tile's last attended key
+  const int n_blk = last / 64 + 1;
+  const int full_blk = (pos0 + t0) / 64;  // blocks every row of the tile attends entirely
+  for (int b = 0; b < n_blk; ++b) {
+    // K first: the scores of both row tiles; V is loaded while the softmax runs (K and V are not
+    // live together, which keeps the wave inside 256 registers)
+    u32x4_t kf[4][KS];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kf[kt][ks] = *(const u32x4_t*)(kb + (size_t)b * 64 * HD + (kt * KS + ks) * 512);
+    f32x4_t s[NT][4];
+#pragma unroll
+    for (int rt = 0; rt < NT; ++rt)
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        s[rt][kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) s[rt][kt] = mfma16x16x32(bits_bf16x8(kf[kt][ks]), bits_bf16x8(qf[rt][ks]), s[rt][kt]);
+      }
+    u32x4_t vf[DT][2];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      vf[dt][0] = *(const u32x4_t*)(vb + (size_t)b * 64 * HD + (dt * 2) * 512);
+      vf[dt][1] = *(const u32x4_t*)(vb + (size_t)b * 64 * HD + (dt * 2 + 1) * 512);
+    }
+    if (b == n_blk - 1) {
+      // slots past the tile's last key hold whatever the cache held (not yet written): their
+      // probabilities are 0, and 0 * V must stay 0, so V is zeroed there. Lane (g, i) of V tile
+      // (dt, c) holds slots 64 b + 32 c + 8 g .. + 8.
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const int s0 = b * 64 + c * 32 + g * 8;
+        u32x4_t keep;
+#pragma unroll
+        for (int w2 = 0; w2 < 4; ++w2)
+          keep[w2] = (s0 + 2 * w2 <= last ? 0x0000ffffu : 0u) | (s0 + 2 * w2 + 1 <= last ? 0xffff0000u : 0u);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) vf[dt][c] &= keep;
+      }
+    }
+    const bool masked = b >= full_blk;
+#pragma unroll
+    for (int rt = 0; rt < NT; ++rt) {
+      float sv[16], mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float v = s[rt][kt][e] * scale_log2;
+          if (masked && b * 64 + pf_perm_key(kt, 4 * g + e) > lim[rt]) v = -INFINITY;
+          sv[kt * 4 + e] = v;
+          mx = fmaxf(mx, v);
+        }
+      mx = pf_max_lanes(mx);
+      const float m_new = fmaxf(m_run[rt], mx);
+      // every row attends key 0, so m_new is finite from the first block on
+      const float alpha = __builtin_amdgcn_exp2f(m_run[rt] - m_new);
+      float l = 0.f;
+      uint32_t pw[2][4];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; e += 2) {
+          const float p0 = __builtin_amdgcn_exp2f(sv[kt * 4 + e] - m_new);
+          const float p1 = __builtin_amdgcn_exp2f(sv[kt * 4 + e + 1] - m_new);
+          l += p0 + p1;
+          pw[kt >> 1][(kt & 1) * 2 + e / 2] = pack_bf16x2(p0, p1);
+        }
+      l = pf_sum_lanes(l);
+      l_run[rt] = l_run[rt] * alpha + l;
+      m_run[rt] = m_new;
+      const u32x4_t pb0 = {pw[0][0], pw[0][1], pw[0][2], pw[0][3]};
+      const u32x4_t pb1 = {pw[1][0], pw[1][1], pw[1][2], pw[1][3]};
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        f32x4_t acc = o[rt][dt] * alpha;
+        acc = mfma16x16x32(bits_bf16x8(vf[dt][0]), bits_bf16x8(pb0), acc);
+        acc = mfma16x16x32(bits_bf16x8(vf[dt][1]), bits_bf16x8(pb1), acc);
+        o[rt][dt] = acc;
+      }
+    }
+  }
+  // lane (g, j) of o[rt][dt] holds dims 16 dt + 4 g + e of row j
+#pragma unroll
+  for (int rt = 0; rt < NT; ++rt) {
+    const int tok = t0 + rt * 16 + j;
+    if (tok >= M) continue;
+    const float inv = 1.f / l_run[rt];
+    bf16_t* dst = out + (size_t)tok * ldo + (size_t)h * HD;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const uint32_t lo = pack_bf16x2(o[rt][dt][0] * inv, o[rt][dt][1] * inv);
+      const uint32_t hi = pack_bf16x2(o[rt][dt][2] * inv, o[rt][dt][3] * inv);
+      *(uint2*)(dst + dt * 16 + 4 * g) = make_uint2(lo, hi);
+    }
+  }
+}
+
+static int launch_prefill_gemm(GemmArgs a, int group, int pos0, int epi, hipStream_t s) {
+  const int n_mt = (a.M + PF_BM - 1) / PF_BM;
+  const int n_nt = (a.N + PF_BN - 1) / PF_BN;
+  const int n_tiles = n_mt * n_nt;
+  const int grid = (n_tiles + 7) / 8 * 8;
+  const bool norm = a.norm_eps > 0.f;
+#define PF_LAUNCH(E)                                                                                          \
+  if (norm) hipLaunchKernelGGL((prefill_gemm_kernel<E, 1>), dim3(grid), dim3(256), 0, s, a, group, n_mt, n_nt, pos0); \
+  else hipLaunchKernelGGL((prefill_gemm_kernel<E, 0>), dim3(grid), dim3(256), 0, s, a, group, n_mt, n_nt, pos0);
+  switch (epi) {
+    case EPI_STORE: PF_LAUNCH(EPI_STORE); break;
+    case EPI_SWIGLU: PF_LAUNCH(EPI_SWIGLU); break;
+    default: PF_LAUNCH(EPI_QKV); break;
+  }
+#undef PF_LAUNCH
+  return check_launch("prefill_gemm");
+}
+
+static int check_packed(int N, int K, int group) {
+  if (N <= 0 || K <= 0 || K % (32 * PF_KB)) return set_error(SSD_EINVAL, "prefill gemm: N=%d K=%d (K %% 64 == 0)", N, K);
+  const int tiles = (N + 127) / 128 * 8;  // packed row tiles (rows padded to 128)
+  if (group < 1 || group > 16 || tiles % group)
+    return set_error(SSD_EINVAL, "prefill gemm: group %d does not divide the %d row tiles", group, tiles);
+  return SSD_OK;
+}
+
+}  // namespace ssd
+
+using namespace ssd;
+
+SSD_API int ssd_prefill_gemm_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int group, int N,
+                                  int K, float norm_eps, int epi, uint16_t* Y, int64_t ldy, const uint16_t* residual,
+                                  int64_t ldr, const SsdQkvEpilogue* qkv, hipStream_t stream) {
+  if (!X || !W_packed || !Y) return set_error(SSD_EINVAL, "prefill gemm: null pointer");
+  if (M <= 0) return set_error(SSD_EINVAL, "prefill gemm: M=%d", M);
+  int rc = check_packed(N, K, group);
+  if (rc) return rc;
+  if (ldx < K || ldx % 8 || ((uintptr_t)X & 15)) return set_error(SSD_EINVAL, "prefill gemm: X rows must be 16-byte aligned");
+  if (epi != SSD_EPI_STORE && epi != SSD_EPI_SWIGLU && epi != SSD_EPI_QKV)
+    return set_error(SSD_EINVAL, "prefill gemm: epilogue %d", epi);
+  if (epi == SSD_EPI_STORE && ldy < N) return set_error(SSD_EINVAL, "prefill gemm: ldy %lld < N", (long long)ldy);
+  if (epi == SSD_EPI_SWIGLU && (N % 16 || ldy < N / 2)) return set_error(SSD_EINVAL, "prefill gemm: swiglu N=%d", N);
+  if (epi != SSD_EPI_STORE && residual) return set_error(SSD_EINVAL, "prefill gemm: residual only with a plain store");
+  GemmArgs a{};
+  a.X = X; a.ldx = ldx; a.M = M; a.W = (const uint4*)W_packed; a.N = N; a.kb_total = K / 32;
+  a.Y = Y; a.ldy = ldy; a.residual = residual; a.ldr = ldr; a.norm_eps = norm_eps;
+  int pos0 = 0;
+  if (epi == SSD_EPI_QKV) {
+    if (!qkv || !qkv->cos || !qkv->sin || !qkv->k_cache || !qkv->vt_cache)
+      return set_error(SSD_EINVAL, "prefill gemm: q/k/v epilogue needs rotary tables and the cache");
+    const int hd = qkv->head_dim;
+    if ((hd != 32 && hd != 64 && hd != 128) || qkv->heads <= 0 || qkv->kv_heads <= 0 ||
+        N != (qkv->heads + 2 * qkv->kv_heads) * hd || ldy < (int64_t)qkv->heads * hd)
+      return set_error(SSD_EINVAL, "prefill gemm: q/k/v shape N=%d heads=%d kv=%d hd=%d", N, qkv->heads,
+                       qkv->kv_heads, hd);
+    if (qkv->pos0 < 0 || qkv->pos0 + M > qkv->max_len || qkv->pos0 + M > qkv->rope_rows || qkv->max_len % 64)
+      return set_error(SSD_EINVAL, "prefill gemm: rows [%d, %d) outside the cache (%lld) or rotary table (%lld)",
+                       qkv->pos0, qkv->pos0 + M, (long long)qkv->max_len, (long long)qkv->rope_rows);
+    a.heads = qkv->heads; a.kv_heads = qkv->kv_heads; a.head_dim = hd;
+    a.cos_tab = qkv->cos; a.sin_tab = qkv->sin; a.rope_rows = qkv->rope_rows;
+    a.k_cache = qkv->k_cache; a.vt_cache = qkv->vt_cache; a.max_len = qkv->max_len;
+    pos0 = qkv->pos0;
+  }
+  return launch_prefill_gemm(a, group, pos0, epi, stream);
+}
+
+SSD_API int ssd_prefill_attention_bf16(const uint16_t* q, int64_t ldq, int M, int pos0, int heads, int kv_heads,
+                                       int head_dim, const uint16_t* k_cache, const uint16_t* vt_cache,
+                                       int64_t max_len, float scale, uint16_t* out, int64_t ldo,
+                                       hipStream_t stream) {
+  if (!q || !k_cache || !vt_cache || !out) return set_error(SSD_EINVAL, "prefill attention: null pointer");
+  if (M <= 0 || pos0 < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads)
+    return set_error(SSD_EINVAL, "prefill attention: M=%d pos0=%d heads=%d kv_heads=%d", M, pos0, heads, kv_heads);
+  if (pos0 + M > max_len || max_len % 64 || ldq % 8 || ((uintptr_t)q & 15) || ((uintptr_t)k_cache & 15) ||
+      ((uintptr_t)vt_cache & 15) || ldo % 4 || ((uintptr_t)out & 7))
+    return set_error(SSD_EINVAL, "prefill attention: rows [%d, %d) vs cache %lld, or misaligned operands", pos0,
+                     pos0 + M, (long long)max_len);
+  const int n_tt = (M + PF_TOK - 1) / PF_TOK;
+  const dim3 grid((unsigned)(n_tt * ((heads + 3) / 4))), block(256);
+  const float sl2 = scale * 1.4426950408889634f;
+  switch (head_dim) {
+    case 64:
+      hipLaunchKernelGGL((prefill_attention_kernel<64>), grid, block, 0, stream, (const bf16_t*)q, ldq, M, pos0, heads,
+                         kv_heads, (const bf16_t*)k_cache, (const bf16_t*)vt_cache, max_len, sl2, (bf16_t*)out, ldo, n_tt);
+      break;
+    case 128:
+      hipLaunchKernelGGL((prefill_attention_kernel<128>), grid, block, 0, stream, (const bf16_t*)q, ldq, M, pos0,
+                         heads, kv_heads, (const bf16_t*)k_cache, (const bf16_t*)vt_cache, max_len, sl2, (bf16_t*)out,
+                         ldo, n_tt);
+      break;
+    default:
+      return set_error(SSD_EINVAL, "prefill attention: head_dim %d unsupported (64, 128)", head_dim);
+  }
+  return check_launch("prefill_attention");
+}
+
+// The target forward over prompt rows [pos0, pos0 + m): embed -> per layer q/k/v (+RoPE, KV
+// write) -> causal attention -> o_proj + residual -> gate/up + SwiGLU -> down + residual; then the
+// full-vocabulary head (head_w, final norm folded; NULL = none) on the last row. Buffers are
+// [m_cap] rows.
+SSD_API int ssd_prefill(const SsdModel* md, const uint16_t* head_w, const SsdPrefillBuffers* pb, const int32_t* ids,
+                        int m, int pos0, hipStream_t s) {
+  if (!md || !pb || !ids) return set_error(SSD_EINVAL, "prefill: null descriptor");
+  if (m <= 0 || m > pb->m_cap) return set_error(SSD_EINVAL, "prefill: m=%d outside [1, %d]", m, pb->m_cap);
+  if (!md->layers) return set_error(SSD_EINVAL, "prefill: null layer table");
+  if (!(md->eps > 0.f)) return set_error(SSD_EINVAL, "prefill: norm eps must be > 0");
+  if (pos0 < 0 || pos0 + m > pb->cache_cap)
+    return set_error(SSD_EINVAL, "prefill: rows [%d, %d) beyond the cache (%lld)", pos0, pos0 + m,
+                     (long long)pb->cache_cap);
+  if (head_w && !pb->logits) return set_error(SSD_EINVAL, "prefill: no logits buffer");
+  const int d = md->hidden, hd = md->head_dim, H = md->heads, KV = md->kv_heads, I = md->inter;
+  const int64_t qdim = (int64_t)H * hd;
+  const int nqkv = (H + 2 * KV) * hd;
+  const size_t layer_elems = (size_t)KV * pb->cache_cap * hd;
+  const int g_qkv = ssd_gemm_weight_group(nqkv, d), g_o = ssd_gemm_residual_group(d, (int)qdim);
+  const int g_gu = md->mlp_fused ? ssd_mlp_group(I, d) : ssd_gemm_weight_group(2 * I, d);
+  const int g_d = ssd_gemm_residual_group(d, I);
+  if (g_qkv < 1 || g_o < 1 || g_gu < 1 || g_d < 1) return set_error(SSD_EINVAL, "prefill: no packing plan for this shape");
+  int rc = ssd_embed_bf16(ids, m, md->embed, md->vocab, d, pb->h, d, s);
+  if (rc) return rc;
+  for (int li = 0; li < md->n_layers; ++li) {
+    const SsdLayerW& L = md->layers[li];
+    SsdQkvEpilogue qe{H, KV, hd, md->cos, md->sin, md->rope_rows, pos0, pb->k_arena + li * layer_elems,
+                      pb->vt_arena + li * layer_elems, pb->cache_cap};
+    if ((rc = ssd_prefill_gemm_bf16(pb->h, d, m, L.wqkv, g_qkv, nqkv, d, md->eps, SSD_EPI_QKV, pb->q, qdim, nullptr, 0,
+                                    &qe, s)))
+      return rc;
+    if ((rc = ssd_prefill_attention_bf16(pb->q, qdim, m, pos0, H, KV, hd, qe.k_cache, qe.vt_cache, pb->cache_cap,
+                                         md->attn_scale, pb->attn, qdim, s)))
+      return rc;
+    if ((rc = ssd_prefill_gemm_bf16(pb->attn, qdim, m, L.wo, g_o, d, (int)qdim, 0.f, SSD_EPI_STORE, pb->h, d, pb->h, d,
+                                    nullptr, s)))
+      return rc;
+    if ((rc = ssd_prefill_gemm_bf16(pb->h, d, m, L.wgu, g_gu, 2 * I, d, md->eps, SSD_EPI_SWIGLU, pb->act, I, nullptr, 0,
+                                    nullptr, s)))
+      return rc;
+    if ((rc = ssd_prefill_gemm_bf16(pb->act, I, m, L.wd, g_d, d, I, 0.f, SSD_EPI_STORE, pb->h, d, pb->h, d, nullptr, s)))
+      return rc;
+  }
+  if (head_w)
+    return ssd_gemm_bf16(pb->h + (size_t)(m - 1) * d, d, 1, head_w, md->vocab, d, md->eps, pb->logits, md->vocab,
+                         nullptr, 0, nullptr, 0, s);
+  return SSD_OK;
+}

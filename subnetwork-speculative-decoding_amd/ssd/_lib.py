@@ -75,6 +75,16 @@ class SsdBuffers(C.Structure):
         ("sync", P)]
 
 
+class SsdQkvEpilogue(C.Structure):
+    _fields_ = [("heads", C.c_int32), ("kv_heads", C.c_int32), ("head_dim", C.c_int32), ("cos", P), ("sin", P),
+                ("rope_rows", I64), ("pos0", C.c_int32), ("k_cache", P), ("vt_cache", P), ("max_len", I64)]
+
+
+class SsdPrefillBuffers(C.Structure):
+    _fields_ = [("m_cap", C.c_int32)] + [(n, P) for n in ("h", "q", "attn", "act", "k_arena", "vt_arena")] + [
+        ("cache_cap", I64), ("logits", P)]
+
+
 _PROTOS = {
     "ssd_last_error": (C.c_char_p, []),
     "ssd_abi_version": (I32, []),
@@ -123,6 +133,10 @@ _PROTOS = {
                                 P]),
     "ssd_forward": (I32, [C.POINTER(SsdModel), C.POINTER(SsdPlan), C.POINTER(SsdBuffers), C.POINTER(SsdRows), I32,
                           I32, I32, I32, I32, P]),
+    "ssd_prefill_gemm_bf16": (I32, [P, I64, I32, P, I32, I32, I32, F32, I32, P, I64, P, I64,
+                                    C.POINTER(SsdQkvEpilogue), P]),
+    "ssd_prefill_attention_bf16": (I32, [P, I64, I32, I32, I32, I32, I32, P, P, I64, F32, P, I64, P]),
+    "ssd_prefill": (I32, [C.POINTER(SsdModel), P, C.POINTER(SsdPrefillBuffers), P, I32, I32, P]),
 }
 
 EXPORTED = tuple(_PROTOS)

@@ -31,7 +31,7 @@ from ssd.config import DraftingConfig
 from ssd.engine.kv_cache import KVCache
 from ssd.engine.sampling import Sampler
 from ssd.engine.tree_drafter import TREE_CAP, DeviceTree, TreeDrafter
-from ssd.models.subnetwork_draft import CHUNK, Rows, SubnetworkDraftModel
+from ssd.models.subnetwork_draft import CHUNK, PREFILL_CHUNK, PREFILL_MIN, Rows, SubnetworkDraftModel
 
 
 @dataclass
@@ -89,23 +89,32 @@ class _Phases:
 
 def _prefill(target: SubnetworkDraftModel, ids: list, cache: KVCache, ws, out_dev: torch.Tensor,
              sampler: Optional[Sampler] = None) -> None:
-    """Target forward over the prompt (chunks of 64 causal rows) and the first token into
-    out_dev[0]: the first-index argmax of the last row, or with ``sampler`` a draw from its warped
-    distribution with counter 0 (reference speculative.py:149-151, :81-84)."""
+    """Target forward over the prompt and the first token into out_dev[0]: the first-index argmax
+    of the last row, or with ``sampler`` a draw from its warped distribution with counter 0
+    (reference speculative.py:149-151, :81-84). Prompts of at least PREFILL_MIN tokens run on the
+    MFMA prefill kernels (chunks of PREFILL_CHUNK rows), shorter ones as causal rows through the
+    decode forward (chunks of 64)."""
     dev = target.model.device
-    rows = Rows(CHUNK, dev)
     past = cache.get_seq_length()
     q = len(ids)
     cache.check_room(past + q)
+    cache.ensure(target.num_kv_heads, target.head_dim, dev)
     logits = None
-    for c0 in range(0, q, CHUNK):
-        c1 = min(q, c0 + CHUNK)
-        m = c1 - c0
-        slots = list(range(past + c0, past + c1))
-        rows.upload(ids[c0:c1], slots, slots, [s + 1 for s in slots], [0] * m)
-        last = c1 == q
-        logits = target.forward_rows(rows, m, past + c0 + 1, past + c1, cache, ws, m - 1 if last else 0, int(last))
-        torch.cuda.current_stream().synchronize()  # the pinned staging buffer is reused next chunk
+    if q >= PREFILL_MIN and target.prefill_capable():
+        for c0 in range(0, q, PREFILL_CHUNK):
+            c1 = min(q, c0 + PREFILL_CHUNK)
+            logits = target.prefill_chunk(ids[c0:c1], past + c0, cache, c1 == q)
+    else:
+        rows = Rows(CHUNK, dev)
+        for c0 in range(0, q, CHUNK):
+            c1 = min(q, c0 + CHUNK)
+            m = c1 - c0
+            slots = list(range(past + c0, past + c1))
+            rows.upload(ids[c0:c1], slots, slots, [s + 1 for s in slots], [0] * m)
+            last = c1 == q
+            logits = target.forward_rows(rows, m, past + c0 + 1, past + c1, cache, ws, m - 1 if last else 0,
+                                         int(last))
+            torch.cuda.current_stream().synchronize()  # the pinned staging buffer is reused next chunk
     ws.check_faults()
     cache.advance(q)
     if sampler is not None:

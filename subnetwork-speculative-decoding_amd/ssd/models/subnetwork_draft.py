@@ -36,6 +36,8 @@ from ssd.models.llama import MI355XLlama
 
 MAXD = 32        # ancestors per row (ssd_attn_max_depth)
 CHUNK = 64       # rows per kernel launch chain (GEMM column tiles of 16 x 4)
+PREFILL_MIN = 256     # causal prompt chunks at least this long run on the MFMA prefill kernels
+PREFILL_CHUNK = 4096  # prompt rows per ssd_prefill call
 
 
 @dataclass
@@ -230,6 +232,34 @@ class Workspace:
         return st, self.logits[: self.m_cap * ld].view(self.m_cap, ld)
 
 
+class PrefillWorkspace:
+    """Activation buffers of ssd_prefill for prompt chunks of up to ``m_cap`` rows."""
+
+    def __init__(self, model: MI355XLlama, m_cap: int):
+        s, dev = model.shape, model.device
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        self.m_cap = m_cap
+        self.h = torch.zeros(m_cap, s.hidden, **bf)
+        self.q = torch.zeros(m_cap, s.heads * s.head_dim, **bf)
+        self.attn = torch.zeros(m_cap, s.heads * s.head_dim, **bf)
+        self.act = torch.zeros(m_cap, s.inter, **bf)
+        self.ids = torch.zeros(m_cap, dtype=torch.int32, device=dev)
+        self.logits = torch.zeros(1, s.vocab, **bf)
+        self._native: dict = {}
+
+    def native(self, cache: KVCache) -> "_lib.SsdPrefillBuffers":
+        key = (cache.k.data_ptr(), cache.vt.data_ptr(), cache.capacity)
+        st = self._native.get(key)
+        if st is None:
+            if len(self._native) >= 8:
+                self._native.pop(next(iter(self._native)))
+            st = _lib.SsdPrefillBuffers(self.m_cap, self.h.data_ptr(), self.q.data_ptr(), self.attn.data_ptr(),
+                                        self.act.data_ptr(), cache.k.data_ptr(), cache.vt.data_ptr(), cache.capacity,
+                                        self.logits.data_ptr())
+            self._native[key] = st
+        return st
+
+
 class _BaseRefs:
     """Plain holder so base weights are never registered as draft parameters."""
 
@@ -263,6 +293,7 @@ class SubnetworkDraftModel(nn.Module):
         self._vocab_inv: Optional[torch.Tensor] = None
         self._sub_head: Optional[torch.Tensor] = None
         self._ws: Optional[Workspace] = None
+        self._pw: Optional[PrefillWorkspace] = None
         self._plan = None
 
     # ------------------------------------------------------------------ setup
@@ -302,6 +333,27 @@ class SubnetworkDraftModel(nn.Module):
         if self._ws is None or self._ws.m_cap < m_cap or self._ws.mids[0].shape[1] < bh:
             self._ws = Workspace(self.model, m_cap, bh)
         return self._ws
+
+    def prefill_capable(self) -> bool:
+        """The full target (every layer in order, no bridges) at shapes the prefill kernels take."""
+        s = self.model.shape
+        return (self.layer_indices == list(range(s.layers)) and not self.bridge_specs and s.head_dim in (64, 128)
+                and s.hidden % 64 == 0 and s.inter % 64 == 0 and (s.heads * s.head_dim) % 64 == 0)
+
+    def prefill_chunk(self, ids: list, pos0: int, cache: KVCache, logits: bool) -> Optional[torch.Tensor]:
+        """ssd_prefill over prompt rows pos0 .. pos0 + len(ids) - 1 (at most PREFILL_CHUNK): K/V
+        of every layer into the cache, the final residual stream in the prefill workspace's h, and
+        with ``logits`` the last row's full-vocabulary logits ([1, V] view)."""
+        m = len(ids)
+        if m > PREFILL_CHUNK:
+            raise ValueError(f"prefill chunk of {m} rows > {PREFILL_CHUNK}")
+        pw = self._pw
+        if pw is None or pw.m_cap < m:
+            pw = self._pw = PrefillWorkspace(self.model, max(m, min(PREFILL_CHUNK, 1024)))
+        pw.ids[:m].copy_(torch.tensor(ids, dtype=torch.int32))
+        _lib.call("ssd_prefill", self.model.native(cache.capacity), self.model.lm_head.data_ptr() if logits else None,
+                  pw.native(cache), pw.ids.data_ptr(), m, int(pos0), ops.stream())
+        return pw.logits if logits else None
 
     def _packed_bridge(self, name: str):
         br = self.bridges[name]
@@ -454,7 +506,17 @@ class SubnetworkDraftModel(nn.Module):
         rows = Rows(CHUNK, self.model.device)
         hraw = torch.empty(q, self.d_model, dtype=torch.bfloat16, device=self.model.device)
         states: dict = {} if output_bridge_states else None
-        for c0 in range(0, q, CHUNK):
+        causal = tree_attention_mask is None and pos == list(range(past, past + q))
+        if causal and states is None and q >= PREFILL_MIN and self.prefill_capable():
+            # a long causal prompt: the MFMA prefill kernels, PREFILL_CHUNK rows per call
+            for c0 in range(0, q, PREFILL_CHUNK):
+                c1 = min(q, c0 + PREFILL_CHUNK)
+                self.prefill_chunk(ids[c0:c1], past + c0, cache, False)
+                hraw[c0:c1].copy_(self._pw.h[:c1 - c0])
+            q_done = q
+        else:
+            q_done = 0
+        for c0 in range(q_done, q, CHUNK):
             c1 = min(q, c0 + CHUNK)
             seen = [a for lst in anc[c0:c1] for a in lst] + [p - 1 for p in prefix[c0:c1]]
             if max(seen) >= past + c1:

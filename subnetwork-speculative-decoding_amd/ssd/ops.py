@@ -7,6 +7,7 @@ device, alignment, shapes) before a launch, so a bad call raises instead of faul
 
 from __future__ import annotations
 
+import ctypes
 from typing import Optional
 
 import torch
@@ -135,6 +136,50 @@ def qkv_rope(x, m, wp, k, heads, kv_heads, head_dim, cos, sin, pos, slot, q_out,
               kv_heads, head_dim, cos.data_ptr(), sin.data_ptr(), cos.shape[0], pos.data_ptr(), slot.data_ptr(),
               q_out.data_ptr(), _rows(q_out, "q", heads * head_dim, m), k_cache.data_ptr(), vt_cache.data_ptr(),
               max_len, stream())
+
+
+# ------------------------------------------------------------------ prefill (long prompt chunks)
+EPI = {"store": 0, "swiglu": 1, "qkv": 2}
+
+
+def prefill_gemm(x, m, wp, group, n, k, out, epi="store", residual=None, norm_eps: float = 0.0, qkv=None):
+    """Y = epilogue(X W^T) for prompt-length M on the LDS-tiled MFMA kernel; ``wp`` packed with
+    ``group`` (as for the decode GEMM of the same weight). epi "store" (+ residual), "swiglu"
+    (n = 2 * inter, out gets inter columns) or "qkv" (qkv = dict(heads, kv_heads, head_dim, cos, sin,
+    pos0, k_cache, vt_cache, max_len); q goes to out, k/v to the cache at slots pos0 + row)."""
+    _check(x, "x"); _check(wp, "w_packed"); _check(out, "out")
+    _len(wp, "w_packed", packed_elems(n, k))
+    cols = n // 2 if epi == "swiglu" else (qkv["heads"] * qkv["head_dim"] if epi == "qkv" else n)
+    ldr = 0
+    if residual is not None:
+        _check(residual, "residual")
+        ldr = _rows(residual, "residual", n, m)
+    ep = None
+    if epi == "qkv":
+        c = qkv
+        for t, nm in ((c["k_cache"], "k_cache"), (c["vt_cache"], "vt_cache"), (c["cos"], "cos"), (c["sin"], "sin")):
+            _check(t, nm)
+        if c["k_cache"].numel() < c["kv_heads"] * c["max_len"] * c["head_dim"]:
+            raise ValueError("prefill_gemm: cache smaller than kv_heads * max_len * head_dim")
+        ep = _lib.SsdQkvEpilogue(c["heads"], c["kv_heads"], c["head_dim"], c["cos"].data_ptr(), c["sin"].data_ptr(),
+                                 c["cos"].shape[0], int(c["pos0"]), c["k_cache"].data_ptr(), c["vt_cache"].data_ptr(),
+                                 int(c["max_len"]))
+    _lib.call("ssd_prefill_gemm_bf16", x.data_ptr(), _rows(x, "x", k, m), m, wp.data_ptr(), int(group), n, k,
+              float(norm_eps), EPI[epi], out.data_ptr(), _rows(out, "out", cols, m), _p(residual), ldr,
+              ctypes.byref(ep) if ep is not None else None, stream())
+    return out
+
+
+def prefill_attention(q, m, pos0, heads, kv_heads, head_dim, k_cache, vt_cache, max_len, out, scale=None):
+    """Causal attention of prompt rows pos0 .. pos0 + m - 1 over cache slots [0, row position]."""
+    _check(q, "q"); _check(k_cache, "k_cache"); _check(vt_cache, "vt_cache"); _check(out, "out")
+    if k_cache.numel() < kv_heads * max_len * head_dim or vt_cache.numel() < kv_heads * max_len * head_dim:
+        raise ValueError("prefill_attention: cache smaller than kv_heads * max_len * head_dim")
+    scale = head_dim ** -0.5 if scale is None else scale
+    _lib.call("ssd_prefill_attention_bf16", q.data_ptr(), _rows(q, "q", heads * head_dim, m), m, int(pos0), heads,
+              kv_heads, head_dim, k_cache.data_ptr(), vt_cache.data_ptr(), int(max_len), float(scale), out.data_ptr(),
+              _rows(out, "out", heads * head_dim, m), stream())
+    return out
 
 
 def attn_workspace_floats(m: int, heads: int, head_dim: int, max_len: int) -> int:

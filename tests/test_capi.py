@@ -67,7 +67,8 @@ def test_descriptor_structs_match_c_layout(tmp_path):
     from ssd import _lib
 
     structs = {name: getattr(_lib, name) for name in ("SsdTree", "SsdRows", "SsdLayerW", "SsdModel", "SsdBridgeW",
-                                                       "SsdPlan", "SsdBuffers")}
+                                                       "SsdPlan", "SsdBuffers", "SsdQkvEpilogue",
+                                                       "SsdPrefillBuffers")}
     lines = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void) {"]
     for name, T in structs.items():
         lines.append(f'printf("{name} %zu\\n", sizeof({name}));')
