@@ -303,6 +303,18 @@ int ssd_accept_sample(const SsdTree* tree, const float* P, int64_t ldp, const fl
                       int committed, int32_t* result, int32_t* keep_src, int32_t* n_keep, int32_t* root_token,
                       hipStream_t stream);
 
+/* Batched acceptance trials for the statistical check of the acceptance rule at scale (no
+ * counterpart in the reference, whose loop is verify.py:60-95 on the CPU): `trials` independent
+ * rounds over fixed per-node distributions P / Q ([rows][ld] fp32; row 0 the root, row 1 + v node v
+ * of the unpruned tree with branch[d] children per level-d node, numbered level by level, children
+ * in draw order), each drawing its children on the walk by Gumbel top-k and accepting / rejecting
+ * exactly as ssd_gumbel_topk + ssd_accept_sample would with round counter counter0 + trial.
+ * cols / col_off: per-row support (CSR, ascending columns where P or Q > 0). Outputs per trial:
+ * out_tokens[trial][depth + 1] (accepted tokens, then the bonus) and out_n[trial]. */
+int ssd_accept_sample_trials(const float* P, int64_t ldp, const float* Q, int64_t ldq, int rows, const int32_t* cols,
+                             const int32_t* col_off, int depth, const int32_t* branch, uint64_t seed,
+                             uint64_t counter0, int trials, int32_t* out_tokens, int32_t* out_n, hipStream_t stream);
+
 /* ---------------------------------------------------------------- forward
  * Descriptors of one model forward; every pointer is device memory in the formats above
  * (weights packed by ssd_pack_weight_bf16). Host structs, read during the call only. */

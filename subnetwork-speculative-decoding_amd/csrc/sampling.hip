@@ -980,6 +980,193 @@ __global__ void sample_walk_kernel(AcceptArgs a, int committed, int* result, int
   *root_token = bonus;
 }
 
+// ------------------------------------------------------ batched acceptance trials
+// Many independent rounds of proposal + acceptance over one fixed set of per-node distributions
+// (row 0 the root, row 1 + v node v; P = warped target, Q = warped draft of the node's
+// children), one wave per trial, trial t drawing with round counter counter0 + t. The tree is
+// unpruned with branch[d] children per node at level d, numbered level by level (level L node with
+// in-level index f has children start[L + 1] + f * branch[L + 1] + i, i = draw order). Each trial
+// draws only the children on its walk; every draw and decision uses the engine's streams,
+// counters and formulas (gumbel_chunk / state0 / statej / sample_walk above): Gumbel keys
+// q / Exp(1) from the PROPOSE stream at (column / 4, f | level << 16), acceptance uniforms at
+// (rejections, row), residual states through chain_p, the bonus race on the unnormalised
+// residual at (column / 4, 0). Sums run over each row's support list (columns where P or Q is
+// nonzero; every other column contributes nothing) in double, in lane-strided order. Only the
+// sums' rounding order differs from the per-round kernels, so a trial reproduces the engine's
+// round with the same counter decision for decision.
+constexpr int TRIAL_MAXD = 8;
+
+struct TrialArgs {
+  const float* P;
+  int64_t ldp;
+  const float* Q;
+  int64_t ldq;
+  const int* cols;  // support columns of row r: cols[off[r] .. off[r + 1]), ascending
+  const int* off;
+  int depth;
+  int branch[TRIAL_MAXD];
+  int start[TRIAL_MAXD + 1];
+  uint64_t seed, counter0;
+  int trials;
+  int* out_tok;  // [trials][depth + 1]: accepted tokens, then the bonus
+  int* out_n;    // [trials]
+};
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
+  return v;
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
+  return v;
+}
+__device__ __forceinline__ KeyIdx wave_argmax(float k, int i) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float ok = __shfl_xor(k, o);
+    const int oi = __shfl_xor(i, o);
+    if (better(ok, oi, k, i)) {
+      k = ok;
+      i = oi;
+    }
+  }
+  return KeyIdx{k, i};
+}
+
+// q_{j-1}(y) as statej_kernel computes it: rejected tokens have no draft mass left.
+__device__ __forceinline__ float trial_qprev(float q0, int y, int j, const float* zq, const int* rej) {
+  if (j - 1 <= 0) return q0;
+  bool r = false;
+  for (int u = 0; u < j - 1; ++u) r |= rej[u] == y;
+  return r ? 0.f : q0 / zq[j - 1];
+}
+
+__global__ __launch_bounds__(256) void accept_trials_kernel(TrialArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int trial = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (trial >= a.trials) return;  // whole wave
+  const uint64_t ctr = a.counter0 + (uint64_t)trial;
+  const Rng rng{(uint32_t)a.seed, (uint32_t)(a.seed >> 32), (uint32_t)ctr, (uint32_t)((ctr >> 32) << 8)};
+  int cur = -1, lv = 0, f = 0, n_out = 0, bonus = 0;
+  for (;;) {
+    const int r = cur + 1;
+    const float* p = a.P + (size_t)r * a.ldp;
+    const float* q = a.Q + (size_t)r * a.ldq;
+    const int* cs = a.cols + a.off[r];
+    const int ns = a.off[r + 1] - a.off[r];
+    int rej[SMP_MAXK];
+    float zr[SMP_MAXK + 1], zq[SMP_MAXK + 1];
+    zr[0] = 0.f;
+    zq[0] = 1.f;
+    int j = 0, chosen = -1;
+    if (lv < a.depth) {
+      const int k = a.branch[lv];
+      // q0's mass and support count, then min(k, support) children by Gumbel top-k
+      double s0 = 0.0;
+      int supp = 0;
+      for (int e = lane; e < ns; e += 64) {
+        const float qv = q[cs[e]];
+        s0 += (double)qv;
+        supp += qv > 0.f;
+      }
+      s0 = wave_sum_d(s0);
+      supp = wave_sum_i(supp);
+      int take = min(k, supp);
+      int tok[SMP_MAXK];
+      for (int c = 0; c < take; ++c) {
+        float bk = -1.f;
+        int bi = NO_IDX;
+        for (int e = lane; e < ns; e += 64) {
+          const int y = cs[e];
+          const float qv = q[y];
+          if (!(qv > 0.f)) continue;
+          bool taken = false;
+          for (int u = 0; u < c; ++u) taken |= tok[u] == y;
+          if (taken) continue;
+          const U4 rb = rng_block(rng, (uint32_t)(y >> 2), (uint32_t)f | ((uint32_t)lv << 16), TAG_PROPOSE);
+          const float key = qv / exp1_from_bits(u4_get(rb, y & 3));
+          if (better(key, y, bk, bi)) {
+            bk = key;
+            bi = y;
+          }
+        }
+        const KeyIdx w = wave_argmax(bk, bi);
+        if (w.idx == NO_IDX) {  // no candidate left (cannot happen below the support count)
+          take = c;
+          break;
+        }
+        tok[c] = w.idx;
+      }
+      // the walk over the children in draw order (sample_walk_kernel)
+      double zqd = s0;
+      for (int i = 0; i < take; ++i) {
+        const int x = tok[i];
+        const float q0x = q[x];
+        const float pj = chain_p(p[x], q0x, x, j, zr, zq, rej);
+        const float qj = j == 0 ? q0x : q0x / zq[j];
+        const double u = uniform_from_bits(rng_block(rng, (uint32_t)j, (uint32_t)r, TAG_ACCEPT).x);
+        if (u < (double)fminf(1.f, pj / qj)) {
+          chosen = i;
+          break;
+        }
+        rej[j] = x;
+        ++j;
+        zqd -= (double)q0x;
+        zq[j] = (float)zqd;
+        // residual mass of state j (statej_kernel with its first j children rejected)
+        double z = 0.0;
+        for (int e = lane; e < ns; e += 64) {
+          const int y = cs[e];
+          const float pprev = chain_p(p[y], q[y], y, j - 1, zr, zq, rej);
+          z += (double)fmaxf(pprev - trial_qprev(q[y], y, j, zq, rej), 0.f);
+        }
+        z = wave_sum_d(z);
+        zr[j] = z > 0.0 ? (float)z : 0.f;
+        if (j >= supp) break;  // no draft mass left
+      }
+      if (chosen >= 0) {
+        const int fc = f * k + chosen;  // in-level index of the accepted child
+        if (lane == 0) a.out_tok[(size_t)trial * (a.depth + 1) + n_out] = tok[chosen];
+        ++n_out;
+        cur = a.start[lv] + fc;
+        f = fc;
+        ++lv;
+        continue;
+      }
+    }
+    // bonus: the categorical draw from the last state with residual mass (state 0 at a leaf)
+    int jj = j;
+    while (jj > 0 && !(zr[jj] > 0.f)) --jj;
+    float bk = -1.f;
+    int bi = NO_IDX;
+    for (int e = lane; e < ns; e += 64) {
+      const int y = cs[e];
+      float w;
+      if (jj == 0) {
+        w = p[y];
+      } else {
+        const float pprev = chain_p(p[y], q[y], y, jj - 1, zr, zq, rej);
+        w = fmaxf(pprev - trial_qprev(q[y], y, jj, zq, rej), 0.f);
+      }
+      if (!(w > 0.f)) continue;
+      const float key = w / exp1_from_bits(u4_get(rng_block(rng, (uint32_t)(y >> 2), 0u, TAG_BONUS), y & 3));
+      if (better(key, y, bk, bi)) {
+        bk = key;
+        bi = y;
+      }
+    }
+    const KeyIdx b = wave_argmax(bk, bi);
+    bonus = b.idx == NO_IDX ? 0 : b.idx;
+    break;
+  }
+  if (lane == 0) {
+    a.out_tok[(size_t)trial * (a.depth + 1) + n_out] = bonus;
+    a.out_n[trial] = n_out + 1;
+  }
+}
+
 }  // namespace ssd
 
 using namespace ssd;
@@ -1086,3 +1273,35 @@ SSD_API int ssd_accept_sample(const SsdTree* tree, const float* P, int64_t ldp, 
                      root_token);
   return check_launch("accept_sample");
 }
+
+// Batched acceptance trials (accept_trials_kernel): trials independent rounds over fixed per-node
+// distributions P/Q ([rows][ld] fp32, rows >= 1 + nodes of the unpruned tree given by branch[0 ..
+// depth)), support lists cols/col_off (CSR over rows: ascending columns where P or Q > 0).
+SSD_API int ssd_accept_sample_trials(const float* P, int64_t ldp, const float* Q, int64_t ldq, int rows,
+                                     const int32_t* cols, const int32_t* col_off, int depth, const int32_t* branch,
+                                     uint64_t seed, uint64_t counter0, int trials, int32_t* out_tokens,
+                                     int32_t* out_n, hipStream_t stream) {
+  if (!P || !Q || !cols || !col_off || !branch || !out_tokens || !out_n)
+    return set_error(SSD_EINVAL, "accept_trials: null pointer");
+  if (depth < 1 || depth > TRIAL_MAXD) return set_error(SSD_ERANGE, "accept_trials: depth %d not in [1, %d]", depth, TRIAL_MAXD);
+  if (trials < 0 || ldp % 4 || ldq % 4 || rows < 1) return set_error(SSD_EINVAL, "accept_trials: bad shape");
+  TrialArgs a{};
+  a.P = P; a.ldp = ldp; a.Q = Q; a.ldq = ldq; a.cols = cols; a.off = col_off; a.depth = depth;
+  int64_t level = 1, nodes = 0;
+  for (int d = 0; d < depth; ++d) {
+    if (branch[d] < 1 || branch[d] > SMP_MAXK)
+      return set_error(SSD_ERANGE, "accept_trials: branch[%d]=%d not in [1, %d]", d, branch[d], SMP_MAXK);
+    a.branch[d] = branch[d];
+    a.start[d] = (int)nodes;
+    level *= branch[d];
+    nodes += level;
+    if (nodes > (1 << 20)) return set_error(SSD_ERANGE, "accept_trials: tree too large");
+  }
+  a.start[depth] = (int)nodes;
+  if (rows < 1 + nodes) return set_error(SSD_EINVAL, "accept_trials: %d rows for a tree of %lld nodes", rows, (long long)nodes);
+  a.seed = seed; a.counter0 = counter0; a.trials = trials; a.out_tok = out_tokens; a.out_n = out_n;
+  if (trials == 0) return SSD_OK;
+  hipLaunchKernelGGL(accept_trials_kernel, dim3((trials + 3) / 4), dim3(256), 0, stream, a);
+  return check_launch("accept_trials");
+}
+

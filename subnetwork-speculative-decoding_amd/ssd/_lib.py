@@ -131,6 +131,7 @@ _PROTOS = {
     "ssd_sample_rows": (I32, [P, I64, I32, I32, U64, U64, P, P, I64, P]),
     "ssd_accept_sample": (I32, [C.POINTER(SsdTree), P, I64, P, I64, I32, I32, I32, U64, U64, P, I64, I32, P, P, P, P,
                                 P]),
+    "ssd_accept_sample_trials": (I32, [P, I64, P, I64, I32, P, P, I32, C.POINTER(C.c_int32), U64, U64, I32, P, P, P]),
     "ssd_forward": (I32, [C.POINTER(SsdModel), C.POINTER(SsdPlan), C.POINTER(SsdBuffers), C.POINTER(SsdRows), I32,
                           I32, I32, I32, I32, P]),
     "ssd_prefill_gemm_bf16": (I32, [P, I64, I32, P, I32, I32, I32, F32, I32, P, I64, P, I64,

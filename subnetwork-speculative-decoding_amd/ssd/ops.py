@@ -502,6 +502,26 @@ def sample_rows(probs, rows, V, seed, counter, out_tok, ws=None):
     return out_tok
 
 
+def accept_sample_trials(P, Q, rows, branch, seed, counter0, trials, out_tokens, out_n):
+    """ssd_accept_sample_trials: ``trials`` independent proposal + acceptance rounds of the
+    unpruned tree ``branch`` over the fixed per-node rows of P and Q (row 0 the root); the
+    per-row supports are derived here (columns where P or Q is nonzero)."""
+    _check(P, "P", torch.float32); _check(Q, "Q", torch.float32)
+    _check(out_tokens, "out_tokens", torch.int32); _check(out_n, "out_n", torch.int32)
+    depth = len(branch)
+    _len(out_tokens, "out_tokens", trials * (depth + 1)); _len(out_n, "out_n", trials)
+    nz = (P[:rows] > 0) | (Q[:rows] > 0)
+    counts = nz.sum(1)
+    off = torch.zeros(rows + 1, dtype=torch.int32, device=P.device)
+    off[1:] = torch.cumsum(counts, 0).to(torch.int32)
+    cols = torch.nonzero(nz)[:, 1].to(torch.int32).contiguous()  # row-major: ascending within a row
+    br = (ctypes.c_int32 * depth)(*branch)
+    _lib.call("ssd_accept_sample_trials", P.data_ptr(), P.stride(0), Q.data_ptr(), Q.stride(0), rows,
+              cols.data_ptr(), off.data_ptr(), depth, br, int(seed), int(counter0), int(trials), out_tokens.data_ptr(),
+              out_n.data_ptr(), stream())
+    torch.cuda.current_stream().synchronize()  # cols / off are temporaries of this call
+
+
 def accept_sample(tree_struct, P, Q, V, rows, max_kids, seed, counter, committed, result, keep_src, n_keep,
                   root_token, ws=None):
     """ssd_accept_sample: speculative-sampling walk over the finalized tree (P: warped target rows,
