@@ -225,7 +225,8 @@ typedef struct SsdTree {
 } SsdTree;
 
 /* Per-row inputs of one forward: token ids, rotary positions, cache slots, and the
- * attention rows (prefix, depth, anc[cap][32]). */
+ * attention rows (prefix, depth, anc[cap][32]); with kv_off, each row reads and writes the KV
+ * arena of its own sequence (every sequence's arena has the layout and capacity of SsdBuffers'). */
 typedef struct SsdRows {
   int32_t* ids;
   int32_t* pos;
@@ -234,6 +235,8 @@ typedef struct SsdRows {
   int32_t* depth;
   int32_t* anc;
   int32_t cap;
+  const int64_t* kv_off;  /* [cap] element offset of each row's sequence in the KV arenas (rows of several
+                             sequences in one forward: batched generation), or NULL (one sequence) */
 } SsdRows;
 
 int ssd_tree_limits(int32_t* out3); /* host: {node capacity, max depth, max ancestors per row} */

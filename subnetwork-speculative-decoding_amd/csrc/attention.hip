@@ -45,6 +45,7 @@ struct AttnArgs {
   const int* prefix;  // [M]
   const int* depth;   // [M]
   const int* anc;     // [M, ATT_MAXD]
+  const int64_t* kv_off;  // [M] element offset of token t's sequence in the K / V arenas, or null
   int p_min, l_max;
   float scale_log2;
   float* ws;  // O [kv_heads][M*rep][n_sb_cap][hd], then (m, l) [kv_heads][M*rep][n_sb_cap]
@@ -104,10 +105,11 @@ __device__ __forceinline__ int logical_slot(int jpos, int P, int L, const int* a
 // afterwards): a load under a per-lane condition compiles to a branch after which the compiler
 // waits for the value, serialising the loads.
 template <int HD>
-__device__ __forceinline__ void load_virtual_frags(Frags<HD>& f, const AttnArgs& a, int kvh, int key0, int P,
-                                                   int L, const int* anc_t, int lane) {
+__device__ __forceinline__ void load_virtual_frags(Frags<HD>& f, const AttnArgs& a, const bf16_t* K,
+                                                   const bf16_t* Vt, int kvh, int key0, int P, int L,
+                                                   const int* anc_t, int lane) {
   const int i = lane & 15, g = lane >> 4;
-  const bf16_t* kb = a.K + (size_t)kvh * a.max_len * HD;
+  const bf16_t* kb = K + (size_t)kvh * a.max_len * HD;
 #pragma unroll
   for (int kt = 0; kt < 4; ++kt) {
     const int slot = logical_slot(key0 + perm_key(kt, i), P, L, anc_t, a.max_len);
@@ -116,7 +118,7 @@ __device__ __forceinline__ void load_virtual_frags(Frags<HD>& f, const AttnArgs&
 #pragma unroll
     for (int ks = 0; ks < Frags<HD>::KS; ++ks) f.k[kt][ks] = *(const u32x4_t*)(kb + k_off(sl, ks * 32 + g * 8, HD)) & keep;
   }
-  const bf16_t* vb = a.Vt + (size_t)kvh * HD * a.max_len;
+  const bf16_t* vb = Vt + (size_t)kvh * HD * a.max_len;
   const int lim = P < a.max_len ? P : (int)a.max_len;  // prefix positions that exist
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
@@ -299,7 +301,14 @@ __global__ __launch_bounds__(256, 2) void attn_partial_kernel(AttnArgs a) {
   __shared__ AttnLds<HD> lds;
   __shared__ int s_anc[ATT_MAXD];
   int r_begin, r_end, P = 0, L = 0, anc_v = 0;
+  const bf16_t* Kt = a.K;  // this token's sequence (tail workgroups of a multi-sequence call)
+  const bf16_t* Vtt = a.Vt;
   if (tail) {
+    if (a.kv_off) {
+      const int64_t off = a.kv_off[tok];
+      Kt += off;
+      Vtt += off;
+    }
     anc_v = a.anc[(size_t)tok * ATT_MAXD + (threadIdx.x & (ATT_MAXD - 1))];
     P = a.prefix[tok];
     L = P + min(max(a.depth[tok], 0), ATT_MAXD);
@@ -354,7 +363,7 @@ __global__ __launch_bounds__(256, 2) void attn_partial_kernel(AttnArgs a) {
     uint32_t av[AIT];
     const int n_av = (L - P) * HD;  // (ancestor, d) pairs to stage
     if (patch) {
-      const bf16_t* vb = a.Vt + (size_t)kvh * HD * a.max_len;
+      const bf16_t* vb = Vtt + (size_t)kvh * HD * a.max_len;
 #pragma unroll
       for (int it = 0; it < AIT; ++it) {
         if (it * 256 >= n_av) break;  // uniform
@@ -368,7 +377,7 @@ __global__ __launch_bounds__(256, 2) void attn_partial_kernel(AttnArgs a) {
     }
     have = key0 < L;
     if (have) {
-      load_virtual_frags<HD>(f, a, kvh, key0, P, L, s_anc, lane);
+      load_virtual_frags<HD>(f, a, Kt, Vtt, kvh, key0, P, L, s_anc, lane);
       bits = 0;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
@@ -531,7 +540,8 @@ static int launch_attn(AttnArgs a, bf16_t* out, int64_t ldo, hipStream_t s) {
   const int n_sb = (a.l_max + SBK - 1) / SBK;
   if (n_sb > a.n_sb_cap) return set_error(SSD_ERANGE, "attention: length %d needs %d superblocks > workspace %d",
                                           a.l_max, n_sb, a.n_sb_cap);
-  a.n_full = a.p_min / SBK < n_sb ? a.p_min / SBK : n_sb;
+  // rows of several sequences share no keys: every superblock is built per token
+  a.n_full = a.kv_off ? 0 : (a.p_min / SBK < n_sb ? a.p_min / SBK : n_sb);
   a.n_tail_sb = n_sb - a.n_full;
   a.tail_slots = (a.n_tail_sb * a.kv_heads + 7) / 8 * 8 * a.M;
   const uint32_t rep = (uint32_t)(a.heads / a.kv_heads);
@@ -577,6 +587,16 @@ SSD_API int ssd_tree_attention_bf16(const uint16_t* q, int64_t ldq, int M, int h
                                     const int32_t* prefix, const int32_t* depth, const int32_t* anc, int p_min,
                                     int l_max, float scale, float* ws, int64_t ws_floats, uint16_t* out,
                                     int64_t ldo, hipStream_t stream) {
+  return ssd::tree_attention(q, ldq, M, heads, kv_heads, head_dim, k_cache, vt_cache, max_len, prefix, depth, anc,
+                             nullptr, p_min, l_max, scale, ws, ws_floats, out, ldo, stream);
+}
+
+// Tree attention whose rows may belong to several sequences: row t's K / V are at kv_off[t]
+// elements past k_cache / vt_cache (same layout and capacity for every sequence).
+int ssd::tree_attention(const uint16_t* q, int64_t ldq, int M, int heads, int kv_heads, int head_dim,
+                        const uint16_t* k_cache, const uint16_t* vt_cache, int64_t max_len, const int32_t* prefix,
+                        const int32_t* depth, const int32_t* anc, const int64_t* kv_off, int p_min, int l_max,
+                        float scale, float* ws, int64_t ws_floats, uint16_t* out, int64_t ldo, hipStream_t stream) {
   if (!q || !k_cache || !vt_cache || !prefix || !depth || !anc || !ws || !out)
     return set_error(SSD_EINVAL, "attention: null pointer");
   if (M <= 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads)
@@ -592,6 +612,7 @@ SSD_API int ssd_tree_attention_bf16(const uint16_t* q, int64_t ldq, int M, int h
   AttnArgs a{};
   a.Q = q; a.ldq = ldq; a.K = k_cache; a.Vt = vt_cache; a.max_len = max_len;
   a.M = M; a.heads = heads; a.kv_heads = kv_heads; a.prefix = prefix; a.depth = depth; a.anc = anc;
+  a.kv_off = kv_off;
   a.p_min = p_min; a.l_max = l_max; a.scale_log2 = scale * 1.4426950408889634f; a.ws = ws;
   a.n_sb_cap = (int)n_sb_cap;
   switch (head_dim) {

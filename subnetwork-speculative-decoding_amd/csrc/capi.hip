@@ -26,7 +26,7 @@ int check_launch(const char* what) {
 
 SSD_API const char* ssd_last_error(void) { return ssd::g_err; }
 
-SSD_API int ssd_abi_version(void) { return 2; }
+SSD_API int ssd_abi_version(void) { return 3; }
 
 #ifndef SSD_BUILD_HASH
 #define SSD_BUILD_HASH "unknown"

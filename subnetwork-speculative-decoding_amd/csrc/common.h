@@ -101,6 +101,18 @@ __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x));
 __device__ __forceinline__ float gelu_f(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f)); }
 __device__ __forceinline__ float relu_f(float x) { return x > 0.f ? x : 0.f; }
 
+// Entry points with per-row KV arena offsets (element offset of each row's sequence, or null), for
+// forwards whose rows belong to several sequences (batched generation); the exported
+// ssd_gemm_qkv_rope_bf16 / ssd_tree_attention_bf16 are these with null offsets.
+int qkv_rope_gemm(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int K, float norm_eps, int heads,
+                  int kv_heads, int head_dim, const uint16_t* cos_tab, const uint16_t* sin_tab, int64_t rope_rows,
+                  const int32_t* row_pos, const int32_t* row_slot, const int64_t* row_kv_off, uint16_t* Q,
+                  int64_t ldq, uint16_t* k_cache, uint16_t* vt_cache, int64_t max_len, hipStream_t stream);
+int tree_attention(const uint16_t* q, int64_t ldq, int M, int heads, int kv_heads, int head_dim,
+                   const uint16_t* k_cache, const uint16_t* vt_cache, int64_t max_len, const int32_t* prefix,
+                   const int32_t* depth, const int32_t* anc, const int64_t* kv_off, int p_min, int l_max, float scale,
+                   float* ws, int64_t ws_floats, uint16_t* out, int64_t ldo, hipStream_t stream);
+
 enum Act { ACT_NONE = 0, ACT_SILU = 1, ACT_GELU = 2, ACT_RELU = 3 };
 
 __device__ __forceinline__ float apply_act(int act, float x) {

@@ -92,12 +92,12 @@ SSD_API int ssd_forward(const SsdModel* md, const SsdPlan* plan, const SsdBuffer
     if (plan->pre_bridge && plan->pre_bridge[st] && (rc = f.bridge(plan->pre_bridge[st]))) return rc;
     uint16_t* kc = buf->k_arena + li * layer_elems;
     uint16_t* vt = buf->vt_arena + li * layer_elems;
-    if ((rc = ssd_gemm_qkv_rope_bf16(buf->h, d, m, L.wqkv, d, md->eps, H, KV, hd, md->cos, md->sin, md->rope_rows,
-                                     rows->pos, rows->slot, buf->q, qdim, kc, vt, buf->cache_cap, s)))
+    if ((rc = qkv_rope_gemm(buf->h, d, m, L.wqkv, d, md->eps, H, KV, hd, md->cos, md->sin, md->rope_rows, rows->pos,
+                            rows->slot, rows->kv_off, buf->q, qdim, kc, vt, buf->cache_cap, s)))
       return rc;
-    if ((rc = ssd_tree_attention_bf16(buf->q, qdim, m, H, KV, hd, kc, vt, buf->cache_cap, rows->prefix, rows->depth,
-                                      rows->anc, p_min, l_max, md->attn_scale, buf->attn_ws, buf->attn_ws_floats,
-                                      buf->attn, qdim, s)))
+    if ((rc = tree_attention(buf->q, qdim, m, H, KV, hd, kc, vt, buf->cache_cap, rows->prefix, rows->depth, rows->anc,
+                             rows->kv_off, p_min, l_max, md->attn_scale, buf->attn_ws, buf->attn_ws_floats, buf->attn,
+                             qdim, s)))
       return rc;
     if ((rc = f.residual(buf->attn, qdim, L.wo, (int)qdim, nullptr))) return rc;
     if (md->mlp_fused) {

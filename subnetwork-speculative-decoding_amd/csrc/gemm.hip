@@ -72,11 +72,13 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
   const int Mv = a.M < CT * 16 ? a.M : CT * 16;
   const bool qkv_pre = EPI == EPI_QKV && 8 * Mv <= 64 * KS;
   int pre_m = 0, pre_r = 0, pre_slot = 0, pre_pos = 0;
+  int64_t pre_off = 0;
   if constexpr (EPI == EPI_QKV) {
     pre_m = min((int)threadIdx.x >> 3, Mv - 1);
     pre_r = threadIdx.x & 7;
     pre_slot = a.row_slot[pre_m];
     pre_pos = min(max(a.row_pos[pre_m], 0), (int)a.rope_rows - 1);
+    if (a.row_kv_off) pre_off = a.row_kv_off[pre_m];
   }
 
   // plain store: thread t owns output (token t / 16, tile row t % 16) of every sub-tile when the
@@ -221,7 +223,7 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
         const int nb = tile * NSUB + s;
         if (nb * 16 < a.N && (int)threadIdx.x < 8 * Mv)
           epi_qkv_pre(a, qkv_tile(a, nb), pre_m, pre_r, val(pre_r, pre_m), val(pre_r + 8, pre_m), pre_slot,
-                      pre_cs[s], pre_sn[s]);
+                      pre_cs[s], pre_sn[s], pre_off);
         continue;
       }
     }
@@ -784,6 +786,16 @@ SSD_API int ssd_gemm_qkv_rope_bf16(const uint16_t* X, int64_t ldx, int M, const 
                                    const int32_t* row_slot,
                                    uint16_t* Q, int64_t ldq, uint16_t* k_cache, uint16_t* vt_cache,
                                    int64_t max_len, hipStream_t stream) {
+  return ssd::qkv_rope_gemm(X, ldx, M, W_packed, K, norm_eps, heads, kv_heads, head_dim, cos_tab, sin_tab, rope_rows,
+                            row_pos, row_slot, nullptr, Q, ldq, k_cache, vt_cache, max_len, stream);
+}
+
+// The q/k/v GEMM with per-row KV arena offsets (rows of several sequences in one launch).
+int ssd::qkv_rope_gemm(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int K, float norm_eps,
+                       int heads, int kv_heads, int head_dim, const uint16_t* cos_tab, const uint16_t* sin_tab,
+                       int64_t rope_rows, const int32_t* row_pos, const int32_t* row_slot, const int64_t* row_kv_off,
+                       uint16_t* Q, int64_t ldq, uint16_t* k_cache, uint16_t* vt_cache, int64_t max_len,
+                       hipStream_t stream) {
   const int N = (heads + 2 * kv_heads) * head_dim;
   int rc = check_common(X, ldx, M, W_packed, N, K);
   if (rc) return rc;
@@ -797,7 +809,7 @@ SSD_API int ssd_gemm_qkv_rope_bf16(const uint16_t* X, int64_t ldx, int M, const 
   a.Y = Q; a.ldy = ldq; a.heads = heads; a.kv_heads = kv_heads; a.head_dim = head_dim;
   if (rope_rows <= 0) return set_error(SSD_EINVAL, "qkv: empty rope table");
   a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.rope_rows = rope_rows; a.row_pos = row_pos; a.row_slot = row_slot;
-  a.k_cache = k_cache; a.vt_cache = vt_cache; a.max_len = max_len;
+  a.k_cache = k_cache; a.vt_cache = vt_cache; a.max_len = max_len; a.row_kv_off = row_kv_off;
   a.norm_eps = norm_eps > 0.f ? norm_eps : 0.f;
   return launch_gemm<EPI_QKV>(a, stream);
 }

@@ -36,6 +36,7 @@ struct GemmArgs {
   bf16_t* k_cache;        // this layer: kv_heads x (max_len x head_dim) in the block layout (k_off)
   bf16_t* vt_cache;       // this layer: kv_heads x (max_len x head_dim) in the block layout (v_off)
   int64_t max_len;
+  const int64_t* row_kv_off;  // [M] element offset of row m's sequence in the cache arena, or null
   // RMSNorm of the rows of X folded into the GEMM (> 0: X is the residual stream h; the norm's
   // weight is already folded into W's columns; each output is scaled by rsqrt(mean(h^2) + eps))
   float norm_eps;
@@ -87,8 +88,9 @@ __device__ __forceinline__ void epi_qkv(const GemmArgs& a, int nb, int m, int r,
   const float xlo = rbf(vlo), xhi = rbf(vhi);
   const int slot = a.row_slot[m];
   if (region != 0 && (slot < 0 || slot >= a.max_len)) return;  // never write outside the cache
+  const int64_t off = a.row_kv_off ? a.row_kv_off[m] : 0;
   if (region == 2) {
-    bf16_t* vt = a.vt_cache + (size_t)head * hd * a.max_len;
+    bf16_t* vt = a.vt_cache + off + (size_t)head * hd * a.max_len;
     vt[v_off(slot, dlo, hd)] = f2bf(xlo);
     vt[v_off(slot, dhi, hd)] = f2bf(xhi);
     return;
@@ -103,7 +105,7 @@ __device__ __forceinline__ void epi_qkv(const GemmArgs& a, int nb, int m, int r,
     q[dlo] = f2bf(olo);
     q[dhi] = f2bf(ohi);
   } else {
-    bf16_t* kc = a.k_cache + (size_t)head * a.max_len * hd;
+    bf16_t* kc = a.k_cache + off + (size_t)head * a.max_len * hd;
     kc[k_off(slot, dlo, hd)] = f2bf(olo);
     kc[k_off(slot, dhi, hd)] = f2bf(ohi);
   }
@@ -126,13 +128,13 @@ __device__ __forceinline__ QkvTile qkv_tile(const GemmArgs& a, int nb) {
 // epi_qkv with the row's cache slot and rotary cos/sin already loaded (prefetched before the
 // main loop, so the epilogue issues no dependent loads).
 __device__ __forceinline__ void epi_qkv_pre(const GemmArgs& a, const QkvTile& q, int m, int r, float vlo,
-                                            float vhi, int slot, float cs, float sn) {
+                                            float vhi, int slot, float cs, float sn, int64_t kv_off) {
   const int hd = a.head_dim, half = hd >> 1;
   const int dlo = q.p * 8 + r, dhi = dlo + half;
   const float xlo = rbf(vlo), xhi = rbf(vhi);
   if (q.region != 0 && (slot < 0 || slot >= a.max_len)) return;  // never write outside the cache
   if (q.region == 2) {
-    bf16_t* vt = a.vt_cache + (size_t)q.head * hd * a.max_len;
+    bf16_t* vt = a.vt_cache + kv_off + (size_t)q.head * hd * a.max_len;
     vt[v_off(slot, dlo, hd)] = f2bf(xlo);
     vt[v_off(slot, dhi, hd)] = f2bf(xhi);
     return;
@@ -144,7 +146,7 @@ __device__ __forceinline__ void epi_qkv_pre(const GemmArgs& a, const QkvTile& q,
     qo[dlo] = f2bf(olo);
     qo[dhi] = f2bf(ohi);
   } else {
-    bf16_t* kc = a.k_cache + (size_t)q.head * a.max_len * hd;
+    bf16_t* kc = a.k_cache + kv_off + (size_t)q.head * a.max_len * hd;
     kc[k_off(slot, dlo, hd)] = f2bf(olo);
     kc[k_off(slot, dhi, hd)] = f2bf(ohi);
   }

@@ -194,7 +194,7 @@ __global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(GemmArgs a, int gr
             for (int e = 0; e < 4; ++e) {
               const int pr = 4 * g + e;
               const size_t at = (size_t)pos * half + q.p * 8 + pr;
-              epi_qkv_pre(a, q, m, pr, lo[e], hi[e], pos0 + m, bf2f(a.cos_tab[at]), bf2f(a.sin_tab[at]));
+              epi_qkv_pre(a, q, m, pr, lo[e], hi[e], pos0 + m, bf2f(a.cos_tab[at]), bf2f(a.sin_tab[at]), 0);
             }
           }
         }

@@ -43,7 +43,8 @@ class SsdTree(C.Structure):
 
 
 class SsdRows(C.Structure):
-    _fields_ = [(n, P) for n in ("ids", "pos", "slot", "prefix", "depth", "anc")] + [("cap", C.c_int32)]
+    _fields_ = [(n, P) for n in ("ids", "pos", "slot", "prefix", "depth", "anc")] + [("cap", C.c_int32),
+                                                                                      ("kv_off", P)]
 
 
 class SsdLayerW(C.Structure):
@@ -141,7 +142,7 @@ _PROTOS = {
 }
 
 EXPORTED = tuple(_PROTOS)
-ABI_VERSION = 2  # descriptor struct layouts (SsdModel.mlp_fused, SsdBuffers.sync)
+ABI_VERSION = 3  # descriptor struct layouts (SsdModel.mlp_fused, SsdBuffers.sync, SsdRows.kv_off)
 
 _lib = None
 

@@ -87,13 +87,11 @@ class _Phases:
         self._pending = self._pending[-1:] if self._pending and self._pending[-1][0] is not None else []
 
 
-def _prefill(target: SubnetworkDraftModel, ids: list, cache: KVCache, ws, out_dev: torch.Tensor,
-             sampler: Optional[Sampler] = None) -> None:
-    """Target forward over the prompt and the first token into out_dev[0]: the first-index argmax
-    of the last row, or with ``sampler`` a draw from its warped distribution with counter 0
-    (reference speculative.py:149-151, :81-84). Prompts of at least PREFILL_MIN tokens run on the
-    MFMA prefill kernels (chunks of PREFILL_CHUNK rows), shorter ones as causal rows through the
-    decode forward (chunks of 64)."""
+def _prefill_logits(target: SubnetworkDraftModel, ids: list, cache: KVCache, ws) -> torch.Tensor:
+    """Target forward over the prompt into ``cache`` (reference speculative.py:149-151); returns the
+    last row's logits (a [1, V] view of a buffer the next forward reuses). Prompts of at least
+    PREFILL_MIN tokens run on the MFMA prefill kernels (chunks of PREFILL_CHUNK rows), shorter
+    ones as causal rows through the decode forward (chunks of 64)."""
     dev = target.model.device
     past = cache.get_seq_length()
     q = len(ids)
@@ -117,6 +115,14 @@ def _prefill(target: SubnetworkDraftModel, ids: list, cache: KVCache, ws, out_de
             torch.cuda.current_stream().synchronize()  # the pinned staging buffer is reused next chunk
     ws.check_faults()
     cache.advance(q)
+    return logits
+
+
+def _prefill(target: SubnetworkDraftModel, ids: list, cache: KVCache, ws, out_dev: torch.Tensor,
+             sampler: Optional[Sampler] = None) -> None:
+    """Prefill and the first token into out_dev[0]: the first-index argmax of the last row, or with
+    ``sampler`` a draw from its warped distribution with counter 0 (reference speculative.py:81-84)."""
+    logits = _prefill_logits(target, ids, cache, ws)
     if sampler is not None:
         sampler.draw(logits, out_dev, counter=0)
     else:

@@ -103,6 +103,12 @@ class Rows:
         self.struct = _lib.SsdRows(self.ids.data_ptr(), self.pos.data_ptr(), self.slot.data_ptr(),
                                    self.prefix.data_ptr(), self.depth.data_ptr(), self.anc.data_ptr(), cap)
 
+    def set_kv_offsets(self, offsets: Optional[torch.Tensor]) -> None:
+        """Per-row element offsets of each row's sequence in the KV arenas (int64 device tensor of
+        length >= rows, kept alive here), or None: rows of several sequences in one forward."""
+        self.kv_off = offsets
+        self.struct.kv_off = offsets.data_ptr() if offsets is not None else None
+
     def view(self, off: int) -> "_RowsView":
         """Rows [off, cap) as a forward's rows (pointer offsets, no copy)."""
         v = _RowsView(self.ids[off:], self.pos[off:], self.slot[off:], self.prefix[off:], self.depth[off:],
