@@ -124,6 +124,12 @@ def kernel_figures(gen, sess) -> dict:
     fig("gemm_qkv_rope", time_launches(qkv, nl), n_qkv * s.hidden * 2 + m * s.hidden * 2 + m * n_qkv * 2)
 
     h_scratch = ws.h.clone()  # the residual projections update h in place
+    qdim = s.heads * s.head_dim
+
+    def o_proj(i):
+        ops.gemm_residual(ws.attn, m, L[i].wo, s.hidden, qdim, h_scratch, ws.part)
+
+    fig("o_proj", time_launches(o_proj, nl), s.hidden * qdim * 2 + m * qdim * 2 + 2 * m * s.hidden * 2)
     sp = ops.gemm_splits(s.hidden, s.inter)
     if model.mlp_fused:
         # gate/up + SwiGLU + down + residual in one launch: weights, h read and written, act and
@@ -164,6 +170,65 @@ def kernel_figures(gen, sess) -> dict:
     fig("kv_compact", time_launches(compact, 8), 2 * n * s.layers * 2 * s.kv_heads * s.head_dim * 2)
     out["kv_compact"]["rows"] = n
     return out
+
+
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+
+
+def prefill_figures(target, ids: list, reps: int = 3) -> dict:
+    """The prompt's target forward alone (ssd_prefill: MFMA GEMMs + causal flash attention), best
+    of ``reps`` into fresh caches: ms, achieved TFLOP/s (2 flop per weight per token for the
+    projections, 4 * hd per (query, key) pair for attention, the causal half) and the fraction of
+    the MI355X dense bf16 MFMA peak."""
+    import torch
+
+    from ssd.engine.speculative import _prefill_logits
+
+    s = target.model.shape
+    P = len(ids)
+    ws = target.workspace()
+    best = float("inf")
+    for _ in range(reps):
+        cache = target.new_cache(P + 64)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        _prefill_logits(target, ids, cache, ws)
+        torch.cuda.synchronize()
+        best = min(best, time.perf_counter() - t0)
+        del cache
+    per_layer = (s.hidden * (s.heads + 2 * s.kv_heads) * s.head_dim + s.hidden * s.heads * s.head_dim
+                 + 3 * s.hidden * s.inter)
+    flops = 2 * P * s.layers * per_layer + 2 * s.vocab * s.hidden + 4 * (P * (P + 1) / 2) * s.heads * s.head_dim * s.layers
+    tf = flops / best / 1e12
+    return {"tokens": P, "ms": round(1000 * best, 3), "tflops": round(tf, 1),
+            "mfma_frac": round(tf / BF16_MFMA_PEAK_TFLOPS, 4), "flops": flops}
+
+
+def batch_generation_figures(target, batch: int, prompt: int, new: int) -> dict:
+    """Greedy batched generation (ssd.data.generate_selfdistill.generate_batch): ``batch`` prompts
+    of ``prompt`` uniform random tokens, ``new`` tokens each; decode tokens/s over the whole batch
+    (prefill of the batch timed separately as a one-token run)."""
+    import torch
+
+    from ssd.data.generate_selfdistill import generate_batch
+
+    V = target.model.shape.vocab
+    g = torch.Generator().manual_seed(11)
+    prompts = [torch.randint(0, V, (prompt,), generator=g).tolist() for _ in range(batch)]
+    generate_batch(target, prompts, 2, {-1}, 0.0, 1.0, 0)  # warm-up
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    generate_batch(target, prompts, 1, {-1}, 0.0, 1.0, 0)
+    torch.cuda.synchronize()
+    t_pre = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    rows = generate_batch(target, prompts, new, {-1}, 0.0, 1.0, 0)
+    torch.cuda.synchronize()
+    t_all = time.perf_counter() - t0
+    toks = sum(len(r) for r in rows)
+    dec = max(t_all - t_pre, 1e-9)
+    return {"batch": batch, "prompt_tokens": prompt, "new_tokens": new, "seconds": round(t_all, 4),
+            "decode_tokens_per_s": round((toks - batch) / dec, 1), "ms_per_step": round(1000 * dec / (new - 1), 4)}
 
 
 def load_traffic(kernel_key: str):
@@ -266,6 +331,10 @@ def main() -> None:
     ap.add_argument("--ar-tokens", type=int, default=128)
     ap.add_argument("--sampled-rounds", type=int, default=30,
                     help="also time this many sampled rounds (T 0.7, top_p 0.9, d3 [3,2,1]); 0 = skip")
+    ap.add_argument("--batch-gen", type=int, default=32,
+                    help="also time greedy batched generation (generate_batch) of this many prompts; 0 = skip")
+    ap.add_argument("--batch-gen-prompt", type=int, default=512)
+    ap.add_argument("--batch-gen-tokens", type=int, default=64)
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="also run one plain device copy of this many MiB (calibrates rocprofv3 byte counters)")
     args = ap.parse_args()
@@ -331,6 +400,12 @@ def main() -> None:
     ar = autoregressive_generate(target, torch.tensor([ids]), args.ar_tokens, {-1})
     ar_tps = (len(ar.tokens) - 1) / ar.times["decode"]
     log(f"autoregressive baseline: {ar_tps:.1f} tok/s")
+    pre = prefill_figures(target, ids)
+    log(f"prefill: {pre}")
+    batch = batch_generation_figures(target, args.batch_gen, args.batch_gen_prompt, args.batch_gen_tokens) \
+        if args.batch_gen else None
+    if batch:
+        log(f"batched generation: {batch}")
 
     bytes_round = model.weight_bytes() + 4 * model.weight_bytes(layers)
     fused = "mlp" in kf
@@ -370,6 +445,9 @@ def main() -> None:
     }
     if sampled is not None:
         line["sampled"] = sampled
+    line["prefill"] = pre
+    if batch:
+        line["batch_generation"] = batch
     if args.copy_probe_mb:
         src = torch.ones(args.copy_probe_mb << 20, dtype=torch.uint8, device=model.device)
         dst = torch.empty_like(src)
