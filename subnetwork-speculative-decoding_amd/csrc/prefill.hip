@@ -13,9 +13,9 @@
 //   every LDS read is one contiguous 1 KiB per wave. The decode epilogues run on the accumulators:
 //   the folded RMSNorm scale (sum of x^2 accumulated by the threads that stage X), RoPE + KV-cache
 //   write for q/k/v, SwiGLU for gate/up (rotary / gate-up row pairs r and r + 8 meet through one
-//   v_permlane32_swap), residual add for o and down. Workgroup ids are mapped XCD-aware: each XCD
-//   (ids b, b + 8, ...) takes a contiguous run of output tiles ordered M-fastest within a band of
-//   N tiles, so the weight and activation tiles it reads stay in its L2.
+//   v_permlane32_swap), residual add for o and down. The launch is persistent and XCD-aware: the
+//   workgroups resident on one XCD sweep blocks of output tiles together, so the weight and
+//   activation tiles they share are fetched into that XCD's L2 once per block.
 // * prefill_attention_kernel: causal flash attention, one wave per (q head, 32 tokens), K/V read
 //   in the cache's 64-slot MFMA-operand blocks; S^T = K Q^T and O^T = V^T P^T on MFMA with the
 //   running max / sum rescaled per 64-key block.
@@ -40,7 +40,8 @@ __device__ __forceinline__ size_t packed_tile(int nb, int kb, int kbt, int group
 }
 
 template <int EPI, int NORM>
-__global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(GemmArgs a, int group, int n_mt, int n_nt, int pos0) {
+__global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(GemmArgs a, int group, int n_mt, int n_nt, int pos0,
+                                                              int sb_n, int sb_m) {
   __shared__ u32x4_t As[2][PF_KB][8][64];
   __shared__ u32x4_t Bs[2][PF_KB][8][64];
   __shared__ float rn_s[PF_BM];
@@ -49,23 +50,25 @@ __global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(GemmArgs a, int gr
   const int wn = w & 1, wm = w >> 1;
   const int kbt = a.kb_total;
 
-  // XCD-aware tile order: XCD x = id % 8 owns logical tiles [x * per, (x + 1) * per); within it,
-  // tiles go M-fastest inside bands of 8 N tiles (the band's weights and all of X cycle through
-  // that XCD's L2).
-  const int n_tiles = n_mt * n_nt;
-  const int per = (n_tiles + 7) / 8;
-  const int lt = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
-  if (lt >= n_tiles) return;
-  constexpr int BAND = 8;
-  const int band = lt / (BAND * n_mt), in_band = lt % (BAND * n_mt);
-  const int band_w = min(BAND, n_nt - band * BAND);
-  const int bn = band * BAND + in_band % band_w, bm = in_band / band_w;
+  // Persistent, XCD-aware schedule: the workgroups resident on one XCD (ids x, x + 8, ...) sweep
+  // blocks of sb_n x sb_m output tiles together -- workgroup j takes tile (j % sb_n, j / sb_n)
+  // of the block -- so each weight tile is read by sb_m and each activation tile by sb_n
+  // workgroups that run in step through K, and the block's k slices stay in that XCD's L2.
+  // Blocks are dealt to the 8 XCDs round-robin, M-fastest (consecutive blocks of an XCD keep
+  // their activation band).
+  const int xcd = blockIdx.x % 8, jw = blockIdx.x / 8;
+  const int n_bn = (n_nt + sb_n - 1) / sb_n, n_bm = (n_mt + sb_m - 1) / sb_m;
+  for (int blk = xcd; blk < n_bn * n_bm; blk += 8) {
+  const int bn = (blk / n_bm) * sb_n + jw % sb_n, bm = (blk % n_bm) * sb_m + jw / sb_n;
+  if (bn >= n_nt || bm >= n_mt || jw >= sb_n * sb_m) continue;  // uniform per workgroup
   const int nb0 = bn * 8, m0 = bm * PF_BM;
 
   // Staging assignment: 1024 16-byte chunks of W and of X per step, 4 of each per thread.
   // W chunk i: k-block i >> 9 of the step, row tile (i >> 6) & 7, lane i & 63 (one tile = 1 KiB).
-  // X chunk i: row i >> 3 of the tile (t >> 3, + 32, + 64, + 96), 16-byte column c = t & 7 of the
-  // step's 64 k (k-block c >> 2, B-operand lane group c & 3).
+  // X: a wave's load covers 8 rows x the step's 8 16-byte columns (whole 128-byte lines); thread
+  // t, load r: row 8 (t >> 6) + 32 r + (t & 7), column c = lane >> 3 (k-block c >> 2, B-operand
+  // lane group c & 3). The 8 lanes that the LDS serves together hold 8 consecutive rows of one
+  // column: 8 consecutive 16-byte slots of the operand layout, free of bank conflicts.
   const u32x4_t* W = (const u32x4_t*)a.W;
   size_t wbase[4];
   int wkb[4];
@@ -76,32 +79,43 @@ __global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(GemmArgs a, int gr
     const int nb = nb0 + ((i >> 6) & 7);
     wbase[r] = packed_tile(nb, 0, kbt, group) * 64 + (i & 63);
   }
-  const int xc = t & 7;
+  const int xc = lane >> 3;
+  auto xrow_of = [&](int r) { return (t >> 6) * 8 + 32 * r + (t & 7); };
   const bf16_t* xrow[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) xrow[r] = a.X + (size_t)min(m0 + (t >> 3) + 32 * r, a.M - 1) * a.ldx + xc * 8;
+  for (int r = 0; r < 4; ++r) xrow[r] = a.X + (size_t)min(m0 + xrow_of(r), a.M - 1) * a.ldx + xc * 8;
   const int xkb = xc >> 2, xg = xc & 3;
 
-  u32x4_t ra[4], rb[4];
+  // Two register sets of staged chunks: a step's global loads are issued two compute steps before
+  // they are written to LDS, so their latency is covered by two steps of MFMAs.
+  struct Stage {
+    u32x4_t a[4], b[4];
+  };
+  Stage s0, s1;
   float ss[4] = {0.f, 0.f, 0.f, 0.f};
-  auto gload = [&](int st) {
+  auto gload = [&](int st, Stage& r) {
     const int k0 = st * PF_KB;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) ra[r] = __builtin_nontemporal_load(W + wbase[r] + (size_t)(k0 + wkb[r]) * group * 64);
+    for (int i = 0; i < 4; ++i) r.a[i] = W[wbase[i] + (size_t)(k0 + wkb[i]) * group * 64];  // shared by sb_m workgroups: cached
 #pragma unroll
-    for (int r = 0; r < 4; ++r) rb[r] = *(const u32x4_t*)(xrow[r] + (size_t)k0 * 32);
+    for (int i = 0; i < 4; ++i) r.b[i] = *(const u32x4_t*)(xrow[i] + (size_t)k0 * 32);
   };
-  auto lstore = [&](int buf) {
+  // real == false stores zeros (the padding step of an odd step count): a mask, not a branch,
+  // so every path through the loop has the same loads in flight
+  auto lstore = [&](int buf, const Stage& r, bool real) {
+    const uint32_t keep = real ? 0xffffffffu : 0u;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) (&As[buf][0][0][0])[t + 256 * r] = ra[r];
+    for (int i = 0; i < 4; ++i) (&As[buf][0][0][0])[t + 256 * i] = r.a[i] & keep;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = (t >> 3) + 32 * r;
-      Bs[buf][xkb][row >> 4][xg * 16 + (row & 15)] = rb[r];
+    for (int i = 0; i < 4; ++i) {
+      const int row = xrow_of(i);
+      Bs[buf][xkb][row >> 4][xg * 16 + (row & 15)] = r.b[i] & keep;
     }
     if constexpr (NORM) {
+      if (real) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) ss[r] += sumsq8(rb[r]);
+        for (int i = 0; i < 4; ++i) ss[i] += sumsq8(r.b[i]);
+      }
     }
   };
 
@@ -111,14 +125,7 @@ __global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(GemmArgs a, int gr
 #pragma unroll
     for (int y = 0; y < 4; ++y) acc[x][y] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int n_st = kbt / PF_KB;
-  gload(0);
-  lstore(0);
-  __syncthreads();
-  for (int st = 0; st < n_st; ++st) {
-    const int buf = st & 1;
-    const bool more = st + 1 < n_st;
-    if (more) gload(st + 1);
+  auto compute = [&](int buf) {
 #pragma unroll
     for (int kb = 0; kb < PF_KB; ++kb) {
       u32x4_t af[4], bf[4];
@@ -131,19 +138,42 @@ __global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(GemmArgs a, int gr
 #pragma unroll
         for (int y = 0; y < 4; ++y) acc[x][y] = mfma16x16x32(bits_bf16x8(af[x]), bits_bf16x8(bf[y]), acc[x][y]);
     }
-    if (more) lstore(buf ^ 1);
+  };
+  // step st: issue the loads of step st + 2 into `nxt`, compute step st from LDS, store step
+  // st + 1 (held in `cur`) into the other LDS buffer. Loads and stores are unconditional: the
+  // last steps re-load the final k slice, and an odd step count runs one more step over zeros.
+  // A load skipped on some path makes the compiler's wait counting assume fewer loads in flight,
+  // and the waits before the LDS stores would then also drain the loads issued at the top of the
+  // same step (the two-step prefetch would shrink to one).
+  const int n_st = kbt / PF_KB, n_run = (n_st + 1) & ~1;
+  // The scheduling barriers keep the three phases in this order (left free, the scheduler hoists
+  // the stores' masking, which waits for data, above the issue of the next loads).
+  auto step = [&](int st, Stage& cur, Stage& nxt) {
+    gload(min(st + 2, n_st - 1), nxt);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(st & 1);
+    __builtin_amdgcn_sched_barrier(0);
+    lstore((st + 1) & 1, cur, st + 1 < n_st);
     __syncthreads();
+  };
+  gload(0, s0);
+  gload(min(1, n_st - 1), s1);
+  lstore(0, s0, true);
+  __syncthreads();
+  for (int st = 0; st < n_run; st += 2) {
+    step(st, s1, s0);
+    step(st + 1, s0, s1);
   }
 
   if constexpr (NORM) {
-    // the 8 threads that staged one row hold its partial sums (consecutive lanes t, t ^ 1, ...)
+    // the 8 lanes that staged one row hold its partial sums (lanes l, l ^ 8, ..., l ^ 56)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       float v = ss[r];
-      v += __shfl_xor(v, 1);
-      v += __shfl_xor(v, 2);
-      v += __shfl_xor(v, 4);
-      if (xc == 0) rn_s[(t >> 3) + 32 * r] = rsqrtf(v / (float)(kbt * 32) + a.norm_eps);
+      v += __shfl_xor(v, 8);
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      if (xc == 0) rn_s[xrow_of(r)] = rsqrtf(v / (float)(kbt * 32) + a.norm_eps);
     }
     __syncthreads();
   }
@@ -201,8 +231,8 @@ __global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(GemmArgs a, int gr
       }
     }
   }
+  }  // tile loop
 }
-
 // ------------------------------------------------------------------ causal flash attention
 // Row (token t, q head h) at position pos0 + t attends cache slots [0, pos0 + t] (the prompt rows
 // before it and itself, whose K/V the q/k/v GEMM of this chunk already wrote).
@@ -365,12 +395,23 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(const bf16_t*
 static int launch_prefill_gemm(GemmArgs a, int group, int pos0, int epi, hipStream_t s) {
   const int n_mt = (a.M + PF_BM - 1) / PF_BM;
   const int n_nt = (a.N + PF_BN - 1) / PF_BN;
-  const int n_tiles = n_mt * n_nt;
-  const int grid = (n_tiles + 7) / 8 * 8;
+  // two workgroups per CU, all resident: 8 XCDs x (per_xcd = CUs / 4) workgroups
+  static int cus_of[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return set_error(SSD_EHIP, "prefill gemm: no current device");
+  int cus = dev >= 0 && dev < 64 ? cus_of[dev] : 0;
+  if (cus <= 0) {
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    if (dev >= 0 && dev < 64) cus_of[dev] = cus;
+  }
+  const int per_xcd = (2 * cus / 8) & ~7;  // 64 on MI355X
+  const int sb_m = n_mt < 8 ? n_mt : 8;
+  const int sb_n = per_xcd / sb_m;
+  const int grid = 8 * sb_n * sb_m;
   const bool norm = a.norm_eps > 0.f;
 #define PF_LAUNCH(E)                                                                                          \
-  if (norm) hipLaunchKernelGGL((prefill_gemm_kernel<E, 1>), dim3(grid), dim3(256), 0, s, a, group, n_mt, n_nt, pos0); \
-  else hipLaunchKernelGGL((prefill_gemm_kernel<E, 0>), dim3(grid), dim3(256), 0, s, a, group, n_mt, n_nt, pos0);
+  if (norm) hipLaunchKernelGGL((prefill_gemm_kernel<E, 1>), dim3(grid), dim3(256), 0, s, a, group, n_mt, n_nt, pos0, sb_n, sb_m); \
+  else hipLaunchKernelGGL((prefill_gemm_kernel<E, 0>), dim3(grid), dim3(256), 0, s, a, group, n_mt, n_nt, pos0, sb_n, sb_m);
   switch (epi) {
     case EPI_STORE: PF_LAUNCH(EPI_STORE); break;
     case EPI_SWIGLU: PF_LAUNCH(EPI_SWIGLU); break;
