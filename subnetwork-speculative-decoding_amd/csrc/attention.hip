@@ -192,13 +192,14 @@ __device__ __forceinline__ void block_attend(const Frags<HD>& f, const u32x4_t (
                                              float scale_log2, float& m_out, float& l_out,
                                              f32x4_t (&o)[HD / 16]) {
   constexpr int KS = HD / 32, DT = HD / 16;
+  // k-step outer: consecutive MFMAs go to different accumulators (each sum keeps its ks order)
   f32x4_t s[4];
 #pragma unroll
-  for (int kt = 0; kt < 4; ++kt) {
-    s[kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int kt = 0; kt < 4; ++kt) s[kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) s[kt] = mfma16x16x32(bits_bf16x8(f.k[kt][ks]), bits_bf16x8(qf[ks]), s[kt]);
-  }
+  for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) s[kt] = mfma16x16x32(bits_bf16x8(f.k[kt][ks]), bits_bf16x8(qf[ks]), s[kt]);
   float sv[16];
   float mx = -INFINITY;
 #pragma unroll
@@ -234,12 +235,9 @@ __device__ __forceinline__ void block_attend(const Frags<HD>& f, const u32x4_t (
   const u32x4_t pb0 = {pw[0][0], pw[0][1], pw[0][2], pw[0][3]};
   const u32x4_t pb1 = {pw[1][0], pw[1][1], pw[1][2], pw[1][3]};
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) {
-    f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    acc = mfma16x16x32(bits_bf16x8(f.v[dt][0]), bits_bf16x8(pb0), acc);
-    acc = mfma16x16x32(bits_bf16x8(f.v[dt][1]), bits_bf16x8(pb1), acc);
-    o[dt] = acc;
-  }
+  for (int dt = 0; dt < DT; ++dt) o[dt] = mfma16x16x32(bits_bf16x8(f.v[dt][0]), bits_bf16x8(pb0), f32x4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] = mfma16x16x32(bits_bf16x8(f.v[dt][1]), bits_bf16x8(pb1), o[dt]);
 }
 
 constexpr int ATT_QROWS = 128;  // query rows staged in LDS at a time
