@@ -345,6 +345,7 @@ def main() -> None:
 
     import torch
 
+    from ssd import _lib
     from ssd.config import BridgeConfig, DraftingConfig
     from ssd.data.token_freq import top_vocab, zipf_counts
     from ssd.engine.speculative import SpeculativeGenerator, TargetRunner, autoregressive_generate
@@ -378,12 +379,14 @@ def main() -> None:
     sess.phases.totals.clear()
     n_warm = len(sess.accepted_per_round)
     torch.cuda.synchronize()
+    launches0 = int(_lib.load().ssd_launch_count())
     t0 = time.perf_counter()
     toks = 0
     for _ in range(args.steps):
         toks += len(sess.step())
     torch.cuda.synchronize()
     secs = time.perf_counter() - t0
+    launches = (int(_lib.load().ssd_launch_count()) - launches0) / args.steps
     acc = sess.accepted_per_round[n_warm:]
     phases = {k: 1000 * v / args.steps for k, v in sess.phases.totals.items()}
     log(f"{args.steps} rounds: {toks} tokens in {secs:.3f}s ({toks / secs:.1f} tok/s, {1000 * secs / args.steps:.3f} "
@@ -431,6 +434,9 @@ def main() -> None:
                    "parallelism": "single GPU"},
         "mean_accepted": round(sum(acc) / len(acc), 4),
         "ms_per_round_phases": {k: round(v, 4) for k, v in phases.items()},
+        # kernels the library enqueues per round (the engine adds two small torch ops and the
+        # result copy)
+        "launches_per_round": round(launches, 2),
         "ar_tokens_per_s": round(ar_tps, 3),
         "speedup_vs_ar": round((toks / secs) / ar_tps, 4),
         "round_weight_bytes": bytes_round,

@@ -29,6 +29,10 @@ typedef struct ihipStream_t* hipStream_t;
 /* ------------------------------------------------------------------ library */
 const char* ssd_last_error(void);
 int ssd_abi_version(void);
+/* Kernels this library has enqueued since it was loaded (all devices and streams): the number
+ * of launches a caller's step costs is the difference around it. No counterpart in the
+ * reference. */
+uint64_t ssd_launch_count(void);
 /* Hash of the csrc/ and include/ sources the library was built from (16 hex digits; "unknown" for a
  * build without it); the Python package refuses a library whose hash differs from its sources. */
 const char* ssd_build_hash(void);

@@ -554,12 +554,12 @@ static int launch_attn(AttnArgs a, bf16_t* out, int64_t ldo, hipStream_t s) {
   a.groups = (n_tiles + a.tiles_per_group - 1) / a.tiles_per_group;
   const int grid = a.tail_slots + units8 * a.groups;
   if (grid > 0) {
-    hipLaunchKernelGGL((attn_partial_kernel<HD>), dim3(grid), dim3(256), 0, s, a);
+    SSD_LAUNCH((attn_partial_kernel<HD>), dim3(grid), dim3(256), 0, s, a);
     const int rc = check_launch("attn_partial");
     if (rc) return rc;
   }
   const int waves = a.M * a.heads;
-  hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3((waves + 3) / 4), dim3(256), 0, s, a.ws, a.n_sb_cap, a.M,
+  SSD_LAUNCH((attn_combine_kernel<HD>), dim3((waves + 3) / 4), dim3(256), 0, s, a.ws, a.n_sb_cap, a.M,
                      a.heads, a.kv_heads, out, ldo, n_sb);
   return check_launch("attn_combine");
 }

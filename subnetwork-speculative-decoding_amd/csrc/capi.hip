@@ -4,6 +4,8 @@
 
 #include "common.h"
 
+#include <atomic>
+
 namespace ssd {
 
 static thread_local char g_err[512] = "";
@@ -16,6 +18,9 @@ int set_error(int code, const char* fmt, ...) {
   return code;
 }
 
+static std::atomic<uint64_t> g_launches{0};
+void count_launch() { g_launches.fetch_add(1, std::memory_order_relaxed); }
+
 int check_launch(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(SSD_EHIP, "%s: launch failed: %s", what, hipGetErrorString(e));
@@ -27,6 +32,9 @@ int check_launch(const char* what) {
 SSD_API const char* ssd_last_error(void) { return ssd::g_err; }
 
 SSD_API int ssd_abi_version(void) { return 3; }
+
+// Kernels enqueued by this library since it was loaded (all devices and streams).
+SSD_API uint64_t ssd_launch_count(void) { return ssd::g_launches.load(std::memory_order_relaxed); }
 
 #ifndef SSD_BUILD_HASH
 #define SSD_BUILD_HASH "unknown"

@@ -21,6 +21,14 @@ namespace ssd {
 // nonzero code and a message retrievable through ssd_last_error().
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
+// Counts every kernel the library enqueues (read with ssd_launch_count); SSD_LAUNCH is
+// hipLaunchKernelGGL plus the count.
+void count_launch();
+#define SSD_LAUNCH(...)          \
+  do {                           \
+    ::ssd::count_launch();       \
+    hipLaunchKernelGGL(__VA_ARGS__); \
+  } while (0)
 
 enum Status {
   SSD_OK = 0,

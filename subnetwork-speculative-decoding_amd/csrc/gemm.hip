@@ -525,11 +525,11 @@ static int launch_finalize(const GemmArgs& a, const float* P, int64_t ldp, int64
   const int64_t threads = (int64_t)a.M * ((a.N + 15) / 16) * 8;
   const dim3 grid((unsigned)((threads + 255) / 256)), block(256);
   switch (S) {
-    case 1: hipLaunchKernelGGL((gemm_finalize_kernel<EPI, 1>), grid, block, 0, s, a, P, ldp, sstride); break;
-    case 2: hipLaunchKernelGGL((gemm_finalize_kernel<EPI, 2>), grid, block, 0, s, a, P, ldp, sstride); break;
-    case 4: hipLaunchKernelGGL((gemm_finalize_kernel<EPI, 4>), grid, block, 0, s, a, P, ldp, sstride); break;
-    case 8: hipLaunchKernelGGL((gemm_finalize_kernel<EPI, 8>), grid, block, 0, s, a, P, ldp, sstride); break;
-    case 16: hipLaunchKernelGGL((gemm_finalize_kernel<EPI, 16>), grid, block, 0, s, a, P, ldp, sstride); break;
+    case 1: SSD_LAUNCH((gemm_finalize_kernel<EPI, 1>), grid, block, 0, s, a, P, ldp, sstride); break;
+    case 2: SSD_LAUNCH((gemm_finalize_kernel<EPI, 2>), grid, block, 0, s, a, P, ldp, sstride); break;
+    case 4: SSD_LAUNCH((gemm_finalize_kernel<EPI, 4>), grid, block, 0, s, a, P, ldp, sstride); break;
+    case 8: SSD_LAUNCH((gemm_finalize_kernel<EPI, 8>), grid, block, 0, s, a, P, ldp, sstride); break;
+    case 16: SSD_LAUNCH((gemm_finalize_kernel<EPI, 16>), grid, block, 0, s, a, P, ldp, sstride); break;
     default: return set_error(SSD_EINVAL, "finalize: split count %d not in {1, 2, 4, 8, 16}", S);
   }
   return SSD_OK;
@@ -563,10 +563,10 @@ static int launch_part(const GemmArgs& a, float* P, int64_t ldp, int64_t sstride
     const int ct = (b.M + 15) / 16;
     dim3 grid(groups, p.S);
     switch (ct) {
-      case 1: hipLaunchKernelGGL((gemm_part_kernel<1, 1, 8>), grid, dim3(512), 0, s, b, Pm, ldp, sstride, p.S); break;
-      case 2: hipLaunchKernelGGL((gemm_part_kernel<2, 1, 8>), grid, dim3(512), 0, s, b, Pm, ldp, sstride, p.S); break;
-      case 3: hipLaunchKernelGGL((gemm_part_kernel<3, 1, 8>), grid, dim3(512), 0, s, b, Pm, ldp, sstride, p.S); break;
-      default: hipLaunchKernelGGL((gemm_part_kernel<4, 1, 8>), grid, dim3(512), 0, s, b, Pm, ldp, sstride, p.S); break;
+      case 1: SSD_LAUNCH((gemm_part_kernel<1, 1, 8>), grid, dim3(512), 0, s, b, Pm, ldp, sstride, p.S); break;
+      case 2: SSD_LAUNCH((gemm_part_kernel<2, 1, 8>), grid, dim3(512), 0, s, b, Pm, ldp, sstride, p.S); break;
+      case 3: SSD_LAUNCH((gemm_part_kernel<3, 1, 8>), grid, dim3(512), 0, s, b, Pm, ldp, sstride, p.S); break;
+      default: SSD_LAUNCH((gemm_part_kernel<4, 1, 8>), grid, dim3(512), 0, s, b, Pm, ldp, sstride, p.S); break;
     }
     const int rc = check_launch("gemm_part");
     if (rc) return rc;
@@ -646,8 +646,8 @@ static int launch_wide(GemmArgs a, int n_groups, hipStream_t s) {
   const dim3 grid((unsigned)std::min(n_groups, cus)), block(64 * WIDE_WAVES);
   const int ct = (a.M + 15) / 16;
 #define SSD_WIDE(CT_, U_)                                                                          \
-  if (a.norm_eps > 0.f) hipLaunchKernelGGL((gemm_wide_kernel<CT_, U_, 1>), grid, block, 0, s, a, n_groups); \
-  else hipLaunchKernelGGL((gemm_wide_kernel<CT_, U_, 0>), grid, block, 0, s, a, n_groups);
+  if (a.norm_eps > 0.f) SSD_LAUNCH((gemm_wide_kernel<CT_, U_, 1>), grid, block, 0, s, a, n_groups); \
+  else SSD_LAUNCH((gemm_wide_kernel<CT_, U_, 0>), grid, block, 0, s, a, n_groups);
   switch (ct) {
     case 1: SSD_WIDE(1, 4) break;
     case 2: SSD_WIDE(2, 2) break;
@@ -682,9 +682,9 @@ static int launch_gemm(GemmArgs a, hipStream_t s) {
 #define SSD_GEMM_CASE(CT_, NS_, KS_) \
   if (ct == CT_ && p.nsub == NS_ && p.ks == KS_) {                                                             \
     if (b.norm_eps > 0.f)                                                                                      \
-      hipLaunchKernelGGL((gemm_kernel<CT_, NS_, KS_, (CT_ == 1 ? 4 : 2), EPI, 1>), grid, dim3(64 * KS_), 0, s, b); \
+      SSD_LAUNCH((gemm_kernel<CT_, NS_, KS_, (CT_ == 1 ? 4 : 2), EPI, 1>), grid, dim3(64 * KS_), 0, s, b); \
     else                                                                                                       \
-      hipLaunchKernelGGL((gemm_kernel<CT_, NS_, KS_, (CT_ == 1 ? 4 : 2), EPI, 0>), grid, dim3(64 * KS_), 0, s, b); \
+      SSD_LAUNCH((gemm_kernel<CT_, NS_, KS_, (CT_ == 1 ? 4 : 2), EPI, 0>), grid, dim3(64 * KS_), 0, s, b); \
   }
 #define SSD_GEMM_PLANS(CT_)                                                                                \
   SSD_GEMM_CASE(CT_, 8, 2) SSD_GEMM_CASE(CT_, 8, 1) SSD_GEMM_CASE(CT_, 4, 2) SSD_GEMM_CASE(CT_, 4, 1)     \
@@ -736,7 +736,7 @@ SSD_API int ssd_pack_weight_bf16(const uint16_t* src, int64_t ld, int N_src, int
   if (group < 1 || group > 16 || n_tiles_n % group)
     return set_error(SSD_EINVAL, "pack: group %d must be in [1, 16] and divide the %d row tiles", group, n_tiles_n);
   const int64_t tiles = (int64_t)n_tiles_n * kb_total;
-  hipLaunchKernelGGL(pack_kernel, dim3((unsigned)((tiles + 3) / 4)), dim3(256), 0, stream, src, ld, K, row_map,
+  SSD_LAUNCH(pack_kernel, dim3((unsigned)((tiles + 3) / 4)), dim3(256), 0, stream, src, ld, K, row_map,
                      n_tiles_n, kb_total, group, col_scale, (uint4*)dst);
   return check_launch("pack");
 }

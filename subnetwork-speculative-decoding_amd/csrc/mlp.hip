@@ -448,10 +448,10 @@ template <int NS1, int TG1, int S>
 static hipError_t launch_mlp_ct(int ct, const MlpArgs& a, hipStream_t s) {
   const dim3 grid(MLP_WGS), block(MLP_THREADS);
   switch (ct) {
-    case 1: hipLaunchKernelGGL((mlp_kernel<1, NS1, TG1, S>), grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL((mlp_kernel<2, NS1, TG1, S>), grid, block, 0, s, a); break;
-    case 3: hipLaunchKernelGGL((mlp_kernel<3, NS1, TG1, S>), grid, block, 0, s, a); break;
-    default: hipLaunchKernelGGL((mlp_kernel<4, NS1, TG1, S>), grid, block, 0, s, a); break;
+    case 1: SSD_LAUNCH((mlp_kernel<1, NS1, TG1, S>), grid, block, 0, s, a); break;
+    case 2: SSD_LAUNCH((mlp_kernel<2, NS1, TG1, S>), grid, block, 0, s, a); break;
+    case 3: SSD_LAUNCH((mlp_kernel<3, NS1, TG1, S>), grid, block, 0, s, a); break;
+    default: SSD_LAUNCH((mlp_kernel<4, NS1, TG1, S>), grid, block, 0, s, a); break;
   }
   return hipGetLastError();
 }

@@ -304,15 +304,18 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(const bf16_t*
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) kf[kt][ks] = *(const u32x4_t*)(kb + (size_t)b * 64 * HD + (kt * KS + ks) * 512);
+    // k-step outer: consecutive MFMAs go to different accumulators (each sum keeps its ks order)
     f32x4_t s[NT][4];
 #pragma unroll
     for (int rt = 0; rt < NT; ++rt)
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        s[rt][kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int kt = 0; kt < 4; ++kt) s[rt][kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) s[rt][kt] = mfma16x16x32(bits_bf16x8(kf[kt][ks]), bits_bf16x8(qf[rt][ks]), s[rt][kt]);
-      }
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int rt = 0; rt < NT; ++rt)
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) s[rt][kt] = mfma16x16x32(bits_bf16x8(kf[kt][ks]), bits_bf16x8(qf[rt][ks]), s[rt][kt]);
     u32x4_t vf[DT][2];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
@@ -368,12 +371,9 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(const bf16_t*
       const u32x4_t pb0 = {pw[0][0], pw[0][1], pw[0][2], pw[0][3]};
       const u32x4_t pb1 = {pw[1][0], pw[1][1], pw[1][2], pw[1][3]};
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        f32x4_t acc = o[rt][dt] * alpha;
-        acc = mfma16x16x32(bits_bf16x8(vf[dt][0]), bits_bf16x8(pb0), acc);
-        acc = mfma16x16x32(bits_bf16x8(vf[dt][1]), bits_bf16x8(pb1), acc);
-        o[rt][dt] = acc;
-      }
+      for (int dt = 0; dt < DT; ++dt) o[rt][dt] = mfma16x16x32(bits_bf16x8(vf[dt][0]), bits_bf16x8(pb0), o[rt][dt] * alpha);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[rt][dt] = mfma16x16x32(bits_bf16x8(vf[dt][1]), bits_bf16x8(pb1), o[rt][dt]);
     }
   }
   // lane (g, j) of o[rt][dt] holds dims 16 dt + 4 g + e of row j
@@ -410,8 +410,8 @@ static int launch_prefill_gemm(GemmArgs a, int group, int pos0, int epi, hipStre
   const int grid = 8 * sb_n * sb_m;
   const bool norm = a.norm_eps > 0.f;
 #define PF_LAUNCH(E)                                                                                          \
-  if (norm) hipLaunchKernelGGL((prefill_gemm_kernel<E, 1>), dim3(grid), dim3(256), 0, s, a, group, n_mt, n_nt, pos0, sb_n, sb_m); \
-  else hipLaunchKernelGGL((prefill_gemm_kernel<E, 0>), dim3(grid), dim3(256), 0, s, a, group, n_mt, n_nt, pos0, sb_n, sb_m);
+  if (norm) SSD_LAUNCH((prefill_gemm_kernel<E, 1>), dim3(grid), dim3(256), 0, s, a, group, n_mt, n_nt, pos0, sb_n, sb_m); \
+  else SSD_LAUNCH((prefill_gemm_kernel<E, 0>), dim3(grid), dim3(256), 0, s, a, group, n_mt, n_nt, pos0, sb_n, sb_m);
   switch (epi) {
     case EPI_STORE: PF_LAUNCH(EPI_STORE); break;
     case EPI_SWIGLU: PF_LAUNCH(EPI_SWIGLU); break;
@@ -485,11 +485,11 @@ SSD_API int ssd_prefill_attention_bf16(const uint16_t* q, int64_t ldq, int M, in
   const float sl2 = scale * 1.4426950408889634f;
   switch (head_dim) {
     case 64:
-      hipLaunchKernelGGL((prefill_attention_kernel<64>), grid, block, 0, stream, (const bf16_t*)q, ldq, M, pos0, heads,
+      SSD_LAUNCH((prefill_attention_kernel<64>), grid, block, 0, stream, (const bf16_t*)q, ldq, M, pos0, heads,
                          kv_heads, (const bf16_t*)k_cache, (const bf16_t*)vt_cache, max_len, sl2, (bf16_t*)out, ldo, n_tt);
       break;
     case 128:
-      hipLaunchKernelGGL((prefill_attention_kernel<128>), grid, block, 0, stream, (const bf16_t*)q, ldq, M, pos0,
+      SSD_LAUNCH((prefill_attention_kernel<128>), grid, block, 0, stream, (const bf16_t*)q, ldq, M, pos0,
                          heads, kv_heads, (const bf16_t*)k_cache, (const bf16_t*)vt_cache, max_len, sl2, (bf16_t*)out,
                          ldo, n_tt);
       break;

@@ -141,32 +141,57 @@ __global__ __launch_bounds__(256) void embed_kernel(const int* __restrict__ ids,
 }
 
 // Move cache entries src[0..n) to [start, start+n) in every layer and kv head
-// (ssd/engine/kv_cache.py:54-70). All sources are read before any destination is
-// written: a destination may be the source of a later entry (start=10, src=[10,12,13]).
+// (ssd/engine/kv_cache.py:54-70), in 16-byte runs. All sources are read before any destination
+// is written: a destination may be the source of a later entry (start=10, src=[10,12,13]).
 // Every (layer, kv head) holds max_len slots of K and of V in the 64-slot block layout (k_off,
-// v_off in common.h). n is read from device memory (n_ptr) so the launch needs no host round
-// trip; n <= n_max.
+// v_off in common.h). K: each entry is hd/8 runs of 8 dims (contiguous in the layout), copied
+// whole. V: the layout keeps 8 consecutive slots of one dim together, so each 16-byte run of
+// the destination range's 8-slot groups is read, the moved entries are put into it, and it is
+// written back whole. n is read from device memory (n_ptr) so the launch needs no host round
+// trip; n <= n_max. An out-of-range source leaves its slot as it is.
 __global__ __launch_bounds__(256) void kv_compact_kernel(bf16_t* __restrict__ kc, bf16_t* __restrict__ vt, int kv_heads,
                                                          int hd, int64_t max_len, int start, const int* __restrict__ src,
                                                          const int* __restrict__ n_ptr, int n_max) {
-  extern __shared__ bf16_t stage[];  // [2][n_max][hd]
-  const int lh = blockIdx.x;         // layer * kv_heads + head
+  extern __shared__ u32x4_t stage16[];  // K runs [n_max][hd / 8], then V runs [groups][hd]
+  const int lh = blockIdx.x;            // layer * kv_heads + head
   const int n = max(0, min(*n_ptr, n_max));
   bf16_t* kbase = kc + (size_t)lh * max_len * hd;
   bf16_t* vbase = vt + (size_t)lh * hd * max_len;
-  const int tot = n * hd;
-  for (int e = threadIdx.x; e < tot; e += 256) {
-    const int i = e / hd, d = e % hd;
-    int s = src[i];
-    s = (s >= 0 && s < max_len) ? s : start + i;  // out-of-range source: leave the slot as is
-    stage[e] = kbase[k_off(s, d, hd)];
-    stage[n_max * hd + e] = vbase[v_off(s, d, hd)];
+  const int hq = hd >> 3;
+  const int g0 = start >> 3, ng = n > 0 ? ((start + n + 7) >> 3) - g0 : 0;
+  u32x4_t* kst = stage16;
+  u32x4_t* vst = stage16 + (size_t)n_max * hq;
+  auto src_of = [&](int i) {
+    const int s = src[i];
+    return (s >= 0 && s < max_len) ? s : start + i;
+  };
+  for (int e = threadIdx.x; e < n * hq; e += 256) {
+    const int i = e / hq, q = e - i * hq;
+    kst[e] = *(const u32x4_t*)(kbase + k_off(src_of(i), q * 8, hd));
+  }
+  for (int e = threadIdx.x; e < ng * hd; e += 256) {
+    const int g = e / hd, d = e - g * hd;
+    const int s0 = (g0 + g) * 8;
+    u32x4_t run = *(const u32x4_t*)(vbase + v_off(s0, d, hd));
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int i = s0 + t - start;
+      if (i >= 0 && i < n) {
+        const uint32_t h = (uint32_t)vbase[v_off(src_of(i), d, hd)];
+        const int w = t >> 1;
+        run[w] = (t & 1) ? ((run[w] & 0x0000ffffu) | (h << 16)) : ((run[w] & 0xffff0000u) | h);
+      }
+    }
+    vst[e] = run;
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < tot; e += 256) {
-    const int i = e / hd, d = e % hd;
-    kbase[k_off(start + i, d, hd)] = stage[e];
-    vbase[v_off(start + i, d, hd)] = stage[n_max * hd + e];
+  for (int e = threadIdx.x; e < n * hq; e += 256) {
+    const int i = e / hq, q = e - i * hq;
+    *(u32x4_t*)(kbase + k_off(start + i, q * 8, hd)) = kst[e];
+  }
+  for (int e = threadIdx.x; e < ng * hd; e += 256) {
+    const int g = e / hd, d = e - g * hd;
+    *(u32x4_t*)(vbase + v_off((g0 + g) * 8, d, hd)) = vst[e];
   }
 }
 
@@ -317,7 +342,7 @@ SSD_API int ssd_rmsnorm_bf16(const uint16_t* x, int64_t ldx, int M, int D, const
   if (!x || !w || !y || M < 0 || D <= 0 || D % 8 || ldx % 8 || ldy % 8)
     return set_error(SSD_EINVAL, "rmsnorm: bad arguments (D=%d must be a multiple of 8)", D);
   if (M == 0) return SSD_OK;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(M), dim3(256), 0, stream, x, ldx, w, y, ldy, D, eps);
+  SSD_LAUNCH(rmsnorm_kernel, dim3(M), dim3(256), 0, stream, x, ldx, w, y, ldy, D, eps);
   return check_launch("rmsnorm");
 }
 
@@ -325,7 +350,7 @@ SSD_API int ssd_embed_bf16(const int32_t* ids, int M, const uint16_t* table, int
                            int64_t ldo, hipStream_t stream) {
   if (!ids || !table || !out || M < 0 || D % 8 || ldo % 8) return set_error(SSD_EINVAL, "embed: bad arguments");
   if (M == 0) return SSD_OK;
-  hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(256), 0, stream, ids, table, V, D, out, ldo);
+  SSD_LAUNCH(embed_kernel, dim3(M), dim3(256), 0, stream, ids, table, V, D, out, ldo);
   return check_launch("embed");
 }
 
@@ -339,9 +364,9 @@ SSD_API int ssd_kv_compact_bf16(uint16_t* k_arena, uint16_t* vt_arena, int layer
                      (long long)max_len);
   if (start < 0 || start + n_max > max_len) return set_error(SSD_EINVAL, "kv_compact: start %d + %d > max_len", start, n_max);
   if (n_max == 0) return SSD_OK;
-  const size_t lds = (size_t)2 * n_max * head_dim * sizeof(bf16_t);
+  const size_t lds = ((size_t)n_max * (head_dim / 8) + (size_t)((n_max + 7) / 8 + 1) * head_dim) * 16;
   if (lds > 64 * 1024) return set_error(SSD_ERANGE, "kv_compact: n_max=%d too large", n_max);
-  hipLaunchKernelGGL(kv_compact_kernel, dim3(layers * kv_heads), dim3(256), lds, stream, (bf16_t*)k_arena,
+  SSD_LAUNCH(kv_compact_kernel, dim3(layers * kv_heads), dim3(256), lds, stream, (bf16_t*)k_arena,
                      (bf16_t*)vt_arena, kv_heads, head_dim, max_len, start, src, n_dev, n_max);
   return check_launch("kv_compact");
 }
@@ -355,10 +380,10 @@ static int row_topk_launch(const uint16_t* logits, int64_t ld, int M, int N, int
                            const int32_t* vocab_ids, int32_t* out_tok, float* out_val, float* out_lse, TopkPart* parts,
                            hipStream_t stream) {
   const int S = (N + TOPK_CHUNK - 1) / TOPK_CHUNK;
-  hipLaunchKernelGGL(row_topk_partial_kernel, dim3(S, M), dim3(256), 0, stream, logits, ld, N, k, mode, parts);
+  SSD_LAUNCH(row_topk_partial_kernel, dim3(S, M), dim3(256), 0, stream, logits, ld, N, k, mode, parts);
   int rc = check_launch("row_topk_partial");
   if (rc) return rc;
-  hipLaunchKernelGGL(row_topk_merge_kernel, dim3(M), dim3(64), 0, stream, (const TopkPart*)parts, S, k, mode,
+  SSD_LAUNCH(row_topk_merge_kernel, dim3(M), dim3(64), 0, stream, (const TopkPart*)parts, S, k, mode,
                      vocab_ids, out_tok, out_val, out_lse);
   return check_launch("row_topk_merge");
 }
@@ -439,7 +464,7 @@ SSD_API int ssd_add_rmsnorm_bf16(const float* P, int64_t ldp, int64_t split_stri
     return set_error(SSD_EINVAL, "add_rmsnorm: partials need 16-byte alignment, ldp >= D, split stride >= M*ldp");
   if (M == 0) return SSD_OK;
 #define SSD_ADD_RMS(S_)                                                                                       \
-  hipLaunchKernelGGL((add_rmsnorm_kernel<S_>), dim3(M), dim3(1024), 0, stream, P, ldp, split_stride,          \
+  SSD_LAUNCH((add_rmsnorm_kernel<S_>), dim3(M), dim3(1024), 0, stream, P, ldp, split_stride,          \
                      (const bf16_t*)bias, (bf16_t*)h, ldh, (const bf16_t*)w, (bf16_t*)y, ldy, D, eps)
   switch (S) {
     case 0: SSD_ADD_RMS(0); break;

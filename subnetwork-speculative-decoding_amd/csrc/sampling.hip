@@ -1213,12 +1213,12 @@ SSD_API int ssd_warp_probs_bf16(const uint16_t* logits, int64_t ld, int rows, in
   const double tp = top_p < 0.f ? 0.0 : (double)top_p;
   WarpArgs a{logits, ld, rows, n, vocab_ids, vocab_inv, V, temperature, top_p,
              (uint64_t)fmin(tp * 0x1p52, 0x1p63), tree_meta, level, probs, ldp, w};
-  hipLaunchKernelGGL(warp_stats_kernel, dim3(C, rows), dim3(SMP_THREADS), 0, stream, a);
+  SSD_LAUNCH(warp_stats_kernel, dim3(C, rows), dim3(SMP_THREADS), 0, stream, a);
   if (top_p < 1.f) {
-    hipLaunchKernelGGL(warp_coarse_kernel, dim3(C, rows), dim3(SMP_THREADS), 0, stream, a);
-    hipLaunchKernelGGL(warp_fine_kernel, dim3(C, rows), dim3(SMP_THREADS), 0, stream, a);
+    SSD_LAUNCH(warp_coarse_kernel, dim3(C, rows), dim3(SMP_THREADS), 0, stream, a);
+    SSD_LAUNCH(warp_fine_kernel, dim3(C, rows), dim3(SMP_THREADS), 0, stream, a);
   }
-  hipLaunchKernelGGL(warp_final_kernel, dim3(vocab_ids ? max(C, CV) : C, rows), dim3(SMP_THREADS), 0, stream, a);
+  SSD_LAUNCH(warp_final_kernel, dim3(vocab_ids ? max(C, CV) : C, rows), dim3(SMP_THREADS), 0, stream, a);
   return check_launch("warp_probs");
 }
 
@@ -1234,8 +1234,8 @@ SSD_API int ssd_gumbel_topk(const float* probs, int64_t ldp, int rows, int V, in
   SmpWs w;
   if (int rc = carve(ws, ws_bytes, rows, V, &w, "gumbel_topk")) return rc;
   TopkArgs a{probs, ldp, rows, V, k, tree_meta, level, make_rng(seed, counter), out_tok, out_lp, w};
-  hipLaunchKernelGGL(gumbel_chunk_kernel, dim3(w.C, rows), dim3(SMP_THREADS), 0, stream, a);
-  hipLaunchKernelGGL(gumbel_merge_kernel, dim3(rows), dim3(SMP_THREADS), 0, stream, a);
+  SSD_LAUNCH(gumbel_chunk_kernel, dim3(w.C, rows), dim3(SMP_THREADS), 0, stream, a);
+  SSD_LAUNCH(gumbel_merge_kernel, dim3(rows), dim3(SMP_THREADS), 0, stream, a);
   return check_launch("gumbel_topk");
 }
 
@@ -1247,9 +1247,9 @@ SSD_API int ssd_sample_rows(const float* probs, int64_t ldp, int rows, int V, ui
   if (rows == 0) return SSD_OK;
   SmpWs w;
   if (int rc = carve(ws, ws_bytes, rows, V, &w, "sample_rows")) return rc;
-  hipLaunchKernelGGL(draw_chunk_kernel, dim3(w.C, rows), dim3(SMP_THREADS), 0, stream, probs, ldp, V,
+  SSD_LAUNCH(draw_chunk_kernel, dim3(w.C, rows), dim3(SMP_THREADS), 0, stream, probs, ldp, V,
                      make_rng(seed, counter), w);
-  hipLaunchKernelGGL(draw_merge_kernel, dim3((rows + 63) / 64), dim3(64), 0, stream, rows, w, out_tok);
+  SSD_LAUNCH(draw_merge_kernel, dim3((rows + 63) / 64), dim3(64), 0, stream, rows, w, out_tok);
   return check_launch("sample_rows");
 }
 
@@ -1266,10 +1266,10 @@ SSD_API int ssd_accept_sample(const SsdTree* tree, const float* P, int64_t ldp, 
   SmpWs w;
   if (int rc = carve(ws, ws_bytes, rows, V, &w, "accept_sample")) return rc;
   AcceptArgs a{*tree, P, ldp, Q, ldq, V, rows, max_kids, make_rng(seed, counter), w};
-  hipLaunchKernelGGL(state0_kernel, dim3(w.C, rows), dim3(SMP_THREADS), 0, stream, a);
+  SSD_LAUNCH(state0_kernel, dim3(w.C, rows), dim3(SMP_THREADS), 0, stream, a);
   for (int j = 1; j <= max_kids; ++j)
-    hipLaunchKernelGGL(statej_kernel, dim3(w.C, rows), dim3(SMP_THREADS), 0, stream, a, j);
-  hipLaunchKernelGGL(sample_walk_kernel, dim3(1), dim3(64), 0, stream, a, committed, result, keep_src, n_keep,
+    SSD_LAUNCH(statej_kernel, dim3(w.C, rows), dim3(SMP_THREADS), 0, stream, a, j);
+  SSD_LAUNCH(sample_walk_kernel, dim3(1), dim3(64), 0, stream, a, committed, result, keep_src, n_keep,
                      root_token);
   return check_launch("accept_sample");
 }
@@ -1301,7 +1301,7 @@ SSD_API int ssd_accept_sample_trials(const float* P, int64_t ldp, const float* Q
   if (rows < 1 + nodes) return set_error(SSD_EINVAL, "accept_trials: %d rows for a tree of %lld nodes", rows, (long long)nodes);
   a.seed = seed; a.counter0 = counter0; a.trials = trials; a.out_tok = out_tokens; a.out_n = out_n;
   if (trials == 0) return SSD_OK;
-  hipLaunchKernelGGL(accept_trials_kernel, dim3((trials + 3) / 4), dim3(256), 0, stream, a);
+  SSD_LAUNCH(accept_trials_kernel, dim3((trials + 3) / 4), dim3(256), 0, stream, a);
   return check_launch("accept_trials");
 }
 

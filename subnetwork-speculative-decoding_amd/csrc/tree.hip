@@ -231,7 +231,7 @@ SSD_API int ssd_round_begin(const SsdTree* tree, const SsdRows* root, int base, 
                             hipStream_t stream) {
   if (!tree || !root || !tree->meta || !root->pos || root->cap < 1) return set_error(SSD_EINVAL, "round_begin: null");
   if (base < 0) return set_error(SSD_EINVAL, "round_begin: base %d < 0", base);
-  hipLaunchKernelGGL(round_begin_kernel, dim3(1), dim3(128), 0, stream, *tree, *root, base, n_new);
+  SSD_LAUNCH(round_begin_kernel, dim3(1), dim3(128), 0, stream, *tree, *root, base, n_new);
   return check_launch("round_begin");
 }
 
@@ -252,7 +252,7 @@ SSD_API int ssd_tree_level(const SsdTree* tree, int d, const int32_t* cand_tok, 
   if (tree->cap > TREE_CAP) return set_error(SSD_ERANGE, "tree_level: capacity %d > %d", tree->cap, TREE_CAP);
   if (feed && (rows_max > rows->cap || rows_max > TREE_CAP)) return set_error(SSD_ERANGE, "tree_level: rows_max too big");
   SsdRows r = feed ? *rows : SsdRows{};
-  hipLaunchKernelGGL(tree_level_kernel, dim3(1), dim3(1024), 0, stream, *tree, d, cand_tok, cand_lp, k, width, feed,
+  SSD_LAUNCH(tree_level_kernel, dim3(1), dim3(1024), 0, stream, *tree, d, cand_tok, cand_lp, k, width, feed,
                      root_pos, tree_start, past, r, feed ? rows_max : 0);
   return check_launch("tree_level");
 }
@@ -262,7 +262,7 @@ SSD_API int ssd_tree_finalize(const SsdTree* tree, int max_nodes, int committed,
   if (!tree || !root_token || !rows) return set_error(SSD_EINVAL, "tree_finalize: null pointer");
   if (rows_max > rows->cap || rows_max > TREE_CAP + 1 || tree->cap > TREE_CAP)
     return set_error(SSD_ERANGE, "tree_finalize: rows_max %d too big", rows_max);
-  hipLaunchKernelGGL(tree_finalize_kernel, dim3(1), dim3(1024), 0, stream, *tree, max_nodes, committed, root_token,
+  SSD_LAUNCH(tree_finalize_kernel, dim3(1), dim3(1024), 0, stream, *tree, max_nodes, committed, root_token,
                      *rows, rows_max);
   return check_launch("tree_finalize");
 }
@@ -271,7 +271,7 @@ SSD_API int ssd_accept_greedy(const SsdTree* tree, const int32_t* argmax, int co
                               int32_t* keep_src, int32_t* n_keep, int32_t* root_token, hipStream_t stream) {
   if (!tree || !argmax || !result || !keep_src || !n_keep || !root_token)
     return set_error(SSD_EINVAL, "accept_greedy: null pointer");
-  hipLaunchKernelGGL(accept_greedy_kernel, dim3(1), dim3(64), 0, stream, *tree, argmax, committed, result, keep_src,
+  SSD_LAUNCH(accept_greedy_kernel, dim3(1), dim3(64), 0, stream, *tree, argmax, committed, result, keep_src,
                      n_keep, root_token);
   return check_launch("accept_greedy");
 }

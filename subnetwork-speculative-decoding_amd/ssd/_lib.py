@@ -89,6 +89,7 @@ class SsdPrefillBuffers(C.Structure):
 _PROTOS = {
     "ssd_last_error": (C.c_char_p, []),
     "ssd_abi_version": (I32, []),
+    "ssd_launch_count": (U64, []),
     "ssd_build_hash": (C.c_char_p, []),
     "ssd_device_arch": (I32, [C.c_char_p, I32]),
     "ssd_packed_weight_elems": (I64, [I32, I32]),

@@ -14,7 +14,7 @@ HEADER = os.path.join(REPO, "include", "ssd_mi355x.h")
 
 def declared():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:const\s+char\s*\*|int64_t|int)\s+(ssd_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:const\s+char\s*\*|u?int64_t|int)\s+(ssd_\w+)\s*\(", text, re.M)))
 
 
 def test_header_declares_entry_points():

@@ -259,18 +259,45 @@ def test_rmsnorm_and_embed():
     assert torch.equal(out, table[ids.long()])
 
 
-def test_kv_compact_overlapping_and_all_layers():
+@pytest.mark.parametrize("hd,start,src", [
+    (64, 10, [10, 12, 13, 17, 70]),          # overlapping: a destination is a later source
+    (128, 14, [20, 15, 30, 14, 90]),         # the range crosses an 8-slot group of the V runs
+    (128, 61, [61, 70, 64, 100, 127, 66]),   # ... and a 64-slot block
+    (64, 5, [5, 6, 7, 8, 9, 10, 11, 12, 13]),  # in place, 9 entries over two groups
+    (128, 3, []),                             # nothing to move
+])
+def test_kv_compact_overlapping_and_all_layers(hd, start, src):
+    """Compaction (reference ssd/engine/kv_cache.py:54-70) in every layer and kv head, in 16-byte
+    runs of the cache layout, against the oracle; entries outside the moved range keep their
+    values, including the neighbours that share a V run with a moved slot."""
     ops = _ops()
-    L, kvh, hd, S = 3, 2, 64, 128
-    k0 = bf(rand(L, kvh, S, hd, seed=23))
-    v0 = bf(rand(L, kvh, S, hd, seed=24))
+    L, kvh, S = 3, 2, 128
+    k0 = bf(rand(L, kvh, S, hd, seed=23 + hd))
+    v0 = bf(rand(L, kvh, S, hd, seed=24 + hd))
     k, vt = ops.kv_tile(k0.to(DEV), "k"), ops.kv_tile(v0.to(DEV), "v")
     assert torch.equal(ops.kv_untile(k, S, hd, "k").cpu(), k0)  # the layout helpers invert each other
-    src = [10, 12, 13, 17, 70]
-    buf = torch.tensor(src + [33], dtype=torch.int32, device=DEV)  # capacity 6, device count 5
-    ops.kv_compact(k, vt, L, kvh, hd, S, 10, buf, torch.tensor([5], dtype=torch.int32, device=DEV), 6)
-    assert torch.equal(ops.kv_untile(k, S, hd, "k").cpu(), ok.kv_compact(k0, 10, src))
-    assert torch.equal(ops.kv_untile(vt, S, hd, "v").cpu(), ok.kv_compact(v0, 10, src))
+    cap = len(src) + 1
+    buf = torch.tensor(src + [33], dtype=torch.int32, device=DEV)  # capacity len + 1, device count len
+    ops.kv_compact(k, vt, L, kvh, hd, S, start, buf, torch.tensor([len(src)], dtype=torch.int32, device=DEV), cap)
+    assert torch.equal(ops.kv_untile(k, S, hd, "k").cpu(), ok.kv_compact(k0, start, src))
+    assert torch.equal(ops.kv_untile(vt, S, hd, "v").cpu(), ok.kv_compact(v0, start, src))
+
+
+def test_kv_compact_out_of_range_source_keeps_slot():
+    ops = _ops()
+    L, kvh, hd, S = 2, 2, 128, 128
+    k0 = bf(rand(L, kvh, S, hd, seed=41))
+    v0 = bf(rand(L, kvh, S, hd, seed=42))
+    k, vt = ops.kv_tile(k0.to(DEV), "k"), ops.kv_tile(v0.to(DEV), "v")
+    src = [40, -1, 45, 1000]  # entries 1 and 3 stay where they are
+    buf = torch.tensor(src, dtype=torch.int32, device=DEV)
+    ops.kv_compact(k, vt, L, kvh, hd, S, 20, buf, torch.tensor([4], dtype=torch.int32, device=DEV), 4)
+    want_k, want_v = k0.clone(), v0.clone()
+    for i, s in enumerate(src):
+        if 0 <= s < S:
+            want_k[:, :, 20 + i], want_v[:, :, 20 + i] = k0[:, :, s], v0[:, :, s]
+    assert torch.equal(ops.kv_untile(k, S, hd, "k").cpu(), want_k)
+    assert torch.equal(ops.kv_untile(vt, S, hd, "v").cpu(), want_v)
 
 
 def test_row_topk_argmax_and_logsoftmax():
