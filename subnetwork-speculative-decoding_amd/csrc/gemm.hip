@@ -41,8 +41,23 @@ struct GemmLds {
   float rn[CT * 16];     // per-row rsqrt(mean(x^2) + eps)
 };
 
-template <int CT, int NSUB, int KS, int U, int EPI, int NORM>
+// X staged through LDS (gemm_kernel<..., XS = true>): K = 4096 (8 rounds of 16 k-blocks), 8 waves.
+// Each round's rows are copied memory -> LDS by DMA as whole 1 KiB row segments (full 128-byte
+// lines, once per workgroup) instead of each wave loading its 64-byte row pieces itself; rows are
+// XS_ROW bytes apart so the 8 lanes a b128 read serves at a time fall in different banks.
+constexpr int XS_ROUNDS = 8, XS_SLOTS = 2, XS_AHEAD = 3, XS_ROW = 16 * 64 + 16;
+
+template <int KS, int NSUB, int CT, bool XS>
+union GemmSmem {
+  GemmLds<KS, NSUB, CT> g;
+  unsigned char ring[XS ? XS_SLOTS * CT * 16 * XS_ROW : 16];
+};
+
+template <int CT, int NSUB, int KS, int U, int EPI, int NORM, bool XS = false>
 __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
+  static_assert(!XS || KS == 8, "the staged path deals 16 k-blocks per round to 8 waves");
+  __shared__ GemmSmem<KS, NSUB, CT, XS> smem;
+  auto& lds = smem.g;
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
   const int tile = blockIdx.x;
@@ -107,6 +122,59 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
   auto wrap = [&](int kb) { return kb >= kbt ? kb - kbt : kb; };
   auto kb_at = [&](int t) { return wrap(((t >> 1) * KS + w) * 2 + (t & 1) + rot); };
   const int kb_rest = (kbt / (KS * 2)) * KS * 2 + w;
+  if constexpr (XS) {
+    // Round r = k-blocks kb_at(2r), kb_at(2r + 1) of every wave, i.e. 16 consecutive (rotated)
+    // k-blocks. The wave loads its CT*2 rows of round r (one 1 KiB row segment per instruction)
+    // and its weight tiles of round r XS_AHEAD rounds ahead, stores the rows into LDS slot r % 2
+    // one round ahead, and every wave reads its fragments back after the barrier that opens
+    // round r.
+    // The MFMAs and the x^2 sums see the same fragments in the same order as the loop below.
+    constexpr int RPW = CT * 2;  // rows each wave stages per round
+    u32x4_t wv[XS_ROUNDS][2][NSUB], xv[XS_ROUNDS][RPW];
+    auto issue = [&](int r) {
+      const int kb = wrap(r * 16 + (lane >> 2) + rot);
+#pragma unroll
+      for (int i = 0; i < RPW; ++i)
+        xv[r][i] = *(const u32x4_t*)(a.X + (size_t)min(w * RPW + i, a.M - 1) * a.ldx + kb * 32 + (lane & 3) * 8);
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s)
+          wv[r][u][s] = __builtin_nontemporal_load(wp[s] + (size_t)kb_at(2 * r + u) * NSUB * 64);
+    };
+    auto stage = [&](int r) {
+      unsigned char* slot = smem.ring + (r % XS_SLOTS) * CT * 16 * XS_ROW;
+#pragma unroll
+      for (int i = 0; i < RPW; ++i) *(u32x4_t*)(slot + (w * RPW + i) * XS_ROW + lane * 16) = xv[r][i];
+    };
+#pragma unroll
+    for (int r = 0; r < XS_AHEAD; ++r) issue(r);
+    stage(0);
+#pragma unroll
+    for (int r = 0; r < XS_ROUNDS; ++r) {
+      // round r's rows are in LDS (every wave's stores done before the barrier); no memory wait
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if (r + XS_AHEAD < XS_ROUNDS) issue(r + XS_AHEAD);
+      const unsigned char* slot = smem.ring + (r % XS_SLOTS) * CT * 16 * XS_ROW;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        u32x4_t xr[CT];
+#pragma unroll
+        for (int c = 0; c < CT; ++c) xr[c] = *(const u32x4_t*)(slot + (c * 16 + j) * XS_ROW + (2 * w + u) * 64 + g * 16);
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+          for (int c = 0; c < CT; ++c) acc[s][c] = mfma16x16x32(bits_bf16x8(wv[r][u][s]), bits_bf16x8(xr[c]), acc[s][c]);
+        if constexpr (NORM) {
+#pragma unroll
+          for (int c = 0; c < CT; ++c) ss[c] += sumsq8(xr[c]);
+        }
+      }
+      // slot (r + 1) % 2 last held round r - 1, which every wave finished before this barrier
+      if (r + 1 < XS_ROUNDS) stage(r + 1);
+    }
+    __syncthreads();  // the ring is reused for the partial sums below
+  } else {
   int t = 0;
   for (; t + U <= n_full; t += U) {
     u32x4_t wr[U][NSUB], xr[U][CT];
@@ -153,6 +221,7 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
       for (int c = 0; c < CT; ++c) ss[c] += sumsq8(xr[c]);
     }
   }
+  }
 
   // rotary cos/sin of this thread's pairs (issued before the reduction so they overlap it)
   float pre_cs[NSUB], pre_sn[NSUB];
@@ -167,7 +236,6 @@ __global__ __launch_bounds__(64 * KS) void gemm_kernel(GemmArgs a) {
     }
   }
 
-  __shared__ GemmLds<KS, NSUB, CT> lds;
 #pragma unroll
   for (int s = 0; s < NSUB; ++s)
 #pragma unroll
@@ -679,6 +747,21 @@ static int launch_gemm(GemmArgs a, hipStream_t s) {
     }
     const int ct = (b.M + 15) / 16;
     dim3 grid(p.tiles);
+    if (b.kb_total == XS_ROUNDS * 16 && p.ks == 8 && p.nsub <= 2 && ct <= 2) {
+      // K = 4096 narrow projections: x staged through LDS
+#define SSD_GEMM_XS(CT_, NS_)                                                                             \
+  if (ct == CT_ && p.nsub == NS_) {                                                                       \
+    if (b.norm_eps > 0.f)                                                                                 \
+      SSD_LAUNCH((gemm_kernel<CT_, NS_, 8, (CT_ == 1 ? 4 : 2), EPI, 1, true>), grid, dim3(512), 0, s, b); \
+    else                                                                                                  \
+      SSD_LAUNCH((gemm_kernel<CT_, NS_, 8, (CT_ == 1 ? 4 : 2), EPI, 0, true>), grid, dim3(512), 0, s, b); \
+  }
+      SSD_GEMM_XS(1, 1) SSD_GEMM_XS(1, 2) SSD_GEMM_XS(2, 1) SSD_GEMM_XS(2, 2)
+#undef SSD_GEMM_XS
+      int rc = check_launch("gemm");
+      if (rc) return rc;
+      continue;
+    }
 #define SSD_GEMM_CASE(CT_, NS_, KS_) \
   if (ct == CT_ && p.nsub == NS_ && p.ks == KS_) {                                                             \
     if (b.norm_eps > 0.f)                                                                                      \
