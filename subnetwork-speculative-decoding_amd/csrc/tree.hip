@@ -98,24 +98,35 @@ __global__ __launch_bounds__(1024) void tree_level_kernel(SsdTree t, int d, cons
   }
 }
 
+// The tree (scores, depths, parents: at most TREE_CAP entries) is staged in LDS with one load per
+// field and thread, issued together with the node count's, so the rank, the ancestor closure and the
+// renumbering run on LDS instead of chains of dependent global loads.
 __global__ __launch_bounds__(1024) void tree_finalize_kernel(SsdTree t, int max_nodes, int committed,
                                                              const int* __restrict__ root_token, SsdRows rows,
                                                              int rows_max) {
   __shared__ int keep[TREE_CAP];
   __shared__ int newidx[TREE_CAP];
-  const int n = t.meta[0];
+  __shared__ double s_sc[TREE_CAP];
+  __shared__ int s_dep[TREE_CAP], s_par[TREE_CAP], s_vdep[TREE_CAP], s_vpar[TREE_CAP], s_vtok[TREE_CAP];
   const int i = threadIdx.x;
+  const int li = min(i, t.cap - 1);  // valid index for every thread (values past n are unused)
+  const int root = *root_token;
+  const int n = min(t.meta[0], t.cap);
+  const double sc_i = t.scores[li];
+  const int dep_i = t.depths[li], par_i = t.parents[li], tok_i = t.tokens[li], rank_i = t.ranks[li];
+  s_sc[i] = sc_i;
+  s_dep[i] = dep_i;
+  s_par[i] = par_i;
+  __syncthreads();
   const bool prune = max_nodes > 0 && n > max_nodes;
   if (i < n) {
     int k = 1;
     if (prune) {
-      const double s = t.scores[i];
-      const int dep = t.depths[i];
       int rank = 0;
       for (int o = 0; o < n; ++o) {
-        const double so = t.scores[o];
-        const int dpo = t.depths[o];
-        if (so > s || (so == s && (dpo < dep || (dpo == dep && o < i)))) ++rank;
+        const double so = s_sc[o];
+        const int dpo = s_dep[o];
+        if (so > sc_i || (so == sc_i && (dpo < dep_i || (dpo == dep_i && o < i)))) ++rank;
       }
       k = rank < max_nodes;
     }
@@ -124,10 +135,10 @@ __global__ __launch_bounds__(1024) void tree_finalize_kernel(SsdTree t, int max_
   __syncthreads();
   // Ancestor closure (a no-op unless float ties broke it; kept for parity with the reference).
   if (i < n && keep[i]) {
-    int p = t.parents[i];
+    int p = par_i;
     for (int step = 0; p >= 0 && p < n && step < TREE_MAXDEPTH; ++step) {
       keep[p] = 1;
-      p = t.parents[p];
+      p = s_par[p];
     }
   }
   __syncthreads();
@@ -141,12 +152,15 @@ __global__ __launch_bounds__(1024) void tree_finalize_kernel(SsdTree t, int max_
   for (int o = 0; o < n; ++o) vn += keep[o];
   if (i < n && keep[i]) {
     const int v = newidx[i];
-    t.vtokens[v] = t.tokens[i];
-    const int p = t.parents[i];
-    t.vparents[v] = p < 0 ? -1 : newidx[p];
-    t.vdepths[v] = t.depths[i];
-    t.vranks[v] = t.ranks[i];
+    const int vp = par_i < 0 ? -1 : newidx[par_i];
+    t.vtokens[v] = tok_i;
+    t.vparents[v] = vp;
+    t.vdepths[v] = dep_i;
+    t.vranks[v] = rank_i;
     t.vorig[v] = i;
+    s_vpar[v] = vp;
+    s_vdep[v] = dep_i;
+    s_vtok[v] = tok_i;
   }
   if (i == 0) t.vmeta[0] = vn;
   __syncthreads();
@@ -156,19 +170,19 @@ __global__ __launch_bounds__(1024) void tree_finalize_kernel(SsdTree t, int max_
     rows.prefix[i] = committed + 1;
     int* anc = rows.anc + (size_t)i * ROW_MAXD;
     if (i == 0) {
-      rows.ids[0] = *root_token;
+      rows.ids[0] = root;
       rows.pos[0] = committed;
       rows.depth[0] = 0;
     } else if (i <= vn) {
       const int v = i - 1;
-      const int dep = t.vdepths[v];
-      rows.ids[i] = t.vtokens[v];
+      const int dep = s_vdep[v];
+      rows.ids[i] = s_vtok[v];
       rows.pos[i] = committed + dep;
       rows.depth[i] = dep;
       int cur = v;
       for (int q = min(dep, ROW_MAXD) - 1; q >= 0 && cur >= 0; --q) {
         anc[q] = committed + 1 + cur;
-        cur = t.vparents[cur];
+        cur = s_vpar[cur];
       }
     } else {
       rows.ids[i] = 0;
@@ -260,6 +274,7 @@ SSD_API int ssd_tree_level(const SsdTree* tree, int d, const int32_t* cand_tok, 
 SSD_API int ssd_tree_finalize(const SsdTree* tree, int max_nodes, int committed, const int32_t* root_token,
                               const SsdRows* rows, int rows_max, hipStream_t stream) {
   if (!tree || !root_token || !rows) return set_error(SSD_EINVAL, "tree_finalize: null pointer");
+  if (tree->cap < 1) return set_error(SSD_EINVAL, "tree_finalize: tree capacity %d", tree->cap);
   if (rows_max > rows->cap || rows_max > TREE_CAP + 1 || tree->cap > TREE_CAP)
     return set_error(SSD_ERANGE, "tree_finalize: rows_max %d too big", rows_max);
   SSD_LAUNCH(tree_finalize_kernel, dim3(1), dim3(1024), 0, stream, *tree, max_nodes, committed, root_token,
