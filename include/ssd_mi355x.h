@@ -207,6 +207,11 @@ int ssd_row_topk_bf16(const uint16_t* logits, int64_t ld, int M, int N, int k, i
 int ssd_row_topk_bf16_noalloc(const uint16_t* logits, int64_t ld, int M, int N, int k, int mode,
                               const int32_t* vocab_ids, int32_t* out_tok, float* out_val, float* out_lse,
                               hipStream_t stream);
+/* The chunk pass of ssd_row_topk_bf16 alone: fills ws (ssd_row_topk_ws_bytes(M, N) bytes) with each
+ * row's 4096-column chunk records, for ssd_tree_level_topk to merge (the first half of the
+ * proposal step, ssd/engine/tree_drafter.py:129-133). */
+int ssd_row_topk_partial_bf16(const uint16_t* logits, int64_t ld, int M, int N, int k, int mode, void* ws,
+                              int64_t ws_bytes, hipStream_t stream);
 
 /* ------------------------------------------------------------------ tree
  * Device-resident DraftTree (ssd/engine/tree_drafter.py:48-95). All members are device
@@ -259,6 +264,14 @@ int ssd_round_begin(const SsdTree* tree, const SsdRows* root, int base, const in
 int ssd_tree_level(const SsdTree* tree, int d, const int32_t* cand_tok, const float* cand_lp, int F_max, int k,
                    int width, int feed, int root_pos, int tree_start, int past, const SsdRows* rows, int rows_max,
                    hipStream_t stream);
+/* ssd_tree_level whose candidates are merged in the same launch from the F_max rows of chunk
+ * records that ssd_row_topk_partial_bf16 (k, mode 1: log-softmax) left in parts: the greedy
+ * proposal's merge (ssd/engine/tree_drafter.py:129-133) and the level expansion
+ * (:165-183) in one launch; identical results to ssd_row_topk_bf16 followed by ssd_tree_level.
+ * N: the logits' columns; vocab_ids as for ssd_row_topk_bf16 (null: identity). */
+int ssd_tree_level_topk(const SsdTree* tree, int d, const void* parts, int64_t parts_bytes, int N,
+                        const int32_t* vocab_ids, int F_max, int k, int width, int feed, int root_pos, int tree_start,
+                        int past, const SsdRows* rows, int rows_max, hipStream_t stream);
 
 /* max_nodes cut by (-score, depth), ancestor closure and renumbering (ssd/engine/tree_drafter.py:202-207),
  * then the verify rows of verify_inputs (ssd/engine/verify.py:32-42); root token read from device. */

@@ -4,6 +4,7 @@
 // Every reduction runs in a fixed order that depends only on the row length,
 // so each row's result is independent of how many rows share the launch.
 #include "common.h"
+#include "topk.h"
 
 #include <math.h>
 
@@ -195,40 +196,6 @@ __global__ __launch_bounds__(256) void kv_compact_kernel(bf16_t* __restrict__ kc
   }
 }
 
-constexpr int TOPK_MAX = 16;
-constexpr int TOPK_CHUNK = 4096;  // columns per partial workgroup: 256 threads x 16 columns
-constexpr int TOPK_PER = TOPK_CHUNK / 256;
-
-// Ranking key of a (value, column) pair: a larger key ranks first, i.e. larger value, then
-// lower column (the oracle's stable-sort order). The value maps to its order-preserving
-// unsigned image; NaN ranks below every number; key 0 is "no candidate".
-__device__ __forceinline__ uint64_t rank_key(float v, int col) {
-  uint32_t b = __float_as_uint(v);
-  b = (v != v) ? 0u : ((b & 0x80000000u) ? ~b : (b | 0x80000000u));
-  return ((uint64_t)b << 32) | (uint32_t)(~(uint32_t)col);
-}
-__device__ __forceinline__ float key_value(uint64_t key) {
-  const uint32_t b = (uint32_t)(key >> 32);
-  return __uint_as_float((b & 0x80000000u) ? (b & 0x7fffffffu) : ~b);
-}
-__device__ __forceinline__ int key_col(uint64_t key) { return (int)~(uint32_t)key; }
-
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const uint32_t lo = __shfl_xor((uint32_t)v, off), hi = __shfl_xor((uint32_t)(v >> 32), off);
-    const uint64_t o = ((uint64_t)hi << 32) | lo;
-    v = o > v ? o : v;
-  }
-  return v;
-}
-
-struct TopkPart {
-  float mx;  // chunk maximum
-  float se;  // sum of exp(x - mx) over the chunk (mode 1)
-  uint64_t key[TOPK_MAX];  // the chunk's k best, best first
-};
-
 // Partial pass: workgroup (s, row) holds columns [s*4096, (s+1)*4096) of one row of bf16 logits
 // in registers (thread t: columns t*8 + [0, 8) and 2048 + t*8 + [0, 8) of the chunk) and takes
 // its k best keys in k rounds of a block-wide maximum, each round retiring the winner; it also
@@ -288,49 +255,13 @@ __global__ __launch_bounds__(256) void row_topk_partial_kernel(const bf16_t* __r
   if (threadIdx.x == 0) { out->mx = mx; out->se = se; }
 }
 
-// Merge pass, one wave per row: global max M; logsumexp = M + log(sum_s se_s * exp(mx_s - M))
-// (lanes own chunks; fixed butterfly order); the k best of the S*k chunk keys, held in
-// registers (lane l: candidates l + 64*j), in k rounds of a wave maximum.
-// mode 0 writes raw values, mode 1 log-softmax values (x - M) - log(sum).
+// Merge pass, one wave per row (topk_merge_row).
 __global__ __launch_bounds__(64) void row_topk_merge_kernel(const TopkPart* __restrict__ parts, int S, int k, int mode,
                                                             const int* __restrict__ vocab_ids, int* __restrict__ out_tok,
                                                             float* __restrict__ out_val, float* __restrict__ out_lse) {
-  const int row = blockIdx.x, lane = threadIdx.x;
-  const TopkPart* p = parts + (size_t)row * S;
-  float mx = -INFINITY;
-  for (int s = lane; s < S; s += 64) mx = fmaxf(mx, p[s].mx);
-  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-  float lse = 0.f;
-  if (mode == 1) {
-    float acc = 0.f;
-    for (int s = lane; s < S; s += 64) acc += p[s].se * __expf(p[s].mx - mx);
-    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
-    lse = logf(acc);
-  }
-  const int total = S * k;  // <= 64 * TOPK_MAX
-  uint64_t key[TOPK_MAX];
-#pragma unroll
-  for (int j = 0; j < TOPK_MAX; ++j) {
-    const int c = lane + 64 * j;
-    key[j] = c < total ? p[c / k].key[c % k] : 0ull;
-  }
-  uint32_t taken = 0;
-  for (int q = 0; q < k; ++q) {
-    uint64_t b = 0;
-    int bj = -1;
-#pragma unroll
-    for (int j = 0; j < TOPK_MAX; ++j)
-      if (!((taken >> j) & 1u) && key[j] > b) { b = key[j]; bj = j; }
-    const uint64_t m = wave_max_u64(b);
-    if (bj >= 0 && b == m) taken |= 1u << bj;
-    if (lane == 0) {
-      const int col = key_col(m);
-      const float v = key_value(m);
-      out_tok[row * k + q] = vocab_ids ? vocab_ids[col] : col;
-      if (out_val) out_val[row * k + q] = mode == 1 ? (v - mx) - lse : v;
-    }
-  }
-  if (lane == 0 && mode == 1 && out_lse) out_lse[row] = mx + lse;
+  const int row = blockIdx.x;
+  topk_merge_row(parts + (size_t)row * S, S, k, mode, vocab_ids, threadIdx.x, out_tok + row * k,
+                 out_val ? out_val + row * k : nullptr, out_lse ? out_lse + row : nullptr);
 }
 
 }  // namespace ssd
@@ -395,6 +326,24 @@ static int row_topk_check(const uint16_t* logits, int64_t ld, int N, int k, int 
   if ((N + TOPK_CHUNK - 1) / TOPK_CHUNK > 64)
     return set_error(SSD_ERANGE, "row_topk: N=%d above %d columns", N, 64 * TOPK_CHUNK);
   return SSD_OK;
+}
+
+// The partial pass alone: the chunk records of ssd_row_topk_bf16's workspace, for a consumer that
+// merges them itself (ssd_tree_level_topk).
+SSD_API int ssd_row_topk_partial_bf16(const uint16_t* logits, int64_t ld, int M, int N, int k, int mode, void* ws,
+                                      int64_t ws_bytes, hipStream_t stream) {
+  if (M < 0 || !ws) return set_error(SSD_EINVAL, "row_topk_partial: bad arguments (M=%d, workspace %p)", M, ws);
+  if (!logits || N <= 0 || k < 1 || k > TOPK_MAX || k > N || (mode != 0 && mode != 1))
+    return set_error(SSD_EINVAL, "row_topk_partial: bad arguments (k=%d, N=%d, mode=%d)", k, N, mode);
+  if (ld % 8 || ((uintptr_t)logits & 15))
+    return set_error(SSD_EINVAL, "row_topk_partial: logits must be 16-byte aligned");
+  const int S = (N + TOPK_CHUNK - 1) / TOPK_CHUNK;
+  if (S > 64) return set_error(SSD_ERANGE, "row_topk_partial: N=%d above %d columns", N, 64 * TOPK_CHUNK);
+  if (ws_bytes < ssd_row_topk_ws_bytes(M, N)) return set_error(SSD_EINVAL, "row_topk_partial: workspace too small");
+  if (M == 0) return SSD_OK;
+  SSD_LAUNCH(row_topk_partial_kernel, dim3(S, M), dim3(256), 0, stream, (const bf16_t*)logits, ld, N, k, mode,
+             (TopkPart*)ws);
+  return check_launch("row_topk_partial");
 }
 
 SSD_API int ssd_row_topk_bf16(const uint16_t* logits, int64_t ld, int M, int N, int k, int mode,

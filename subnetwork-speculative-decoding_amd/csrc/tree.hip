@@ -16,6 +16,7 @@
 // thread compares its candidate against all others), which is exact and
 // deterministic.
 #include "common.h"
+#include "topk.h"
 
 #include <math.h>
 
@@ -29,47 +30,67 @@ constexpr int ROW_MAXD = 32;  // ancestors per row (matches the attention gather
 
 namespace ssd {
 
-__global__ __launch_bounds__(1024) void tree_level_kernel(SsdTree t, int d, const int* __restrict__ cand_tok,
-                                                          const float* __restrict__ cand_lp, int k, int width,
-                                                          int feed, int root_pos, int tree_start, int past,
-                                                          SsdRows rows, int rows_max) {
-  __shared__ double sc[TREE_CAP];
-  __shared__ int vd[TREE_CAP];
-  __shared__ int s_nvalid;
-  const int n0 = t.meta[0];
-  const int F = d == 0 ? 1 : t.meta[1 + TREE_MAXDEPTH + (d - 1)];
-  const int prev_start = d == 0 ? 0 : t.meta[1 + (d - 1)];
+// Level d's expansion from its candidates (cand_tok / cand_lp: frontier node f's k proposals at
+// f*k .. f*k + k - 1, in global memory or LDS). The tree's parents, draft slots and scores are
+// staged in LDS at the start (one load per thread, with the level counts), and the new nodes are
+// mirrored there, so the parents' scores and the fed rows' ancestor walks read LDS instead of
+// chains of dependent global loads. tree_level_stage must run first (before a barrier).
+struct TreeLevelLds {
+  double sc[TREE_CAP];   // candidate scores
+  int vd[TREE_CAP];      // candidate valid
+  double tsc[TREE_CAP];  // tree node scores
+  int par[TREE_CAP];     // tree node parents
+  int dpos[TREE_CAP];    // tree node draft slots
+  int tok[TREE_CAP];     // new node j's token (this level)
+  int nvalid;
+};
+
+__device__ __forceinline__ void tree_level_stage(const SsdTree& t, TreeLevelLds& L) {
+  const int i = threadIdx.x, li = min(i, t.cap - 1);
+  L.tsc[i] = t.scores[li];
+  L.par[i] = t.parents[li];
+  L.dpos[i] = t.draft_pos[li];
+  if (i == 0) L.nvalid = 0;
+}
+
+__device__ __forceinline__ void tree_level_body(SsdTree t, int d, const int* cand_tok, const float* cand_lp, int k,
+                                                int width, int feed, int root_pos, int tree_start, int past,
+                                                SsdRows rows, int rows_max, int n0, int F, int prev_start,
+                                                TreeLevelLds& L) {
   const int C = F * k;
   const int c = threadIdx.x;
-  if (c == 0) s_nvalid = 0;
   int parent = -1, tok = -1;
   double score = -INFINITY;
   if (c < C) {
     const int f = c / k;
     parent = d == 0 ? -1 : prev_start + f;
     tok = cand_tok[c];
-    if (tok >= 0) score = (parent < 0 ? 0.0 : t.scores[parent]) + (double)cand_lp[c];
-    sc[c] = score;
-    vd[c] = tok >= 0;
+    if (tok >= 0) score = (parent < 0 ? 0.0 : L.tsc[parent]) + (double)cand_lp[c];
+    L.sc[c] = score;
+    L.vd[c] = tok >= 0;
   }
   __syncthreads();
-  if (c < C && tok >= 0) atomicAdd(&s_nvalid, 1);
+  if (c < C && tok >= 0) atomicAdd(&L.nvalid, 1);
   int rank = 0;
   if (c < C && tok >= 0) {
     for (int o = 0; o < C; ++o)
-      if (vd[o] && (sc[o] > score || (sc[o] == score && o < c))) ++rank;
+      if (L.vd[o] && (L.sc[o] > score || (L.sc[o] == score && o < c))) ++rank;
   }
   __syncthreads();
-  const int nvalid = s_nvalid;
+  const int nvalid = L.nvalid;
   const int n_level = (width > 0 && width < nvalid) ? width : nvalid;
   if (c < C && tok >= 0 && rank < n_level && n0 + rank < t.cap) {
     const int node = n0 + rank;
+    const int dp = feed ? past + rank : -1;
     t.tokens[node] = tok;
     t.parents[node] = parent;
     t.depths[node] = d + 1;
     t.scores[node] = score;
     t.ranks[node] = c % k;
-    t.draft_pos[node] = feed ? past + rank : -1;
+    t.draft_pos[node] = dp;
+    L.par[node] = parent;
+    L.dpos[node] = dp;
+    L.tok[rank] = tok;
   }
   __syncthreads();
   if (c == 0) {
@@ -85,17 +106,58 @@ __global__ __launch_bounds__(1024) void tree_level_kernel(SsdTree t, int d, cons
     int* anc = rows.anc + (size_t)j * ROW_MAXD;
     if (j < n_level && n0 + j < t.cap) {
       int cur = n0 + j;
-      rows.ids[j] = t.tokens[cur];
+      rows.ids[j] = L.tok[j];
       rows.depth[j] = d + 1;
       for (int i = d; i >= 0 && cur >= 0; --i) {
-        anc[i] = t.draft_pos[cur];
-        cur = t.parents[cur];
+        anc[i] = L.dpos[cur];
+        cur = L.par[cur];
       }
     } else {  // padding row (fewer candidates than the launch assumed): attends the prefix only
       rows.ids[j] = 0;
       rows.depth[j] = 0;
     }
   }
+}
+
+// Level counts: n0 nodes so far, F frontier nodes (level d - 1) starting at prev_start.
+__device__ __forceinline__ void tree_level_counts(const SsdTree& t, int d, int& n0, int& F, int& prev_start) {
+  n0 = t.meta[0];
+  F = d == 0 ? 1 : t.meta[1 + TREE_MAXDEPTH + (d - 1)];
+  prev_start = d == 0 ? 0 : t.meta[1 + (d - 1)];
+}
+
+__global__ __launch_bounds__(1024) void tree_level_kernel(SsdTree t, int d, const int* __restrict__ cand_tok,
+                                                          const float* __restrict__ cand_lp, int k, int width,
+                                                          int feed, int root_pos, int tree_start, int past,
+                                                          SsdRows rows, int rows_max) {
+  __shared__ TreeLevelLds L;
+  int n0, F, prev_start;
+  tree_level_counts(t, d, n0, F, prev_start);
+  tree_level_stage(t, L);
+  __syncthreads();
+  tree_level_body(t, d, cand_tok, cand_lp, k, width, feed, root_pos, tree_start, past, rows, rows_max, n0, F,
+                  prev_start, L);
+}
+
+// The same expansion with the proposals' top-k merge in front: wave w merges the chunk partials
+// of frontier rows w, w + 16, ... (topk_merge_row, log-softmax values, vocab_ids mapping) into
+// LDS, exactly as row_topk_merge_kernel would write them to memory.
+__global__ __launch_bounds__(1024) void tree_level_topk_kernel(SsdTree t, int d, const TopkPart* __restrict__ parts,
+                                                               int S, int f_rows, const int* __restrict__ vocab_ids,
+                                                               int k, int width, int feed, int root_pos,
+                                                               int tree_start, int past, SsdRows rows, int rows_max) {
+  __shared__ int s_tok[TREE_CAP];
+  __shared__ float s_lp[TREE_CAP];
+  __shared__ TreeLevelLds L;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int n0, F, prev_start;
+  tree_level_counts(t, d, n0, F, prev_start);
+  tree_level_stage(t, L);
+  for (int f = w; f < f_rows; f += 16)
+    topk_merge_row(parts + (size_t)f * S, S, k, 1, vocab_ids, lane, s_tok + f * k, s_lp + f * k, nullptr);
+  __syncthreads();
+  tree_level_body(t, d, s_tok, s_lp, k, width, feed, root_pos, tree_start, past, rows, rows_max, n0, F, prev_start,
+                  L);
 }
 
 // The tree (scores, depths, parents: at most TREE_CAP entries) is staged in LDS with one load per
@@ -257,13 +319,38 @@ SSD_API int ssd_tree_limits(int32_t* out) {
   return SSD_OK;
 }
 
+SSD_API int ssd_tree_level_topk(const SsdTree* tree, int d, const void* parts, int64_t parts_bytes, int N,
+                                const int32_t* vocab_ids, int F_max, int k, int width, int feed, int root_pos,
+                                int tree_start, int past, const SsdRows* rows, int rows_max, hipStream_t stream) {
+  if (!tree || !parts || (feed && !rows)) return set_error(SSD_EINVAL, "tree_level_topk: null pointer");
+  if (d < 0 || d >= TREE_MAXDEPTH || d + 1 > ROW_MAXD)
+    return set_error(SSD_ERANGE, "tree_level_topk: depth %d too deep", d);
+  if (F_max < 1 || k < 1 || k > TOPK_MAX || F_max * k > TREE_CAP)
+    return set_error(SSD_ERANGE, "tree_level_topk: %d x %d candidates (k <= %d, total <= %d)", F_max, k, TOPK_MAX,
+                     TREE_CAP);
+  const int S = (N + TOPK_CHUNK - 1) / TOPK_CHUNK;
+  if (N < k || S > 64) return set_error(SSD_EINVAL, "tree_level_topk: N=%d", N);
+  if (parts_bytes < (int64_t)F_max * S * (int64_t)sizeof(TopkPart))
+    return set_error(SSD_EINVAL, "tree_level_topk: partials of %lld bytes < %lld", (long long)parts_bytes,
+                     (long long)F_max * S * (long long)sizeof(TopkPart));
+  if (tree->cap > TREE_CAP || tree->cap < 1)
+    return set_error(SSD_ERANGE, "tree_level_topk: capacity %d outside [1, %d]", tree->cap, TREE_CAP);
+  if (feed && (rows_max > rows->cap || rows_max > TREE_CAP))
+    return set_error(SSD_ERANGE, "tree_level_topk: rows_max too big");
+  SsdRows r = feed ? *rows : SsdRows{};
+  SSD_LAUNCH(tree_level_topk_kernel, dim3(1), dim3(1024), 0, stream, *tree, d, (const TopkPart*)parts, S, F_max,
+             vocab_ids, k, width, feed, root_pos, tree_start, past, r, feed ? rows_max : 0);
+  return check_launch("tree_level_topk");
+}
+
 SSD_API int ssd_tree_level(const SsdTree* tree, int d, const int32_t* cand_tok, const float* cand_lp, int F_max,
                            int k, int width, int feed, int root_pos, int tree_start, int past, const SsdRows* rows,
                            int rows_max, hipStream_t stream) {
   if (!tree || !cand_tok || !cand_lp || (feed && !rows)) return set_error(SSD_EINVAL, "tree_level: null pointer");
   if (d < 0 || d >= TREE_MAXDEPTH || d + 1 > ROW_MAXD) return set_error(SSD_ERANGE, "tree_level: depth %d too deep", d);
   if (F_max * k > TREE_CAP || k < 1) return set_error(SSD_ERANGE, "tree_level: %d x %d candidates > %d", F_max, k, TREE_CAP);
-  if (tree->cap > TREE_CAP) return set_error(SSD_ERANGE, "tree_level: capacity %d > %d", tree->cap, TREE_CAP);
+  if (tree->cap > TREE_CAP || tree->cap < 1)
+    return set_error(SSD_ERANGE, "tree_level: capacity %d outside [1, %d]", tree->cap, TREE_CAP);
   if (feed && (rows_max > rows->cap || rows_max > TREE_CAP)) return set_error(SSD_ERANGE, "tree_level: rows_max too big");
   SsdRows r = feed ? *rows : SsdRows{};
   SSD_LAUNCH(tree_level_kernel, dim3(1), dim3(1024), 0, stream, *tree, d, cand_tok, cand_lp, k, width, feed,

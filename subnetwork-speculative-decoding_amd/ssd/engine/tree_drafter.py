@@ -147,6 +147,9 @@ class TreeDrafter:
             raise ValueError(f"tree of {sum(self.levels)} nodes exceeds {TREE_CAP}")
         if self.max_verify_nodes() + 1 > ROW_CAP:
             raise ValueError(f"{self.max_verify_nodes()} verify nodes > {ROW_CAP - 1}; set drafting.max_nodes")
+        # greedy proposals: the chunk records of the last proposal, merged by the next level's launch
+        self._parts: Optional[torch.Tensor] = None
+        self._parts_n = 0
 
     def max_nodes_per_level(self) -> list:
         return self.cfg.level_sizes()
@@ -162,8 +165,14 @@ class TreeDrafter:
     # ------------------------------------------------------------------ device
     def _propose(self, logits, rows: int, d: int, tree: DeviceTree, cand_tok, cand_lp, sampler) -> None:
         if self.greedy:
-            ops.row_topk(logits, rows, logits.shape[1], self.branch[d], 1, self.draft._vocab_ids_i32, cand_tok,
-                         cand_lp)
+            # log-softmax top-k (tree_drafter.py:129-133 of the reference) in two halves: the chunk
+            # pass here, the merge inside the next level's expansion (ssd_tree_level_topk)
+            n = logits.shape[1]
+            need = ops.row_topk_ws_bytes(max([1] + self.levels), n)
+            if self._parts is None or self._parts.numel() < need or self._parts.device != logits.device:
+                self._parts = torch.empty(need, dtype=torch.uint8, device=logits.device)
+            ops.row_topk_partial(logits, rows, n, self.branch[d], 1, self._parts)
+            self._parts_n = n
         else:
             sampler.propose(self.draft, logits, rows, d, self.branch[d], tree.meta, cand_tok, cand_lp)
 
@@ -194,9 +203,16 @@ class TreeDrafter:
             feed = d < self.cfg.depth - 1
             f_max = 1 if d == 0 else self.levels[d - 1]
             m = self.levels[d]
-            _lib.call("ssd_tree_level", tree.struct, d, cand_tok.data_ptr(), cand_lp.data_ptr(), f_max,
-                      self.branch[d], self.width[d] or 0, int(feed), root_pos, tree_start, past,
-                      level_rows.struct, m if feed else 0, ops.stream())
+            if self.greedy:
+                vocab_ids = self.draft._vocab_ids_i32
+                _lib.call("ssd_tree_level_topk", tree.struct, d, self._parts.data_ptr(), self._parts.numel(),
+                          self._parts_n, None if vocab_ids is None else vocab_ids.data_ptr(), f_max, self.branch[d],
+                          self.width[d] or 0, int(feed), root_pos, tree_start, past, level_rows.struct,
+                          m if feed else 0, ops.stream())
+            else:
+                _lib.call("ssd_tree_level", tree.struct, d, cand_tok.data_ptr(), cand_lp.data_ptr(), f_max,
+                          self.branch[d], self.width[d] or 0, int(feed), root_pos, tree_start, past,
+                          level_rows.struct, m if feed else 0, ops.stream())
             if not feed:
                 break
             logits = self.draft.forward_rows(level_rows, m, tree_start, tree_start + d + 1, cache, ws)

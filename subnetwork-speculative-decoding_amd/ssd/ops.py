@@ -299,6 +299,19 @@ def row_topk(logits, m, n, k, mode, vocab_ids, out_tok, out_val=None, out_lse=No
               out_tok.data_ptr(), _p(out_val), _p(out_lse), ws.data_ptr(), ws.numel(), stream())
 
 
+def row_topk_ws_bytes(m: int, n: int) -> int:
+    return int(_lib.load().ssd_row_topk_ws_bytes(m, n))
+
+
+def row_topk_partial(logits, m, n, k, mode, parts):
+    """The chunk pass of row_topk alone: each row's 4096-column chunk records into ``parts`` (a uint8
+    tensor of row_topk_ws_bytes(m, n) bytes), for ssd_tree_level_topk to merge."""
+    _check(logits, "logits"); _check(parts, "parts", torch.uint8)
+    _len(parts, "parts", row_topk_ws_bytes(m, n))
+    _lib.call("ssd_row_topk_partial_bf16", logits.data_ptr(), _rows(logits, "logits", n, m), m, n, k, mode,
+              parts.data_ptr(), parts.numel(), stream())
+
+
 # ------------------------------------------------------------------ split-K GEMMs
 def gemm_splits(n: int, k: int) -> int:
     s = int(_lib.load().ssd_gemm_splits(n, k))

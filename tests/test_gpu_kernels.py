@@ -496,6 +496,54 @@ def test_tree_level_and_finalize_match_oracle(seed):
         assert attended == torch.nonzero(mask[r]).flatten().tolist()
 
 
+@pytest.mark.parametrize("seed,V,mapped", [(0, 128256, False), (1, 5000, True), (2, 32768, True), (3, 72, False)])
+def test_tree_level_topk_equals_topk_then_level(seed, V, mapped):
+    """The greedy proposal's merge done inside the level launch (ssd_row_topk_partial_bf16 +
+    ssd_tree_level_topk) builds the same tree and draft rows as ssd_row_topk_bf16 +
+    ssd_tree_level, level by level, including ties between logits and a vocabulary-subset mapping."""
+    from ssd import _lib, ops
+    from ssd.models.subnetwork_draft import Rows
+
+    rng = random.Random(seed)
+    g = torch.Generator().manual_seed(seed)
+    depth = 4
+    branch = [3, 2, 2, 1] if seed % 2 == 0 else [4, 3, 2, 2]
+    width = [None, 4, 5, None] if seed % 2 else [None, None, 8, 6]
+    committed, tree_start = 40, 41
+    vocab_ids = torch.randperm(128256, generator=g)[:V].to(torch.int32).to(DEV) if mapped else None
+    trees = [_device_tree(), _device_tree()]
+    rows = [Rows(64, DEV), Rows(64, DEV)]
+    ct = torch.zeros(1024, dtype=torch.int32, device=DEV)
+    cl = torch.zeros(1024, dtype=torch.float32, device=DEV)
+    F, past = 1, tree_start
+    for d in range(depth):
+        k = branch[d]
+        # logits on a coarse grid so that exact ties occur across chunks and rows
+        logits = bf(torch.randint(-40, 8, (F, V), generator=g).float() * 0.25).to(DEV)
+        feed = d < depth - 1
+        m = min(F * k, width[d] or F * k)
+        ops.row_topk(logits, F, V, k, 1, vocab_ids, ct, cl)
+        _lib.call("ssd_tree_level", trees[0].struct, d, ct.data_ptr(), cl.data_ptr(), F, k, width[d] or 0, int(feed),
+                  committed, tree_start, past, rows[0].struct, m if feed else 0, ops.stream())
+        parts = torch.empty(ops.row_topk_ws_bytes(F, V), dtype=torch.uint8, device=DEV)
+        ops.row_topk_partial(logits, F, V, k, 1, parts)
+        _lib.call("ssd_tree_level_topk", trees[1].struct, d, parts.data_ptr(), parts.numel(), V,
+                  None if vocab_ids is None else vocab_ids.data_ptr(), F, k, width[d] or 0, int(feed), committed,
+                  tree_start, past, rows[1].struct, m if feed else 0, ops.stream())
+        torch.cuda.synchronize()
+        if feed:
+            for name in ("ids", "pos", "slot", "prefix", "depth"):
+                assert getattr(rows[0], name)[:m].tolist() == getattr(rows[1], name)[:m].tolist(), (d, name)
+            assert rows[0].anc[:m, :d + 1].tolist() == rows[1].anc[:m, :d + 1].tolist()
+            past += m
+        F = m
+    n = int(trees[0].meta[0])
+    assert n == int(trees[1].meta[0]) and n > 0
+    for name in ("tokens", "parents", "depths", "scores", "ranks", "draft_pos"):
+        assert getattr(trees[0], name)[:n].tolist() == getattr(trees[1], name)[:n].tolist(), name
+    assert trees[0].meta.tolist() == trees[1].meta.tolist()
+
+
 @pytest.mark.parametrize("seed", range(5))
 def test_accept_greedy_matches_oracle(seed):
     from ssd import _lib, ops
