@@ -600,12 +600,13 @@ def _exact_norm_linear(h, g, eps, w):
 
 
 @pytest.mark.parametrize("m", [1, 25, 64, 70])
-@pytest.mark.parametrize("n,k", [(1040, 2048), (16384, 4096), (128256, 512)])
+@pytest.mark.parametrize("n,k", [(1040, 2048), (16384, 4096), (128256, 512), (6144, 4096), (4096, 4096)])
 def test_gemm_folded_rmsnorm(m, n, k):
     """RMSNorm folded into the GEMM (norm weight in the packed columns, row scale computed in the
     kernel) against the exact norm + linear (abs/rel 2e-2, the per-node logit tolerance) and
     against the reference's bf16 chain (oracle rmsnorm then linear) for >= 99% of outputs;
-    batch-invariant bitwise."""
+    batch-invariant bitwise. K = 4096 with N < 16384 and up to 32 rows takes the path with the
+    activations staged through LDS (q/k/v- and bridge-shaped projections)."""
     ops = _ops()
     h = bf(rand(m, k, std=3.0, seed=60))
     g = bf(1 + rand(k, std=0.2, seed=61))
