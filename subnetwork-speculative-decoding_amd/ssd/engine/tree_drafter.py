@@ -6,11 +6,12 @@ depth d every kept node proposes ``branch[d]`` children (top log-probs for greed
 fed through the draft in one batched forward where each attends to the committed prefix
 and its own ancestors; finally the best ``max_nodes`` nodes go to verification.
 
-Here every step of that loop is a kernel: the draft forward, the draft head with the fused
-log-softmax top-k (``ssd_row_topk_bf16``; sampled drafts: the warp ``ssd_warp_probs_bf16`` and
-the Gumbel top-k draw ``ssd_gumbel_topk``), and the level expansion / width cut / next-level
-attention rows (``ssd_tree_level``), then the max_nodes cut and the verify rows
-(``ssd_tree_finalize``). No host round trip happens inside a round.
+Here every step of that loop is a kernel: the draft forward, the draft head, the proposals
+(greedy: the log-softmax top-k's chunk pass ``ssd_row_topk_partial_bf16``, whose merge runs inside
+the level launch ``ssd_tree_level_topk``; sampled drafts: the warp ``ssd_warp_probs_bf16`` and the
+Gumbel top-k draw ``ssd_gumbel_topk``, then ``ssd_tree_level``), the level expansion / width cut /
+next-level attention rows, then the max_nodes cut and the verify rows (``ssd_tree_finalize``). No
+host round trip happens inside a round.
 """
 
 from __future__ import annotations
