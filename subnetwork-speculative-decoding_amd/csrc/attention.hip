@@ -240,14 +240,13 @@ __device__ __forceinline__ void block_attend(const Frags<HD>& f, const u32x4_t (
   for (int dt = 0; dt < DT; ++dt) o[dt] = mfma16x16x32(bits_bf16x8(f.v[dt][1]), bits_bf16x8(pb1), o[dt]);
 }
 
-constexpr int ATT_QROWS = 128;  // query rows staged in LDS at a time
-
+// The four block partials of a row tile meet in LDS; two such areas alternate between consecutive
+// tiles, so one barrier per tile suffices (see the tile loop).
 template <int HD>
 struct alignas(16) AttnLds {
-  float o[ATT_SB][16][HD + 4];
-  float m[ATT_SB][16];
-  float l[ATT_SB][16];
-  bf16_t q[ATT_QROWS][HD + 8];
+  float o[2][ATT_SB][16][HD + 4];
+  float m[2][ATT_SB][16];
+  float l[2][ATT_SB][16];
   bf16_t avt[ATT_MAXD][HD];  // tail: the token's ancestors' V^T columns
 };
 
@@ -259,10 +258,10 @@ struct alignas(16) AttnLds {
 //    superblock; the wave loads its block's K and V^T into MFMA operand registers once and runs
 //    every 16-row tile of its group against them. The groups of a superblock sit on one XCD, so
 //    K/V bytes come from HBM once and the other groups read them from that XCD's L2.
-// Query rows are staged in LDS up front (their loads overlap the K/V loads). Both kinds end in
-// the same code: the four block partials of a tile meet in LDS and are folded left to right into
-// the superblock partial, so a superblock's result does not depend on which kind of workgroup
-// produced it. Ids are decoded XCD-aware: the workgroups that read one (superblock, kv head)
+// Each wave loads the query fragments of a row tile straight from memory, one tile ahead (the first
+// tile's loads are issued before the K/V loads). Both kinds end in the same code: the four block
+// partials of a tile meet in LDS and are folded left to right into the superblock partial, so a
+// superblock's result does not depend on which kind of workgroup produced it. Ids are decoded XCD-aware: the workgroups that read one (superblock, kv head)
 // -- its tokens (tail) or tile groups (shared) -- get ids 8 apart, i.e. one XCD (workgroups are
 // dealt to the 8 XCDs round-robin), so their re-reads of that K/V hit the XCD's L2.
 //
@@ -317,31 +316,19 @@ __global__ __launch_bounds__(256, 2) void attn_partial_kernel(AttnArgs a) {
     r_end = min(n_rows, r_begin + a.tiles_per_group * 16);
   }
 
-  // Query rows are staged through LDS in chunks of ATT_QROWS (R = token * rep + GQA head within
-  // the kv group). The first chunk's loads are issued before the K/V loads, so they land first
-  // (memory returns in issue order) and are written to LDS while K/V are still in flight.
-  constexpr int QCH = HD / 8;                     // 16-byte chunks per row
-  constexpr int QIT = ATT_QROWS * QCH / 256;
-  u32x4_t qv[QIT];
-  auto load_q = [&](int c0, int c1) {
-    const int nq = (c1 - c0) * QCH;
+  // Query fragments of the 16-row tile starting at row t0 (R = token * rep + GQA head within the kv
+  // group): lane (j, g) holds row t0 + j, dims ks * 32 + 8g ... + 8 -- the MFMA B operand. Rows at
+  // or past r_end load row r_begin (a valid address): every score, softmax and output column
+  // belongs to one row, so a padding row only produces its own partial, which is never stored.
+  auto load_qf = [&](int t0, u32x4_t (&qf)[KS]) {
+    const int R = t0 + j < r_end ? t0 + j : r_begin;
+    const int qt = (int)__umulhi((uint32_t)R, a.rep_magic);
+    const bf16_t* qp = a.Q + (size_t)qt * a.ldq + (size_t)(kvh * rep + R - qt * rep) * HD + g * 8;
 #pragma unroll
-    for (int it = 0; it < QIT; ++it) {
-      const int idx = min((int)threadIdx.x + it * 256, nq - 1);
-      const int R = c0 + idx / QCH;
-      const int qt = (int)__umulhi((uint32_t)R, a.rep_magic);
-      qv[it] = *(const u32x4_t*)(a.Q + (size_t)qt * a.ldq + (size_t)(kvh * rep + R - qt * rep) * HD + (idx % QCH) * 8);
-    }
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = *(const u32x4_t*)(qp + ks * 32);
   };
-  auto store_q = [&](int c0, int c1) {
-    const int nq = (c1 - c0) * QCH;
-#pragma unroll
-    for (int it = 0; it < QIT; ++it) {
-      const int idx = threadIdx.x + it * 256;
-      if (idx < nq) *(u32x4_t*)&lds.q[idx / QCH][(idx % QCH) * 8] = qv[it];
-    }
-  };
-  load_q(r_begin, min(r_end, r_begin + ATT_QROWS));
+  u32x4_t qn[KS];
+  load_qf(r_begin, qn);
 
   Frags<HD> f;
   uint32_t bits = 0xffffu;
@@ -397,74 +384,73 @@ __global__ __launch_bounds__(256, 2) void attn_partial_kernel(AttnArgs a) {
     load_shared_frags<HD>(f, a, kvh, key0, lane);
   }
 
-  for (int c0 = r_begin; c0 < r_end; c0 += ATT_QROWS) {
-    const int c1 = min(r_end, c0 + ATT_QROWS);
-    if (c0 != r_begin) load_q(c0, c1);
-    store_q(c0, c1);
-    __syncthreads();
-    for (int t0 = c0; t0 < c1; t0 += 16) {
-      const int nv = min(16, c1 - t0);
-      const bool rv = j < nv;
-      u32x4_t qf[KS];
-      const uint32_t qkeep = rv ? 0xffffffffu : 0u;
+  // Row tiles in turn. Tile i's block partials go to LDS area i % 2; one barrier makes them visible
+  // and the fold reads them. Area i % 2 is written next by tile i + 2, which no wave starts before
+  // it has passed tile i + 1's barrier, i.e. before every wave has finished folding tile i. The
+  // loop is unrolled by two so that the query fragments alternate between two register sets
+  // (a copy would wait for the previous tile's stores when it reuses their registers).
+  auto row_tile = [&](int t0, int buf, const u32x4_t (&qf)[KS], u32x4_t (&qnext)[KS]) {
+    const int nv = min(16, r_end - t0);
+    load_qf(t0 + 16, qnext);  // next tile (rows past the last one clamped)
+    if (have) {
+      float m, l;
+      f32x4_t o[DT];
+      if (tail)
+        block_attend<HD, true>(f, qf, bits, a.scale_log2, m, l, o);
+      else
+        block_attend<HD, false>(f, qf, bits, a.scale_log2, m, l, o);
+      if (g == 0) { lds.m[buf][w][j] = m; lds.l[buf][w][j] = l; }
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) qf[ks] = *(const u32x4_t*)&lds.q[rv ? t0 - c0 + j : 0][ks * 32 + g * 8] & qkeep;
-      if (have) {
-        float m, l;
-        f32x4_t o[DT];
-        if (tail)
-          block_attend<HD, true>(f, qf, bits, a.scale_log2, m, l, o);
-        else
-          block_attend<HD, false>(f, qf, bits, a.scale_log2, m, l, o);
-        if (g == 0) { lds.m[w][j] = m; lds.l[w][j] = l; }
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) *(f32x4_t*)&lds.o[w][j][dt * 16 + 4 * g] = o[dt];
-      } else if (g == 0) {
-        lds.m[w][j] = -INFINITY;
-        lds.l[w][j] = 0.f;
-      }
-      __syncthreads();
-
-      // Fold the 4 block partials of each row: superblock max first, then the weighted sums in
-      // block order -> superblock partial.
-      {
-        const int rr = threadIdx.x >> 4;       // tile row
-        const int dc = threadIdx.x & 15;       // d chunk
-        constexpr int DPT = HD / 16;           // d per thread
-        if (rr < nv) {
-          float mb[ATT_SB], mS = -INFINITY;
-#pragma unroll
-          for (int ww = 0; ww < ATT_SB; ++ww) {
-            mb[ww] = lds.m[ww][rr];
-            mS = fmaxf(mS, mb[ww]);
-          }
-          float lS = 0.f, oS[DPT];
-#pragma unroll
-          for (int d = 0; d < DPT; ++d) oS[d] = 0.f;
-#pragma unroll
-          for (int ww = 0; ww < ATT_SB; ++ww) {
-            if (mb[ww] == -INFINITY) continue;
-            const float wgt = fast_exp2(mb[ww] - mS);
-            lS += lds.l[ww][rr] * wgt;
-#pragma unroll
-            for (int d = 0; d < DPT; ++d) oS[d] += lds.o[ww][rr][dc * DPT + d] * wgt;
-          }
-          const size_t rec = ((size_t)kvh * n_rows + t0 + rr) * a.n_sb_cap + sb;
-          if (mS != -INFINITY) {
-            float* dst = ws_o + rec * HD + dc * DPT;
-            if constexpr (DPT % 4 == 0) {
-#pragma unroll
-              for (int d = 0; d < DPT; d += 4) *(float4*)(dst + d) = make_float4(oS[d], oS[d + 1], oS[d + 2], oS[d + 3]);
-            } else {
-#pragma unroll
-              for (int d = 0; d < DPT; ++d) dst[d] = oS[d];
-            }
-          }
-          if (dc == 0) ws_ml[rec] = make_float2(mS, lS);
-        }
-      }
-      __syncthreads();
+      for (int dt = 0; dt < DT; ++dt) *(f32x4_t*)&lds.o[buf][w][j][dt * 16 + 4 * g] = o[dt];
+    } else if (g == 0) {
+      lds.m[buf][w][j] = -INFINITY;
+      lds.l[buf][w][j] = 0.f;
     }
+    __syncthreads();
+
+    // Fold the 4 block partials of each row: superblock max first, then the weighted sums in
+    // block order -> superblock partial. Every thread stores (threads of padding rows fold row
+    // nv - 1 again and write the same values; a superblock without keys gets O = 0, which the combine
+    // never reads since its m is -inf), so the number of stores per tile is fixed and the next
+    // tile's query loads, issued before them, are waited for without waiting for the stores.
+    {
+      const int rr = min((int)threadIdx.x >> 4, nv - 1);  // tile row
+      const int dc = threadIdx.x & 15;                    // d chunk
+      constexpr int DPT = HD / 16;                        // d per thread
+      float mb[ATT_SB], mS = -INFINITY;
+#pragma unroll
+      for (int ww = 0; ww < ATT_SB; ++ww) {
+        mb[ww] = lds.m[buf][ww][rr];
+        mS = fmaxf(mS, mb[ww]);
+      }
+      float lS = 0.f, oS[DPT];
+#pragma unroll
+      for (int d = 0; d < DPT; ++d) oS[d] = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < ATT_SB; ++ww) {
+        if (mb[ww] == -INFINITY) continue;
+        const float wgt = fast_exp2(mb[ww] - mS);
+        lS += lds.l[buf][ww][rr] * wgt;
+#pragma unroll
+        for (int d = 0; d < DPT; ++d) oS[d] += lds.o[buf][ww][rr][dc * DPT + d] * wgt;
+      }
+      const size_t rec = ((size_t)kvh * n_rows + t0 + rr) * a.n_sb_cap + sb;
+      float* dst = ws_o + rec * HD + dc * DPT;
+      if constexpr (DPT % 4 == 0) {
+#pragma unroll
+        for (int d = 0; d < DPT; d += 4) *(float4*)(dst + d) = make_float4(oS[d], oS[d + 1], oS[d + 2], oS[d + 3]);
+      } else {
+#pragma unroll
+        for (int d = 0; d < DPT; ++d) dst[d] = oS[d];
+      }
+      ws_ml[rec] = make_float2(mS, lS);  // the same pair from each of the row's 16 threads
+    }
+  };
+  u32x4_t qa[KS];
+  for (int t0 = r_begin; t0 < r_end; t0 += 32) {
+    row_tile(t0, 0, qn, qa);
+    if (t0 + 16 >= r_end) break;  // uniform
+    row_tile(t0 + 16, 1, qa, qn);
   }
 }
 
