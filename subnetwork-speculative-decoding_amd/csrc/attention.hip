@@ -386,71 +386,106 @@ __global__ __launch_bounds__(256, 2) void attn_partial_kernel(AttnArgs a) {
 
   // Row tiles in turn. Tile i's block partials go to LDS area i % 2; one barrier makes them visible
   // and the fold reads them. Area i % 2 is written next by tile i + 2, which no wave starts before
-  // it has passed tile i + 1's barrier, i.e. before every wave has finished folding tile i. The
-  // loop is unrolled by two so that the query fragments alternate between two register sets
-  // (a copy would wait for the previous tile's stores when it reuses their registers).
-  auto row_tile = [&](int t0, int buf, const u32x4_t (&qf)[KS], u32x4_t (&qnext)[KS]) {
-    const int nv = min(16, r_end - t0);
-    load_qf(t0 + 16, qnext);  // next tile (rows past the last one clamped)
-    if (have) {
-      float m, l;
-      f32x4_t o[DT];
-      if (tail)
-        block_attend<HD, true>(f, qf, bits, a.scale_log2, m, l, o);
-      else
-        block_attend<HD, false>(f, qf, bits, a.scale_log2, m, l, o);
-      if (g == 0) { lds.m[buf][w][j] = m; lds.l[buf][w][j] = l; }
+  // it has passed tile i + 1's barrier, i.e. before every wave has finished folding tile i. Query
+  // fragments alternate between two register sets (a copy would wait for the previous tile's
+  // stores when it reuses their registers).
+  auto publish = [&](int buf, float m, float l, const f32x4_t (&o)[DT]) {
+    lds.m[buf][w][j] = m;  // the four lanes of row j write the same value
+    lds.l[buf][w][j] = l;
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) *(f32x4_t*)&lds.o[buf][w][j][dt * 16 + 4 * g] = o[dt];
-    } else if (g == 0) {
-      lds.m[buf][w][j] = -INFINITY;
-      lds.l[buf][w][j] = 0.f;
-    }
+    for (int dt = 0; dt < DT; ++dt) *(f32x4_t*)&lds.o[buf][w][j][dt * 16 + 4 * g] = o[dt];
     __syncthreads();
-
-    // Fold the 4 block partials of each row: superblock max first, then the weighted sums in
-    // block order -> superblock partial. Every thread stores (threads of padding rows fold row
-    // nv - 1 again and write the same values; a superblock without keys gets O = 0, which the combine
-    // never reads since its m is -inf), so the number of stores per tile is fixed and the next
-    // tile's query loads, issued before them, are waited for without waiting for the stores.
-    {
-      const int rr = min((int)threadIdx.x >> 4, nv - 1);  // tile row
-      const int dc = threadIdx.x & 15;                    // d chunk
-      constexpr int DPT = HD / 16;                        // d per thread
-      float mb[ATT_SB], mS = -INFINITY;
+  };
+  // Fold the 4 block partials of each row of the tile at t0: superblock max first, then the
+  // weighted sums in block order -> superblock partial. Branch-free, and every thread stores (threads of padding rows fold row nv - 1 again and
+  // write the same values; a superblock without keys gets O = 0, which the combine never reads
+  // since its m is -inf), so the number of stores per tile is fixed and the next tile's query
+  // loads, issued before them, are waited for without waiting for the stores.
+  auto fold = [&](int t0, int buf) {
+    const int nv = min(16, r_end - t0);
+    const int rr = min((int)threadIdx.x >> 4, nv - 1);  // tile row
+    const int dc = threadIdx.x & 15;                    // d chunk
+    constexpr int DPT = HD / 16;                        // d per thread
+    float mb[ATT_SB], mS = -INFINITY;
 #pragma unroll
-      for (int ww = 0; ww < ATT_SB; ++ww) {
-        mb[ww] = lds.m[buf][ww][rr];
-        mS = fmaxf(mS, mb[ww]);
-      }
-      float lS = 0.f, oS[DPT];
-#pragma unroll
-      for (int d = 0; d < DPT; ++d) oS[d] = 0.f;
-#pragma unroll
-      for (int ww = 0; ww < ATT_SB; ++ww) {
-        if (mb[ww] == -INFINITY) continue;
-        const float wgt = fast_exp2(mb[ww] - mS);
-        lS += lds.l[buf][ww][rr] * wgt;
-#pragma unroll
-        for (int d = 0; d < DPT; ++d) oS[d] += lds.o[buf][ww][rr][dc * DPT + d] * wgt;
-      }
-      const size_t rec = ((size_t)kvh * n_rows + t0 + rr) * a.n_sb_cap + sb;
-      float* dst = ws_o + rec * HD + dc * DPT;
-      if constexpr (DPT % 4 == 0) {
-#pragma unroll
-        for (int d = 0; d < DPT; d += 4) *(float4*)(dst + d) = make_float4(oS[d], oS[d + 1], oS[d + 2], oS[d + 3]);
-      } else {
-#pragma unroll
-        for (int d = 0; d < DPT; ++d) dst[d] = oS[d];
-      }
-      ws_ml[rec] = make_float2(mS, lS);  // the same pair from each of the row's 16 threads
+    for (int ww = 0; ww < ATT_SB; ++ww) {
+      mb[ww] = lds.m[buf][ww][rr];
+      mS = fmaxf(mS, mb[ww]);
     }
+    float lS = 0.f, oS[DPT];
+#pragma unroll
+    for (int d = 0; d < DPT; ++d) oS[d] = 0.f;
+    // A block without keys gets weight 0: its l and O in LDS are finite zeros (published by every
+    // wave), and adding an exact zero leaves a sum that is never -0 unchanged, so this equals
+    // skipping the block.
+#pragma unroll
+    for (int ww = 0; ww < ATT_SB; ++ww) {
+      const float wgt = mb[ww] != -INFINITY ? fast_exp2(mb[ww] - mS) : 0.f;
+      lS += lds.l[buf][ww][rr] * wgt;
+#pragma unroll
+      for (int d = 0; d < DPT; ++d) oS[d] += lds.o[buf][ww][rr][dc * DPT + d] * wgt;
+    }
+    const size_t rec = ((size_t)kvh * n_rows + t0 + rr) * a.n_sb_cap + sb;
+    float* dst = ws_o + rec * HD + dc * DPT;
+    if constexpr (DPT % 4 == 0) {
+#pragma unroll
+      for (int d = 0; d < DPT; d += 4) *(float4*)(dst + d) = make_float4(oS[d], oS[d + 1], oS[d + 2], oS[d + 3]);
+    } else {
+#pragma unroll
+      for (int d = 0; d < DPT; ++d) dst[d] = oS[d];
+    }
+    ws_ml[rec] = make_float2(mS, lS);  // the same pair from each of the row's 16 threads
   };
   u32x4_t qa[KS];
-  for (int t0 = r_begin; t0 < r_end; t0 += 32) {
-    row_tile(t0, 0, qn, qa);
-    if (t0 + 16 >= r_end) break;  // uniform
-    row_tile(t0 + 16, 1, qa, qn);
+  float m, l;
+  f32x4_t o[DT];
+  if (tail) {
+    // one token's rows (rep <= 16 at every supported shape: one tile, at most a few): in turn
+    for (int t0 = r_begin; t0 < r_end; t0 += 32) {
+      load_qf(t0 + 16, qa);
+      if (have) {
+        block_attend<HD, true>(f, qn, bits, a.scale_log2, m, l, o);
+      } else {
+        m = -INFINITY;
+        l = 0.f;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
+      publish(0, m, l, o);
+      fold(t0, 0);
+      if (t0 + 16 >= r_end) break;  // uniform
+      load_qf(t0 + 32, qn);
+      if (have) {
+        block_attend<HD, true>(f, qa, bits, a.scale_log2, m, l, o);
+      } else {
+        m = -INFINITY;
+        l = 0.f;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
+      publish(1, m, l, o);
+      fold(t0 + 16, 1);
+    }
+  } else {
+    // Shared workgroups run many tiles: software-pipelined, each wave folds tile i in the same
+    // straight-line code that computes tile i + 1, so the fold's LDS reads and stores overlap the
+    // next tile's MFMAs.
+    load_qf(r_begin + 16, qa);
+    block_attend<HD, false>(f, qn, bits, a.scale_log2, m, l, o);
+    publish(0, m, l, o);
+    for (int t0 = r_begin;; t0 += 32) {
+      // tile t0 is in area 0, tile t0 + 16's query fragments in qa
+      if (t0 + 16 >= r_end) { fold(t0, 0); break; }  // uniform
+      load_qf(t0 + 32, qn);
+      block_attend<HD, false>(f, qa, bits, a.scale_log2, m, l, o);
+      fold(t0, 0);
+      publish(1, m, l, o);
+      if (t0 + 32 >= r_end) { fold(t0 + 16, 1); break; }
+      load_qf(t0 + 48, qa);
+      block_attend<HD, false>(f, qn, bits, a.scale_log2, m, l, o);
+      fold(t0 + 16, 1);
+      publish(0, m, l, o);
+    }
   }
 }
 
