@@ -381,7 +381,9 @@ def _run_attn(q, k, v, prefix, anc, S, m_cap=None):
     return out.view(m, heads, hd).cpu()
 
 
-@pytest.mark.parametrize("hd,heads,kvh", [(64, 4, 2), (128, 8, 2), (128, 32, 8)])
+# (64, 32, 1) and (128, 48, 1): 32 and 48 query heads per kv head, so one token's rows span two and
+# three 16-row tiles in the workgroups that build its own superblocks
+@pytest.mark.parametrize("hd,heads,kvh", [(64, 4, 2), (128, 8, 2), (128, 32, 8), (64, 32, 1), (128, 48, 1)])
 @pytest.mark.parametrize("P", [1, 63, 64, 200, 1000, 4100])
 def test_tree_attention_matches_oracle(hd, heads, kvh, P):
     rng = random.Random(P * 7 + hd)
