@@ -6,10 +6,11 @@
 // the target's forward over the prompt):
 //
 // * prefill_gemm_kernel: Y = X W^T over the same packed weights as the decode GEMMs (16 x 32
-//   MFMA A-operand tiles, any tile grouping), as an LDS-tiled MFMA GEMM: a workgroup of 4 waves
-//   owns a 128 (N) x 128 (M) output tile, stages 128 x 64 of W and of X per step in LDS (double
-//   buffered, the next step's global loads in flight while the MFMAs run), and each wave computes a
-//   64 x 64 sub-tile with v_mfma_f32_16x16x32_bf16. X is staged in the MFMA B-operand lane order so
+//   MFMA A-operand tiles, any tile grouping), as an LDS-tiled MFMA GEMM: a workgroup of 8 waves
+//   (one per CU, two per SIMD) owns a 256 (N) x 128 (M) output tile, stages 256 x 64 of W and
+//   128 x 64 of X per step in LDS (double buffered, the next step's global loads in flight while the
+//   MFMAs run), and each wave computes a 64 x 64 sub-tile with v_mfma_f32_16x16x32_bf16 (against
+//   two 4-wave 128 x 128 workgroups per CU, a quarter fewer bytes staged per MFMA). X is staged in the MFMA B-operand lane order so
 //   every LDS read is one contiguous 1 KiB per wave. The decode epilogues run on the accumulators:
 //   the folded RMSNorm scale (sum of x^2 accumulated by the threads that stage X), RoPE + KV-cache
 //   write for q/k/v, SwiGLU for gate/up (rotary / gate-up row pairs r and r + 8 meet through one
@@ -30,7 +31,7 @@
 
 namespace ssd {
 
-constexpr int PF_BN = 128;  // output rows of W per workgroup
+constexpr int PF_WN = 4;    // waves along N (x 2 along M): 64 * PF_WN = 256 output rows of W per workgroup
 constexpr int PF_BM = 128;  // tokens per workgroup
 constexpr int PF_KB = 2;    // 32-wide k-blocks per pipeline step
 
@@ -40,14 +41,19 @@ __device__ __forceinline__ size_t packed_tile(int nb, int kb, int kbt, int group
 }
 
 template <int EPI, int NORM>
-__global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(GemmArgs a, int group, int n_mt, int n_nt, int pos0,
-                                                              int sb_n, int sb_m) {
-  __shared__ u32x4_t As[2][PF_KB][8][64];
+__global__ __launch_bounds__(128 * PF_WN, 4 / PF_WN) void prefill_gemm_kernel(GemmArgs a, int group, int n_mt,
+                                                                              int n_nt, int pos0, int sb_n, int sb_m) {
+  constexpr int WN = PF_WN;
+  constexpr int NT = 128 * WN;   // threads
+  constexpr int RT = 4 * WN;     // 16-row tiles of W per workgroup
+  constexpr int XL = 8 / WN;     // X chunks each thread stages per step
+  __shared__ u32x4_t As[2][PF_KB][RT][64];
   __shared__ u32x4_t Bs[2][PF_KB][8][64];
   __shared__ float rn_s[PF_BM];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int j = lane & 15, g = lane >> 4;
-  const int wn = w & 1, wm = w >> 1;
+  const int wn = w % WN, wm = w / WN;
+  const int n_rt = (a.N + 127) / 128 * 8;  // row tiles of the packed weight (rows padded to 128)
   const int kbt = a.kb_total;
 
   // Persistent, XCD-aware schedule: the workgroups resident on one XCD (ids x, x + 8, ...) sweep
@@ -61,12 +67,13 @@ __global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(GemmArgs a, int gr
   for (int blk = xcd; blk < n_bn * n_bm; blk += 8) {
   const int bn = (blk / n_bm) * sb_n + jw % sb_n, bm = (blk % n_bm) * sb_m + jw / sb_n;
   if (bn >= n_nt || bm >= n_mt || jw >= sb_n * sb_m) continue;  // uniform per workgroup
-  const int nb0 = bn * 8, m0 = bm * PF_BM;
+  const int nb0 = bn * RT, m0 = bm * PF_BM;
 
-  // Staging assignment: 1024 16-byte chunks of W and of X per step, 4 of each per thread.
-  // W chunk i: k-block i >> 9 of the step, row tile (i >> 6) & 7, lane i & 63 (one tile = 1 KiB).
+  // Staging assignment: 512 WN 16-byte chunks of W and 1024 of X per step, 4 and XL per thread.
+  // W chunk i: k-block i / (64 RT) of the step, row tile (i >> 6) % RT, lane i & 63 (one tile =
+  // 1 KiB; row tiles past the weight's last load that one, their outputs are never stored).
   // X: a wave's load covers 8 rows x the step's 8 16-byte columns (whole 128-byte lines); thread
-  // t, load r: row 8 (t >> 6) + 32 r + (t & 7), column c = lane >> 3 (k-block c >> 2, B-operand
+  // t, load r: row 8 (t >> 6) + 16 WN r + (t & 7), column c = lane >> 3 (k-block c >> 2, B-operand
   // lane group c & 3). The 8 lanes that the LDS serves together hold 8 consecutive rows of one
   // column: 8 consecutive 16-byte slots of the operand layout, free of bank conflicts.
   const u32x4_t* W = (const u32x4_t*)a.W;
@@ -74,47 +81,47 @@ __global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(GemmArgs a, int gr
   int wkb[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int i = t + 256 * r;
-    wkb[r] = i >> 9;
-    const int nb = nb0 + ((i >> 6) & 7);
+    const int i = t + NT * r;
+    wkb[r] = i / (64 * RT);
+    const int nb = min(nb0 + ((i >> 6) % RT), n_rt - 1);
     wbase[r] = packed_tile(nb, 0, kbt, group) * 64 + (i & 63);
   }
   const int xc = lane >> 3;
-  auto xrow_of = [&](int r) { return (t >> 6) * 8 + 32 * r + (t & 7); };
-  const bf16_t* xrow[4];
+  auto xrow_of = [&](int r) { return (t >> 6) * 8 + 16 * WN * r + (t & 7); };
+  const bf16_t* xrow[XL];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) xrow[r] = a.X + (size_t)min(m0 + xrow_of(r), a.M - 1) * a.ldx + xc * 8;
+  for (int r = 0; r < XL; ++r) xrow[r] = a.X + (size_t)min(m0 + xrow_of(r), a.M - 1) * a.ldx + xc * 8;
   const int xkb = xc >> 2, xg = xc & 3;
 
   // Two register sets of staged chunks: a step's global loads are issued two compute steps before
   // they are written to LDS, so their latency is covered by two steps of MFMAs.
   struct Stage {
-    u32x4_t a[4], b[4];
+    u32x4_t a[4], b[XL];
   };
   Stage s0, s1;
-  float ss[4] = {0.f, 0.f, 0.f, 0.f};
+  float ss[XL] = {};
   auto gload = [&](int st, Stage& r) {
     const int k0 = st * PF_KB;
 #pragma unroll
     for (int i = 0; i < 4; ++i) r.a[i] = W[wbase[i] + (size_t)(k0 + wkb[i]) * group * 64];  // shared by sb_m workgroups: cached
 #pragma unroll
-    for (int i = 0; i < 4; ++i) r.b[i] = *(const u32x4_t*)(xrow[i] + (size_t)k0 * 32);
+    for (int i = 0; i < XL; ++i) r.b[i] = *(const u32x4_t*)(xrow[i] + (size_t)k0 * 32);
   };
   // real == false stores zeros (the padding step of an odd step count): a mask, not a branch,
   // so every path through the loop has the same loads in flight
   auto lstore = [&](int buf, const Stage& r, bool real) {
     const uint32_t keep = real ? 0xffffffffu : 0u;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) (&As[buf][0][0][0])[t + 256 * i] = r.a[i] & keep;
+    for (int i = 0; i < 4; ++i) (&As[buf][0][0][0])[t + NT * i] = r.a[i] & keep;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < XL; ++i) {
       const int row = xrow_of(i);
       Bs[buf][xkb][row >> 4][xg * 16 + (row & 15)] = r.b[i] & keep;
     }
     if constexpr (NORM) {
       if (real) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ss[i] += sumsq8(r.b[i]);
+        for (int i = 0; i < XL; ++i) ss[i] += sumsq8(r.b[i]);
       }
     }
   };
@@ -168,7 +175,7 @@ __global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(GemmArgs a, int gr
   if constexpr (NORM) {
     // the 8 lanes that staged one row hold its partial sums (lanes l, l ^ 8, ..., l ^ 56)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < XL; ++r) {
       float v = ss[r];
       v += __shfl_xor(v, 8);
       v += __shfl_xor(v, 16);
@@ -394,8 +401,8 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(const bf16_t*
 
 static int launch_prefill_gemm(GemmArgs a, int group, int pos0, int epi, hipStream_t s) {
   const int n_mt = (a.M + PF_BM - 1) / PF_BM;
-  const int n_nt = (a.N + PF_BN - 1) / PF_BN;
-  // two workgroups per CU, all resident: 8 XCDs x (per_xcd = CUs / 4) workgroups
+  const int n_nt = (a.N + 64 * PF_WN - 1) / (64 * PF_WN);
+  // 4 / PF_WN workgroups per CU, all resident: 8 XCDs x per_xcd workgroups
   static int cus_of[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return set_error(SSD_EHIP, "prefill gemm: no current device");
@@ -404,14 +411,14 @@ static int launch_prefill_gemm(GemmArgs a, int group, int pos0, int epi, hipStre
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
     if (dev >= 0 && dev < 64) cus_of[dev] = cus;
   }
-  const int per_xcd = (2 * cus / 8) & ~7;  // 64 on MI355X
+  const int per_xcd = (4 / PF_WN * cus / 8) & ~7;  // 32 on MI355X
   const int sb_m = n_mt < 8 ? n_mt : 8;
   const int sb_n = per_xcd / sb_m;
   const int grid = 8 * sb_n * sb_m;
   const bool norm = a.norm_eps > 0.f;
-#define PF_LAUNCH(E)                                                                                          \
-  if (norm) SSD_LAUNCH((prefill_gemm_kernel<E, 1>), dim3(grid), dim3(256), 0, s, a, group, n_mt, n_nt, pos0, sb_n, sb_m); \
-  else SSD_LAUNCH((prefill_gemm_kernel<E, 0>), dim3(grid), dim3(256), 0, s, a, group, n_mt, n_nt, pos0, sb_n, sb_m);
+#define PF_LAUNCH(E)                                                                                                   \
+  if (norm) SSD_LAUNCH((prefill_gemm_kernel<E, 1>), dim3(grid), dim3(128 * PF_WN), 0, s, a, group, n_mt, n_nt, pos0, sb_n, sb_m); \
+  else SSD_LAUNCH((prefill_gemm_kernel<E, 0>), dim3(grid), dim3(128 * PF_WN), 0, s, a, group, n_mt, n_nt, pos0, sb_n, sb_m);
   switch (epi) {
     case EPI_STORE: PF_LAUNCH(EPI_STORE); break;
     case EPI_SWIGLU: PF_LAUNCH(EPI_SWIGLU); break;
