@@ -46,8 +46,9 @@ def close_bf16(got, ref, frac=0.97, rtol=1.6e-2, atol=1e-2):
 
 
 @pytest.mark.parametrize("m", [1, 77, 300])
+# N = 384 and 640: the last 256-row workgroup tile reaches past the weight's (128-row padded) tiles
 @pytest.mark.parametrize("n,k,residual", [(256, 256, False), (6144, 4096, False), (4096, 4096, True),
-                                          (4096, 14336, True)])
+                                          (4096, 14336, True), (384, 512, False), (640, 1024, True)])
 def test_prefill_gemm_store_and_residual(m, n, k, residual):
     ops = _ops()
     x, w = bf(rand(m, k, seed=1)), bf(rand(n, k, std=0.02, seed=2))
