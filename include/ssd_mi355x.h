@@ -314,6 +314,17 @@ int ssd_gumbel_topk(const float* probs, int64_t ldp, int rows, int V, int k, con
 int ssd_sample_rows(const float* probs, int64_t ldp, int rows, int V, uint64_t seed, uint64_t counter,
                     int32_t* out_tok, void* ws, int64_t ws_bytes, hipStream_t stream);
 
+/* sample_next at temperature > 0 (ssd/data/generate_selfdistill.py:50-60): per row of bf16 logits,
+ * the 64 largest values (equal values: lower column first), warp_probs over those 64 alone
+ * (softmax(v / T), an entry dropped when the fp32 cumulative mass before it exceeds top_p), one
+ * categorical draw among them; out_tok[r] is the drawn column. Needs 64 <= V <= 262144 (the
+ * reference's topk(64) needs V >= 64), temperature > 0, top_p > 0, and a workspace of
+ * ssd_sample_top64_ws_bytes(rows, V) bytes, 8-byte aligned. */
+int64_t ssd_sample_top64_ws_bytes(int rows, int V);
+int ssd_sample_top64_bf16(const uint16_t* logits, int64_t ld, int rows, int V, float temperature, float top_p,
+                          uint64_t seed, uint64_t counter, int32_t* out_tok, void* ws, int64_t ws_bytes,
+                          hipStream_t stream);
+
 /* sample_verify (ssd/engine/verify.py:60-95) over the finalized tree plus the bookkeeping of
  * ssd_accept_greedy. P[rows][V]: warped target rows (row 0 root, 1 + v verify node v; rows <= 64);
  * Q: warped draft rows as written by ssd_warp_probs_bf16 with tree_meta (row 1 + draft index).

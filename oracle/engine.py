@@ -232,8 +232,7 @@ def prune_tree(tree: DraftTree, max_nodes: Optional[int]) -> DraftTree:
     under ancestors, renumbered in original order."""
     if max_nodes is None or len(tree) <= max_nodes:
         return tree
-    order = sorted(range(len(tree)), key=lambda i: (-tree.scores[i], tree.depths[i]))
-    keep = set(order[:max_nodes])
+    keep = set(prune_order(tree.scores, tree.depths, max_nodes))
     for i in list(keep):
         keep.update(tree.ancestors(i))
     return tree.subset(sorted(keep))

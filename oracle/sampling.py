@@ -36,7 +36,7 @@ import torch
 ROOT = -1
 MARGIN = 1e-4
 
-TAG_PROPOSE, TAG_ACCEPT, TAG_BONUS, TAG_DRAW = 1, 2, 3, 4
+TAG_PROPOSE, TAG_ACCEPT, TAG_BONUS, TAG_DRAW, TAG_TOP64 = 1, 2, 3, 4, 5
 
 _M0, _M1 = np.uint64(0xD2511F53), np.uint64(0xCD9E8D57)
 _W0, _W1 = np.uint32(0x9E3779B9), np.uint32(0xBB67AE85)
@@ -175,6 +175,29 @@ def categorical(p: torch.Tensor, stream: Stream, row: int, tag: int = TAG_DRAW, 
     order = np.lexsort((np.arange(V), -keys.astype(np.float64)))
     a, b = keys[order[0]], keys[order[1]] if V > 1 else -1.0
     return int(order[0]), bool(V > 1 and b > 0 and abs(a - b) <= MARGIN * abs(a))
+
+
+def sample_next_top64(logits: torch.Tensor, temperature: float, top_p: float, stream: Stream, row: int,
+                      k: int = 64):
+    """sample_next at temperature > 0 (ssd/data/generate_selfdistill.py:50-60): the k largest
+    logits of the row (equal logits: lower column first), warp_probs over those k alone, one
+    draw among them (Gumbel-max over the k ranks, Exp(1) of rank j from the TAG_TOP64 stream).
+    Returns (column, fragile)."""
+    x = logits.float()
+    order = np.lexsort((np.arange(x.shape[0]), -x.numpy().astype(np.float64)))[:k]
+    p, fr = warp_probs(x[torch.from_numpy(order)], temperature, top_p)
+    j, fr2 = categorical(p, stream, row, TAG_TOP64)
+    return int(order[j]), fr or fr2
+
+
+def top64_probs(logits: torch.Tensor, temperature: float, top_p: float, k: int = 64) -> torch.Tensor:
+    """The distribution sample_next draws from, over the full row: warp_probs of the k largest
+    logits, zero elsewhere (float64)."""
+    x = logits.double()
+    order = np.lexsort((np.arange(x.shape[0]), -x.numpy()))[:k]
+    idx = torch.from_numpy(order)
+    p, _ = warp_probs(x[idx].float(), temperature, top_p)
+    return torch.zeros(x.shape[0], dtype=torch.float64).index_copy_(0, idx, p.double())
 
 
 # ---------------------------------------------------------------- acceptance

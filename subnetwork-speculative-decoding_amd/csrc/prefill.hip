@@ -411,7 +411,9 @@ static int launch_prefill_gemm(GemmArgs a, int group, int pos0, int epi, hipStre
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
     if (dev >= 0 && dev < 64) cus_of[dev] = cus;
   }
-  const int per_xcd = (4 / PF_WN * cus / 8) & ~7;  // 32 on MI355X
+  // 32 on MI355X; at least one block row of 8 M-tiles, so a device reporting fewer CUs (a compute
+  // partition) still gets a nonempty grid (the schedule loops, so any grid size is correct)
+  const int per_xcd = max((4 / PF_WN * cus / 8) & ~7, 8);
   const int sb_m = n_mt < 8 ? n_mt : 8;
   const int sb_n = per_xcd / sb_m;
   const int grid = 8 * sb_n * sb_m;

@@ -45,7 +45,7 @@ constexpr int SMP_MAXK = 16;      // children per node / draws per row
 constexpr int SMP_MAXC = 256;     // chunks per row (rows up to 1M columns)
 constexpr int SMP_MAXDEPTH = 32;  // tree depth (matches the tree kernels)
 
-enum SmpTag { TAG_PROPOSE = 1, TAG_ACCEPT = 2, TAG_BONUS = 3, TAG_DRAW = 4 };
+enum SmpTag { TAG_PROPOSE = 1, TAG_ACCEPT = 2, TAG_BONUS = 3, TAG_DRAW = 4, TAG_TOP64 = 5 };
 
 struct Rng {
   uint32_t k0, k1;       // key: seed
@@ -1167,6 +1167,148 @@ __global__ __launch_bounds__(256) void accept_trials_kernel(TrialArgs a) {
   }
 }
 
+// ------------------------------------------------- top-64 draws (batched generation)
+// sample_next of ssd/data/generate_selfdistill.py:50-60: the 64 largest logits of a row, the
+// temperature + nucleus warp of those 64 alone, one categorical draw among them.
+// Candidates are 64-bit records key << 32 | ~column (key = the bf16 logit's monotone key), so
+// a larger record is a larger logit or, among equal logits, a lower column; 0 marks no entry.
+constexpr int T64 = 64;
+constexpr int T64_MAXC = 64;  // chunks per row (rows up to 262144 columns)
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
+  const uint32_t lo = __shfl_xor((uint32_t)v, o), hi = __shfl_xor((uint32_t)(v >> 32), o);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Chunk pass: the chunk's min(64, columns) best records, sorted best first, into
+// parts[row][chunk][64] (0-padded). The 64th-best key is found by two 256-bin count histograms
+// (key high byte, then low byte inside the cut bin); the records above it are collected in any
+// order, its ties by column rank (a block scan of per-thread tie counts: thread order is column
+// order), then one wave sorts the 64 (bitonic network over the lanes).
+__global__ __launch_bounds__(SMP_THREADS) void top64_chunk_kernel(const bf16_t* __restrict__ logits, int64_t ld,
+                                                                  int n, int C, uint64_t* __restrict__ parts) {
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t red[16];
+  __shared__ uint64_t list[T64];
+  __shared__ uint32_t cut_sh, above_sh, cnt_sh;
+  const int row = blockIdx.y, c = blockIdx.x, t = threadIdx.x;
+  const int i = c * SMP_CHUNK + t * 4;
+  uint32_t h[4], k[4];
+  load4_bf16(logits + (size_t)row * ld, i, n, h);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) k[e] = bf_key(h[e]);
+  const uint32_t want = (uint32_t)min(T64, n - c * SMP_CHUNK);
+  if (t < 256) hist[t] = 0;
+  if (t == 0) cnt_sh = 0;
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (i + e < n) atomicAdd(&hist[k[e] >> 8], 1u);
+  __syncthreads();
+  // bins from the largest key down: the bin holding the want-th record
+  uint32_t hv = t < 256 ? hist[255 - t] : 0u;
+  uint32_t incl = block_scan(hv, red);
+  if (t < 256 && hv > 0 && incl - hv < want && incl >= want) {
+    cut_sh = 255u - (uint32_t)t;
+    above_sh = incl - hv;
+  }
+  __syncthreads();
+  const uint32_t cb = cut_sh, above1 = above_sh;
+  if (t < 256) hist[t] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (i + e < n && (k[e] >> 8) == cb) atomicAdd(&hist[k[e] & 255u], 1u);
+  __syncthreads();
+  hv = t < 256 ? hist[255 - t] : 0u;
+  incl = above1 + block_scan(hv, red);
+  __syncthreads();
+  if (t < 256 && hv > 0 && incl - hv < want && incl >= want) {
+    cut_sh = (cb << 8) | (255u - (uint32_t)t);
+    above_sh = incl - hv;
+  }
+  __syncthreads();
+  const uint32_t ck = cut_sh, above = above_sh, ties_keep = want - above;
+  uint32_t nt = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) nt += (i + e < n && k[e] == ck) ? 1u : 0u;
+  uint32_t rank = block_scan(nt, red) - nt;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if (i + e >= n) continue;
+    const uint64_t rec = ((uint64_t)k[e] << 32) | (uint32_t)~(uint32_t)(i + e);
+    if (k[e] > ck) {
+      list[atomicAdd(&cnt_sh, 1u)] = rec;  // exactly `above` of these
+    } else if (k[e] == ck) {
+      if (rank < ties_keep) list[above + rank] = rec;
+      ++rank;
+    }
+  }
+  __syncthreads();
+  if (t < T64) {
+    uint64_t x = (uint32_t)t < want ? list[t] : 0ull;
+#pragma unroll
+    for (int size = 2; size <= T64; size <<= 1) {
+#pragma unroll
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        const uint64_t y = shfl_xor_u64(x, stride);
+        const bool desc = (t & size) == 0, lo = (t & stride) == 0;
+        x = (lo == desc) ? (x > y ? x : y) : (x < y ? x : y);
+      }
+    }
+    parts[((size_t)row * C + c) * T64 + t] = x;
+  }
+}
+
+// Merge + warp + draw, one wave per row: the 64 best of the chunk lists (lane c walks list c;
+// each round takes the wave's largest head), then in rank order p = softmax(v / T), the
+// nucleus cut of warp_probs (an entry is dropped when the sequential fp32 cumulative mass before
+// it exceeds top_p; none with top_p >= 1) and a Gumbel-max draw over the kept ranks, Exp(1) of
+// rank j from the draw stream (counter (j / 4, row), tag TAG_TOP64).
+__global__ __launch_bounds__(64) void top64_draw_kernel(const uint64_t* __restrict__ parts, int C, float temp,
+                                                        float top_p, Rng rng, int* __restrict__ out_tok) {
+  __shared__ uint64_t L[T64_MAXC * T64];
+  const int row = blockIdx.x, lane = threadIdx.x;
+  const uint64_t* P = parts + (size_t)row * C * T64;
+  for (int j = lane; j < C * T64; j += 64) L[j] = P[j];
+  __syncthreads();
+  int head = 0;
+  uint64_t cur = lane < C ? L[lane * T64] : 0ull, mine = 0ull;
+  for (int r = 0; r < T64; ++r) {
+    uint64_t best = cur;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint64_t y = shfl_xor_u64(best, o);
+      best = y > best ? y : best;
+    }
+    if (r == lane) mine = best;
+    if (best != 0ull && cur == best) {  // records are distinct: exactly one lane advances
+      ++head;
+      cur = head < T64 ? L[lane * T64 + head] : 0ull;
+    }
+  }
+  const bool has = mine != 0ull;
+  const float x = has ? bf2f((bf16_t)key_bf((uint32_t)(mine >> 32))) / temp : -INFINITY;
+  const float M = __shfl(x, 0);  // rank 0 holds the largest logit
+  const float e = has ? expf(x - M) : 0.f;
+  float S = e;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) S += __shfl_xor(S, o);
+  const float p = e / S;
+  float acc = 0.f, cum = 0.f;
+  for (int j = 0; j < 64; ++j) {  // torch.cumsum order: rank 0 first
+    acc += __shfl(p, j);
+    if (j == lane) cum = acc;
+  }
+  const bool keep = has && p > 0.f && (top_p >= 1.f || !(cum - p > top_p));
+  const U4 rb = rng_block(rng, (uint32_t)(lane >> 2), (uint32_t)row, TAG_TOP64);
+  const float key = keep ? p / exp1_from_bits(u4_get(rb, lane & 3)) : -1.f;
+  const KeyIdx w = wave_argmax(key, lane);
+  const int col = (int)~(uint32_t)mine;
+  const int pick = __shfl(col, w.idx == NO_IDX ? 0 : w.idx);
+  if (lane == 0) out_tok[row] = pick;
+}
+
 }  // namespace ssd
 
 using namespace ssd;
@@ -1251,6 +1393,35 @@ SSD_API int ssd_sample_rows(const float* probs, int64_t ldp, int rows, int V, ui
                      make_rng(seed, counter), w);
   SSD_LAUNCH(draw_merge_kernel, dim3((rows + 63) / 64), dim3(64), 0, stream, rows, w, out_tok);
   return check_launch("sample_rows");
+}
+
+SSD_API int64_t ssd_sample_top64_ws_bytes(int rows, int V) {
+  if (rows < 0 || V < T64 || chunks_of(V) > T64_MAXC) return -1;
+  return (int64_t)rows * chunks_of(V) * T64 * (int64_t)sizeof(uint64_t);
+}
+
+SSD_API int ssd_sample_top64_bf16(const uint16_t* logits, int64_t ld, int rows, int V, float temperature, float top_p,
+                                  uint64_t seed, uint64_t counter, int32_t* out_tok, void* ws, int64_t ws_bytes,
+                                  hipStream_t stream) {
+  if (!logits || !out_tok) return set_error(SSD_EINVAL, "sample_top64: null pointer");
+  if (rows < 0 || V < T64 || chunks_of(V) > T64_MAXC)
+    return set_error(SSD_ERANGE, "sample_top64: V=%d outside [%d, %d]", V, T64, SMP_CHUNK * T64_MAXC);
+  if (ld % 4 || ld < (V + 3) / 4 * 4)
+    return set_error(SSD_EINVAL, "sample_top64: ld %lld must be a multiple of 4 covering the row", (long long)ld);
+  if (!(temperature > 0.f) || !(top_p > 0.f))
+    return set_error(SSD_EINVAL, "sample_top64: temperature and top_p must be > 0");
+  if (rows > 65535) return set_error(SSD_ERANGE, "sample_top64: %d rows", rows);
+  if (rows == 0) return SSD_OK;
+  const int64_t need = ssd_sample_top64_ws_bytes(rows, V);
+  if (!ws || ws_bytes < need || ((uintptr_t)ws & 7))
+    return set_error(SSD_EINVAL, "sample_top64: workspace %lld < %lld bytes or misaligned", (long long)ws_bytes,
+                     (long long)need);
+  const int C = chunks_of(V);
+  SSD_LAUNCH(top64_chunk_kernel, dim3(C, rows), dim3(SMP_THREADS), 0, stream, (const bf16_t*)logits, ld, V, C,
+             (uint64_t*)ws);
+  SSD_LAUNCH(top64_draw_kernel, dim3(rows), dim3(64), 0, stream, (const uint64_t*)ws, C, temperature, top_p,
+             make_rng(seed, counter), out_tok);
+  return check_launch("sample_top64");
 }
 
 SSD_API int ssd_accept_sample(const SsdTree* tree, const float* P, int64_t ldp, const float* Q, int64_t ldq, int V,

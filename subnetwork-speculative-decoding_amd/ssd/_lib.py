@@ -134,6 +134,8 @@ _PROTOS = {
     "ssd_warp_probs_bf16": (I32, [P, I64, I32, I32, P, P, I32, F32, F32, P, I32, P, I64, P, I64, P]),
     "ssd_gumbel_topk": (I32, [P, I64, I32, I32, I32, P, I32, U64, U64, P, P, P, I64, P]),
     "ssd_sample_rows": (I32, [P, I64, I32, I32, U64, U64, P, P, I64, P]),
+    "ssd_sample_top64_ws_bytes": (I64, [I32, I32]),
+    "ssd_sample_top64_bf16": (I32, [P, I64, I32, I32, F32, F32, U64, U64, P, P, I64, P]),
     "ssd_accept_sample": (I32, [C.POINTER(SsdTree), P, I64, P, I64, I32, I32, I32, U64, U64, P, I64, I32, P, P, P, P,
                                 P]),
     "ssd_accept_sample_trials": (I32, [P, I64, P, I64, I32, P, P, I32, C.POINTER(C.c_int32), U64, U64, I32, P, P, P]),

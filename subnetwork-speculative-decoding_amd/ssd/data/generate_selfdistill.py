@@ -11,10 +11,12 @@ arena offsets, ``SsdRows.kv_off``). The weight-streaming GEMMs are shared by all
 arithmetic is independent of the others, so a greedy batch reproduces greedy decoding of each
 prompt alone bit for bit.
 
-Sampling (temperature > 0) draws from the temperature + nucleus warp of the full row on the GPU
-(ssd_warp_probs_bf16 / ssd_sample_rows, Philox keyed by (step, row), seeded from ``generator``);
-the reference's ``sample_next`` first keeps the 64 largest logits (a speed shortcut of its CPU/MPS
-path), which only changes rows whose nucleus holds more than 64 tokens.
+Sampling (temperature > 0) follows the reference's ``sample_next``: the 64 largest logits of each
+row, the temperature + nucleus warp of those 64 alone, one categorical draw among them
+(ssd_sample_top64_bf16: one launch finds each 4096-column chunk's 64 best, a second merges them and
+draws; Philox keyed by (step, row)). The Philox seed is drawn from ``generator``, which advances it
+as torch.multinomial would: successive calls with one generator draw independently, and a
+generator seeded alike reproduces them.
 """
 
 from __future__ import annotations
@@ -25,19 +27,16 @@ import torch
 
 from ssd import ops
 from ssd.engine.kv_cache import KVCache
-from ssd.engine.sampling import Sampler
+from ssd.engine.sampling import seed_from_generator
 from ssd.engine.speculative import TargetRunner, _prefill_logits
 from ssd.models.subnetwork_draft import CHUNK, Rows
 
 
-def _seed_of(generator: Optional[torch.Generator]) -> Optional[int]:
-    return None if generator is None else int(generator.initial_seed())
-
-
 def sample_next(logits: torch.Tensor, temperature: float, top_p: float,
                 generator: Optional[torch.Generator] = None) -> torch.Tensor:
-    """[B, V] logits -> [B, 1] token ids: the first-index argmax at temperature 0, otherwise one
-    draw per row from the warped distribution (reference generate_selfdistill.py:50-60)."""
+    """[B, V] logits -> [B, 1] token ids (reference generate_selfdistill.py:50-60): the first-index
+    argmax at temperature 0; otherwise, per row, the 64 largest logits (equal logits: lower column
+    first), warp_probs over those 64 and one draw among them. Needs V >= 64 when sampling."""
     if logits.dim() != 2:
         raise ValueError("sample_next: logits must be [B, V]")
     B, V = logits.shape
@@ -49,9 +48,9 @@ def sample_next(logits: torch.Tensor, temperature: float, top_p: float,
     if temperature == 0:
         ops.row_topk(lg, B, V, 1, 0, None, out)
     else:
-        s = Sampler(temperature, top_p, V, logits.device, 0, B, _seed_of(generator))
-        ops.warp_probs(lg, B, V, s.temperature, s.top_p, s.P, ws=s.ws)
-        ops.sample_rows(s.P, B, V, s.seed, 0, out, ws=s.ws)
+        if not temperature > 0:
+            raise ValueError("sample_next: temperature must be >= 0")
+        ops.sample_top64(lg, B, V, temperature, top_p, seed_from_generator(generator), 0, out)
     return out.long()[:, None]
 
 
@@ -84,20 +83,22 @@ def generate_batch(target: TargetRunner, prompts: list, max_new_tokens: int, eos
     ws = target.workspace(CHUNK)
     V = s.vocab
     ld = (V + 7) // 8 * 8
-    sampler = Sampler(temperature, top_p, V, dev, 0, B, _seed_of(generator)) if temperature != 0 else None
+    sampled = temperature != 0
+    if sampled and not temperature > 0:
+        raise ValueError("generate_batch: temperature must be >= 0")
+    seed = seed_from_generator(generator) if sampled else 0
     out = torch.zeros(max_new_tokens, B, dtype=torch.int32, device=dev)
-    batch_logits = torch.zeros(B, ld, dtype=torch.bfloat16, device=dev) if sampler is not None else None
+    batch_logits = torch.zeros(B, ld, dtype=torch.bfloat16, device=dev) if sampled else None
 
     def choose(step: int, logits: torch.Tensor, c0: int, m: int) -> None:
-        if sampler is None:
+        if not sampled:
             ops.row_topk(logits, m, V, 1, 0, None, out[step, c0:c0 + m])
         else:
             batch_logits[c0:c0 + m, :V].copy_(logits[:m, :V])
 
     def draw_all(step: int) -> None:
-        if sampler is not None:
-            ops.warp_probs(batch_logits, B, V, sampler.temperature, sampler.top_p, sampler.P, ws=sampler.ws)
-            ops.sample_rows(sampler.P, B, V, sampler.seed, step, out[step], ws=sampler.ws)
+        if sampled:
+            ops.sample_top64(batch_logits, B, V, temperature, top_p, seed, step, out[step])
 
     for b in range(B):  # each prompt into its own region; first token from its last row
         choose(0, _prefill_logits(target, list(prompts[b]), caches[b], ws), b, 1)

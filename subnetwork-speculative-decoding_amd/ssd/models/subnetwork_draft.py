@@ -115,6 +115,10 @@ class Rows:
                       self.anc[off:])
         v.struct = _lib.SsdRows(v.ids.data_ptr(), v.pos.data_ptr(), v.slot.data_ptr(), v.prefix.data_ptr(),
                                 v.depth.data_ptr(), v.anc.data_ptr(), self.cap - off)
+        kv_off = getattr(self, "kv_off", None)
+        if kv_off is not None:  # rows of several sequences: the view keeps each row's arena offset
+            v.kv_off = kv_off[off:]
+            v.struct.kv_off = v.kv_off.data_ptr()
         return v
 
     def upload(self, ids, pos, slot, prefix, depth, anc=None) -> None:
@@ -151,6 +155,7 @@ class _RowsView:
     depth: torch.Tensor
     anc: torch.Tensor
     struct: Optional[_lib.SsdRows] = None
+    kv_off: Optional[torch.Tensor] = None
 
 
 class Workspace:

@@ -515,6 +515,21 @@ def sample_rows(probs, rows, V, seed, counter, out_tok, ws=None):
     return out_tok
 
 
+def sample_top64(logits, rows, V, temperature, top_p, seed, counter, out_tok):
+    """sample_next at temperature > 0 (ssd_sample_top64_bf16): per row, one draw among the 64
+    largest logits after the temperature + nucleus warp of those 64."""
+    _check(logits, "logits"); _check(out_tok, "out_tok", torch.int32)
+    _len(out_tok, "out_tok", rows)
+    need = int(_lib.load().ssd_sample_top64_ws_bytes(rows, V))
+    if need < 0:
+        raise RuntimeError(f"sample_next: top-64 needs 64 <= V <= 262144 columns, got V={V}")
+    ws = _topk_ws(logits.device, need)
+    _lib.call("ssd_sample_top64_bf16", logits.data_ptr(), _rows(logits, "logits", V, rows), rows, V,
+              float(temperature), float(top_p), seed & (2**64 - 1), counter & (2**64 - 1), out_tok.data_ptr(),
+              ws.data_ptr(), ws.numel(), stream())
+    return out_tok
+
+
 def accept_sample_trials(P, Q, rows, branch, seed, counter0, trials, out_tokens, out_n):
     """ssd_accept_sample_trials: ``trials`` independent proposal + acceptance rounds of the
     unpruned tree ``branch`` over the fixed per-node rows of P and Q (row 0 the root); the

@@ -93,6 +93,23 @@ def test_warp_ties_at_the_cut_keep_lower_columns():
     check_warp_rows(got, lg, 4000, 1.0, 0.6)
 
 
+@pytest.mark.parametrize("T", [1.0, 0.7])
+def test_warp_exact_equality_at_the_cut(T):
+    """Four tied leaders in four different 4096-column chunks of a 128256 row (bf16 logit 0,
+    p = 0.25 exactly; every other logit -1000, p = 0). The reference keeps an entry while the mass
+    before it is <= top_p (tree_drafter.py:41): top_p 0.5 keeps three, 0.25 two, 0.75 four, each
+    tie at the cut by lowest column; probabilities 1/n exactly. No boundary band."""
+    V = 128256
+    leaders = [5, 4100, 70000, 128255]
+    ld = (V + 7) // 8 * 8
+    lg = torch.full((3, ld), -1000.0).to(torch.bfloat16)
+    lg[:, leaders] = 0.0
+    got = torch.stack([run_warp(lg[i:i + 1], V, T, tp)[0] for i, tp in enumerate((0.5, 0.25, 0.75))])
+    for r, n in enumerate((3, 2, 4)):
+        assert (got[r] > 0).nonzero().flatten().tolist() == leaders[:n], (T, r)
+        assert torch.equal(got[r, leaders[:n]], torch.full((n,), 1.0 / n))
+
+
 def test_warp_tie_ranks_cross_chunks():
     """A tie group spread over every 4096-column chunk of a 128256 row: the kept ties are the
     lowest columns across chunks (per-chunk tie counts give the prefix)."""

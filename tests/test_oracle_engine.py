@@ -118,6 +118,27 @@ def test_prune_order_known_answer():
     assert oe.prune_order(scores, depths, 5) == [0, 1, 2, 3, 4]
 
 
+def test_prune_tree_cross_depth_ties_prefer_smaller_depth():
+    """A log-prob of exactly 0 gives a child its parent's score, so (score) ties across depths
+    are real. Nodes: 0 (d1, 0.0), 1 (d1, -1.0), 2 (d2 under 0, 0.0), 3 (d2 under 1, -1.0).
+    (-score, depth) order is 0, 2, 1, 3: max_nodes 3 keeps {0, 1, 2}, max_nodes 1 keeps {0}.
+    The reversed depth order (2, 0, 3, 1) would keep {2, 0, 3} and close it to all four nodes,
+    or keep {2} and close it to {0, 2}."""
+    def tree():
+        return oe.DraftTree(tokens=[10, 11, 12, 13], parents=[-1, -1, 0, 1], depths=[1, 1, 2, 2],
+                            scores=[0.0, -1.0, 0.0, -1.0], ranks=[0, 1, 0, 0], draft_pos=[-1] * 4)
+    t = oe.prune_tree(tree(), 3)
+    assert t.tokens == [10, 11, 12] and t.parents == [-1, -1, 0]
+    t = oe.prune_tree(tree(), 1)
+    assert t.tokens == [10] and t.parents == [-1]
+    t = oe.prune_tree(tree(), 2)
+    assert t.tokens == [10, 12] and t.parents == [-1, 0]
+    # equal (score, depth): index order decides
+    t = oe.DraftTree(tokens=[1, 2, 3], parents=[-1, -1, -1], depths=[1, 1, 1], scores=[-0.5, -0.5, -0.5],
+                     ranks=[0, 1, 2], draft_pos=[-1] * 3)
+    assert oe.prune_tree(t, 2).tokens == [1, 2]
+
+
 def test_greedy_topk_ties_lower_column_first():
     logits = torch.tensor([[1.0, 3.0, 3.0, 2.0, 3.0]])
     lp, idx = oe.greedy_topk(logits, 4)
@@ -139,6 +160,21 @@ def test_warp_probs_nucleus_boundary_known_answer():
     torch.testing.assert_close(p, torch.tensor([1.0, 0.0, 0.0, 0.0]))
     p = oe.warp_probs(logits * 2, 2.0, 1.0)
     torch.testing.assert_close(p, torch.tensor([0.5, 0.3, 0.15, 0.05]))
+
+
+@pytest.mark.parametrize("V", [8, 128256])
+def test_warp_probs_exact_equality_at_the_cut(V):
+    """Masses that are exact in fp32: four tied leaders at logit 0 (p = 0.25 each), every other
+    logit -1000 (its probability underflows to 0). The mass before the leaders is 0, .25, .5, .75;
+    an entry is dropped only when that mass is strictly greater than top_p, so top_p 0.5 keeps
+    three (a >= rule would keep two) and top_p 0.25 keeps two."""
+    x = torch.full((V,), -1000.0)
+    x[[1, 3, 5, 7]] = 0.0
+    for T in (1.0, 0.7):
+        for top_p, n in ((0.5, 3), (0.25, 2), (0.75, 4), (0.0, 1)):
+            p = oe.warp_probs(x, T, top_p)
+            assert int((p > 0).sum()) == n, (T, top_p)
+            torch.testing.assert_close(p[p > 0], torch.full((n,), 1.0 / n))
 
 
 def test_top_vocab_known_answer():

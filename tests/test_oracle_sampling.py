@@ -72,6 +72,25 @@ def test_warp_known_answers():
     torch.testing.assert_close(p, torch.tensor([1 / 3, 2 / 3, 0.0, 0.0]), atol=1e-6, rtol=0)
 
 
+@pytest.mark.parametrize("V", [8, 128256])
+def test_warp_exact_equality_at_the_cut(V):
+    """Four tied leaders (logit 0, p = 0.25 exactly; every other logit -1000, p = 0): the mass
+    before them is 0, .25, .5, .75 and an entry survives while that mass is <= top_p. top_p 0.5
+    keeps three, 0.25 two, 0.75 all four; ties keep the lowest columns. Both the fp32 rule and
+    the float64 checker must agree exactly, without a band."""
+    x = torch.full((V,), -1000.0)
+    leaders = [2, 3, 6, 7] if V == 8 else [5, 4100, 70000, 128255]
+    x[leaders] = 0.0
+    for T in (1.0, 0.7):
+        for top_p, n in ((0.5, 3), (0.25, 2), (0.75, 4)):
+            p, _ = osm.warp_probs(x, T, top_p)
+            assert (p > 0).nonzero().flatten().tolist() == leaders[:n], (T, top_p)
+            torch.testing.assert_close(p[leaders[:n]], torch.full((n,), 1.0 / n))
+            p64, kept, _ = osm.warp_probs64(x, T, top_p)
+            assert kept.nonzero().flatten().tolist() == leaders[:n], (T, top_p)
+            assert float(p64[leaders[0]]) == 0.25
+
+
 def test_warp_matches_engine_without_ties():
     g = torch.Generator().manual_seed(0)
     for top_p in (1.0, 0.9, 0.5, 0.05):
@@ -181,3 +200,47 @@ def test_warp64_checker_agrees_with_fp32_rule():
                                            p32[kept].double(), rtol=1e-5, atol=0)
     p64, kept, band = osm.warp_probs64(torch.zeros(4), 1.0, 0.3)
     assert kept.tolist() == [True, True, False, False] and not band.any()
+
+
+def test_sample_next_top64_known_answers():
+    """generate_selfdistill.py:50-60: topk(64) of the logits, then warp_probs over those 64.
+    100 equal logits: the candidates are columns 0..63 (equal logits rank lower column first),
+    uniform at top_p 1; at top_p 0.5 the mass before rank j is j/64, kept while <= 0.5: ranks
+    0..32 (33 entries); at top_p 0.25, 17."""
+    x = torch.zeros(100)
+    for top_p, n in ((1.0, 64), (0.5, 33), (0.25, 17)):
+        p = osm.top64_probs(x, 0.7, top_p)
+        assert torch.equal((p > 0).nonzero().flatten(), torch.arange(n)), top_p
+        torch.testing.assert_close(p[:n], torch.full((n,), 1.0 / n, dtype=torch.float64))
+    # against torch.topk and the engine's warp where no two logits tie
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(5000, generator=g) * 3
+    val, idx = torch.topk(x, 64)
+    ref = torch.zeros(5000).index_copy_(0, idx, oe.warp_probs(val, 0.7, 0.9))
+    torch.testing.assert_close(osm.top64_probs(x, 0.7, 0.9).float(), ref)
+    # a draw never leaves the candidates
+    for s in range(50):
+        tok, _ = osm.sample_next_top64(torch.zeros(100), 1.0, 0.5, osm.Stream(s, 0), 0)
+        assert 0 <= tok <= 32
+
+
+def test_sample_next_top64_draws_follow_the_top64_warp():
+    """20000 seeded draws from one row whose 0.9-nucleus over the full row holds ~390 tokens: the
+    counts fit warp(top-64(logits)) by chi-square and reject the full-row warp (which puts a third
+    of its mass outside the 64 candidates)."""
+    g = torch.Generator().manual_seed(11)
+    x = (torch.randn(4000, generator=g) * 3.0).to(torch.bfloat16).float()
+    N = 20000
+    counts = np.bincount([osm.sample_next_top64(x, 0.7, 0.9, osm.Stream(s, 5), 2)[0] for s in range(N)],
+                         minlength=4000)
+    p = osm.top64_probs(x, 0.7, 0.9).numpy()
+    p = p / p.sum()
+    support = p > 0
+    assert counts[~support].sum() == 0
+    assert stats.chisquare(counts[support], p[support] * N).pvalue > 0.01
+    full, _, _ = osm.warp_probs64(x, 0.7, 0.9)
+    full = full.numpy() / full.numpy().sum()
+    bins = full * N >= 5
+    obs = np.append(counts[bins], counts[~bins].sum())
+    exp = np.append(full[bins] * N, full[~bins].sum() * N)
+    assert stats.chisquare(obs, exp).pvalue < 1e-6
