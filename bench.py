@@ -326,6 +326,7 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="llama3_8b_tree", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--graphs", action="store_true", help="replay captured greedy rounds (HIP graphs)")
     ap.add_argument("--cpu-rounds", type=int, default=40)
     ap.add_argument("--cpu-prompt", type=int, default=128)
     ap.add_argument("--ar-tokens", type=int, default=128)
@@ -368,25 +369,31 @@ def main() -> None:
     gen = SpeculativeGenerator(model, draft, cfg, target)
     ids = torch.randint(0, shape.vocab, (n_prompt,), generator=torch.Generator().manual_seed(1)).tolist()
     rounds = args.warmup + args.steps
-    sess = gen.session(n_prompt + rounds * (cfg.depth + 1) + gen.capacity(0, 0), seed=0)
+    sess = gen.session(n_prompt + rounds * (cfg.depth + 1) + gen.capacity(0, 0), seed=0,
+                       graphs=args.graphs)
     log(f"model + draft ready in {time.perf_counter() - t0:.1f}s")
     t0 = time.perf_counter()
     sess.prefill(ids)
     torch.cuda.synchronize()
     log(f"prefill {n_prompt} tokens: {time.perf_counter() - t0:.2f}s")
-    for _ in range(args.warmup):
-        sess.step()
+    # exactly `steps` rounds in the timed region: nothing of a later round is enqueued by the last
+    # warm-up step or by the last timed step (graph rounds otherwise keep one round queued)
+    for i in range(args.warmup):
+        sess.step(lookahead=i < args.warmup - 1)
     sess.phases.totals.clear()
     n_warm = len(sess.accepted_per_round)
     torch.cuda.synchronize()
     launches0 = int(_lib.load().ssd_launch_count())
     t0 = time.perf_counter()
     toks = 0
-    for _ in range(args.steps):
-        toks += len(sess.step())
+    for i in range(args.steps):
+        toks += len(sess.step(lookahead=i < args.steps - 1))
     torch.cuda.synchronize()
     secs = time.perf_counter() - t0
     launches = (int(_lib.load().ssd_launch_count()) - launches0) / args.steps
+    if sess.graph_rounds:  # replays do not pass through the library's launch counter
+        launches = sess.graph_launches
+    graph_info = {"enabled": sess.graphs, "rounds_replayed": sess.graph_rounds, "captures": sess.captures}
     acc = sess.accepted_per_round[n_warm:]
     phases = {k: 1000 * v / args.steps for k, v in sess.phases.totals.items()}
     log(f"{args.steps} rounds: {toks} tokens in {secs:.3f}s ({toks / secs:.1f} tok/s, {1000 * secs / args.steps:.3f} "
@@ -437,6 +444,7 @@ def main() -> None:
         # kernels the library enqueues per round (the engine adds two small torch ops and the
         # result copy)
         "launches_per_round": round(launches, 2),
+        "graph": graph_info,
         "ar_tokens_per_s": round(ar_tps, 3),
         "speedup_vs_ar": round((toks / secs) / ar_tps, 4),
         "round_weight_bytes": bytes_round,

@@ -182,10 +182,12 @@ int ssd_rmsnorm_bf16(const uint16_t* x, int64_t ldx, int M, int D, const uint16_
 int ssd_embed_bf16(const int32_t* ids, int M, const uint16_t* table, int64_t V, int D, uint16_t* out, int64_t ldo,
                    hipStream_t stream);
 /* KVCache.keep_positions (ssd/engine/kv_cache.py:54-70): move src[0..*n_dev) to [start, ...) in every
- * layer in one launch; all sources are read before any destination is written. */
+ * layer in one launch; all sources are read before any destination is written. pos_base (NULL or a
+ * device word): start is relative to *pos_base, read on the device (a destination range outside
+ * the cache then moves nothing). */
 int ssd_kv_compact_bf16(uint16_t* k_arena, uint16_t* vt_arena, int layers, int kv_heads, int head_dim,
                         int64_t max_len, int start, const int32_t* src, const int32_t* n_dev, int n_max,
-                        hipStream_t stream);
+                        const int32_t* pos_base, hipStream_t stream);
 /* Row top-k over bf16 logits. mode 0: raw values (k=1 is the first-index argmax of
  * ssd/engine/verify.py:47, speculative.py:83). mode 1: log_softmax values + logsumexp
  * (ssd/engine/tree_drafter.py:129-133); columns map through vocab_ids (subset head,
@@ -252,18 +254,23 @@ int ssd_tree_limits(int32_t* out3); /* host: {node capacity, max depth, max ance
 
 /* Start of a draft phase (ssd/engine/tree_drafter.py:147-160: a fresh DraftTree and the root fed
  * at root_pos): tree level counts to zero and root row 0 = position/slot root_pos, prefix
- * root_pos + 1, depth 0, on the device (no host copy). root_pos = base + n_new[0], read on the
- * device (n_new: the committed count of the previous round's record; NULL: root_pos = base), so
- * a round can start before the host has read the previous one. */
-int ssd_round_begin(const SsdTree* tree, const SsdRows* root, int base, const int32_t* n_new, hipStream_t stream);
+ * root_pos + 1, depth 0, on the device (no host copy). root_pos = base + n_new[0] + pos_base[0],
+ * read on the device (n_new: the committed count of the previous round's record; pos_base: a
+ * device word holding the previous round's root position; either may be NULL), so a round can
+ * start before the host has read the previous one. With pos_base, root_pos is stored back into
+ * *pos_base: the round's other calls given the same pos_base take their positions relative to
+ * it, so the whole round has no host-side position and can be captured once and replayed. */
+int ssd_round_begin(const SsdTree* tree, const SsdRows* root, int base, const int32_t* n_new, int32_t* pos_base,
+                    hipStream_t stream);
 
 /* One level of TreeDrafter.build (ssd/engine/tree_drafter.py:165-200): candidates of the current
  * frontier (cand_tok/cand_lp [F, k]; tok < 0 = none) -> score = parent score + lp, stable sort,
  * width cut, append; if feed, write the next draft forward's rows (positions root_pos+d+1, slots
- * past+j, prefix tree_start, ancestors' draft slots). */
+ * past+j, prefix tree_start, ancestors' draft slots). pos_base (NULL or a device word): root_pos,
+ * tree_start and past are relative to *pos_base. */
 int ssd_tree_level(const SsdTree* tree, int d, const int32_t* cand_tok, const float* cand_lp, int F_max, int k,
                    int width, int feed, int root_pos, int tree_start, int past, const SsdRows* rows, int rows_max,
-                   hipStream_t stream);
+                   const int32_t* pos_base, hipStream_t stream);
 /* ssd_tree_level whose candidates are merged in the same launch from the F_max rows of chunk
  * records that ssd_row_topk_partial_bf16 (k, mode 1: log-softmax) left in parts: the greedy
  * proposal's merge (ssd/engine/tree_drafter.py:129-133) and the level expansion
@@ -271,17 +278,20 @@ int ssd_tree_level(const SsdTree* tree, int d, const int32_t* cand_tok, const fl
  * N: the logits' columns; vocab_ids as for ssd_row_topk_bf16 (null: identity). */
 int ssd_tree_level_topk(const SsdTree* tree, int d, const void* parts, int64_t parts_bytes, int N,
                         const int32_t* vocab_ids, int F_max, int k, int width, int feed, int root_pos, int tree_start,
-                        int past, const SsdRows* rows, int rows_max, hipStream_t stream);
+                        int past, const SsdRows* rows, int rows_max, const int32_t* pos_base, hipStream_t stream);
 
 /* max_nodes cut by (-score, depth), ancestor closure and renumbering (ssd/engine/tree_drafter.py:202-207),
- * then the verify rows of verify_inputs (ssd/engine/verify.py:32-42); root token read from device. */
+ * then the verify rows of verify_inputs (ssd/engine/verify.py:32-42); root token read from device.
+ * pos_base (NULL or a device word): committed is relative to *pos_base. */
 int ssd_tree_finalize(const SsdTree* tree, int max_nodes, int committed, const int32_t* root_token,
-                      const SsdRows* rows, int rows_max, hipStream_t stream);
+                      const SsdRows* rows, int rows_max, const int32_t* pos_base, hipStream_t stream);
 
 /* greedy_verify (ssd/engine/verify.py:45-57) plus the bookkeeping of speculative.py:166-171:
- * result = [n_new, tokens...], keep_src/n_keep for ssd_kv_compact_bf16, next root token. */
+ * result = [n_new, tokens...], keep_src/n_keep for ssd_kv_compact_bf16, next root token.
+ * pos_base (NULL or a device word): committed is relative to *pos_base. */
 int ssd_accept_greedy(const SsdTree* tree, const int32_t* argmax, int committed, int32_t* result,
-                      int32_t* keep_src, int32_t* n_keep, int32_t* root_token, hipStream_t stream);
+                      int32_t* keep_src, int32_t* n_keep, int32_t* root_token, const int32_t* pos_base,
+                      hipStream_t stream);
 
 /* ---------------------------------------------------------------- sampling
  * Randomness is Philox4x32-10 keyed by a 64-bit seed; `counter` separates draws (one value per

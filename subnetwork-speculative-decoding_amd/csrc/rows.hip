@@ -152,10 +152,13 @@ __global__ __launch_bounds__(256) void embed_kernel(const int* __restrict__ ids,
 // trip; n <= n_max. An out-of-range source leaves its slot as it is.
 __global__ __launch_bounds__(256) void kv_compact_kernel(bf16_t* __restrict__ kc, bf16_t* __restrict__ vt, int kv_heads,
                                                          int hd, int64_t max_len, int start, const int* __restrict__ src,
-                                                         const int* __restrict__ n_ptr, int n_max) {
+                                                         const int* __restrict__ n_ptr, int n_max,
+                                                         const int* __restrict__ pos_base) {
   extern __shared__ u32x4_t stage16[];  // K runs [n_max][hd / 8], then V runs [groups][hd]
   const int lh = blockIdx.x;            // layer * kv_heads + head
-  const int n = max(0, min(*n_ptr, n_max));
+  if (pos_base) start += *pos_base;
+  // a destination range outside the cache moves nothing (the host checks absolute starts itself)
+  const int n = (start < 0 || start + n_max > max_len) ? 0 : max(0, min(*n_ptr, n_max));
   bf16_t* kbase = kc + (size_t)lh * max_len * hd;
   bf16_t* vbase = vt + (size_t)lh * hd * max_len;
   const int hq = hd >> 3;
@@ -287,18 +290,19 @@ SSD_API int ssd_embed_bf16(const int32_t* ids, int M, const uint16_t* table, int
 
 SSD_API int ssd_kv_compact_bf16(uint16_t* k_arena, uint16_t* vt_arena, int layers, int kv_heads, int head_dim,
                                 int64_t max_len, int start, const int32_t* src, const int32_t* n_dev, int n_max,
-                                hipStream_t stream) {
+                                const int32_t* pos_base, hipStream_t stream) {
   if (!k_arena || !vt_arena || !src || !n_dev || layers <= 0 || kv_heads <= 0 || head_dim <= 0 || n_max < 0)
     return set_error(SSD_EINVAL, "kv_compact: bad arguments");
   if (head_dim % 32 || max_len % 64)
     return set_error(SSD_EINVAL, "kv_compact: head_dim %d / max_len %lld must be multiples of 32 / 64", head_dim,
                      (long long)max_len);
-  if (start < 0 || start + n_max > max_len) return set_error(SSD_EINVAL, "kv_compact: start %d + %d > max_len", start, n_max);
+  if (!pos_base && (start < 0 || start + n_max > max_len))
+    return set_error(SSD_EINVAL, "kv_compact: start %d + %d > max_len", start, n_max);
   if (n_max == 0) return SSD_OK;
   const size_t lds = ((size_t)n_max * (head_dim / 8) + (size_t)((n_max + 7) / 8 + 1) * head_dim) * 16;
   if (lds > 64 * 1024) return set_error(SSD_ERANGE, "kv_compact: n_max=%d too large", n_max);
   SSD_LAUNCH(kv_compact_kernel, dim3(layers * kv_heads), dim3(256), lds, stream, (bf16_t*)k_arena,
-                     (bf16_t*)vt_arena, kv_heads, head_dim, max_len, start, src, n_dev, n_max);
+                     (bf16_t*)vt_arena, kv_heads, head_dim, max_len, start, src, n_dev, n_max, pos_base);
   return check_launch("kv_compact");
 }
 

@@ -129,8 +129,14 @@ __device__ __forceinline__ void tree_level_counts(const SsdTree& t, int d, int& 
 __global__ __launch_bounds__(1024) void tree_level_kernel(SsdTree t, int d, const int* __restrict__ cand_tok,
                                                           const float* __restrict__ cand_lp, int k, int width,
                                                           int feed, int root_pos, int tree_start, int past,
-                                                          SsdRows rows, int rows_max) {
+                                                          SsdRows rows, int rows_max, const int* pos_base) {
   __shared__ TreeLevelLds L;
+  if (pos_base) {
+    const int b = *pos_base;
+    root_pos += b;
+    tree_start += b;
+    past += b;
+  }
   int n0, F, prev_start;
   tree_level_counts(t, d, n0, F, prev_start);
   tree_level_stage(t, L);
@@ -145,11 +151,18 @@ __global__ __launch_bounds__(1024) void tree_level_kernel(SsdTree t, int d, cons
 __global__ __launch_bounds__(1024) void tree_level_topk_kernel(SsdTree t, int d, const TopkPart* __restrict__ parts,
                                                                int S, int f_rows, const int* __restrict__ vocab_ids,
                                                                int k, int width, int feed, int root_pos,
-                                                               int tree_start, int past, SsdRows rows, int rows_max) {
+                                                               int tree_start, int past, SsdRows rows, int rows_max,
+                                                               const int* pos_base) {
   __shared__ int s_tok[TREE_CAP];
   __shared__ float s_lp[TREE_CAP];
   __shared__ TreeLevelLds L;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (pos_base) {
+    const int b = *pos_base;
+    root_pos += b;
+    tree_start += b;
+    past += b;
+  }
   int n0, F, prev_start;
   tree_level_counts(t, d, n0, F, prev_start);
   tree_level_stage(t, L);
@@ -165,7 +178,8 @@ __global__ __launch_bounds__(1024) void tree_level_topk_kernel(SsdTree t, int d,
 // renumbering run on LDS instead of chains of dependent global loads.
 __global__ __launch_bounds__(1024) void tree_finalize_kernel(SsdTree t, int max_nodes, int committed,
                                                              const int* __restrict__ root_token, SsdRows rows,
-                                                             int rows_max) {
+                                                             int rows_max, const int* pos_base) {
+  if (pos_base) committed += *pos_base;
   __shared__ int keep[TREE_CAP];
   __shared__ int newidx[TREE_CAP];
   __shared__ double s_sc[TREE_CAP];
@@ -258,8 +272,9 @@ __global__ __launch_bounds__(1024) void tree_finalize_kernel(SsdTree t, int max_
 // for verify row r. Writes result = [n_new, tok_0..tok_{n_new-1}], keep_src = compaction
 // sources ([committed] + [committed + 1 + accepted]), n_keep, and the next root token.
 __global__ void accept_greedy_kernel(SsdTree t, const int* __restrict__ argmax, int committed, int* result,
-                                     int* keep_src, int* n_keep, int* root_token) {
+                                     int* keep_src, int* n_keep, int* root_token, const int* pos_base) {
   if (threadIdx.x != 0) return;
+  if (pos_base) committed += *pos_base;
   const int vn = t.vmeta[0];
   int cur = -1, n_acc = 0;
   int want;
@@ -285,13 +300,15 @@ __global__ void accept_greedy_kernel(SsdTree t, const int* __restrict__ argmax, 
 }
 
 // Start of a round: empty tree (level counts zero) and the root's draft row (position and slot
-// root_pos = base + n_new[0] (n_new null: base), prefix root_pos + 1, no ancestors); the root
-// token stays as the last round left it.
-__global__ void round_begin_kernel(SsdTree t, SsdRows r, int base, const int32_t* n_new) {
+// root_pos = base + n_new[0] + pos_base[0], each term present when its pointer is; prefix
+// root_pos + 1, no ancestors); the root token stays as the last round left it. With pos_base the
+// new root position is stored back there: the round's other kernels read it as their base.
+__global__ void round_begin_kernel(SsdTree t, SsdRows r, int base, const int32_t* n_new, int32_t* pos_base) {
   const int i = threadIdx.x;
   if (i < 1 + 2 * TREE_MAXDEPTH) t.meta[i] = 0;
   if (i == 0) {
-    const int root_pos = base + (n_new ? n_new[0] : 0);
+    const int root_pos = base + (n_new ? n_new[0] : 0) + (pos_base ? pos_base[0] : 0);
+    if (pos_base) pos_base[0] = root_pos;
     r.pos[0] = root_pos;
     r.slot[0] = root_pos;
     r.prefix[0] = root_pos + 1;
@@ -304,10 +321,10 @@ __global__ void round_begin_kernel(SsdTree t, SsdRows r, int base, const int32_t
 using namespace ssd;
 
 SSD_API int ssd_round_begin(const SsdTree* tree, const SsdRows* root, int base, const int32_t* n_new,
-                            hipStream_t stream) {
+                            int32_t* pos_base, hipStream_t stream) {
   if (!tree || !root || !tree->meta || !root->pos || root->cap < 1) return set_error(SSD_EINVAL, "round_begin: null");
   if (base < 0) return set_error(SSD_EINVAL, "round_begin: base %d < 0", base);
-  SSD_LAUNCH(round_begin_kernel, dim3(1), dim3(128), 0, stream, *tree, *root, base, n_new);
+  SSD_LAUNCH(round_begin_kernel, dim3(1), dim3(128), 0, stream, *tree, *root, base, n_new, pos_base);
   return check_launch("round_begin");
 }
 
@@ -321,7 +338,8 @@ SSD_API int ssd_tree_limits(int32_t* out) {
 
 SSD_API int ssd_tree_level_topk(const SsdTree* tree, int d, const void* parts, int64_t parts_bytes, int N,
                                 const int32_t* vocab_ids, int F_max, int k, int width, int feed, int root_pos,
-                                int tree_start, int past, const SsdRows* rows, int rows_max, hipStream_t stream) {
+                                int tree_start, int past, const SsdRows* rows, int rows_max, const int32_t* pos_base,
+                                hipStream_t stream) {
   if (!tree || !parts || (feed && !rows)) return set_error(SSD_EINVAL, "tree_level_topk: null pointer");
   if (d < 0 || d >= TREE_MAXDEPTH || d + 1 > ROW_MAXD)
     return set_error(SSD_ERANGE, "tree_level_topk: depth %d too deep", d);
@@ -339,13 +357,13 @@ SSD_API int ssd_tree_level_topk(const SsdTree* tree, int d, const void* parts, i
     return set_error(SSD_ERANGE, "tree_level_topk: rows_max too big");
   SsdRows r = feed ? *rows : SsdRows{};
   SSD_LAUNCH(tree_level_topk_kernel, dim3(1), dim3(1024), 0, stream, *tree, d, (const TopkPart*)parts, S, F_max,
-             vocab_ids, k, width, feed, root_pos, tree_start, past, r, feed ? rows_max : 0);
+             vocab_ids, k, width, feed, root_pos, tree_start, past, r, feed ? rows_max : 0, pos_base);
   return check_launch("tree_level_topk");
 }
 
 SSD_API int ssd_tree_level(const SsdTree* tree, int d, const int32_t* cand_tok, const float* cand_lp, int F_max,
                            int k, int width, int feed, int root_pos, int tree_start, int past, const SsdRows* rows,
-                           int rows_max, hipStream_t stream) {
+                           int rows_max, const int32_t* pos_base, hipStream_t stream) {
   if (!tree || !cand_tok || !cand_lp || (feed && !rows)) return set_error(SSD_EINVAL, "tree_level: null pointer");
   if (d < 0 || d >= TREE_MAXDEPTH || d + 1 > ROW_MAXD) return set_error(SSD_ERANGE, "tree_level: depth %d too deep", d);
   if (F_max * k > TREE_CAP || k < 1) return set_error(SSD_ERANGE, "tree_level: %d x %d candidates > %d", F_max, k, TREE_CAP);
@@ -354,26 +372,27 @@ SSD_API int ssd_tree_level(const SsdTree* tree, int d, const int32_t* cand_tok, 
   if (feed && (rows_max > rows->cap || rows_max > TREE_CAP)) return set_error(SSD_ERANGE, "tree_level: rows_max too big");
   SsdRows r = feed ? *rows : SsdRows{};
   SSD_LAUNCH(tree_level_kernel, dim3(1), dim3(1024), 0, stream, *tree, d, cand_tok, cand_lp, k, width, feed,
-                     root_pos, tree_start, past, r, feed ? rows_max : 0);
+                     root_pos, tree_start, past, r, feed ? rows_max : 0, pos_base);
   return check_launch("tree_level");
 }
 
 SSD_API int ssd_tree_finalize(const SsdTree* tree, int max_nodes, int committed, const int32_t* root_token,
-                              const SsdRows* rows, int rows_max, hipStream_t stream) {
+                              const SsdRows* rows, int rows_max, const int32_t* pos_base, hipStream_t stream) {
   if (!tree || !root_token || !rows) return set_error(SSD_EINVAL, "tree_finalize: null pointer");
   if (tree->cap < 1) return set_error(SSD_EINVAL, "tree_finalize: tree capacity %d", tree->cap);
   if (rows_max > rows->cap || rows_max > TREE_CAP + 1 || tree->cap > TREE_CAP)
     return set_error(SSD_ERANGE, "tree_finalize: rows_max %d too big", rows_max);
   SSD_LAUNCH(tree_finalize_kernel, dim3(1), dim3(1024), 0, stream, *tree, max_nodes, committed, root_token,
-                     *rows, rows_max);
+                     *rows, rows_max, pos_base);
   return check_launch("tree_finalize");
 }
 
 SSD_API int ssd_accept_greedy(const SsdTree* tree, const int32_t* argmax, int committed, int32_t* result,
-                              int32_t* keep_src, int32_t* n_keep, int32_t* root_token, hipStream_t stream) {
+                              int32_t* keep_src, int32_t* n_keep, int32_t* root_token, const int32_t* pos_base,
+                              hipStream_t stream) {
   if (!tree || !argmax || !result || !keep_src || !n_keep || !root_token)
     return set_error(SSD_EINVAL, "accept_greedy: null pointer");
   SSD_LAUNCH(accept_greedy_kernel, dim3(1), dim3(64), 0, stream, *tree, argmax, committed, result, keep_src,
-                     n_keep, root_token);
+                     n_keep, root_token, pos_base);
   return check_launch("accept_greedy");
 }

@@ -99,10 +99,12 @@ class KVCache:
                        n_dev, n)
         self.seq_len = start + n
 
-    def compact_device(self, start: int, src: torch.Tensor, n_dev: torch.Tensor, n_max: int) -> None:
-        """Compaction with sources and count already on the device (the engine's path: no host sync)."""
+    def compact_device(self, start: int, src: torch.Tensor, n_dev: torch.Tensor, n_max: int,
+                       pos_base: Optional[torch.Tensor] = None) -> None:
+        """Compaction with sources and count already on the device (the engine's path: no host sync);
+        with ``pos_base`` the destination start is relative to that device word."""
         ops.kv_compact(self.k, self.vt, self.num_slots, self.kv_heads, self.head_dim, self.capacity, start, src,
-                       n_dev, n_max)
+                       n_dev, n_max, pos_base)
 
     def reset(self) -> None:
         self.seq_len = 0

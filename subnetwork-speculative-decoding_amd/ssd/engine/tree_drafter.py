@@ -178,28 +178,42 @@ class TreeDrafter:
             sampler.propose(self.draft, logits, rows, d, self.branch[d], tree.meta, cand_tok, cand_lp)
 
     def begin_device(self, cache: KVCache, root_rows, base_pos: int, tree: DeviceTree, cand_tok, cand_lp, ws,
-                     sampler=None, n_new_dev: Optional[torch.Tensor] = None) -> None:
+                     sampler=None, n_new_dev: Optional[torch.Tensor] = None,
+                     pos_base: Optional[torch.Tensor] = None, window: Optional[tuple] = None) -> None:
         """First part of the draft phase: empty tree, the root (token in ``root_rows.ids[0]``) fed
         at root_pos = base_pos + n_new_dev[0] (``n_new_dev`` None: base_pos), and the root's
         proposals. With ``n_new_dev`` the position is only read on the device, so this can be
         enqueued before the host has read the previous round; the root forward then gets bounds
-        (root_pos is at most depth + 1 past base_pos) instead of the exact position."""
+        (root_pos is at most depth + 1 past base_pos) instead of the exact position.
+
+        ``pos_base`` (a device int32 word holding the previous round's root position; base_pos is
+        then 0) makes the round position-free on the host: the root position is pos_base +
+        n_new_dev[0], stored back into pos_base for the round's other calls, and ``window`` =
+        (lo, hi) bounds the root positions the call may see (attention bounds, room check)."""
         if not self.greedy and sampler is None:
             raise ValueError("sampled drafting needs a Sampler")
-        hi = base_pos + (self.cfg.depth + 1 if n_new_dev is not None else 0)
+        if window is not None:
+            lo, hi = window
+        else:
+            lo, hi = base_pos, base_pos + (self.cfg.depth + 1 if n_new_dev is not None else 0)
         cache.check_room(hi + 1 + self.max_tree_cache())
         _lib.call("ssd_round_begin", tree.struct, root_rows.struct, base_pos,
-                  None if n_new_dev is None else n_new_dev.data_ptr(), ops.stream())
-        logits = self.draft.forward_rows(root_rows, 1, base_pos + 1, hi + 1, cache, ws)
+                  None if n_new_dev is None else n_new_dev.data_ptr(),
+                  None if pos_base is None else pos_base.data_ptr(), ops.stream())
+        logits = self.draft.forward_rows(root_rows, 1, lo + 1, hi + 1, cache, ws)
         self._propose(logits, 1, 0, tree, cand_tok, cand_lp, sampler)
 
     def levels_device(self, cache: KVCache, root_pos: int, tree: DeviceTree, level_rows, cand_tok, cand_lp, ws,
-                      sampler=None) -> None:
+                      sampler=None, pos_base: Optional[torch.Tensor] = None, window: Optional[tuple] = None) -> None:
         """Rest of the draft phase once root_pos is known on the host: every level's expansion /
-        width cut and the forwards of the fed levels; leaves the unpruned tree in ``tree``."""
+        width cut and the forwards of the fed levels; leaves the unpruned tree in ``tree``. With
+        ``pos_base`` root_pos is relative to that device word (0) and ``window`` bounds the root
+        positions, as in begin_device."""
+        lo, hi = window if window is not None else (root_pos, root_pos)
         tree_start = root_pos + 1
-        cache.check_room(tree_start + self.max_tree_cache())
+        cache.check_room(hi + 1 + self.max_tree_cache())
         past = tree_start
+        pb = None if pos_base is None else pos_base.data_ptr()
         for d in range(self.cfg.depth):
             feed = d < self.cfg.depth - 1
             f_max = 1 if d == 0 else self.levels[d - 1]
@@ -209,17 +223,18 @@ class TreeDrafter:
                 _lib.call("ssd_tree_level_topk", tree.struct, d, self._parts.data_ptr(), self._parts.numel(),
                           self._parts_n, None if vocab_ids is None else vocab_ids.data_ptr(), f_max, self.branch[d],
                           self.width[d] or 0, int(feed), root_pos, tree_start, past, level_rows.struct,
-                          m if feed else 0, ops.stream())
+                          m if feed else 0, pb, ops.stream())
             else:
                 _lib.call("ssd_tree_level", tree.struct, d, cand_tok.data_ptr(), cand_lp.data_ptr(), f_max,
                           self.branch[d], self.width[d] or 0, int(feed), root_pos, tree_start, past,
-                          level_rows.struct, m if feed else 0, ops.stream())
+                          level_rows.struct, m if feed else 0, pb, ops.stream())
             if not feed:
                 break
-            logits = self.draft.forward_rows(level_rows, m, tree_start, tree_start + d + 1, cache, ws)
+            logits = self.draft.forward_rows(level_rows, m, lo + 1, hi + 1 + d + 1, cache, ws)
             self._propose(logits, m, d + 1, tree, cand_tok, cand_lp, sampler)
             past += m
-        cache.seq_len = past
+        if pos_base is None:
+            cache.seq_len = past
 
     def build_device(self, cache: KVCache, root_rows, root_pos: int, tree: DeviceTree, level_rows, cand_tok,
                      cand_lp, ws, sampler=None) -> None:
@@ -230,11 +245,13 @@ class TreeDrafter:
         self.begin_device(cache, root_rows, root_pos, tree, cand_tok, cand_lp, ws, sampler)
         self.levels_device(cache, root_pos, tree, level_rows, cand_tok, cand_lp, ws, sampler)
 
-    def finalize_device(self, tree: DeviceTree, committed: int, root_rows, verify_rows) -> int:
-        """max_nodes cut + verify rows; returns the verify row count used for the launch."""
+    def finalize_device(self, tree: DeviceTree, committed: int, root_rows, verify_rows,
+                        pos_base: Optional[torch.Tensor] = None) -> int:
+        """max_nodes cut + verify rows; returns the verify row count used for the launch. With
+        ``pos_base`` committed is relative to that device word."""
         rows = self.max_verify_nodes() + 1
         _lib.call("ssd_tree_finalize", tree.struct, self.cfg.max_nodes or 0, committed, root_rows.ids.data_ptr(),
-                  verify_rows.struct, rows, ops.stream())
+                  verify_rows.struct, rows, None if pos_base is None else pos_base.data_ptr(), ops.stream())
         return rows
 
     # -------------------------------------------------------------- reference API

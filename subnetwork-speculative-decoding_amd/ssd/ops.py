@@ -258,14 +258,17 @@ def kv_untile(flat: torch.Tensor, cap: int, hd: int, which: str) -> torch.Tensor
     return flat[..., idx]
 
 
-def kv_compact(k_arena, vt_arena, layers, kv_heads, head_dim, max_len, start, src, n_dev, n_max):
+def kv_compact(k_arena, vt_arena, layers, kv_heads, head_dim, max_len, start, src, n_dev, n_max, pos_base=None):
+    """ssd_kv_compact_bf16; with ``pos_base`` (a device int32 word) ``start`` is relative to it."""
     _check(k_arena, "k_arena"); _check(vt_arena, "vt_arena")
+    if pos_base is not None:
+        _check(pos_base, "pos_base", torch.int32)
     _check(src, "src", torch.int32); _check(n_dev, "n", torch.int32)
     _len(src, "src", n_max)
     if k_arena.numel() < layers * kv_heads * max_len * head_dim or vt_arena.numel() < k_arena.numel():
         raise ValueError("kv_compact: arenas smaller than layers * kv_heads * max_len * head_dim")
     _lib.call("ssd_kv_compact_bf16", k_arena.data_ptr(), vt_arena.data_ptr(), layers, kv_heads, head_dim, max_len,
-              int(start), src.data_ptr(), n_dev.data_ptr(), int(n_max), stream())
+              int(start), src.data_ptr(), n_dev.data_ptr(), int(n_max), _p(pos_base), stream())
 
 
 _TOPK_WS: dict = {}

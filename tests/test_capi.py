@@ -42,7 +42,7 @@ def test_host_only_entry_points():
     from ssd import _lib
 
     lib = _lib.load()
-    assert lib.ssd_abi_version() == _lib.ABI_VERSION == 3
+    assert lib.ssd_abi_version() == _lib.ABI_VERSION == 4
     assert lib.ssd_packed_weight_elems(17, 40) == 128 * 64  # rows padded to 128, K to 32
     assert [lib.ssd_gemm_weight_group(n, 4096) for n in (4096, 8192, 28672, 128256)] == [1, 2, 4, 8]
     assert lib.ssd_gemm_weight_group(4096, 100) == 0
@@ -107,3 +107,30 @@ def test_unpack_rows_inverts_grouped_packing():
         ids = torch.tensor([0, 5, 17, 100, 255])
         assert torch.equal(unpack_rows(grouped, n, k, ids, group), w[ids])
 
+
+
+def test_every_call_site_passes_the_declared_argument_count():
+    """Each _lib.call("ssd_x", ...) in the package, bench.py and the tests passes exactly as many
+    arguments as the ctypes prototype of ssd_x declares (caught on the CPU, before a GPU run)."""
+    import ast
+    import glob
+
+    from ssd import _lib
+
+    files = glob.glob(os.path.join(REPO, "subnetwork-speculative-decoding_amd", "ssd", "**", "*.py"), recursive=True)
+    files += glob.glob(os.path.join(REPO, "tests", "*.py")) + [os.path.join(REPO, "bench.py")]
+    checked = 0
+    for f in files:
+        for node in ast.walk(ast.parse(open(f).read())):
+            if not (isinstance(node, ast.Call) and isinstance(node.func, ast.Attribute) and node.func.attr == "call"
+                    and isinstance(node.func.value, ast.Name) and node.func.value.id == "_lib"):
+                continue
+            if not node.args or not isinstance(node.args[0], ast.Constant) or any(
+                    isinstance(a, ast.Starred) for a in node.args):
+                continue
+            name = node.args[0].value
+            assert name in _lib._PROTOS, f"{f}:{node.lineno}: {name} has no prototype"
+            want = len(_lib._PROTOS[name][1])
+            assert len(node.args) - 1 == want, f"{f}:{node.lineno}: {name} given {len(node.args) - 1} args, takes {want}"
+            checked += 1
+    assert checked > 30

@@ -219,6 +219,34 @@ def test_greedy_sd_bitwise_equals_autoregressive(hf, tree_name, kind):
             assert res.mean_accepted > cfg.depth
 
 
+@pytest.mark.parametrize("kind,n_new", [("untrained", 330), ("perfect", 600)])
+def test_graph_rounds_across_segments_bitwise(hf, kind, n_new):
+    """Captured rounds (one HIP graph per 256-position segment of root positions, replayed with one
+    round queued behind the one being read) give exactly the tokens of plain launches and of
+    autoregressive decoding, across segment boundaries (prompt 250: roots cross 256 and 512) and up
+    to the end of the cache."""
+    sp, _, DraftingConfig, _ = ssd()
+    target = sp.TargetRunner(hf)
+    draft = make_draft(hf, kind)
+    cfg = DraftingConfig(depth=4, branch=[3, 2, 2, 1], max_nodes=24)
+    ids = prompt(250, 4)
+    ref = sp.autoregressive_generate(target, ids, n_new, {-1}).tokens
+    gen = sp.SpeculativeGenerator(hf, draft, cfg, target)
+    sess = gen.session(gen.capacity(ids.shape[1], n_new), graphs=True)
+    assert sess.graphs
+    out = [sess.prefill(ids[0].tolist())]
+    while len(out) < n_new:
+        out.extend(sess.step())
+    sess.drain()
+    assert out[:n_new] == ref
+    rounds = len(sess.accepted_per_round)
+    assert sess.captures >= 2 and sess.graph_rounds >= rounds - 3, (sess.captures, sess.graph_rounds, rounds)
+    assert sess.graph_launches > 20
+    plain = gen.generate(ids, n_new, {-1})
+    assert plain.tokens == ref
+    assert gen.generate(ids, 40, {-1}, graphs=True).tokens == ref[:40]
+
+
 def test_greedy_sd_with_draft_vocab_subset(hf):
     sp, _, DraftingConfig, _ = ssd()
     from ssd.data.token_freq import top_vocab

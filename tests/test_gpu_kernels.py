@@ -283,6 +283,26 @@ def test_kv_compact_overlapping_and_all_layers(hd, start, src):
     assert torch.equal(ops.kv_untile(vt, S, hd, "v").cpu(), ok.kv_compact(v0, start, src))
 
 
+def test_kv_compact_start_relative_to_device_base():
+    """The start read relative to a device base word (captured rounds) moves the same entries as the
+    absolute start; a destination range past the cache moves nothing."""
+    ops = _ops()
+    L, kvh, hd, S = 2, 2, 128, 128
+    k0 = bf(rand(L, kvh, S, hd, seed=43))
+    v0 = bf(rand(L, kvh, S, hd, seed=44))
+    src = [61, 70, 64, 100]
+    buf = torch.tensor(src, dtype=torch.int32, device=DEV)
+    n = torch.tensor([4], dtype=torch.int32, device=DEV)
+    for base_v, start, moved in ((61, 0, True), (50, 11, True), (126, 0, False)):
+        k, vt = ops.kv_tile(k0.to(DEV), "k"), ops.kv_tile(v0.to(DEV), "v")
+        base = torch.tensor([base_v], dtype=torch.int32, device=DEV)
+        ops.kv_compact(k, vt, L, kvh, hd, S, start, buf, n, 4, pos_base=base)
+        want_k = ok.kv_compact(k0, base_v + start, src) if moved else k0
+        want_v = ok.kv_compact(v0, base_v + start, src) if moved else v0
+        assert torch.equal(ops.kv_untile(k, S, hd, "k").cpu(), want_k), base_v
+        assert torch.equal(ops.kv_untile(vt, S, hd, "v").cpu(), want_v), base_v
+
+
 def test_kv_compact_out_of_range_source_keeps_slot():
     ops = _ops()
     L, kvh, hd, S = 2, 2, 128, 128
@@ -464,7 +484,7 @@ def test_tree_level_and_finalize_match_oracle(seed):
         feed = d < depth - 1
         m = oe.level_sizes(oe.Drafting(depth=depth, branch=branch, width=width))[d]
         _lib.call("ssd_tree_level", tree.struct, d, ct.data_ptr(), cl.data_ptr(), F, k, width[d] or 0, int(feed),
-                  committed, tree_start, past, level_rows.struct, m if feed else 0, ops.stream())
+                  committed, tree_start, past, level_rows.struct, m if feed else 0, None, ops.stream())
         level = oe.expand_level(ref, frontier, [(t, [float(torch.tensor(x, dtype=torch.float32)) for x in l])
                                                 for t, l in zip(toks, lps)], d, width[d])
         if feed:
@@ -484,7 +504,7 @@ def test_tree_level_and_finalize_match_oracle(seed):
     assert tree.scores[:n].tolist() == ref.scores and tree.ranks[:n].tolist() == ref.ranks
     rows = min(n, max_nodes or n) + 1
     _lib.call("ssd_tree_finalize", tree.struct, max_nodes or 0, committed, root_rows.ids.data_ptr(), vrows.struct,
-              rows, ops.stream())
+              rows, None, ops.stream())
     pruned = oe.prune_tree(ref, max_nodes)
     torch.cuda.synchronize()
     vn = int(tree.vmeta[0])
@@ -502,7 +522,9 @@ def test_tree_level_and_finalize_match_oracle(seed):
 def test_tree_level_topk_equals_topk_then_level(seed, V, mapped):
     """The greedy proposal's merge done inside the level launch (ssd_row_topk_partial_bf16 +
     ssd_tree_level_topk) builds the same tree and draft rows as ssd_row_topk_bf16 +
-    ssd_tree_level, level by level, including ties between logits and a vocabulary-subset mapping."""
+    ssd_tree_level, level by level, including ties between logits and a vocabulary-subset mapping.
+    The merged launch takes its positions relative to a device base word (the form captured rounds
+    use): the same absolute positions must come out."""
     from ssd import _lib, ops
     from ssd.models.subnetwork_draft import Rows
 
@@ -518,6 +540,7 @@ def test_tree_level_topk_equals_topk_then_level(seed, V, mapped):
     ct = torch.zeros(1024, dtype=torch.int32, device=DEV)
     cl = torch.zeros(1024, dtype=torch.float32, device=DEV)
     F, past = 1, tree_start
+    base = torch.tensor([committed], dtype=torch.int32, device=DEV)
     for d in range(depth):
         k = branch[d]
         # logits on a coarse grid so that exact ties occur across chunks and rows
@@ -526,12 +549,13 @@ def test_tree_level_topk_equals_topk_then_level(seed, V, mapped):
         m = min(F * k, width[d] or F * k)
         ops.row_topk(logits, F, V, k, 1, vocab_ids, ct, cl)
         _lib.call("ssd_tree_level", trees[0].struct, d, ct.data_ptr(), cl.data_ptr(), F, k, width[d] or 0, int(feed),
-                  committed, tree_start, past, rows[0].struct, m if feed else 0, ops.stream())
+                  committed, tree_start, past, rows[0].struct, m if feed else 0, None, ops.stream())
         parts = torch.empty(ops.row_topk_ws_bytes(F, V), dtype=torch.uint8, device=DEV)
         ops.row_topk_partial(logits, F, V, k, 1, parts)
         _lib.call("ssd_tree_level_topk", trees[1].struct, d, parts.data_ptr(), parts.numel(), V,
-                  None if vocab_ids is None else vocab_ids.data_ptr(), F, k, width[d] or 0, int(feed), committed,
-                  tree_start, past, rows[1].struct, m if feed else 0, ops.stream())
+                  None if vocab_ids is None else vocab_ids.data_ptr(), F, k, width[d] or 0, int(feed), 0,
+                  tree_start - committed, past - committed, rows[1].struct, m if feed else 0, base.data_ptr(),
+                  ops.stream())
         torch.cuda.synchronize()
         if feed:
             for name in ("ids", "pos", "slot", "prefix", "depth"):
@@ -583,13 +607,17 @@ def test_accept_greedy_matches_oracle(seed):
     keep = torch.zeros(40, dtype=torch.int32, device=DEV)
     nkeep = torch.zeros(1, dtype=torch.int32, device=DEV)
     root = torch.zeros(1, dtype=torch.int32, device=DEV)
-    _lib.call("ssd_accept_greedy", tree.struct, i32(argmax).data_ptr(), 30, result.data_ptr(), keep.data_ptr(),
-              nkeep.data_ptr(), root.data_ptr(), ops.stream())
-    torch.cuda.synchronize()
-    nn_ = int(result[0])
-    assert nn_ == len(acc_ref) + 1
-    assert result[1:1 + nn_].tolist() == [t.tokens[i] for i in acc_ref] + [bonus_ref]
-    assert keep[:nn_].tolist() == [30] + [31 + i for i in acc_ref] and int(nkeep) == nn_ and int(root) == bonus_ref
+    # committed 30 given directly, then as 0 relative to a device base word holding 30
+    for committed, base in ((30, None), (0, i32([30]))):
+        result.zero_(); keep.zero_(); nkeep.zero_(); root.zero_()
+        _lib.call("ssd_accept_greedy", tree.struct, i32(argmax).data_ptr(), committed, result.data_ptr(),
+                  keep.data_ptr(), nkeep.data_ptr(), root.data_ptr(), None if base is None else base.data_ptr(),
+                  ops.stream())
+        torch.cuda.synchronize()
+        nn_ = int(result[0])
+        assert nn_ == len(acc_ref) + 1
+        assert result[1:1 + nn_].tolist() == [t.tokens[i] for i in acc_ref] + [bonus_ref]
+        assert keep[:nn_].tolist() == [30] + [31 + i for i in acc_ref] and int(nkeep) == nn_ and int(root) == bonus_ref
 
 
 # ---------------------------------------------- folded RMSNorm / fused residual projection
