@@ -17,11 +17,22 @@ row, the temperature + nucleus warp of those 64 alone, one categorical draw amon
 draws; Philox keyed by (step, row)). The Philox seed is drawn from ``generator``, which advances it
 as torch.multinomial would: successive calls with one generator draw independently, and a
 generator seeded alike reproduces them.
-"""
 
+The module also keeps the reference's command-line entry point (``python -m
+ssd.data.generate_selfdistill --config ... --out data/x.jsonl --tokens N``, reference :110-178): prompts
+are the first user turns of a chat dataset (``iter_prompts``; a local ``data.local_path`` .jsonl or the
+``data.dataset`` split), generated in length-sorted batches and written in dataset order as
+``{"messages": [user, assistant], "n_tokens": n}`` lines; a rerun resumes after the rows already in
+the file, seeding with ``--seed`` + rows done.
+"""
 from __future__ import annotations
 
-from typing import Optional
+import argparse
+import json
+import logging
+import time
+from pathlib import Path
+from typing import Callable, Iterable, Iterator, Optional
 
 import torch
 
@@ -137,3 +148,118 @@ def generate_batch(target: TargetRunner, prompts: list, max_new_tokens: int, eos
         cut = next((i + 1 for i, t in enumerate(r) if t in eos_ids), len(r))
         rows_out.append(r[:cut])
     return rows_out
+
+
+log = logging.getLogger("ssd")
+
+
+def _examples(cfg) -> Iterator[dict]:
+    if cfg.data.local_path:
+        with open(cfg.data.local_path) as f:
+            for line in f:
+                if line.strip():
+                    yield json.loads(line)
+    else:
+        from datasets import load_dataset  # streams from the hub: needs network access
+
+        yield from load_dataset(cfg.data.dataset, split=cfg.data.split, streaming=True)
+
+
+def iter_prompts(cfg, tokenizer, max_prompt_tokens: int) -> Iterator[tuple]:
+    """(user text, chat-formatted prompt ids) for each example's first user turn (reference
+    generate_selfdistill.py:38-47); examples whose first message is not the user's, or whose prompt
+    is longer than ``max_prompt_tokens``, are skipped. Examples come from ``data.local_path`` (a .jsonl
+    with a ``data.messages_field`` column) when set, else from the ``data.dataset`` split."""
+    for ex in _examples(cfg):
+        msgs = ex.get(cfg.data.messages_field) or []
+        if not msgs or msgs[0].get("role") != "user":
+            continue
+        ids = tokenizer.apply_chat_template([msgs[0]], add_generation_prompt=True, return_dict=True)["input_ids"]
+        if len(ids) <= max_prompt_tokens:
+            yield msgs[0]["content"], list(ids)
+
+
+def write_selfdistill(target, prompts: Iterable, out_path, tokens: int, batch_size: int, max_new_tokens: int,
+                      eos_ids: set, temperature: float, top_p: float, pad_id: int, seed: int,
+                      decode: Callable[[list], str], generate: Callable = generate_batch) -> tuple:
+    """The generation loop of the reference's main (generate_selfdistill.py:134-178). Rows already in
+    ``out_path`` are counted (rows and their ``n_tokens``) and that many prompts skipped, so a rerun
+    resumes where the file ends; sampling is seeded with ``seed`` + rows done (a torch.Generator; the
+    reference seeds the global generator the same way). Prompts are pulled batch_size * 8 at a time,
+    generated in batches of similar length, and written in dataset order until ``tokens`` generated
+    tokens are in the file. Returns (rows, tokens) in the file."""
+    out_path = Path(out_path)
+    out_path.parent.mkdir(parents=True, exist_ok=True)
+    done_rows, done_tokens = 0, 0
+    if out_path.exists():
+        with open(out_path) as f:
+            for line in f:
+                done_rows += 1
+                done_tokens += json.loads(line)["n_tokens"]
+        log.info("resuming: %d rows / %d tokens already in %s", done_rows, done_tokens, out_path)
+    generator = torch.Generator().manual_seed(seed + done_rows)
+    it = iter(prompts)
+    for _ in zip(range(done_rows), it):
+        pass
+    t0, new_tokens = time.perf_counter(), 0
+    with open(out_path, "a") as f:
+        while done_tokens < tokens:
+            chunk = [x for _, x in zip(range(batch_size * 8), it)]
+            if not chunk:
+                break
+            order = sorted(range(len(chunk)), key=lambda i: len(chunk[i][1]))  # similar lengths together
+            results: dict = {}
+            for s0 in range(0, len(order), batch_size):
+                idx = order[s0:s0 + batch_size]
+                rows = generate(target, [chunk[i][1] for i in idx], max_new_tokens, eos_ids, temperature, top_p,
+                                pad_id, generator)
+                results.update(zip(idx, rows))
+            for i, (text, _) in enumerate(chunk):  # dataset order keeps a resume exact
+                toks = results[i]
+                f.write(json.dumps({"messages": [{"role": "user", "content": text},
+                                                 {"role": "assistant", "content": decode(toks)}],
+                                    "n_tokens": len(toks)}) + "\n")
+                done_rows += 1
+                done_tokens += len(toks)
+                new_tokens += len(toks)
+            f.flush()
+            log.info("%d / %d tokens (%.0f tok/s)", done_tokens, tokens, new_tokens / (time.perf_counter() - t0))
+    return done_rows, done_tokens
+
+
+def main(argv: Optional[list] = None) -> None:
+    """``python -m ssd.data.generate_selfdistill`` (reference generate_selfdistill.py:110-178)."""
+    from ssd.config import SSDConfig
+    from ssd.runtime import eos_ids_of, load_base_model, setup_env
+
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--config", required=True)
+    p.add_argument("--out", required=True)
+    p.add_argument("--tokens", type=int, default=3_000_000,
+                   help="stop after this many generated tokens (total, incl. resumed)")
+    p.add_argument("--batch-size", type=int, default=32)
+    p.add_argument("--max-new-tokens", type=int, default=384)
+    p.add_argument("--max-prompt-tokens", type=int, default=384)
+    p.add_argument("--temperature", type=float, default=0.7)
+    p.add_argument("--top-p", type=float, default=0.9, help="applied within the top 64 tokens")
+    p.add_argument("--seed", type=int, default=0)
+    args = p.parse_args(argv)
+
+    setup_env()
+    cfg = SSDConfig.from_yaml(args.config)
+    if not Path(cfg.model.base_model).is_dir():
+        raise FileNotFoundError("self-distillation needs a local checkpoint directory with its tokenizer "
+                                f"(model.base_model = {cfg.model.base_model!r})")
+    from transformers import AutoTokenizer
+
+    tokenizer = AutoTokenizer.from_pretrained(cfg.model.base_model, local_files_only=True)
+    base = load_base_model(cfg)
+    target = TargetRunner(base)
+    pad_id = tokenizer.convert_tokens_to_ids("<|finetune_right_pad_id|>")
+    write_selfdistill(target, iter_prompts(cfg, tokenizer, args.max_prompt_tokens), args.out, args.tokens,
+                      args.batch_size, args.max_new_tokens, eos_ids_of(base), args.temperature, args.top_p, pad_id,
+                      args.seed, lambda toks: tokenizer.decode(toks, skip_special_tokens=True))
+
+
+if __name__ == "__main__":
+    main()

@@ -14,6 +14,7 @@
 """
 
 import glob
+import json
 import os
 
 import pytest
@@ -187,3 +188,60 @@ def test_ssd_run_flags():
         parse(["--config", "c.yaml", "--prompt", "a", "--bridges", "b.pt", "--untrained"])
     with pytest.raises(SystemExit):
         parse(["--config", "c.yaml"])
+
+
+def test_selfdistill_resume_keeps_dataset_order(tmp_path):
+    """The self-distillation loop (reference generate_selfdistill.py:134-178) with a stub generator:
+    batches are formed from length-sorted chunks but rows land in dataset order; a run stopped by
+    --tokens and resumed writes exactly the file of one uninterrupted run, skipping the written
+    prompts and seeding with seed + rows done."""
+    from ssd.data import generate_selfdistill as gs
+
+    prompts = [(f"q{i}", [i] + [0] * ((i * 7) % 5)) for i in range(40)]
+    seeds = []
+
+    def fake_generate(target, batch, n, eos, T, top_p, pad, generator):
+        seeds.append(generator.initial_seed())
+        return [[p[0], len(p), 9] for p in batch]  # a reply depends on its prompt only
+
+    kw = dict(batch_size=3, max_new_tokens=8, eos_ids=set(), temperature=0.7, top_p=0.9, pad_id=0, seed=5,
+              decode=lambda toks: " ".join(map(str, toks)), generate=fake_generate)
+    full = tmp_path / "full.jsonl"
+    assert gs.write_selfdistill(None, iter(prompts), full, 10 ** 9, **kw) == (40, 120)
+    assert seeds and set(seeds) == {5}
+    rows = [json.loads(x) for x in full.read_text().splitlines()]
+    assert [r["messages"][0]["content"] for r in rows] == [t for t, _ in prompts]
+    assert [r["messages"][1]["content"] for r in rows] == [f"{i} {1 + (i * 7) % 5} 9" for i in range(40)]
+    part = tmp_path / "part.jsonl"
+    seeds.clear()
+    done = gs.write_selfdistill(None, iter(prompts), part, 30, **kw)  # stops after the first chunk of 24
+    assert done == (24, 72) and set(seeds) == {5}
+    seeds.clear()
+    assert gs.write_selfdistill(None, iter(prompts), part, 10 ** 9, **kw) == (40, 120)
+    assert set(seeds) == {5 + 24}
+    assert part.read_text() == full.read_text()
+
+
+def test_selfdistill_iter_prompts_local_jsonl(tmp_path):
+    """iter_prompts takes each example's first user turn, chat-formatted, and skips examples that
+    start with another role or exceed max_prompt_tokens."""
+    from ssd.config import SSDConfig
+    from ssd.data.generate_selfdistill import iter_prompts
+
+    data = tmp_path / "chat.jsonl"
+    exs = [{"messages": [{"role": "user", "content": "hi there"}, {"role": "assistant", "content": "x"}]},
+           {"messages": [{"role": "system", "content": "s"}, {"role": "user", "content": "no"}]},
+           {"messages": []},
+           {"messages": [{"role": "user", "content": "one two three four five six"}]},
+           {"messages": [{"role": "user", "content": "ok"}]}]
+    data.write_text("\n".join(json.dumps(e) for e in exs) + "\n")
+
+    class Tok:
+        def apply_chat_template(self, msgs, add_generation_prompt, return_dict):
+            assert add_generation_prompt and return_dict and len(msgs) == 1
+            return {"input_ids": [1] + [len(w) for w in msgs[0]["content"].split()] + [2]}
+
+    cfg = SSDConfig()
+    cfg.data.local_path = str(data)
+    got = list(iter_prompts(cfg, Tok(), 5))
+    assert got == [("hi there", [1, 2, 5, 2]), ("ok", [1, 2, 2])]
