@@ -319,6 +319,62 @@ def sampled_rounds(model, draft, target, ids: list, steps: int, warmup: int = 5)
             "ms_per_round_phases": {k: round(1000 * v / steps, 4) for k, v in sess.phases.totals.items()}}
 
 
+# Standalone tree-attention shapes (--attention): (kv heads, q heads, head_dim, prefix slots, rows, depth,
+# layers rotated so every call streams its K/V from HBM).
+ATTN_SHAPES = {
+    "8b_verify": (8, 32, 128, 4097, 25, 4, 32),
+    "8b_draft": (8, 32, 128, 4098, 12, 4, 32),
+    "8b_ar": (8, 32, 128, 4100, 1, 0, 32),
+    "70b_verify": (8, 64, 128, 16385, 25, 4, 8),
+    "70b_draft": (8, 64, 128, 16386, 12, 4, 8),
+}
+
+
+def attention_figures(name: str, reps: int = 20) -> dict:
+    """One tree-attention call (partial + combine) at a decode shape: the root row attends the prefix,
+    the tree rows the prefix plus 1..depth ancestors among the tree slots; best of `reps` passes over
+    the rotated layers, us per call, and the algorithmic bytes (K/V over P + depth slots, queries,
+    outputs)."""
+    import torch
+
+    from ssd import ops
+
+    kvh, heads, hd, P, M, depth, layers = ATTN_SHAPES[name]
+    dev = "cuda"
+    cap = (P + 2 * 64 + 63) // 64 * 64
+    g = torch.Generator().manual_seed(0)
+    ks = [ops.kv_tile(torch.randn(kvh, cap, hd, generator=g).to(torch.bfloat16).to(dev), "k") for _ in range(layers)]
+    vs = [ops.kv_tile(torch.randn(kvh, cap, hd, generator=g).to(torch.bfloat16).to(dev), "v") for _ in range(layers)]
+    q = torch.randn(M, heads * hd, generator=g).to(torch.bfloat16).to(dev)
+    pre = torch.full((M,), P, dtype=torch.int32, device=dev)
+    dep = torch.tensor([0] + [min(depth, 1 + i % depth) for i in range(M - 1)], dtype=torch.int32, device=dev)
+    an = torch.zeros(M, 32, dtype=torch.int32)
+    for t in range(1, M):
+        an[t, :int(dep[t])] = torch.arange(P + 1, P + 1 + int(dep[t])) + (t % 3)
+    an = an.to(dev)
+    ws = torch.zeros(ops.attn_workspace_floats(M, heads, hd, cap), dtype=torch.float32, device=dev)
+    out = torch.zeros(M, heads * hd, dtype=torch.bfloat16, device=dev)
+
+    def call(i):
+        ops.tree_attention(q, M, heads, kvh, hd, ks[i], vs[i], cap, pre, dep, an, P, P + depth + 3, ws, out)
+
+    for i in range(layers):
+        call(i)
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(layers):
+            call(i)
+        b.record()
+        b.synchronize()
+        best = min(best, a.elapsed_time(b) * 1000 / layers)
+    byts = 2 * kvh * (P + depth) * hd * 2 + 2 * M * heads * hd * 2
+    return {"shape": name, "us": round(best, 2), "bytes": byts, "gbs": round(byts / best / 1e3, 1),
+            "frac": round(byts / best / 1e3 / HBM_PEAK_GBS, 4)}
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -338,6 +394,9 @@ def main() -> None:
     ap.add_argument("--batch-gen-tokens", type=int, default=64)
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="also run one plain device copy of this many MiB (calibrates rocprofv3 byte counters)")
+    ap.add_argument("--attention", default="",
+                    help=f"only time tree attention at these shapes (comma list of {', '.join(ATTN_SHAPES)}), "
+                         "one JSON line each")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: bench.py runs on exactly one GPU (got --gpus {args.gpus}); multi-GPU runs are not supported",
@@ -345,6 +404,17 @@ def main() -> None:
         sys.exit(3)
 
     import torch
+
+    if args.attention:
+        torch.cuda.set_device(0)
+        for name in args.attention.split(","):
+            print(json.dumps(attention_figures(name)), flush=True)
+        if args.copy_probe_mb:
+            src = torch.ones(args.copy_probe_mb << 20, dtype=torch.uint8, device="cuda")
+            torch.empty_like(src).copy_(src)
+            torch.cuda.synchronize()
+            log(f"copy probe: {args.copy_probe_mb} MiB read + {args.copy_probe_mb} MiB written")
+        return
 
     from ssd import _lib
     from ssd.config import BridgeConfig, DraftingConfig
