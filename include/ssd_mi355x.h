@@ -71,6 +71,22 @@ int ssd_gemm_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packe
                   uint16_t* Y, int64_t ldy, const uint16_t* bias, int act, const uint16_t* residual, int64_t ldr,
                   hipStream_t stream);
 
+/* The vocabulary head fused with its per-row top-k chunk pass: the draft head's logits
+ * (ssd/models/subnetwork_draft.py:345-349) reduced in the GEMM's epilogue to the records that the
+ * proposal's top-k (ssd/engine/tree_drafter.py:129-133) merges, so the logits never make a round trip
+ * through memory. parts (8-byte aligned, >= M * ssd_gemm_topk_parts(N) * 136 bytes) gets, for row m
+ * and slab s (consecutive 128-column groups, the slabs a function of N only), the slab's k best
+ * (value, column) keys of the bf16-rounded logits, its maximum and (mode 1) its sum of exp(x - max);
+ * merge them with ssd_tree_level_topk or ssd_row_topk_merge (S = ssd_gemm_topk_parts(N)). The keys
+ * are exact; the sums of exp differ from ssd_row_topk_partial_bf16's only in summation order.
+ * W_packed as for ssd_gemm_bf16 (tiles grouped by ssd_gemm_weight_group(N, K)). Y (NULL or ldy >= N)
+ * also receives the logits, bit-identical to ssd_gemm_bf16's for N >= 65536.
+ * k in [1, 16], mode 0 (raw values) or 1 (log-softmax). */
+int ssd_gemm_topk_parts(int N);
+int ssd_gemm_topk_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int N, int K,
+                       float norm_eps, int k, int mode, void* parts, int64_t parts_bytes, uint16_t* Y, int64_t ldy,
+                       hipStream_t stream);
+
 /* Y[M, I] = silu(X Wg^T + bg) * (X Wu^T + bu), gate/up interleaved per 16-row tile.
  * Replaces LlamaMLP's gate/up/act (modeling_llama MLP called at ssd/models/subnetwork_draft.py:245)
  * and the swiglu bridge (ssd/models/bridges.py:57-65). */
@@ -214,6 +230,12 @@ int ssd_row_topk_bf16_noalloc(const uint16_t* logits, int64_t ld, int M, int N, 
  * proposal step, ssd/engine/tree_drafter.py:129-133). */
 int ssd_row_topk_partial_bf16(const uint16_t* logits, int64_t ld, int M, int N, int k, int mode, void* ws,
                               int64_t ws_bytes, hipStream_t stream);
+/* The merge pass of ssd_row_topk_bf16 alone, over S records per row (S = ceil(N / 4096) from
+ * ssd_row_topk_partial_bf16, ssd_gemm_topk_parts(N) from ssd_gemm_topk_bf16; S <= 256 and
+ * S * k <= 1024): out_tok[M * k], out_val (NULL or M * k), out_lse (NULL or M, mode 1). */
+int ssd_row_topk_merge(const void* parts, int64_t parts_bytes, int M, int S, int k, int mode,
+                       const int32_t* vocab_ids, int32_t* out_tok, float* out_val, float* out_lse,
+                       hipStream_t stream);
 
 /* ------------------------------------------------------------------ tree
  * Device-resident DraftTree (ssd/engine/tree_drafter.py:48-95). All members are device
@@ -271,12 +293,13 @@ int ssd_round_begin(const SsdTree* tree, const SsdRows* root, int base, const in
 int ssd_tree_level(const SsdTree* tree, int d, const int32_t* cand_tok, const float* cand_lp, int F_max, int k,
                    int width, int feed, int root_pos, int tree_start, int past, const SsdRows* rows, int rows_max,
                    const int32_t* pos_base, hipStream_t stream);
-/* ssd_tree_level whose candidates are merged in the same launch from the F_max rows of chunk
- * records that ssd_row_topk_partial_bf16 (k, mode 1: log-softmax) left in parts: the greedy
- * proposal's merge (ssd/engine/tree_drafter.py:129-133) and the level expansion
- * (:165-183) in one launch; identical results to ssd_row_topk_bf16 followed by ssd_tree_level.
+/* ssd_tree_level whose candidates are merged in the same launch from the F_max rows of S records
+ * each that ssd_row_topk_partial_bf16 (S = ceil(N / 4096)) or ssd_gemm_topk_bf16 (S =
+ * ssd_gemm_topk_parts(N)) left in parts (k, mode 1: log-softmax; S <= 256, S * k <= 1024): the
+ * greedy proposal's merge (ssd/engine/tree_drafter.py:129-133) and the level expansion (:165-183) in
+ * one launch; identical results to ssd_row_topk_bf16 followed by ssd_tree_level.
  * N: the logits' columns; vocab_ids as for ssd_row_topk_bf16 (null: identity). */
-int ssd_tree_level_topk(const SsdTree* tree, int d, const void* parts, int64_t parts_bytes, int N,
+int ssd_tree_level_topk(const SsdTree* tree, int d, const void* parts, int64_t parts_bytes, int N, int S,
                         const int32_t* vocab_ids, int F_max, int k, int width, int feed, int root_pos, int tree_start,
                         int past, const SsdRows* rows, int rows_max, const int32_t* pos_base, hipStream_t stream);
 

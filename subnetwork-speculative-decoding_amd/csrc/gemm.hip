@@ -27,6 +27,7 @@
 //   activation, residual add, SwiGLU (gate rows 0-7 / up rows 8-15 of a tile),
 //   and QKV + RoPE + KV-cache write (rotary pair dims in rows r and r+8).
 #include "gemm_epi.h"
+#include "topk.h"
 
 #include <algorithm>
 
@@ -313,12 +314,36 @@ struct WideCfg {
   static constexpr int SC = SC0 < 8 ? SC0 : 8;  // sub-tiles reduced per LDS pass
 };
 
-template <int CT, int U, int NORM>
-__global__ __launch_bounds__(64 * WIDE_WAVES) void gemm_wide_kernel(GemmArgs a, int n_groups) {
+// Top-k records of a vocabulary head (ssd_gemm_topk_bf16). The 8-tile groups are cut into S slabs
+// of G consecutive groups (a function of N only); a workgroup walks slabs blockIdx.x, + gridDim.x,
+// ..., the groups of a slab in order, and leaves one TopkPart per (row, slab): the slab's k best
+// (value, column) keys, its maximum and (mode 1) its sum of exp(x - max), accumulated group by group
+// (the sum rescaled when the maximum grows). Values are the bf16-rounded logits, exactly what the
+// plain head would store.
+struct WideTopk {
+  TopkPart* parts;  // [M][S]
+  int k, mode;      // k <= TOPK_MAX; mode 1 adds the sum of exp
+  int G, S;
+  int pg;           // tiles per packing group of W (the layout ssd_gemm_bf16 reads for this N)
+};
+
+__device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
+  const uint32_t lo = __shfl((uint32_t)v, src), hi = __shfl((uint32_t)(v >> 32), src);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// PG: W packed in 8-tile groups (8), or (0) in tk.pg-tile groups, pg in {1, 2, 4, 8}: tile t, k-block kb at
+// ((t / pg) * kb_total * pg + kb * pg + t % pg) * 64 lanes.
+template <int CT, int U, int NORM, int TOPK, int PG>
+__global__ __launch_bounds__(64 * WIDE_WAVES) void gemm_wide_kernel(GemmArgs a, int n_groups, WideTopk tk) {
   constexpr int SC = WideCfg<CT>::SC;
+  constexpr int TR = TOPK ? CT * 16 : 1;  // rows of the top-k state
   __shared__ float red[WIDE_WAVES][SC][CT][4][68];
   __shared__ float ssw[WIDE_WAVES][CT][16];
   __shared__ float rn[CT * 16];
+  __shared__ float tv[TR][128];                // one group's bf16-rounded logits per row
+  __shared__ uint64_t tkey[TR][TOPK_MAX];      // running k best per row (0: none)
+  __shared__ float tmx[TR], tse[TR];           // running max / sum of exp per row
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int kbt = a.kb_total;
@@ -331,8 +356,17 @@ __global__ __launch_bounds__(64 * WIDE_WAVES) void gemm_wide_kernel(GemmArgs a, 
   const int kb_rest = (kbt / (WIDE_WAVES * WIDE_DEAL)) * WIDE_WAVES * WIDE_DEAL + w;
   // plain logits: two adjacent outputs per 4-byte store
   const bool pair_store = !a.bias && !a.act && !a.residual && a.ldy % 2 == 0 && ((uintptr_t)a.Y & 3) == 0;
+  const bool store = a.Y != nullptr;  // the top-k head stores its logits only when asked
+  const int G = TOPK ? tk.G : 1, n_slabs = TOPK ? tk.S : n_groups;
   bool first = true;
-  for (int grp = blockIdx.x; grp < n_groups; grp += gridDim.x, first = false) {
+  for (int slab = blockIdx.x; slab < n_slabs; slab += gridDim.x) {
+  if constexpr (TOPK) {
+    for (int i = threadIdx.x; i < TR * TOPK_MAX; i += 64 * WIDE_WAVES) tkey[i / TOPK_MAX][i % TOPK_MAX] = 0ull;
+    if ((int)threadIdx.x < TR) { tmx[threadIdx.x] = -INFINITY; tse[threadIdx.x] = 0.f; }
+    // the first group's epilogue barriers order these writes before the state is read
+  }
+  const int g_end = min((slab + 1) * G, n_groups);
+  for (int grp = slab * G; grp < g_end; ++grp, first = false) {
     f32x4_t acc[8][CT];
 #pragma unroll
     for (int s = 0; s < 8; ++s)
@@ -342,6 +376,21 @@ __global__ __launch_bounds__(64 * WIDE_WAVES) void gemm_wide_kernel(GemmArgs a, 
 #pragma unroll
     for (int c = 0; c < CT; ++c) ss[c] = 0.f;
     const u32x4_t* wp = (const u32x4_t*)a.W + (size_t)grp * kbt * 8 * 64 + lane;
+    uint32_t wq[8];  // PG == 0: 16-byte offset of tile s of the group (packed heads stay below 2^32 of them)
+    uint32_t wstride = 0;
+    if constexpr (PG == 0) {
+      const int pg = tk.pg;
+      wstride = (uint32_t)pg * 64;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const int t = grp * 8 + s;
+        wq[s] = ((uint32_t)(t / pg) * kbt * pg + t % pg) * 64 + lane;
+      }
+    }
+    auto wload = [&](int kb, int s) -> u32x4_t {
+      if constexpr (PG == 8) return __builtin_nontemporal_load(wp + ((size_t)kb * 8 + s) * 64);
+      else return __builtin_nontemporal_load((const u32x4_t*)a.W + (wq[s] + (uint32_t)kb * wstride));
+    };
     int t = 0;
     for (; t + U <= n_full; t += U) {
       u32x4_t wr[U][8], xr[U][CT];
@@ -349,7 +398,7 @@ __global__ __launch_bounds__(64 * WIDE_WAVES) void gemm_wide_kernel(GemmArgs a, 
       for (int u = 0; u < U; ++u) {
         const int kb = kb_at(t + u);
 #pragma unroll
-        for (int s = 0; s < 8; ++s) wr[u][s] = __builtin_nontemporal_load(wp + ((size_t)kb * 8 + s) * 64);
+        for (int s = 0; s < 8; ++s) wr[u][s] = wload(kb, s);
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -377,7 +426,7 @@ __global__ __launch_bounds__(64 * WIDE_WAVES) void gemm_wide_kernel(GemmArgs a, 
       if (kb >= kbt) break;
       u32x4_t wr[8], xr[CT];
 #pragma unroll
-      for (int s = 0; s < 8; ++s) wr[s] = __builtin_nontemporal_load(wp + ((size_t)kb * 8 + s) * 64);
+      for (int s = 0; s < 8; ++s) wr[s] = wload(kb, s);
 #pragma unroll
       for (int c = 0; c < CT; ++c) xr[c] = *(const u32x4_t*)(xp[c] + kb * 32);
 #pragma unroll
@@ -436,6 +485,11 @@ __global__ __launch_bounds__(64 * WIDE_WAVES) void gemm_wide_kernel(GemmArgs a, 
         const int n = (grp * 8 + s0 + sl) * 16 + 2 * q;
         if (n >= a.N) continue;
         const float v0 = val(2 * q), v1 = val(2 * q + 1);
+        if constexpr (TOPK) {
+          tv[m][(s0 + sl) * 16 + 2 * q] = rbf(v0);
+          tv[m][(s0 + sl) * 16 + 2 * q + 1] = rbf(v1);  // past N: never read
+          if (!store) continue;
+        }
         if (pair_store && n + 1 < a.N) {
           *(uint32_t*)(a.Y + (size_t)m * a.ldy + n) = pack_bf16x2(rbf(v0), rbf(v1));
         } else {
@@ -445,6 +499,56 @@ __global__ __launch_bounds__(64 * WIDE_WAVES) void gemm_wide_kernel(GemmArgs a, 
       }
       __syncthreads();  // the next pass (or group) overwrites red
     }
+    if constexpr (TOPK) {
+      // wave w updates rows w, w + 8, ...: lane l holds columns 2l, 2l + 1 of the group
+      const int n0 = grp * 128 + 2 * lane;
+      const bool ok0 = n0 < a.N, ok1 = n0 + 1 < a.N;
+      for (int m = w; m < Mv; m += WIDE_WAVES) {
+        const float va = tv[m][2 * lane], vb = tv[m][2 * lane + 1];
+        float gm = fmaxf(ok0 ? va : -INFINITY, ok1 ? vb : -INFINITY);
+        for (int off = 32; off >= 1; off >>= 1) gm = fmaxf(gm, __shfl_xor(gm, off));
+        const float om = tmx[m], nm = fmaxf(om, gm);
+        if (tk.mode == 1) {
+          float e = (ok0 ? __expf(va - nm) : 0.f) + (ok1 ? __expf(vb - nm) : 0.f);
+          for (int off = 32; off >= 1; off >>= 1) e += __shfl_xor(e, off);
+          const float os = tse[m];
+          if (lane == 0) tse[m] = (om == -INFINITY ? 0.f : os * __expf(om - nm)) + e;
+        }
+        if (lane == 0) tmx[m] = nm;
+        const uint64_t ka = ok0 ? rank_key(va, n0) : 0ull, kb = ok1 ? rank_key(vb, n0 + 1) : 0ull;
+        uint64_t c0 = lane < TOPK_MAX ? tkey[m][lane] : 0ull;
+        const uint64_t kth = shfl_u64(c0, tk.k - 1);
+        if (!__any(ka > kth || kb > kth)) continue;  // nothing in this group enters the row's k best
+        // the k best of (list, group): k rounds of a wave maximum (keys are distinct)
+        uint64_t c1 = ka, c2 = kb, nk = 0ull;
+        for (int q = 0; q < tk.k; ++q) {
+          uint64_t b = c0 > c1 ? c0 : c1;
+          b = b > c2 ? b : c2;
+          const uint64_t mq = wave_max_u64(b);
+          if (mq != 0ull) {
+            if (c0 == mq) c0 = 0ull;
+            else if (c1 == mq) c1 = 0ull;
+            else if (c2 == mq) c2 = 0ull;
+          }
+          if (lane == q) nk = mq;
+        }
+        if (lane < TOPK_MAX) tkey[m][lane] = nk;
+      }
+      // the next group's first barrier orders these updates before tv is rewritten
+    }
+  }
+  if constexpr (TOPK) {
+    // each row's state was last written by its own wave: no barrier needed to read it here
+    for (int m = w; m < Mv; m += WIDE_WAVES) {
+      TopkPart* o = tk.parts + (size_t)m * tk.S + slab;
+      if (lane < TOPK_MAX) o->key[lane] = tkey[m][lane];
+      if (lane == 0) {
+        o->mx = tmx[m];
+        o->se = tk.mode == 1 ? tse[m] : 0.f;
+      }
+    }
+    __syncthreads();  // the next slab's reset follows every wave's record
+  }
   }
 }
 
@@ -701,7 +805,7 @@ static GemmPlan plan_for(int N, int K) {
 static bool use_wide(const GemmPlan& p) { return p.nsub == 8; }
 
 template <int EPI>
-static int launch_wide(GemmArgs a, int n_groups, hipStream_t s) {
+static int launch_wide(GemmArgs a, int n_groups, hipStream_t s, const WideTopk* tk = nullptr) {
   // one workgroup per CU (the CU count is read once per device)
   static int cus_of[64] = {0};
   int dev = 0;
@@ -711,11 +815,18 @@ static int launch_wide(GemmArgs a, int n_groups, hipStream_t s) {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
     if (dev >= 0 && dev < 64) cus_of[dev] = cus;
   }
-  const dim3 grid((unsigned)std::min(n_groups, cus)), block(64 * WIDE_WAVES);
+  const dim3 grid((unsigned)std::min(tk ? tk->S : n_groups, cus)), block(64 * WIDE_WAVES);
   const int ct = (a.M + 15) / 16;
-#define SSD_WIDE(CT_, U_)                                                                          \
-  if (a.norm_eps > 0.f) SSD_LAUNCH((gemm_wide_kernel<CT_, U_, 1>), grid, block, 0, s, a, n_groups); \
-  else SSD_LAUNCH((gemm_wide_kernel<CT_, U_, 0>), grid, block, 0, s, a, n_groups);
+  const WideTopk t = tk ? *tk : WideTopk{};
+  const bool pg8 = !tk || tk->pg == 8;
+#define SSD_WIDE_K(CT_, U_, NORM_, TOPK_)                                                                \
+  if (pg8) SSD_LAUNCH((gemm_wide_kernel<CT_, U_, NORM_, TOPK_, 8>), grid, block, 0, s, a, n_groups, t); \
+  else SSD_LAUNCH((gemm_wide_kernel<CT_, (U_ > 2 ? 2 : U_), NORM_, TOPK_, 0>), grid, block, 0, s, a, n_groups, t);
+#define SSD_WIDE(CT_, U_)                                                                            \
+  if (tk) {                                                                                          \
+    if (a.norm_eps > 0.f) { SSD_WIDE_K(CT_, U_, 1, 1) } else { SSD_WIDE_K(CT_, U_, 0, 1) }           \
+  } else if (a.norm_eps > 0.f) SSD_LAUNCH((gemm_wide_kernel<CT_, U_, 1, 0, 8>), grid, block, 0, s, a, n_groups, t); \
+  else SSD_LAUNCH((gemm_wide_kernel<CT_, U_, 0, 0, 8>), grid, block, 0, s, a, n_groups, t);
   switch (ct) {
     case 1: SSD_WIDE(1, 4) break;
     case 2: SSD_WIDE(2, 2) break;
@@ -723,7 +834,16 @@ static int launch_wide(GemmArgs a, int n_groups, hipStream_t s) {
     default: SSD_WIDE(4, 1) break;
   }
 #undef SSD_WIDE
+#undef SSD_WIDE_K
   return check_launch("gemm_wide");
+}
+
+// Slabs of the top-k head: G consecutive 8-tile groups each, at most TOPK_MAX_PARTS of them; a
+// function of N only, so a row's records do not depend on M or on the device.
+static void topk_slabs(int N, int& G, int& S) {
+  const int groups = (N + 127) / 128;
+  G = (groups + TOPK_MAX_PARTS - 1) / TOPK_MAX_PARTS;
+  S = (groups + G - 1) / G;
 }
 
 template <int EPI>
@@ -841,6 +961,49 @@ SSD_API int ssd_gemm_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t*
   a.Y = Y; a.ldy = ldy; a.bias = bias; a.act = act; a.residual = residual; a.ldr = ldr;
   a.norm_eps = norm_eps > 0.f ? norm_eps : 0.f;
   return launch_gemm<EPI_STORE>(a, stream);
+}
+
+SSD_API int ssd_gemm_topk_parts(int N) {
+  if (N <= 0) return set_error(SSD_EINVAL, "gemm_topk_parts: N=%d", N);
+  int G, S;
+  topk_slabs(N, G, S);
+  return S;
+}
+
+// The vocabulary head with its per-row top-k chunk pass in the epilogue: parts[m * S + s] (S =
+// ssd_gemm_topk_parts(N)) gets slab s's k best keys, max and (mode 1) sum of exp of row m of
+// X W^T (final norm folded when norm_eps > 0), for a merge (ssd_tree_level_topk,
+// ssd_row_topk_merge_bf16). The logits themselves are stored only when Y is not null.
+SSD_API int ssd_gemm_topk_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int N, int K,
+                               float norm_eps, int k, int mode, void* parts, int64_t parts_bytes, uint16_t* Y,
+                               int64_t ldy, hipStream_t stream) {
+  int rc = check_common(X, ldx, M, W_packed, N, K);
+  if (rc) return rc;
+  if (k < 1 || k > TOPK_MAX || k > N) return set_error(SSD_EINVAL, "gemm_topk: k=%d outside [1, min(%d, N)]", k, TOPK_MAX);
+  if (mode != 0 && mode != 1) return set_error(SSD_EINVAL, "gemm_topk: mode %d", mode);
+  if (!parts || ((uintptr_t)parts & 7)) return set_error(SSD_EINVAL, "gemm_topk: parts must be 8-byte aligned");
+  if (Y && ldy < N) return set_error(SSD_EINVAL, "gemm_topk: ldy %lld < N=%d", (long long)ldy, N);
+  WideTopk t{};
+  topk_slabs(N, t.G, t.S);
+  if (parts_bytes < (int64_t)M * t.S * (int64_t)sizeof(TopkPart))
+    return set_error(SSD_EINVAL, "gemm_topk: parts of %lld bytes < %lld", (long long)parts_bytes,
+                     (long long)M * t.S * (long long)sizeof(TopkPart));
+  t.k = k;
+  t.mode = mode;
+  t.pg = plan_for(N, K).nsub;  // W is packed as ssd_gemm_bf16 reads it for this shape
+  if (t.pg != 8 && ((N + 127) / 128 * 128) * (int64_t)K / 8 >= ((int64_t)1 << 32))
+    return set_error(SSD_ERANGE, "gemm_topk: packed head of %d x %d too large", N, K);
+  const int n_groups = (N + 127) / 128;
+  for (int m0 = 0; m0 < M; m0 += 64) {
+    GemmArgs a{};
+    a.X = X + (size_t)m0 * ldx; a.ldx = ldx; a.M = std::min(64, M - m0); a.W = (const uint4*)W_packed;
+    a.N = N; a.kb_total = K / 32;
+    a.Y = Y ? Y + (size_t)m0 * ldy : nullptr; a.ldy = ldy;
+    a.norm_eps = norm_eps > 0.f ? norm_eps : 0.f;
+    t.parts = (TopkPart*)parts + (size_t)m0 * t.S;
+    if ((rc = launch_wide<EPI_STORE>(a, n_groups, stream, &t))) return rc;
+  }
+  return SSD_OK;
 }
 
 // Y[M, I] = silu(X Wg^T + bg) * (X Wu^T + bu); W_packed holds, per 16-row tile i, gate rows

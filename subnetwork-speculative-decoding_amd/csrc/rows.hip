@@ -306,6 +306,25 @@ SSD_API int ssd_kv_compact_bf16(uint16_t* k_arena, uint16_t* vt_arena, int layer
   return check_launch("kv_compact");
 }
 
+// Merge pass alone, over S records per row written by ssd_row_topk_partial_bf16 (S = ceil(N / 4096))
+// or ssd_gemm_topk_bf16 (S = ssd_gemm_topk_parts(N)).
+SSD_API int ssd_row_topk_merge(const void* parts, int64_t parts_bytes, int M, int S, int k, int mode,
+                               const int32_t* vocab_ids, int32_t* out_tok, float* out_val, float* out_lse,
+                               hipStream_t stream) {
+  if (!parts || !out_tok) return set_error(SSD_EINVAL, "row_topk_merge: null pointer");
+  if (M < 0 || k < 1 || k > TOPK_MAX || (mode != 0 && mode != 1))
+    return set_error(SSD_EINVAL, "row_topk_merge: M=%d k=%d mode=%d", M, k, mode);
+  if (S < 1 || S > TOPK_MAX_PARTS || S * k > 64 * TOPK_MAX)
+    return set_error(SSD_EINVAL, "row_topk_merge: %d records of %d keys per row", S, k);
+  if (parts_bytes < (int64_t)M * S * (int64_t)sizeof(TopkPart))
+    return set_error(SSD_EINVAL, "row_topk_merge: parts of %lld bytes < %lld", (long long)parts_bytes,
+                     (long long)M * S * (long long)sizeof(TopkPart));
+  if (M == 0) return SSD_OK;
+  SSD_LAUNCH(row_topk_merge_kernel, dim3(M), dim3(64), 0, stream, (const TopkPart*)parts, S, k, mode, vocab_ids,
+             out_tok, out_val, out_lse);
+  return check_launch("row_topk_merge");
+}
+
 SSD_API int64_t ssd_row_topk_ws_bytes(int M, int N) {
   const int S = (N + TOPK_CHUNK - 1) / TOPK_CHUNK;
   return (int64_t)M * S * (int64_t)sizeof(TopkPart);

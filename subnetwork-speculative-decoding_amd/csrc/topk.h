@@ -44,20 +44,29 @@ struct TopkPart {
   uint64_t key[TOPK_MAX];  // the chunk's k best, best first
 };
 
-// Merge of one row's S <= 64 chunk partials by one wave: global max M; logsumexp = M + log(sum_s se_s *
-// exp(mx_s - M)) (lanes own chunks; fixed butterfly order); the k best of the S*k chunk keys, held
-// in registers (lane l: candidates l + 64*j), in k rounds of a wave maximum. Lane 0 writes token q
-// (vocab_ids[column] when vocab_ids is set) to tok[q] and, when val is set, its value to val[q]:
-// mode 0 the raw value, mode 1 the log-softmax value (x - M) - log(sum); lse (mode 1, when set)
-// gets M + log(sum).
+constexpr int TOPK_MAX_PARTS = 256;  // records per row a merge takes (S * k <= 64 * TOPK_MAX as well)
+
+// Merge of one row's S <= 256 partial records (each the k best keys and the max / sum of exp of a
+// disjoint column range) by one wave: global max M; logsumexp = M + log(sum_s se_s exp(mx_s - M))
+// (lane l sums its records l, l + 64, ... in that order, then a fixed butterfly); the k best of
+// the S*k keys, held in registers (lane l: candidates l + 64*j, S*k <= 64 * TOPK_MAX), in k rounds
+// of a wave maximum. Lane 0 writes token q (vocab_ids[column] when vocab_ids is set) to tok[q]
+// and, when val is set, its value to val[q]: mode 0 the raw value, mode 1 the log-softmax value
+// (x - M) - log(sum); lse (mode 1, when set) gets M + log(sum).
 __device__ __forceinline__ void topk_merge_row(const TopkPart* __restrict__ p, int S, int k, int mode,
                                                const int* __restrict__ vocab_ids, int lane, int* tok, float* val,
                                                float* lse_out) {
-  // S <= 64: lane s owns chunk s. Every load is issued up front from a clamped index (one memory
-  // round trip instead of one per step); values past S and past S*k are masked afterwards.
+  // Every load is issued up front from a clamped index (one memory round trip instead of one per
+  // step); values past S and past S*k are masked afterwards.
   const int total = S * k;  // <= 64 * TOPK_MAX
-  const TopkPart& own = p[min(lane, S - 1)];
-  const float mx_l = own.mx, se_l = own.se;
+  constexpr int PER = TOPK_MAX_PARTS / 64;
+  float mx_o[PER], se_o[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const TopkPart& own = p[min(lane + 64 * i, S - 1)];
+    mx_o[i] = own.mx;
+    se_o[i] = own.se;
+  }
   uint64_t key[TOPK_MAX];
 #pragma unroll
   for (int j = 0; j < TOPK_MAX; ++j) {
@@ -67,12 +76,17 @@ __device__ __forceinline__ void topk_merge_row(const TopkPart* __restrict__ p, i
 #pragma unroll
   for (int j = 0; j < TOPK_MAX; ++j)
     if (lane + 64 * j >= total) key[j] = 0ull;
-  float mx = lane < S ? mx_l : -INFINITY;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < PER; ++i)
+    if (lane + 64 * i < S) mx = fmaxf(mx, mx_o[i]);
   for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
   float lse = 0.f;
   if (mode == 1) {
     float acc = 0.f;
-    if (lane < S) acc += se_l * __expf(mx_l - mx);
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      if (lane + 64 * i < S) acc += se_o[i] * __expf(mx_o[i] - mx);
     for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
     lse = logf(acc);
   }

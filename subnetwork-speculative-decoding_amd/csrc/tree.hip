@@ -336,7 +336,7 @@ SSD_API int ssd_tree_limits(int32_t* out) {
   return SSD_OK;
 }
 
-SSD_API int ssd_tree_level_topk(const SsdTree* tree, int d, const void* parts, int64_t parts_bytes, int N,
+SSD_API int ssd_tree_level_topk(const SsdTree* tree, int d, const void* parts, int64_t parts_bytes, int N, int S,
                                 const int32_t* vocab_ids, int F_max, int k, int width, int feed, int root_pos,
                                 int tree_start, int past, const SsdRows* rows, int rows_max, const int32_t* pos_base,
                                 hipStream_t stream) {
@@ -346,8 +346,8 @@ SSD_API int ssd_tree_level_topk(const SsdTree* tree, int d, const void* parts, i
   if (F_max < 1 || k < 1 || k > TOPK_MAX || F_max * k > TREE_CAP)
     return set_error(SSD_ERANGE, "tree_level_topk: %d x %d candidates (k <= %d, total <= %d)", F_max, k, TOPK_MAX,
                      TREE_CAP);
-  const int S = (N + TOPK_CHUNK - 1) / TOPK_CHUNK;
-  if (N < k || S > 64) return set_error(SSD_EINVAL, "tree_level_topk: N=%d", N);
+  if (N < k || S < 1 || S > TOPK_MAX_PARTS || S > N || S * k > 64 * TOPK_MAX)
+    return set_error(SSD_EINVAL, "tree_level_topk: N=%d with %d records of %d keys per row", N, S, k);
   if (parts_bytes < (int64_t)F_max * S * (int64_t)sizeof(TopkPart))
     return set_error(SSD_EINVAL, "tree_level_topk: partials of %lld bytes < %lld", (long long)parts_bytes,
                      (long long)F_max * S * (long long)sizeof(TopkPart));

@@ -113,12 +113,15 @@ _PROTOS = {
     "ssd_row_topk_bf16": (I32, [P, I64, I32, I32, I32, I32, P, P, P, P, P, I64, P]),
     "ssd_row_topk_bf16_noalloc": (I32, [P, I64, I32, I32, I32, I32, P, P, P, P, P]),
     "ssd_row_topk_partial_bf16": (I32, [P, I64, I32, I32, I32, I32, P, I64, P]),
+    "ssd_row_topk_merge": (I32, [P, I64, I32, I32, I32, I32, P, P, P, P, P]),
+    "ssd_gemm_topk_parts": (I32, [I32]),
+    "ssd_gemm_topk_bf16": (I32, [P, I64, I32, P, I32, I32, F32, I32, I32, P, I64, P, I64, P]),
     "ssd_tree_limits": (I32, [P]),
     "ssd_round_begin": (I32, [C.POINTER(SsdTree), C.POINTER(SsdRows), I32, P, P, P]),
     "ssd_tree_level": (I32, [C.POINTER(SsdTree), I32, P, P, I32, I32, I32, I32, I32, I32, I32, C.POINTER(SsdRows),
                              I32, P, P]),
-    "ssd_tree_level_topk": (I32, [C.POINTER(SsdTree), I32, P, I64, I32, P, I32, I32, I32, I32, I32, I32, I32,
-                                  C.POINTER(SsdRows), I32, P, P]),
+    "ssd_tree_level_topk": (I32, [C.POINTER(SsdTree), I32, P, I64, I32, I32, P, I32, I32, I32, I32, I32, I32,
+                                  I32, C.POINTER(SsdRows), I32, P, P]),
     "ssd_tree_finalize": (I32, [C.POINTER(SsdTree), I32, I32, P, C.POINTER(SsdRows), I32, P, P]),
     "ssd_accept_greedy": (I32, [C.POINTER(SsdTree), P, I32, P, P, P, P, P, P]),
     "ssd_gemm_splits": (I32, [I32, I32]),
@@ -148,7 +151,8 @@ _PROTOS = {
 }
 
 EXPORTED = tuple(_PROTOS)
-ABI_VERSION = 4  # descriptor struct layouts (SsdModel.mlp_fused, SsdBuffers.sync, SsdRows.kv_off); pos_base arguments
+ABI_VERSION = 5  # descriptor struct layouts (SsdModel.mlp_fused, SsdBuffers.sync, SsdRows.kv_off); pos_base
+# arguments; ssd_tree_level_topk's record count S
 
 _lib = None
 

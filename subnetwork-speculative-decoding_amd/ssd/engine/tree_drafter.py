@@ -151,6 +151,10 @@ class TreeDrafter:
         # greedy proposals: the chunk records of the last proposal, merged by the next level's launch
         self._parts: Optional[torch.Tensor] = None
         self._parts_n = 0
+        self._parts_s = 0
+        # greedy proposals from the head launch itself (ssd_gemm_topk_bf16) where its records fit
+        # the merge (records * k <= 1024); False: head logits, then ssd_row_topk_partial_bf16
+        self.fused_head = True
 
     def max_nodes_per_level(self) -> list:
         return self.cfg.level_sizes()
@@ -164,16 +168,39 @@ class TreeDrafter:
         return min(total, self.cfg.max_nodes) if self.cfg.max_nodes else total
 
     # ------------------------------------------------------------------ device
+    def _parts_buf(self, need: int, device) -> torch.Tensor:
+        if self._parts is None or self._parts.numel() < need or self._parts.device != device:
+            self._parts = torch.empty(need, dtype=torch.uint8, device=device)
+        return self._parts
+
+    def _uses_fused_head(self, d: int) -> bool:
+        if not (self.greedy and self.fused_head and hasattr(self.draft, "head_topk")):
+            return False
+        return ops.gemm_topk_parts(self.draft._head_n()) * self.branch[d] <= 64 * TOPK_MAX
+
+    def _forward_propose(self, rows, m: int, d: int, p_min: int, l_max: int, cache: KVCache, ws, tree: DeviceTree,
+                         cand_tok, cand_lp, sampler) -> None:
+        """Draft forward over ``m`` rows and the proposals of depth ``d`` from its head."""
+        if self._uses_fused_head(d):
+            # log-softmax top-k (tree_drafter.py:129-133 of the reference) in two halves: the chunk
+            # pass in the head launch's epilogue, the merge inside the next level's expansion
+            self.draft.forward_rows(rows, m, p_min, l_max, cache, ws, head_rows=0)
+            n = self.draft._head_n()
+            parts = self._parts_buf(ops.gemm_topk_bytes(max([1] + self.levels), n), ws.h.device)
+            self._parts_s = self.draft.head_topk(ws.h, m, self.branch[d], parts)
+            self._parts_n = n
+            return
+        logits = self.draft.forward_rows(rows, m, p_min, l_max, cache, ws)
+        self._propose(logits, m, d, tree, cand_tok, cand_lp, sampler)
+
     def _propose(self, logits, rows: int, d: int, tree: DeviceTree, cand_tok, cand_lp, sampler) -> None:
         if self.greedy:
-            # log-softmax top-k (tree_drafter.py:129-133 of the reference) in two halves: the chunk
-            # pass here, the merge inside the next level's expansion (ssd_tree_level_topk)
+            # the same two halves from stored logits: the chunk pass here (4096-column chunks)
             n = logits.shape[1]
-            need = ops.row_topk_ws_bytes(max([1] + self.levels), n)
-            if self._parts is None or self._parts.numel() < need or self._parts.device != logits.device:
-                self._parts = torch.empty(need, dtype=torch.uint8, device=logits.device)
-            ops.row_topk_partial(logits, rows, n, self.branch[d], 1, self._parts)
+            parts = self._parts_buf(ops.row_topk_ws_bytes(max([1] + self.levels), n), logits.device)
+            ops.row_topk_partial(logits, rows, n, self.branch[d], 1, parts)
             self._parts_n = n
+            self._parts_s = (n + 4095) // 4096
         else:
             sampler.propose(self.draft, logits, rows, d, self.branch[d], tree.meta, cand_tok, cand_lp)
 
@@ -200,8 +227,7 @@ class TreeDrafter:
         _lib.call("ssd_round_begin", tree.struct, root_rows.struct, base_pos,
                   None if n_new_dev is None else n_new_dev.data_ptr(),
                   None if pos_base is None else pos_base.data_ptr(), ops.stream())
-        logits = self.draft.forward_rows(root_rows, 1, lo + 1, hi + 1, cache, ws)
-        self._propose(logits, 1, 0, tree, cand_tok, cand_lp, sampler)
+        self._forward_propose(root_rows, 1, 0, lo + 1, hi + 1, cache, ws, tree, cand_tok, cand_lp, sampler)
 
     def levels_device(self, cache: KVCache, root_pos: int, tree: DeviceTree, level_rows, cand_tok, cand_lp, ws,
                       sampler=None, pos_base: Optional[torch.Tensor] = None, window: Optional[tuple] = None) -> None:
@@ -221,7 +247,8 @@ class TreeDrafter:
             if self.greedy:
                 vocab_ids = self.draft._vocab_ids_i32
                 _lib.call("ssd_tree_level_topk", tree.struct, d, self._parts.data_ptr(), self._parts.numel(),
-                          self._parts_n, None if vocab_ids is None else vocab_ids.data_ptr(), f_max, self.branch[d],
+                          self._parts_n, self._parts_s, None if vocab_ids is None else vocab_ids.data_ptr(), f_max,
+                          self.branch[d],
                           self.width[d] or 0, int(feed), root_pos, tree_start, past, level_rows.struct,
                           m if feed else 0, pb, ops.stream())
             else:
@@ -230,8 +257,8 @@ class TreeDrafter:
                           level_rows.struct, m if feed else 0, pb, ops.stream())
             if not feed:
                 break
-            logits = self.draft.forward_rows(level_rows, m, lo + 1, hi + 1 + d + 1, cache, ws)
-            self._propose(logits, m, d + 1, tree, cand_tok, cand_lp, sampler)
+            self._forward_propose(level_rows, m, d + 1, lo + 1, hi + 1 + d + 1, cache, ws, tree, cand_tok, cand_lp,
+                                  sampler)
             past += m
         if pos_base is None:
             cache.seq_len = past

@@ -453,6 +453,14 @@ class SubnetworkDraftModel(nn.Module):
         ops.gemm(h, m, w, n, self.d_model, out, norm_eps=self.model.shape.eps)
         return out[:, :n]
 
+    def head_topk(self, h: torch.Tensor, m: int, k: int, parts: torch.Tensor, mode: int = 1) -> int:
+        """The head over h[:m] (final norm folded) fused with its top-k chunk pass: ``parts`` gets
+        each row's per-slab records (k best keys, max, sum of exp) for a merge; the logits are not
+        stored. Returns the record count per row."""
+        n = self._head_n()
+        w = self._sub_head if self._sub_head is not None else self.model.lm_head
+        return ops.gemm_topk(h, m, w, n, self.d_model, k, mode, parts, norm_eps=self.model.shape.eps)
+
     def final_norm(self, h: torch.Tensor, m: int, out: torch.Tensor) -> torch.Tensor:
         return ops.rmsnorm(h, m, self.model.norm, self.model.shape.eps, out)
 

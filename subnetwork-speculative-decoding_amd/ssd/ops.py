@@ -315,6 +315,56 @@ def row_topk_partial(logits, m, n, k, mode, parts):
               parts.data_ptr(), parts.numel(), stream())
 
 
+def row_topk_merge(parts, m, s, k, mode, vocab_ids, out_tok, out_val=None, out_lse=None):
+    """The merge pass alone over ``s`` records per row (ssd_row_topk_partial_bf16: ceil(n / 4096);
+    ssd_gemm_topk_bf16: gemm_topk_parts(n))."""
+    _check(parts, "parts", torch.uint8); _check(out_tok, "out_tok", torch.int32)
+    if vocab_ids is not None:
+        _check(vocab_ids, "vocab_ids", torch.int32)
+    _len(out_tok, "out_tok", m * k)
+    if out_val is not None:
+        _check(out_val, "out_val", torch.float32)
+        _len(out_val, "out_val", m * k)
+    if out_lse is not None:
+        _check(out_lse, "out_lse", torch.float32)
+        _len(out_lse, "out_lse", m)
+    _lib.call("ssd_row_topk_merge", parts.data_ptr(), parts.numel(), m, s, k, mode, _p(vocab_ids), out_tok.data_ptr(),
+              _p(out_val), _p(out_lse), stream())
+
+
+TOPK_PART_BYTES = 136  # TopkPart: max, sum of exp, 16 keys
+
+
+def gemm_topk_parts(n: int) -> int:
+    """Records per row that gemm_topk writes for an n-column head."""
+    s = int(_lib.load().ssd_gemm_topk_parts(n))
+    if s < 1:
+        raise ValueError(f"gemm_topk_parts: bad N={n}")
+    return s
+
+
+def gemm_topk_bytes(m: int, n: int) -> int:
+    return m * gemm_topk_parts(n) * TOPK_PART_BYTES
+
+
+def gemm_topk(x, m, wp, n, k_dim, k, mode, parts, norm_eps: float = 0.0, out=None) -> int:
+    """Vocabulary head fused with its top-k chunk pass: ``parts`` (uint8, gemm_topk_bytes(m, n)) gets
+    each row's per-slab records of X W^T (k best keys, max, mode 1: sum of exp), for row_topk_merge or
+    ssd_tree_level_topk; ``out`` (optional) also receives the bf16 logits. Returns the record count
+    per row."""
+    _check(x, "x"); _check(wp, "w_packed"); _check(parts, "parts", torch.uint8)
+    ldx = _rows(x, "x", k_dim, m)
+    _len(wp, "w_packed", packed_elems(n, k_dim))
+    _len(parts, "parts", gemm_topk_bytes(m, n))
+    ldy = 0
+    if out is not None:
+        _check(out, "out")
+        ldy = _rows(out, "out", n, m)
+    _lib.call("ssd_gemm_topk_bf16", x.data_ptr(), ldx, m, wp.data_ptr(), n, k_dim, float(norm_eps), k, mode,
+              parts.data_ptr(), parts.numel(), _p(out), ldy, stream())
+    return gemm_topk_parts(n)
+
+
 # ------------------------------------------------------------------ split-K GEMMs
 def gemm_splits(n: int, k: int) -> int:
     s = int(_lib.load().ssd_gemm_splits(n, k))

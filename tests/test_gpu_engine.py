@@ -274,6 +274,25 @@ def test_greedy_sd_stops_at_eos(hf):
     assert res.tokens == ref and res.tokens[-1] in eos
 
 
+@pytest.mark.parametrize("tree", ["pruned", "d4_3221_max24"])
+def test_fused_head_proposals_equal_two_launch_proposals(hf, tree):
+    """Greedy drafting with the proposals' top-k chunk pass in the head launch (ssd_gemm_topk_bf16)
+    and with stored logits + ssd_row_topk_partial_bf16: both decode exactly like AR, with the same
+    accepted counts and tree sizes round by round."""
+    sp, _, DraftingConfig, _ = ssd()
+    target = sp.TargetRunner(hf)
+    ids = prompt(40, 5)
+    ref = sp.autoregressive_generate(target, ids, 40, {-1}).tokens
+    out = []
+    for fused in (True, False):
+        gen = sp.SpeculativeGenerator(hf, make_draft(hf, "untrained"), DraftingConfig(**TREES[tree]), target)
+        gen.drafter.fused_head = fused
+        res = gen.generate(ids, 40, {-1})
+        assert res.tokens == ref, f"fused_head={fused}"
+        out.append((res.accepted_per_round, res.tree_sizes))
+    assert out[0] == out[1]
+
+
 def test_tree_shape_limits(hf):
     _, _, DraftingConfig, _ = ssd()
     from ssd.engine.tree_drafter import TreeDrafter

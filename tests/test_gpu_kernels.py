@@ -552,7 +552,7 @@ def test_tree_level_topk_equals_topk_then_level(seed, V, mapped):
                   committed, tree_start, past, rows[0].struct, m if feed else 0, None, ops.stream())
         parts = torch.empty(ops.row_topk_ws_bytes(F, V), dtype=torch.uint8, device=DEV)
         ops.row_topk_partial(logits, F, V, k, 1, parts)
-        _lib.call("ssd_tree_level_topk", trees[1].struct, d, parts.data_ptr(), parts.numel(), V,
+        _lib.call("ssd_tree_level_topk", trees[1].struct, d, parts.data_ptr(), parts.numel(), V, (V + 4095) // 4096,
                   None if vocab_ids is None else vocab_ids.data_ptr(), F, k, width[d] or 0, int(feed), 0,
                   tree_start - committed, past - committed, rows[1].struct, m if feed else 0, base.data_ptr(),
                   ops.stream())
