@@ -17,6 +17,10 @@
 //   v_permlane32_swap), residual add for o and down. The launch is persistent and XCD-aware: the
 //   workgroups resident on one XCD sweep blocks of output tiles together, so the weight and
 //   activation tiles they share are fetched into that XCD's L2 once per block.
+// * prefill_gemm4_kernel: the plain and SwiGLU projections (o, down, gate/up) on one 4-wave
+//   workgroup per CU with a 256 x 256 output tile and 128 x 128 per wave (accumulators pinned to
+//   the accumulator registers), operands loaded straight into a five-slot LDS ring, outputs staged
+//   through LDS and stored as whole rows; q/k/v stays on prefill_gemm_kernel.
 // * prefill_attention_kernel: causal flash attention, one wave per (q head, 32 tokens), K/V read
 //   in the cache's 64-slot MFMA-operand blocks; S^T = K Q^T and O^T = V^T P^T on MFMA with the
 //   running max / sum rescaled per 64-key block.
@@ -29,6 +33,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace ssd {
 
 constexpr int PF_WN = 4;    // waves along N (x 2 along M): 64 * PF_WN = 256 output rows of W per workgroup
@@ -38,6 +44,55 @@ constexpr int PF_KB = 2;    // 32-wide k-blocks per pipeline step
 // Tile (nb, kb) of a packed weight with `group` row tiles per k-block group: 64 lanes x 16 B.
 __device__ __forceinline__ size_t packed_tile(int nb, int kb, int kbt, int group) {
   return ((size_t)(nb / group) * kbt + kb) * group + nb % group;
+}
+
+// Epilogue of one 16 x 16 accumulator tile: lane (g, j) holds rows n = 16 nb + 4 g + e of token m
+// (scaled by the folded RMSNorm factor sc). Every lane must call it (the q/k/v and SwiGLU pairs meet
+// through a cross-lane swap).
+template <int EPI>
+__device__ __forceinline__ void pf_tile_epilogue(const GemmArgs& a, const f32x4_t& acc, int nb, int m, float sc,
+                                                 int g, int pos0) {
+  const bool mv = m < a.M;
+  float v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = acc[e] * sc;
+  if constexpr (EPI == EPI_STORE) {
+    const int n = nb * 16 + 4 * g;
+    if (mv) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (n + e < a.N) {
+          float r = rbf(v[e]);
+          if (a.residual) r = rbf(bf2f(a.residual[(size_t)m * a.ldr + n + e]) + r);
+          a.Y[(size_t)m * a.ldy + n + e] = f2bf(r);
+        }
+    }
+  } else {
+    // rows r (lanes g < 2) and r + 8 (lanes g >= 2) of the tile meet: r[0] = the lower
+    // half's value, r[1] = the upper half's, on every lane
+    float lo[4], hi[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[e]), __float_as_uint(v[e]), false, false);
+      lo[e] = __uint_as_float(p[0]);
+      hi[e] = __uint_as_float(p[1]);
+    }
+    if (mv && g < 2 && nb * 16 < a.N) {
+      if constexpr (EPI == EPI_SWIGLU) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) epi_swiglu(a, nb * 8 + 4 * g + e, m, lo[e], hi[e]);
+      } else {
+        const QkvTile q = qkv_tile(a, nb);
+        const int pos = min(max(pos0 + m, 0), (int)a.rope_rows - 1), half = a.head_dim >> 1;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int pr = 4 * g + e;
+          const size_t at = (size_t)pos * half + q.p * 8 + pr;
+          epi_qkv_pre(a, q, m, pr, lo[e], hi[e], pos0 + m, bf2f(a.cos_tab[at]), bf2f(a.sin_tab[at]), 0);
+        }
+      }
+    }
+  }
 }
 
 template <int EPI, int NORM>
@@ -190,56 +245,260 @@ __global__ __launch_bounds__(128 * PF_WN, 4 / PF_WN) void prefill_gemm_kernel(Ge
 #pragma unroll
   for (int y = 0; y < 4; ++y) {
     const int mr = wm * 64 + y * 16 + j;
-    const int m = m0 + mr;
     const float sc = NORM ? rn_s[mr] : 1.f;
-    const bool mv = m < a.M;
 #pragma unroll
-    for (int x = 0; x < 4; ++x) {
-      const int nb = nb0 + wn * 4 + x;
-      float v[4];
+    for (int x = 0; x < 4; ++x) pf_tile_epilogue<EPI>(a, acc[x][y], nb0 + wn * 4 + x, m0 + mr, sc, g, pos0);
+  }
+  }  // tile loop
+}
+// ------------------------------------------------------------------ 4-wave variant
+// One workgroup of 4 waves per CU (one per SIMD) owns a 256 (N) x 256 (M) output tile; wave (wn,
+// wm) computes 128 x 128 of it (64 accumulator tiles, held in the accumulator registers), so each
+// k-block it reads 16 KiB of operands from LDS for 64 MFMAs -- half the LDS bytes per MFMA of the
+// 8-wave 64 x 64 layout, whose LDS reads matched the LDS bandwidth at full MFMA rate. Operands
+// reach LDS by direct global-to-LDS loads (16 bytes per lane, one contiguous KiB per wave
+// instruction: a packed W tile, or 16 tokens x 32 k of X gathered into the MFMA B-operand lane
+// order) into a ring of five k-block slots (all 160 KiB of LDS). Step kb: wait until this wave's
+// loads of k-block kb + 1 have landed (those of kb + 2 and kb + 3 may still run) and pass one
+// barrier; issue the loads of kb + 4 into the slot k-block kb - 1 used; read k-block kb + 1's
+// fragments; run k-block kb's 64 MFMAs on the fragments read one step earlier. The step body takes
+// its LDS slots as restrict pointers, which lets the compiler see that the fragment reads do not
+// touch the slot being loaded (otherwise it waits for every load in flight before each LDS read).
+// The folded RMSNorm's sums of squares come from the X fragments the waves already hold (wave wn
+// sums fragments 4 wn .. 4 wn + 3 of its 8). Plain and SwiGLU outputs are staged through LDS after
+// the k loop and leave as whole 16-byte row pieces (residual read the same way); q/k/v keeps the
+// per-element RoPE / KV-cache epilogue.
+constexpr int P4_BM = 256, P4_SLOTS = 5, P4_AHEAD = 4;
+constexpr int P4_SLOT_BYTES = 32768;                 // 16 W tiles + 16 X tiles of one k-block
+constexpr int P4_ROW = 264;                           // staged output row: 256 (or 128) bf16 + 8 of pad
+constexpr int P4_RN_OFF = P4_BM * P4_ROW * 2;         // norm scales after the staged tile
+typedef __attribute__((address_space(3))) u32x4_t lds_u32x4;
+
+// The k loop's MFMAs are written as inline assembly with the accumulators bound to the accumulator
+// registers ("a"): left to the register allocator, some of the 256 accumulator values land in vector
+// registers and are copied in and out around their MFMAs, which costs up to half the loop's rate
+// depending on the epilogue compiled after it. The first k-block uses srcC = 0 (no read of
+// uninitialised accumulators, no VALU-write-to-MFMA-read hazard); accumulator reuse is 64 MFMAs
+// apart, and p4_drain() puts the wait states before the epilogue reads them.
+template <bool INIT>
+__device__ __forceinline__ void mfma_acc(f32x4_t& c, const u32x4_t& a, const u32x4_t& b) {
+  if constexpr (INIT) asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=a"(c) : "v"(a), "v"(b));
+  else asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+
+__device__ __forceinline__ void p4_drain(f32x4_t (&acc)[8][8]) {
+  // the epilogue's reads of every accumulator depend on these statements, which follow the wait
+  // states (more than the 16x16x32 MFMA's write latency) in program order
+  asm volatile("s_nop 15\n\ts_nop 15" : "+a"(acc[0][0]));
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = acc[x][y][e] * sc;
-      if constexpr (EPI == EPI_STORE) {
-        const int n = nb * 16 + 4 * g;
-        if (mv) {
+  for (int x = 0; x < 8; ++x)
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (n + e < a.N) {
-              float r = rbf(v[e]);
-              if (a.residual) r = rbf(bf2f(a.residual[(size_t)m * a.ldr + n + e]) + r);
-              a.Y[(size_t)m * a.ldy + n + e] = f2bf(r);
-            }
-        }
-      } else {
-        // rows r (lanes g < 2) and r + 8 (lanes g >= 2) of the tile meet: r[0] = the lower
-        // half's value, r[1] = the upper half's, on every lane
-        float lo[4], hi[4];
+    for (int y = 0; y < 8; ++y)
+      if (x | y) asm volatile("" : "+a"(acc[x][y]));
+}
+
+template <int NORM, bool INIT = false>
+__device__ __forceinline__ void p4_step(const u32x4_t* const (&wsrc)[4], const bf16_t* const (&xsrc)[4], size_t woff,
+                                        size_t xoff, bool issue, lds_u32x4* __restrict__ dA,
+                                        lds_u32x4* __restrict__ dB, const lds_u32x4* __restrict__ nA,
+                                        const lds_u32x4* __restrict__ nB, bool fetch, const u32x4_t (&fa)[8],
+                                        const u32x4_t (&fb)[8], u32x4_t (&na)[8], u32x4_t (&nb)[8],
+                                        f32x4_t (&acc)[8][8], float (&ss)[4], int y0, int lane) {
+  if (issue) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[e]), __float_as_uint(v[e]), false, false);
-          lo[e] = __uint_as_float(p[0]);
-          hi[e] = __uint_as_float(p[1]);
-        }
-        if (mv && g < 2 && nb * 16 < a.N) {
-          if constexpr (EPI == EPI_SWIGLU) {
+    for (int r = 0; r < 4; ++r)
+      __builtin_amdgcn_global_load_lds((const void*)(wsrc[r] + woff), (__attribute__((address_space(3))) void*)(dA + r * 64),
+                                       16, 0, 0);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) epi_swiglu(a, nb * 8 + 4 * g + e, m, lo[e], hi[e]);
-          } else {
-            const QkvTile q = qkv_tile(a, nb);
-            const int pos = min(max(pos0 + m, 0), (int)a.rope_rows - 1), half = a.head_dim >> 1;
+    for (int r = 0; r < 4; ++r)
+      __builtin_amdgcn_global_load_lds((const void*)(xsrc[r] + xoff), (__attribute__((address_space(3))) void*)(dB + r * 64),
+                                       16, 0, 0);
+  }
+  if (fetch) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int pr = 4 * g + e;
-              const size_t at = (size_t)pos * half + q.p * 8 + pr;
-              epi_qkv_pre(a, q, m, pr, lo[e], hi[e], pos0 + m, bf2f(a.cos_tab[at]), bf2f(a.sin_tab[at]), 0);
-            }
+    for (int y = 0; y < 8; ++y) nb[y] = nB[y * 64 + lane];
+#pragma unroll
+    for (int x = 0; x < 8; ++x) na[x] = nA[x * 64 + lane];
+  }
+  if constexpr (NORM) {
+#pragma unroll
+    for (int y = 0; y < 4; ++y) ss[y] += sumsq8(y0 ? fb[4 + y] : fb[y]);
+  }
+#pragma unroll
+  for (int x = 0; x < 8; ++x)
+#pragma unroll
+    for (int y = 0; y < 8; ++y) mfma_acc<INIT>(acc[x][y], fa[x], fb[y]);
+}
+
+// this wave's loads of k-block kb + 1 have landed (the 8 each of up to `later` later k-blocks may
+// still run), then the workgroup barrier (no wait for other memory operations)
+__device__ __forceinline__ void p4_wait(int later) {
+  if (later >= 2) asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+  else if (later == 1) asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <int EPI, int NORM>
+__global__ __launch_bounds__(256, 1) void prefill_gemm4_kernel(GemmArgs a, int group, int n_mt, int n_nt, int pos0,
+                                                               int sb_n, int sb_m) {
+  __shared__ __align__(16) unsigned char smem[P4_SLOTS * P4_SLOT_BYTES];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int wn = w & 1, wm = w >> 1;
+  const int n_rt = (a.N + 127) / 128 * 8;
+  const int kbt = a.kb_total;
+  const u32x4_t* W = (const u32x4_t*)a.W;
+  // slot s: W tiles at s * 32 KiB, X tiles 16 KiB further; tile i is 64 lanes x 16 bytes
+  auto slotA = [&](int kb, int tile) { return (lds_u32x4*)(smem + (kb % P4_SLOTS) * P4_SLOT_BYTES) + tile * 64; };
+  auto slotB = [&](int kb, int tile) {
+    return (lds_u32x4*)(smem + (kb % P4_SLOTS) * P4_SLOT_BYTES + 16384) + tile * 64;
+  };
+  float* rn_s = (float*)(smem + P4_RN_OFF);
+  bf16_t* stage = (bf16_t*)smem;  // [256 tokens][P4_ROW] after the k loop
+  // the same XCD-aware persistent schedule as prefill_gemm_kernel
+  const int xcd = blockIdx.x % 8, jw = blockIdx.x / 8;
+  const int n_bn = (n_nt + sb_n - 1) / sb_n, n_bm = (n_mt + sb_m - 1) / sb_m;
+  for (int blk = xcd; blk < n_bn * n_bm; blk += 8) {
+  const int bn = (blk / n_bm) * sb_n + jw % sb_n, bm = (blk % n_bm) * sb_m + jw / sb_n;
+  if (bn >= n_nt || bm >= n_mt || jw >= sb_n * sb_m) continue;  // uniform per workgroup
+  const int nb0 = bn * 16, m0 = bm * P4_BM;
+  // wave w loads W tiles 4w .. 4w + 3 and X tiles 4w .. 4w + 3 of every k-block (row tiles past
+  // the weight's last load that one; tokens past M load the last row: neither is stored)
+  const u32x4_t* wsrc[4];
+  const bf16_t* xsrc[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int nb = min(nb0 + 4 * w + r, n_rt - 1);
+    wsrc[r] = W + packed_tile(nb, 0, kbt, group) * 64 + lane;
+    xsrc[r] = a.X + (size_t)min(m0 + 16 * (4 * w + r) + j, a.M - 1) * a.ldx + g * 8;
+  }
+  const size_t wstep = (size_t)group * 64;
+
+  f32x4_t acc[8][8];  // written first by k-block 0's srcC = 0 MFMAs
+  float ss[4] = {};
+
+  // prologue: loads of k-blocks 0 .. 3, fragments of k-block 0
+  u32x4_t a0[8], b0[8], a1[8], b1[8];
+  for (int p = 0; p < P4_AHEAD; ++p)
+    if (p < kbt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        __builtin_amdgcn_global_load_lds((const void*)(wsrc[r] + p * wstep),
+                                         (__attribute__((address_space(3))) void*)(slotA(p, 4 * w) + r * 64), 16, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        __builtin_amdgcn_global_load_lds((const void*)(xsrc[r] + (size_t)p * 32),
+                                         (__attribute__((address_space(3))) void*)(slotB(p, 4 * w) + r * 64), 16, 0, 0);
+    }
+  // k-block 0 landed (up to three later ones may still run), fragments of 0
+  if (kbt >= 4) asm volatile("s_waitcnt vmcnt(24)\n\ts_barrier" ::: "memory");
+  else if (kbt == 3) asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+#pragma unroll
+  for (int y = 0; y < 8; ++y) b0[y] = slotB(0, wm * 8)[y * 64 + lane];
+#pragma unroll
+  for (int x = 0; x < 8; ++x) a0[x] = slotA(0, wn * 8)[x * 64 + lane];
+
+  auto step = [&](auto init, int kb, const u32x4_t (&fa)[8], const u32x4_t (&fb)[8], u32x4_t (&na)[8],
+                  u32x4_t (&nb)[8]) {
+    p4_wait(min(kbt - 2 - kb, 2));  // loads of kb + 2 .. kb + 3 may still run
+    const int ki = kb + P4_AHEAD;
+    p4_step<NORM, decltype(init)::value>(wsrc, xsrc, (size_t)ki * wstep, (size_t)ki * 32, ki < kbt, slotA(ki, 4 * w),
+                                         slotB(ki, 4 * w), slotA(kb + 1, wn * 8), slotB(kb + 1, wm * 8), kb + 1 < kbt,
+                                         fa, fb, na, nb, acc, ss, wn, lane);
+  };
+  using first_t = std::integral_constant<bool, true>;
+  using rest_t = std::integral_constant<bool, false>;
+  // kbt is even (K % 64 == 0): step 0, pairs (1, 2) .. (kbt - 3, kbt - 2), step kbt - 1
+  step(first_t{}, 0, a0, b0, a1, b1);
+  for (int kb = 1; kb + 1 < kbt; kb += 2) {
+    step(rest_t{}, kb, a1, b1, a0, b0);
+    step(rest_t{}, kb + 1, a0, b0, a1, b1);
+  }
+  step(rest_t{}, kbt - 1, a1, b1, a0, b0);
+  p4_drain(acc);
+  __syncthreads();  // every wave is done with the slots: the staged tile and the scales reuse LDS
+
+  if constexpr (NORM) {
+    // lanes j, j + 16, j + 32, j + 48 hold the four k-chunks of token 16 y + j
+#pragma unroll
+    for (int y = 0; y < 4; ++y) {
+      float v = ss[y];
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      if (g == 0) rn_s[wm * 128 + 16 * (4 * wn + y) + j] = rsqrtf(v / (float)(kbt * 32) + a.norm_eps);
+    }
+    __syncthreads();
+  }
+  static_assert(EPI != EPI_QKV, "q/k/v runs on prefill_gemm_kernel");
+  {
+    // stage: lane (g, j) of tile (x, y) holds output rows 16 (wn 8 + x) + 4 g + e of token
+    // wm 128 + 16 y + j -- four consecutive columns (plain) or, for SwiGLU, rows r (gate) and
+    // r + 8 (up) meeting through a lane swap, four consecutive intermediate columns on lanes g < 2
+    constexpr int COLS = EPI == EPI_SWIGLU ? 128 : 256;
+#pragma unroll
+    for (int y = 0; y < 8; ++y) {
+      const int mr = wm * 128 + y * 16 + j;
+      const float sc = NORM ? rn_s[mr] : 1.f;
+#pragma unroll
+      for (int x = 0; x < 8; ++x) {
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[x][y][e] * sc;
+        uint32_t lo2, hi2;
+        int col;
+        if constexpr (EPI == EPI_SWIGLU) {
+          float o[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[e]), __float_as_uint(v[e]), false, false);
+            const float gt = __uint_as_float(p[0]), up = __uint_as_float(p[1]);
+            o[e] = rbf(silu_f(rbf(gt))) * rbf(up);
           }
+          lo2 = pack_bf16x2(o[0], o[1]);
+          hi2 = pack_bf16x2(o[2], o[3]);
+          col = (wn * 8 + x) * 8 + 4 * g;
+        } else {
+          lo2 = pack_bf16x2(v[0], v[1]);
+          hi2 = pack_bf16x2(v[2], v[3]);
+          col = (wn * 8 + x) * 16 + 4 * g;
+        }
+        if (EPI != EPI_SWIGLU || g < 2) *(uint2*)(stage + mr * P4_ROW + col) = make_uint2(lo2, hi2);
+      }
+    }
+    __syncthreads();
+    // write out: 8 columns (16 bytes) per item, a row's items on consecutive threads
+    const int n_out = EPI == EPI_SWIGLU ? a.N / 2 : a.N;
+    const int c0 = (EPI == EPI_SWIGLU ? nb0 * 8 : nb0 * 16);
+    const bool vec = a.ldy % 8 == 0 && ((uintptr_t)a.Y & 15) == 0 &&
+                     (!a.residual || (a.ldr % 8 == 0 && ((uintptr_t)a.residual & 15) == 0));
+    for (int it = t; it < P4_BM * (COLS / 8); it += 256) {
+      const int row = it / (COLS / 8), c8 = (it % (COLS / 8)) * 8;
+      const int m = m0 + row, n = c0 + c8;
+      if (m >= a.M || n >= n_out) continue;
+      Pack8 v;
+      v.u = *(const uint4*)(stage + row * P4_ROW + c8);
+      if (vec && n + 8 <= n_out) {
+        if (EPI == EPI_STORE && a.residual) {
+          Pack8 r;
+          r.u = *(const uint4*)(a.residual + (size_t)m * a.ldr + n);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v.h[e] = f2bf(bf2f(r.h[e]) + bf2f(v.h[e]));
+        }
+        *(uint4*)(a.Y + (size_t)m * a.ldy + n) = v.u;
+      } else {
+        for (int e = 0; e < 8 && n + e < n_out; ++e) {
+          float r = bf2f(v.h[e]);
+          if (EPI == EPI_STORE && a.residual) r = rbf(bf2f(a.residual[(size_t)m * a.ldr + n + e]) + r);
+          a.Y[(size_t)m * a.ldy + n + e] = f2bf(r);
         }
       }
     }
   }
+  __syncthreads();  // the next tile's loads reuse LDS
   }  // tile loop
 }
+
 // ------------------------------------------------------------------ causal flash attention
 // Row (token t, q head h) at position pos0 + t attends cache slots [0, pos0 + t] (the prompt rows
 // before it and itself, whose K/V the q/k/v GEMM of this chunk already wrote).
@@ -399,6 +658,26 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(const bf16_t*
   }
 }
 
+static int launch_prefill_gemm4(GemmArgs a, int group, int pos0, int epi, int cus, hipStream_t s) {
+  const int n_mt = (a.M + P4_BM - 1) / P4_BM;
+  const int n_nt = (a.N + 255) / 256;
+  const int per_xcd = max((cus / 8) & ~3, 4);  // one workgroup per CU
+  const int sb_m = n_mt < 4 ? n_mt : 4;
+  const int sb_n = per_xcd / sb_m;
+  const int grid = 8 * sb_n * sb_m;
+  const bool norm = a.norm_eps > 0.f;
+#define PF4_LAUNCH(E)                                                                                             \
+  if (norm) SSD_LAUNCH((prefill_gemm4_kernel<E, 1>), dim3(grid), dim3(256), 0, s, a, group, n_mt, n_nt, pos0, sb_n, sb_m); \
+  else SSD_LAUNCH((prefill_gemm4_kernel<E, 0>), dim3(grid), dim3(256), 0, s, a, group, n_mt, n_nt, pos0, sb_n, sb_m);
+  if (epi == EPI_SWIGLU) {
+    PF4_LAUNCH(EPI_SWIGLU);
+  } else {
+    PF4_LAUNCH(EPI_STORE);
+  }
+#undef PF4_LAUNCH
+  return check_launch("prefill_gemm4");
+}
+
 static int launch_prefill_gemm(GemmArgs a, int group, int pos0, int epi, hipStream_t s) {
   const int n_mt = (a.M + PF_BM - 1) / PF_BM;
   const int n_nt = (a.N + 64 * PF_WN - 1) / (64 * PF_WN);
@@ -411,6 +690,11 @@ static int launch_prefill_gemm(GemmArgs a, int group, int pos0, int epi, hipStre
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
     if (dev >= 0 && dev < 64) cus_of[dev] = cus;
   }
+  // plain and SwiGLU outputs: the 4-wave 256 x 256 kernel (measured at 4096 tokens, 8B shapes: gate/up
+  // 1295 against 1440 us, o_proj 160 against 226, down 481 against 602); q/k/v keeps the 8-wave
+  // kernel (its RoPE / KV-cache epilogue, and 384 256 x 256 tiles would leave half the CUs idle in a
+  // second round)
+  if (epi != EPI_QKV) return launch_prefill_gemm4(a, group, pos0, epi, cus, s);
   // 32 on MI355X; at least one block row of 8 M-tiles, so a device reporting fewer CUs (a compute
   // partition) still gets a nonempty grid (the schedule loops, so any grid size is correct)
   const int per_xcd = max((4 / PF_WN * cus / 8) & ~7, 8);
