@@ -40,6 +40,9 @@ struct GemmArgs {
   // RMSNorm of the rows of X folded into the GEMM (> 0: X is the residual stream h; the norm's
   // weight is already folded into W's columns; each output is scaled by rsqrt(mean(h^2) + eps))
   float norm_eps;
+  // prefill: the folded RMSNorm's row scales, computed beforehand (rsqrt(mean(x^2) + eps) per row of
+  // X, [M] floats); used instead of norm_eps's in-loop sums where a kernel supports it
+  const float* row_scale;
 };
 
 

@@ -320,7 +320,7 @@ __device__ __forceinline__ void p4_step(const u32x4_t* const (&wsrc)[4], const b
 #pragma unroll
     for (int x = 0; x < 8; ++x) na[x] = nA[x * 64 + lane];
   }
-  if constexpr (NORM) {
+  if constexpr (NORM == 1) {
 #pragma unroll
     for (int y = 0; y < 4; ++y) ss[y] += sumsq8(y0 ? fb[4 + y] : fb[y]);
   }
@@ -419,7 +419,7 @@ __global__ __launch_bounds__(256, 1) void prefill_gemm4_kernel(GemmArgs a, int g
   p4_drain(acc);
   __syncthreads();  // every wave is done with the slots: the staged tile and the scales reuse LDS
 
-  if constexpr (NORM) {
+  if constexpr (NORM == 1) {
     // lanes j, j + 16, j + 32, j + 48 hold the four k-chunks of token 16 y + j
 #pragma unroll
     for (int y = 0; y < 4; ++y) {
@@ -428,6 +428,9 @@ __global__ __launch_bounds__(256, 1) void prefill_gemm4_kernel(GemmArgs a, int g
       v += __shfl_xor(v, 32);
       if (g == 0) rn_s[wm * 128 + 16 * (4 * wn + y) + j] = rsqrtf(v / (float)(kbt * 32) + a.norm_eps);
     }
+    __syncthreads();
+  } else if constexpr (NORM == 2) {
+    rn_s[t] = a.row_scale[min(m0 + t, a.M - 1)];  // 256 threads, 256 rows
     __syncthreads();
   }
   static_assert(EPI != EPI_QKV, "q/k/v runs on prefill_gemm_kernel");
@@ -658,6 +661,20 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(const bf16_t*
   }
 }
 
+// Row scales of the folded RMSNorm, rn[m] = rsqrt(mean(X[m, :K]^2) + eps), one wave per row: lane l
+// sums its 8-element pieces l, l + 64, ... of the row in order, then a fixed butterfly (the order
+// depends only on K, so a row's scale does not depend on M or on the chunking).
+__global__ __launch_bounds__(256) void prefill_rowscale_kernel(const bf16_t* __restrict__ X, int64_t ldx, int M,
+                                                               int K, float eps, float* __restrict__ rn) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= M) return;
+  const bf16_t* x = X + (size_t)row * ldx;
+  float acc = 0.f;
+  for (int c = lane * 8; c < K; c += 512) acc += sumsq8(*(const u32x4_t*)(x + c));
+  for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
+  if (lane == 0) rn[row] = rsqrtf(acc / (float)K + eps);
+}
+
 static int launch_prefill_gemm4(GemmArgs a, int group, int pos0, int epi, int cus, hipStream_t s) {
   const int n_mt = (a.M + P4_BM - 1) / P4_BM;
   const int n_nt = (a.N + 255) / 256;
@@ -670,7 +687,11 @@ static int launch_prefill_gemm4(GemmArgs a, int group, int pos0, int epi, int cu
   if (norm) SSD_LAUNCH((prefill_gemm4_kernel<E, 1>), dim3(grid), dim3(256), 0, s, a, group, n_mt, n_nt, pos0, sb_n, sb_m); \
   else SSD_LAUNCH((prefill_gemm4_kernel<E, 0>), dim3(grid), dim3(256), 0, s, a, group, n_mt, n_nt, pos0, sb_n, sb_m);
   if (epi == EPI_SWIGLU) {
-    PF4_LAUNCH(EPI_SWIGLU);
+    if (a.row_scale)
+      SSD_LAUNCH((prefill_gemm4_kernel<EPI_SWIGLU, 2>), dim3(grid), dim3(256), 0, s, a, group, n_mt, n_nt, pos0, sb_n,
+                 sb_m);
+    else
+      PF4_LAUNCH(EPI_SWIGLU);
   } else {
     PF4_LAUNCH(EPI_STORE);
   }
@@ -726,9 +747,21 @@ static int check_packed(int N, int K, int group) {
 
 using namespace ssd;
 
+static int prefill_gemm(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int group, int N, int K,
+                        float norm_eps, int epi, uint16_t* Y, int64_t ldy, const uint16_t* residual, int64_t ldr,
+                        const SsdQkvEpilogue* qkv, const float* row_scale, hipStream_t stream);
+
 SSD_API int ssd_prefill_gemm_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int group, int N,
                                   int K, float norm_eps, int epi, uint16_t* Y, int64_t ldy, const uint16_t* residual,
                                   int64_t ldr, const SsdQkvEpilogue* qkv, hipStream_t stream) {
+  return prefill_gemm(X, ldx, M, W_packed, group, N, K, norm_eps, epi, Y, ldy, residual, ldr, qkv, nullptr, stream);
+}
+
+// ssd_prefill_gemm_bf16 with the folded RMSNorm's row scales given (row_scale, [M] floats, with
+// norm_eps > 0; used by the 4-wave kernel's plain and SwiGLU outputs instead of in-loop sums).
+static int prefill_gemm(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int group, int N, int K,
+                        float norm_eps, int epi, uint16_t* Y, int64_t ldy, const uint16_t* residual, int64_t ldr,
+                        const SsdQkvEpilogue* qkv, const float* row_scale, hipStream_t stream) {
   if (!X || !W_packed || !Y) return set_error(SSD_EINVAL, "prefill gemm: null pointer");
   if (M <= 0) return set_error(SSD_EINVAL, "prefill gemm: M=%d", M);
   int rc = check_packed(N, K, group);
@@ -742,6 +775,7 @@ SSD_API int ssd_prefill_gemm_bf16(const uint16_t* X, int64_t ldx, int M, const u
   GemmArgs a{};
   a.X = X; a.ldx = ldx; a.M = M; a.W = (const uint4*)W_packed; a.N = N; a.kb_total = K / 32;
   a.Y = Y; a.ldy = ldy; a.residual = residual; a.ldr = ldr; a.norm_eps = norm_eps;
+  a.row_scale = norm_eps > 0.f ? row_scale : nullptr;
   int pos0 = 0;
   if (epi == SSD_EPI_QKV) {
     if (!qkv || !qkv->cos || !qkv->sin || !qkv->k_cache || !qkv->vt_cache)
@@ -829,8 +863,12 @@ SSD_API int ssd_prefill(const SsdModel* md, const uint16_t* head_w, const SsdPre
     if ((rc = ssd_prefill_gemm_bf16(pb->attn, qdim, m, L.wo, g_o, d, (int)qdim, 0.f, SSD_EPI_STORE, pb->h, d, pb->h, d,
                                     nullptr, s)))
       return rc;
-    if ((rc = ssd_prefill_gemm_bf16(pb->h, d, m, L.wgu, g_gu, 2 * I, d, md->eps, SSD_EPI_SWIGLU, pb->act, I, nullptr, 0,
-                                    nullptr, s)))
+    // gate/up's norm scales computed once per row into the q buffer (free after the attention)
+    float* rs = (float*)pb->q;
+    SSD_LAUNCH(prefill_rowscale_kernel, dim3((m + 3) / 4), dim3(256), 0, s, pb->h, (int64_t)d, m, d, md->eps, rs);
+    if ((rc = check_launch("prefill_rowscale"))) return rc;
+    if ((rc = prefill_gemm(pb->h, d, m, L.wgu, g_gu, 2 * I, d, md->eps, SSD_EPI_SWIGLU, pb->act, I, nullptr, 0, nullptr,
+                           rs, s)))
       return rc;
     if ((rc = ssd_prefill_gemm_bf16(pb->act, I, m, L.wd, g_d, d, I, 0.f, SSD_EPI_STORE, pb->h, d, pb->h, d, nullptr, s)))
       return rc;
