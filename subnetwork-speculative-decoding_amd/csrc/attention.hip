@@ -191,6 +191,10 @@ template <int HD, bool MASKED>
 __device__ __forceinline__ void block_attend(const Frags<HD>& f, const u32x4_t (&qf)[HD / 32], uint32_t valid_bits,
                                              float scale_log2, float& m_out, float& l_out,
                                              f32x4_t (&o)[HD / 16]) {
+  // No multiply-add contraction: the masked instance has a select between s * scale_log2 and the
+  // exponent's subtraction, the unmasked one does not, and a fused multiply-subtract in one of them
+  // only would give the two kinds of workgroup p values an ulp apart.
+#pragma clang fp contract(off)
   constexpr int KS = HD / 32, DT = HD / 16;
   // k-step outer: consecutive MFMAs go to different accumulators (each sum keeps its ks order)
   f32x4_t s[4];
@@ -421,9 +425,9 @@ __global__ __launch_bounds__(256, 2) void attn_partial_kernel(AttnArgs a) {
 #pragma unroll
     for (int ww = 0; ww < ATT_SB; ++ww) {
       const float wgt = mb[ww] != -INFINITY ? fast_exp2(mb[ww] - mS) : 0.f;
-      lS += lds.l[buf][ww][rr] * wgt;
+      lS = fmaf(lds.l[buf][ww][rr], wgt, lS);
 #pragma unroll
-      for (int d = 0; d < DPT; ++d) oS[d] += lds.o[buf][ww][rr][dc * DPT + d] * wgt;
+      for (int d = 0; d < DPT; ++d) oS[d] = fmaf(lds.o[buf][ww][rr][dc * DPT + d], wgt, oS[d]);
     }
     const size_t rec = ((size_t)kvh * n_rows + t0 + rr) * a.n_sb_cap + sb;
     float* dst = ws_o + rec * HD + dc * DPT;
