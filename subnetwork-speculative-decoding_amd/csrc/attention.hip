@@ -48,7 +48,7 @@ struct AttnArgs {
   const int64_t* kv_off;  // [M] element offset of token t's sequence in the K / V arenas, or null
   int p_min, l_max;
   float scale_log2;
-  float* ws;  // O [kv_heads][M*rep][n_sb_cap][hd], then (m, l) [kv_heads][M*rep][n_sb_cap]
+  float* ws;  // fp16 O / l [kv_heads][M*rep][n_sb_cap][hd], then fp32 (m, l) [kv_heads][M*rep][n_sb_cap]
   int n_sb_cap;
   // launch geometry (set by launch_attn)
   int n_full;         // superblocks entirely below p_min (shared by every row)
@@ -57,6 +57,8 @@ struct AttnArgs {
   int groups, tiles_per_group;  // row tile groups of the shared workgroups
   uint32_t rep_magic;  // ceil(2^32 / (heads / kv_heads)): R / rep == umulhi(R, rep_magic) for R < 2^16
 };
+
+typedef _Float16 h16x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int perm_key(int kt, int i) {
   // key offset (within a 64-key block) that sits in row i of key tile kt
@@ -269,7 +271,8 @@ struct alignas(16) AttnLds {
 // -- its tokens (tail) or tile groups (shared) -- get ids 8 apart, i.e. one XCD (workgroups are
 // dealt to the 8 XCDs round-robin), so their re-reads of that K/V hit the XCD's L2.
 //
-// Workspace: O partials [kv_heads][M*rep][n_sb_cap][HD], then (m, l) pairs [kv_heads][M*rep][n_sb_cap].
+// Workspace: normalised O partials (O / l, fp16) [kv_heads][M*rep][n_sb_cap][HD], then fp32 (m, l) pairs
+// [kv_heads][M*rep][n_sb_cap].
 // Every (row, superblock < n_sb) pair of the call is written; m = -inf marks "no keys".
 template <int HD>
 __global__ __launch_bounds__(256, 2) void attn_partial_kernel(AttnArgs a) {
@@ -296,8 +299,8 @@ __global__ __launch_bounds__(256, 2) void attn_partial_kernel(AttnArgs a) {
     kvh = u % a.kv_heads;
   }
   const int key0 = (sb * ATT_SB + w) * ATT_BLK;
-  float* ws_o = a.ws;
-  float2* ws_ml = (float2*)(a.ws + (size_t)a.kv_heads * n_rows * a.n_sb_cap * HD);
+  _Float16* ws_o = (_Float16*)a.ws;
+  float2* ws_ml = (float2*)(a.ws + (size_t)a.kv_heads * n_rows * a.n_sb_cap * (HD / 2));
 
   __shared__ AttnLds<HD> lds;
   __shared__ int s_anc[ATT_MAXD];
@@ -430,13 +433,19 @@ __global__ __launch_bounds__(256, 2) void attn_partial_kernel(AttnArgs a) {
       for (int d = 0; d < DPT; ++d) oS[d] = fmaf(lds.o[buf][ww][rr][dc * DPT + d], wgt, oS[d]);
     }
     const size_t rec = ((size_t)kvh * n_rows + t0 + rr) * a.n_sb_cap + sb;
-    float* dst = ws_o + rec * HD + dc * DPT;
+    // the superblock's normalised output O / l in fp16 (|O / l| <= max |v|; 0 without keys)
+    const float inv = lS > 0.f ? 1.f / lS : 0.f;
+    _Float16* dst = ws_o + rec * HD + dc * DPT;
     if constexpr (DPT % 4 == 0) {
 #pragma unroll
-      for (int d = 0; d < DPT; d += 4) *(float4*)(dst + d) = make_float4(oS[d], oS[d + 1], oS[d + 2], oS[d + 3]);
+      for (int d = 0; d < DPT; d += 4) {
+        const h16x4_t q = {(_Float16)(oS[d] * inv), (_Float16)(oS[d + 1] * inv), (_Float16)(oS[d + 2] * inv),
+                           (_Float16)(oS[d + 3] * inv)};
+        *(h16x4_t*)(dst + d) = q;
+      }
     } else {
 #pragma unroll
-      for (int d = 0; d < DPT; ++d) dst[d] = oS[d];
+      for (int d = 0; d < DPT; ++d) dst[d] = (_Float16)(oS[d] * inv);
     }
     ws_ml[rec] = make_float2(mS, lS);  // the same pair from each of the row's 16 threads
   };
@@ -494,10 +503,10 @@ __global__ __launch_bounds__(256, 2) void attn_partial_kernel(AttnArgs a) {
 }
 
 // Cross-superblock combine, one wave per (token, q head). Canonical arithmetic for a row with
-// superblocks s = 0..n-1: M = max_s m_s; w_s = 2^(m_s - M) (0 where m_s = -inf); l = sum_s l_s w_s
-// and O = sum_s O_s w_s, both summed in increasing s; out = O / l. The partials of up to 32
-// superblocks (a batch divides the 64-superblock window) are loaded in one batch, issued before
-// the max is reduced.
+// superblocks s = 0..n-1 (record: m_s, l_s and the normalised output o_s = O_s / l_s in fp16):
+// M = max_s m_s; w_s = l_s 2^(m_s - M) (0 where m_s = -inf); L = sum_s w_s and O = sum_s o_s w_s,
+// both summed in increasing s; out = O / L. The partials of up to 32 superblocks (a batch divides
+// the 64-superblock window) are loaded in one batch, issued before the max is reduced.
 template <int HD>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ ws, int n_sb_cap, int M,
                                                            int heads, int kv_heads, bf16_t* __restrict__ out,
@@ -510,8 +519,8 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
   const int rep = heads / kv_heads, kvh = hq / rep;
   const int n_rows = M * rep;
   const size_t row = (size_t)kvh * n_rows + tok * rep + hq % rep;
-  const float* O = ws + row * n_sb_cap * HD;
-  const float2* ml = (const float2*)(ws + (size_t)kv_heads * n_rows * n_sb_cap * HD) + row * n_sb_cap;
+  const _Float16* O = (const _Float16*)ws + row * n_sb_cap * HD;
+  const float2* ml = (const float2*)(ws + (size_t)kv_heads * n_rows * n_sb_cap * (HD / 2)) + row * n_sb_cap;
   // Lane s of a 64-superblock window holds record (m, l) of superblock window + s; the fold reads
   // it back with readlane (no registers per superblock).
   float v[CH][PER];
@@ -522,7 +531,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
     for (int q = 0; q < CH; ++q) {
       const int sq = min(s0 + q, n - 1);
 #pragma unroll
-      for (int i = 0; i < PER; ++i) v[q][i] = O[(size_t)sq * HD + min(lane + 64 * i, HD - 1)];
+      for (int i = 0; i < PER; ++i) v[q][i] = (float)O[(size_t)sq * HD + min(lane + 64 * i, HD - 1)];
     }
   };
   float2 win = ml[min(lane, n - 1)];
@@ -539,9 +548,9 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
       const int ln = (s0 & 63) + q;
       const float mq = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(win.x), ln));
       const float lq = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(win.y), ln));
-      const float wq = (s0 + q >= n || mq == -INFINITY) ? 0.f : fast_exp2(mq - mx);
+      const float wq = (s0 + q >= n || mq == -INFINITY) ? 0.f : lq * fast_exp2(mq - mx);
       if (wq != 0.f) {
-        l += lq * wq;
+        l += wq;
 #pragma unroll
         for (int i = 0; i < PER; ++i) o[i] += v[q][i] * wq;
       }
@@ -595,7 +604,7 @@ using namespace ssd;
 
 SSD_API int ssd_attn_workspace_floats(int M, int heads, int head_dim, int64_t max_len) {
   const int64_t n_sb = (max_len + ATT_BLK * ATT_SB - 1) / (ATT_BLK * ATT_SB);
-  return (int)((int64_t)M * heads * n_sb * (head_dim + 2));
+  return (int)((int64_t)M * heads * n_sb * (head_dim / 2 + 2));  // fp16 O / l, then fp32 (m, l)
 }
 
 SSD_API int ssd_attn_max_depth(void) { return ATT_MAXD; }
@@ -630,7 +639,7 @@ int ssd::tree_attention(const uint16_t* q, int64_t ldq, int M, int heads, int kv
     return set_error(SSD_EINVAL, "attention: bad bounds p_min=%d l_max=%d max_len=%lld", p_min, l_max,
                      (long long)max_len);
   const int64_t n_sb_cap = (max_len + ATT_BLK * ATT_SB - 1) / (ATT_BLK * ATT_SB);
-  if (ws_floats < (int64_t)M * heads * n_sb_cap * (head_dim + 2))
+  if (ws_floats < (int64_t)M * heads * n_sb_cap * (head_dim / 2 + 2))
     return set_error(SSD_EINVAL, "attention: workspace too small");
   AttnArgs a{};
   a.Q = q; a.ldq = ldq; a.K = k_cache; a.Vt = vt_cache; a.max_len = max_len;
