@@ -471,12 +471,20 @@ typedef struct SsdQkvEpilogue {
   int64_t max_len;
 } SsdQkvEpilogue;
 
+/* Row scales of an RMSNorm folded into a prefill GEMM's packed weight (the LlamaRMSNorm before the
+ * target layers' q/k/v and gate/up projections, ssd/models/subnetwork_draft.py:209-212, :243-245):
+ * row_scale[m] = rsqrt(mean(X[m, :K]^2) + eps), [M] floats; K % 8 == 0, 16-byte rows. */
+int ssd_prefill_row_scale_bf16(const uint16_t* X, int64_t ldx, int M, int K, float eps, float* row_scale,
+                               hipStream_t stream);
+
 /* Y = epilogue(X[M, K] W^T) for any M (W packed by ssd_pack_weight_bf16 with `group`, K % 64 == 0);
- * norm_eps > 0 folds the RMSNorm of X's rows as the decode GEMMs do. Replaces the prompt-length
- * F.linear / nn.Linear calls of the target layers (ssd/models/subnetwork_draft.py:209-212, :243-245). */
+ * row_scale ([M] floats from ssd_prefill_row_scale_bf16, or NULL) multiplies row m's products, which
+ * with the RMSNorm weight folded into W's columns is the RMSNorm of X's rows. Replaces the
+ * prompt-length F.linear / nn.Linear calls of the target layers (ssd/models/subnetwork_draft.py:209-212,
+ * :243-245). */
 int ssd_prefill_gemm_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int group, int N, int K,
-                          float norm_eps, int epi, uint16_t* Y, int64_t ldy, const uint16_t* residual, int64_t ldr,
-                          const SsdQkvEpilogue* qkv, hipStream_t stream);
+                          const float* row_scale, int epi, uint16_t* Y, int64_t ldy, const uint16_t* residual,
+                          int64_t ldr, const SsdQkvEpilogue* qkv, hipStream_t stream);
 
 /* Causal attention of prompt rows: row t (position pos0 + t) attends cache slots [0, pos0 + t],
  * scale * q.k, GQA (heads / kv_heads q heads per kv head). Replaces the causal SDPA of the prompt

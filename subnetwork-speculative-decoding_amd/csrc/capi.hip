@@ -31,7 +31,7 @@ int check_launch(const char* what) {
 
 SSD_API const char* ssd_last_error(void) { return ssd::g_err; }
 
-SSD_API int ssd_abi_version(void) { return 5; }
+SSD_API int ssd_abi_version(void) { return 6; }
 
 // Kernels enqueued by this library since it was loaded (all devices and streams).
 SSD_API uint64_t ssd_launch_count(void) { return ssd::g_launches.load(std::memory_order_relaxed); }

@@ -5,22 +5,16 @@
 // through them re-reads every weight 64 times. Here (reference ssd/engine/speculative.py:149-151,
 // the target's forward over the prompt):
 //
-// * prefill_gemm_kernel: Y = X W^T over the same packed weights as the decode GEMMs (16 x 32
-//   MFMA A-operand tiles, any tile grouping), as an LDS-tiled MFMA GEMM: a workgroup of 8 waves
-//   (one per CU, two per SIMD) owns a 256 (N) x 128 (M) output tile, stages 256 x 64 of W and
-//   128 x 64 of X per step in LDS (double buffered, the next step's global loads in flight while the
-//   MFMAs run), and each wave computes a 64 x 64 sub-tile with v_mfma_f32_16x16x32_bf16 (against
-//   two 4-wave 128 x 128 workgroups per CU, a quarter fewer bytes staged per MFMA). X is staged in the MFMA B-operand lane order so
-//   every LDS read is one contiguous 1 KiB per wave. The decode epilogues run on the accumulators:
-//   the folded RMSNorm scale (sum of x^2 accumulated by the threads that stage X), RoPE + KV-cache
-//   write for q/k/v, SwiGLU for gate/up (rotary / gate-up row pairs r and r + 8 meet through one
-//   v_permlane32_swap), residual add for o and down. The launch is persistent and XCD-aware: the
-//   workgroups resident on one XCD sweep blocks of output tiles together, so the weight and
-//   activation tiles they share are fetched into that XCD's L2 once per block.
-// * prefill_gemm4_kernel: the plain and SwiGLU projections (o, down, gate/up) on one 4-wave
-//   workgroup per CU with a 256 x 256 output tile and 128 x 128 per wave (accumulators pinned to
-//   the accumulator registers), operands loaded straight into a five-slot LDS ring, outputs staged
-//   through LDS and stored as whole rows; q/k/v stays on prefill_gemm_kernel.
+// * prefill_gemm4_kernel: Y = X W^T over the same packed weights as the decode GEMMs (16 x 32 MFMA
+//   A-operand tiles, any tile grouping) with v_mfma_f32_16x16x32_bf16: one 4-wave workgroup per CU
+//   with a 256 x 256 (o, down, gate/up) or 192 x 256 (q/k/v) output tile, accumulators pinned to the
+//   accumulator registers, operands loaded straight into a five-slot LDS ring, outputs staged through
+//   LDS and stored as 16-byte pieces. The decode epilogues run on the staged tile: SwiGLU for gate/up
+//   (gate / up rows r and r + 8 meet through one v_permlane32_swap), residual add for o and down,
+//   RoPE + KV-cache write for q/k/v; the folded RMSNorm scale comes from a row-scale pass. The launch
+//   is persistent and XCD-aware: the workgroups resident on one XCD sweep blocks of output tiles
+//   together, so the weight and activation tiles they share are fetched into that XCD's L2 once per
+//   block.
 // * prefill_attention_kernel: causal flash attention, one wave per (q head, 32 tokens), K/V read
 //   in the cache's 64-slot MFMA-operand blocks; S^T = K Q^T and O^T = V^T P^T on MFMA with the
 //   running max / sum rescaled per 64-key block.
@@ -37,248 +31,42 @@
 
 namespace ssd {
 
-constexpr int PF_WN = 4;    // waves along N (x 2 along M): 64 * PF_WN = 256 output rows of W per workgroup
-constexpr int PF_BM = 128;  // tokens per workgroup
-constexpr int PF_KB = 2;    // 32-wide k-blocks per pipeline step
-
 // Tile (nb, kb) of a packed weight with `group` row tiles per k-block group: 64 lanes x 16 B.
 __device__ __forceinline__ size_t packed_tile(int nb, int kb, int kbt, int group) {
   return ((size_t)(nb / group) * kbt + kb) * group + nb % group;
 }
 
-// Epilogue of one 16 x 16 accumulator tile: lane (g, j) holds rows n = 16 nb + 4 g + e of token m
-// (scaled by the folded RMSNorm factor sc). Every lane must call it (the q/k/v and SwiGLU pairs meet
-// through a cross-lane swap).
-template <int EPI>
-__device__ __forceinline__ void pf_tile_epilogue(const GemmArgs& a, const f32x4_t& acc, int nb, int m, float sc,
-                                                 int g, int pos0) {
-  const bool mv = m < a.M;
-  float v[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) v[e] = acc[e] * sc;
-  if constexpr (EPI == EPI_STORE) {
-    const int n = nb * 16 + 4 * g;
-    if (mv) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (n + e < a.N) {
-          float r = rbf(v[e]);
-          if (a.residual) r = rbf(bf2f(a.residual[(size_t)m * a.ldr + n + e]) + r);
-          a.Y[(size_t)m * a.ldy + n + e] = f2bf(r);
-        }
-    }
-  } else {
-    // rows r (lanes g < 2) and r + 8 (lanes g >= 2) of the tile meet: r[0] = the lower
-    // half's value, r[1] = the upper half's, on every lane
-    float lo[4], hi[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[e]), __float_as_uint(v[e]), false, false);
-      lo[e] = __uint_as_float(p[0]);
-      hi[e] = __uint_as_float(p[1]);
-    }
-    if (mv && g < 2 && nb * 16 < a.N) {
-      if constexpr (EPI == EPI_SWIGLU) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) epi_swiglu(a, nb * 8 + 4 * g + e, m, lo[e], hi[e]);
-      } else {
-        const QkvTile q = qkv_tile(a, nb);
-        const int pos = min(max(pos0 + m, 0), (int)a.rope_rows - 1), half = a.head_dim >> 1;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int pr = 4 * g + e;
-          const size_t at = (size_t)pos * half + q.p * 8 + pr;
-          epi_qkv_pre(a, q, m, pr, lo[e], hi[e], pos0 + m, bf2f(a.cos_tab[at]), bf2f(a.sin_tab[at]), 0);
-        }
-      }
-    }
-  }
-}
-
-template <int EPI, int NORM>
-__global__ __launch_bounds__(128 * PF_WN, 4 / PF_WN) void prefill_gemm_kernel(GemmArgs a, int group, int n_mt,
-                                                                              int n_nt, int pos0, int sb_n, int sb_m) {
-  constexpr int WN = PF_WN;
-  constexpr int NT = 128 * WN;   // threads
-  constexpr int RT = 4 * WN;     // 16-row tiles of W per workgroup
-  constexpr int XL = 8 / WN;     // X chunks each thread stages per step
-  __shared__ u32x4_t As[2][PF_KB][RT][64];
-  __shared__ u32x4_t Bs[2][PF_KB][8][64];
-  __shared__ float rn_s[PF_BM];
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  const int j = lane & 15, g = lane >> 4;
-  const int wn = w % WN, wm = w / WN;
-  const int n_rt = (a.N + 127) / 128 * 8;  // row tiles of the packed weight (rows padded to 128)
-  const int kbt = a.kb_total;
-
-  // Persistent, XCD-aware schedule: the workgroups resident on one XCD (ids x, x + 8, ...) sweep
-  // blocks of sb_n x sb_m output tiles together -- workgroup j takes tile (j % sb_n, j / sb_n)
-  // of the block -- so each weight tile is read by sb_m and each activation tile by sb_n
-  // workgroups that run in step through K, and the block's k slices stay in that XCD's L2.
-  // Blocks are dealt to the 8 XCDs round-robin, M-fastest (consecutive blocks of an XCD keep
-  // their activation band).
-  const int xcd = blockIdx.x % 8, jw = blockIdx.x / 8;
-  const int n_bn = (n_nt + sb_n - 1) / sb_n, n_bm = (n_mt + sb_m - 1) / sb_m;
-  for (int blk = xcd; blk < n_bn * n_bm; blk += 8) {
-  const int bn = (blk / n_bm) * sb_n + jw % sb_n, bm = (blk % n_bm) * sb_m + jw / sb_n;
-  if (bn >= n_nt || bm >= n_mt || jw >= sb_n * sb_m) continue;  // uniform per workgroup
-  const int nb0 = bn * RT, m0 = bm * PF_BM;
-
-  // Staging assignment: 512 WN 16-byte chunks of W and 1024 of X per step, 4 and XL per thread.
-  // W chunk i: k-block i / (64 RT) of the step, row tile (i >> 6) % RT, lane i & 63 (one tile =
-  // 1 KiB; row tiles past the weight's last load that one, their outputs are never stored).
-  // X: a wave's load covers 8 rows x the step's 8 16-byte columns (whole 128-byte lines); thread
-  // t, load r: row 8 (t >> 6) + 16 WN r + (t & 7), column c = lane >> 3 (k-block c >> 2, B-operand
-  // lane group c & 3). The 8 lanes that the LDS serves together hold 8 consecutive rows of one
-  // column: 8 consecutive 16-byte slots of the operand layout, free of bank conflicts.
-  const u32x4_t* W = (const u32x4_t*)a.W;
-  size_t wbase[4];
-  int wkb[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int i = t + NT * r;
-    wkb[r] = i / (64 * RT);
-    const int nb = min(nb0 + ((i >> 6) % RT), n_rt - 1);
-    wbase[r] = packed_tile(nb, 0, kbt, group) * 64 + (i & 63);
-  }
-  const int xc = lane >> 3;
-  auto xrow_of = [&](int r) { return (t >> 6) * 8 + 16 * WN * r + (t & 7); };
-  const bf16_t* xrow[XL];
-#pragma unroll
-  for (int r = 0; r < XL; ++r) xrow[r] = a.X + (size_t)min(m0 + xrow_of(r), a.M - 1) * a.ldx + xc * 8;
-  const int xkb = xc >> 2, xg = xc & 3;
-
-  // Two register sets of staged chunks: a step's global loads are issued two compute steps before
-  // they are written to LDS, so their latency is covered by two steps of MFMAs.
-  struct Stage {
-    u32x4_t a[4], b[XL];
-  };
-  Stage s0, s1;
-  float ss[XL] = {};
-  auto gload = [&](int st, Stage& r) {
-    const int k0 = st * PF_KB;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r.a[i] = W[wbase[i] + (size_t)(k0 + wkb[i]) * group * 64];  // shared by sb_m workgroups: cached
-#pragma unroll
-    for (int i = 0; i < XL; ++i) r.b[i] = *(const u32x4_t*)(xrow[i] + (size_t)k0 * 32);
-  };
-  // real == false stores zeros (the padding step of an odd step count): a mask, not a branch,
-  // so every path through the loop has the same loads in flight
-  auto lstore = [&](int buf, const Stage& r, bool real) {
-    const uint32_t keep = real ? 0xffffffffu : 0u;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) (&As[buf][0][0][0])[t + NT * i] = r.a[i] & keep;
-#pragma unroll
-    for (int i = 0; i < XL; ++i) {
-      const int row = xrow_of(i);
-      Bs[buf][xkb][row >> 4][xg * 16 + (row & 15)] = r.b[i] & keep;
-    }
-    if constexpr (NORM) {
-      if (real) {
-#pragma unroll
-        for (int i = 0; i < XL; ++i) ss[i] += sumsq8(r.b[i]);
-      }
-    }
-  };
-
-  f32x4_t acc[4][4];
-#pragma unroll
-  for (int x = 0; x < 4; ++x)
-#pragma unroll
-    for (int y = 0; y < 4; ++y) acc[x][y] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  auto compute = [&](int buf) {
-#pragma unroll
-    for (int kb = 0; kb < PF_KB; ++kb) {
-      u32x4_t af[4], bf[4];
-#pragma unroll
-      for (int x = 0; x < 4; ++x) af[x] = As[buf][kb][wn * 4 + x][lane];
-#pragma unroll
-      for (int y = 0; y < 4; ++y) bf[y] = Bs[buf][kb][wm * 4 + y][lane];
-#pragma unroll
-      for (int x = 0; x < 4; ++x)
-#pragma unroll
-        for (int y = 0; y < 4; ++y) acc[x][y] = mfma16x16x32(bits_bf16x8(af[x]), bits_bf16x8(bf[y]), acc[x][y]);
-    }
-  };
-  // step st: issue the loads of step st + 2 into `nxt`, compute step st from LDS, store step
-  // st + 1 (held in `cur`) into the other LDS buffer. Loads and stores are unconditional: the
-  // last steps re-load the final k slice, and an odd step count runs one more step over zeros.
-  // A load skipped on some path makes the compiler's wait counting assume fewer loads in flight,
-  // and the waits before the LDS stores would then also drain the loads issued at the top of the
-  // same step (the two-step prefetch would shrink to one).
-  const int n_st = kbt / PF_KB, n_run = (n_st + 1) & ~1;
-  // The scheduling barriers keep the three phases in this order (left free, the scheduler hoists
-  // the stores' masking, which waits for data, above the issue of the next loads).
-  auto step = [&](int st, Stage& cur, Stage& nxt) {
-    gload(min(st + 2, n_st - 1), nxt);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(st & 1);
-    __builtin_amdgcn_sched_barrier(0);
-    lstore((st + 1) & 1, cur, st + 1 < n_st);
-    __syncthreads();
-  };
-  gload(0, s0);
-  gload(min(1, n_st - 1), s1);
-  lstore(0, s0, true);
-  __syncthreads();
-  for (int st = 0; st < n_run; st += 2) {
-    step(st, s1, s0);
-    step(st + 1, s0, s1);
-  }
-
-  if constexpr (NORM) {
-    // the 8 lanes that staged one row hold its partial sums (lanes l, l ^ 8, ..., l ^ 56)
-#pragma unroll
-    for (int r = 0; r < XL; ++r) {
-      float v = ss[r];
-      v += __shfl_xor(v, 8);
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
-      if (xc == 0) rn_s[xrow_of(r)] = rsqrtf(v / (float)(kbt * 32) + a.norm_eps);
-    }
-    __syncthreads();
-  }
-
-  // Lane (g, j) of acc[x][y] holds rows n = 16 (nb0 + 4 wn + x) + 4 g + e of token m = m0 + 64 wm
-  // + 16 y + j.
-#pragma unroll
-  for (int y = 0; y < 4; ++y) {
-    const int mr = wm * 64 + y * 16 + j;
-    const float sc = NORM ? rn_s[mr] : 1.f;
-#pragma unroll
-    for (int x = 0; x < 4; ++x) pf_tile_epilogue<EPI>(a, acc[x][y], nb0 + wn * 4 + x, m0 + mr, sc, g, pos0);
-  }
-  }  // tile loop
-}
 // ------------------------------------------------------------------ 4-wave variant
-// One workgroup of 4 waves per CU (one per SIMD) owns a 256 (N) x 256 (M) output tile; wave (wn,
-// wm) computes 128 x 128 of it (64 accumulator tiles, held in the accumulator registers), so each
-// k-block it reads 16 KiB of operands from LDS for 64 MFMAs -- half the LDS bytes per MFMA of the
-// 8-wave 64 x 64 layout, whose LDS reads matched the LDS bandwidth at full MFMA rate. Operands
-// reach LDS by direct global-to-LDS loads (16 bytes per lane, one contiguous KiB per wave
-// instruction: a packed W tile, or 16 tokens x 32 k of X gathered into the MFMA B-operand lane
-// order) into a ring of five k-block slots (all 160 KiB of LDS). Step kb: wait until this wave's
-// loads of k-block kb + 1 have landed (those of kb + 2 and kb + 3 may still run) and pass one
-// barrier; issue the loads of kb + 4 into the slot k-block kb - 1 used; read k-block kb + 1's
-// fragments; run k-block kb's 64 MFMAs on the fragments read one step earlier. The step body takes
-// its LDS slots as restrict pointers, which lets the compiler see that the fragment reads do not
-// touch the slot being loaded (otherwise it waits for every load in flight before each LDS read).
-// The folded RMSNorm's sums of squares come from the X fragments the waves already hold (wave wn
-// sums fragments 4 wn .. 4 wn + 3 of its 8). Plain and SwiGLU outputs are staged through LDS after
-// the k loop and leave as whole 16-byte row pieces (residual read the same way); q/k/v keeps the
-// per-element RoPE / KV-cache epilogue.
+// One workgroup of 4 waves per CU (one per SIMD) owns a 32 XT (N) x 256 (M) output tile; wave (wn,
+// wm) computes 16 XT x 128 of it (8 XT accumulator tiles, held in the accumulator registers), so
+// with XT = 8 each k-block it reads 16 KiB of operands from LDS for 64 MFMAs -- half the LDS bytes
+// per MFMA of a 64 x 64-per-wave layout, whose LDS reads would match the LDS bandwidth at full MFMA
+// rate. XT = 8 (256 x 256 tiles) serves the plain and SwiGLU projections; q/k/v uses XT = 6
+// (192 x 256 tiles), which at the 8B shape (N 6144) makes 512 tiles, two full rounds of 256 CUs
+// instead of 384 tiles whose second round leaves half the CUs idle. Operands reach LDS by direct
+// global-to-LDS loads (16 bytes per lane, one contiguous KiB per wave instruction: a packed W tile,
+// or 16 tokens x 32 k of X gathered into the MFMA B-operand lane order) into a ring of five k-block
+// slots (all 160 KiB of LDS). Step kb: wait until this wave's loads of k-block kb + 1 have landed
+// (those of kb + 2 and kb + 3 may still run) and pass one barrier; issue the loads of kb + 4 into
+// the slot k-block kb - 1 used; read k-block kb + 1's fragments; run k-block kb's MFMAs on the
+// fragments read one step earlier. The step body takes its LDS slots as restrict pointers, which
+// lets the compiler see that the fragment reads do not touch the slot being loaded (otherwise it
+// waits for every load in flight before each LDS read). The folded RMSNorm's row scales come either
+// from the caller (a row-scale pass) or from sums of squares of the X fragments the waves already
+// hold (wave wn sums fragments 4 wn .. 4 wn + 3 of its 8). Outputs are staged through LDS after the
+// k loop and leave as whole 16-byte pieces: rows of Y (residual read the same way); for q/k/v, rows
+// of q and K-cache slots with RoPE applied on the way out, and 8-slot runs of the V^T cache.
 constexpr int P4_BM = 256, P4_SLOTS = 5, P4_AHEAD = 4;
-constexpr int P4_SLOT_BYTES = 32768;                 // 16 W tiles + 16 X tiles of one k-block
-constexpr int P4_ROW = 264;                           // staged output row: 256 (or 128) bf16 + 8 of pad
+constexpr int P4_SLOT_BYTES = 32768;                 // up to 16 W tiles + 16 X tiles of one k-block
+constexpr int P4_ROW = 264;                           // staged output row: up to 256 bf16 + 8 of pad
 constexpr int P4_RN_OFF = P4_BM * P4_ROW * 2;         // norm scales after the staged tile
 typedef __attribute__((address_space(3))) u32x4_t lds_u32x4;
 
 // The k loop's MFMAs are written as inline assembly with the accumulators bound to the accumulator
-// registers ("a"): left to the register allocator, some of the 256 accumulator values land in vector
+// registers ("a"): left to the register allocator, some of the accumulator values land in vector
 // registers and are copied in and out around their MFMAs, which costs up to half the loop's rate
 // depending on the epilogue compiled after it. The first k-block uses srcC = 0 (no read of
-// uninitialised accumulators, no VALU-write-to-MFMA-read hazard); accumulator reuse is 64 MFMAs
+// uninitialised accumulators, no VALU-write-to-MFMA-read hazard); accumulator reuse is 8 XT MFMAs
 // apart, and p4_drain() puts the wait states before the epilogue reads them.
 template <bool INIT>
 __device__ __forceinline__ void mfma_acc(f32x4_t& c, const u32x4_t& a, const u32x4_t& b) {
@@ -286,27 +74,28 @@ __device__ __forceinline__ void mfma_acc(f32x4_t& c, const u32x4_t& a, const u32
   else asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
 }
 
-__device__ __forceinline__ void p4_drain(f32x4_t (&acc)[8][8]) {
+template <int XT>
+__device__ __forceinline__ void p4_drain(f32x4_t (&acc)[XT][8]) {
   // the epilogue's reads of every accumulator depend on these statements, which follow the wait
   // states (more than the 16x16x32 MFMA's write latency) in program order
   asm volatile("s_nop 15\n\ts_nop 15" : "+a"(acc[0][0]));
 #pragma unroll
-  for (int x = 0; x < 8; ++x)
+  for (int x = 0; x < XT; ++x)
 #pragma unroll
     for (int y = 0; y < 8; ++y)
       if (x | y) asm volatile("" : "+a"(acc[x][y]));
 }
 
-template <int NORM, bool INIT = false>
-__device__ __forceinline__ void p4_step(const u32x4_t* const (&wsrc)[4], const bf16_t* const (&xsrc)[4], size_t woff,
-                                        size_t xoff, bool issue, lds_u32x4* __restrict__ dA,
+template <bool INIT, int XT>
+__device__ __forceinline__ void p4_step(const u32x4_t* const (&wsrc)[XT / 2], const bf16_t* const (&xsrc)[4],
+                                        size_t woff, size_t xoff, bool issue, lds_u32x4* __restrict__ dA,
                                         lds_u32x4* __restrict__ dB, const lds_u32x4* __restrict__ nA,
-                                        const lds_u32x4* __restrict__ nB, bool fetch, const u32x4_t (&fa)[8],
-                                        const u32x4_t (&fb)[8], u32x4_t (&na)[8], u32x4_t (&nb)[8],
-                                        f32x4_t (&acc)[8][8], float (&ss)[4], int y0, int lane) {
+                                        const lds_u32x4* __restrict__ nB, bool fetch, const u32x4_t (&fa)[XT],
+                                        const u32x4_t (&fb)[8], u32x4_t (&na)[XT], u32x4_t (&nb)[8],
+                                        f32x4_t (&acc)[XT][8], int lane) {
   if (issue) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int r = 0; r < XT / 2; ++r)
       __builtin_amdgcn_global_load_lds((const void*)(wsrc[r] + woff), (__attribute__((address_space(3))) void*)(dA + r * 64),
                                        16, 0, 0);
 #pragma unroll
@@ -318,29 +107,140 @@ __device__ __forceinline__ void p4_step(const u32x4_t* const (&wsrc)[4], const b
 #pragma unroll
     for (int y = 0; y < 8; ++y) nb[y] = nB[y * 64 + lane];
 #pragma unroll
-    for (int x = 0; x < 8; ++x) na[x] = nA[x * 64 + lane];
-  }
-  if constexpr (NORM == 1) {
-#pragma unroll
-    for (int y = 0; y < 4; ++y) ss[y] += sumsq8(y0 ? fb[4 + y] : fb[y]);
+    for (int x = 0; x < XT; ++x) na[x] = nA[x * 64 + lane];
   }
 #pragma unroll
-  for (int x = 0; x < 8; ++x)
+  for (int x = 0; x < XT; ++x)
 #pragma unroll
     for (int y = 0; y < 8; ++y) mfma_acc<INIT>(acc[x][y], fa[x], fb[y]);
 }
 
-// this wave's loads of k-block kb + 1 have landed (the 8 each of up to `later` later k-blocks may
-// still run), then the workgroup barrier (no wait for other memory operations)
+// this wave's loads of k-block kb + 1 have landed (the PER = XT / 2 + 4 each of up to `later`
+// later k-blocks may still run), then the workgroup barrier (no wait for other memory operations)
+template <int PER>
 __device__ __forceinline__ void p4_wait(int later) {
-  if (later >= 2) asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
-  else if (later == 1) asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
-  else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  static_assert(PER == 8 || PER == 7, "XT = 8 or 6");
+  if constexpr (PER == 8) {
+    if (later >= 3) asm volatile("s_waitcnt vmcnt(24)\n\ts_barrier" ::: "memory");
+    else if (later == 2) asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+    else if (later == 1) asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  } else {
+    if (later >= 3) asm volatile("s_waitcnt vmcnt(21)\n\ts_barrier" ::: "memory");
+    else if (later == 2) asm volatile("s_waitcnt vmcnt(14)\n\ts_barrier" ::: "memory");
+    else if (later == 1) asm volatile("s_waitcnt vmcnt(7)\n\ts_barrier" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  }
 }
 
-template <int EPI, int NORM>
+// SiLU of the prefill's SwiGLU staging: x sigma(x) with the logistic function through the hardware
+// base-2 exponential and reciprocal, 1 / (1 + 2^(-x log2 e)) (a few ulp of fp32, then rounded to
+// bf16; the exact division and exponential of silu_f cost half of the gate/up tile's staging).
+// exp2 overflows to +inf for x < -88 (sigma = 0, silu = -0) and underflows to 0 for large x (silu = x).
+__device__ __forceinline__ float pf_silu(float x) {
+  return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+}
+
+// q/k/v write-out of one staged tile: rows of q and K-cache slots (RoPE applied here), then 8-slot
+// runs of V^T. Staged column 16 t + i holds weight tile nb0 + t's row i: rotary dim p 8 + i
+// (i < 8) or hd / 2 + p 8 + i - 8 (i >= 8) of its head -- both halves of each rotary pair. Thread
+// t's q/k items are (token, weight tile) = divmod(t + 256 i, 2 XT), i < 2 XT; their rotary cos / sin
+// pieces are loaded by p4_qkv_rope() before the tile is staged (clamped addresses for items that
+// are not q/k, so the loads are unconditional), so their latency overlaps the staging.
+template <int XT>
+struct P4Rope {
+  Pack8 cs[2 * XT], sn[2 * XT];
+};
+
+template <int XT>
+__device__ __forceinline__ void p4_qkv_rope(const GemmArgs& a, int nb0, int m0, int pos0, int t, P4Rope<XT>& r) {
+  constexpr int NWT = 2 * XT;
+  const int half = a.head_dim >> 1;
+#pragma unroll
+  for (int i = 0; i < NWT; ++i) {
+    const int it = t + 256 * i, row = it / NWT, tt = it % NWT;
+    const QkvTile q = qkv_tile(a, nb0 + tt);
+    const int pos = min(max(pos0 + m0 + row, 0), (int)a.rope_rows - 1);
+    const size_t at = (size_t)pos * half + (q.p & (half / 8 - 1)) * 8;
+    r.cs[i].u = *(const uint4*)(a.cos_tab + at);
+    r.sn[i].u = *(const uint4*)(a.sin_tab + at);
+  }
+}
+
+template <int XT>
+__device__ __forceinline__ void p4_qkv_out(const GemmArgs& a, const bf16_t* stage, int nb0, int m0, int pos0, int t,
+                                           const P4Rope<XT>& r) {
+  constexpr int NWT = 2 * XT;  // weight tiles of the workgroup tile
+  const int hd = a.head_dim, half = hd >> 1;
+  const int n_wt = min(NWT, a.N / 16 - nb0);  // N is a multiple of 16 (q/k/v shape)
+  const bool qvec = a.ldy % 8 == 0 && ((uintptr_t)a.Y & 15) == 0;
+  // q and K: one (token, weight tile) per item, two 16-byte pieces (the pair's halves)
+#pragma unroll
+  for (int i = 0; i < NWT; ++i) {
+    const int it = t + 256 * i, row = it / NWT, tt = it % NWT, m = m0 + row;
+    if (tt >= n_wt || m >= a.M) continue;
+    const QkvTile q = qkv_tile(a, nb0 + tt);
+    if (q.region == 2) continue;
+    Pack8 lo, hi, olo, ohi;
+    lo.u = *(const uint4*)(stage + row * P4_ROW + tt * 16);
+    hi.u = *(const uint4*)(stage + row * P4_ROW + tt * 16 + 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float xl = bf2f(lo.h[e]), xh = bf2f(hi.h[e]), c = bf2f(r.cs[i].h[e]), s = bf2f(r.sn[i].h[e]);
+      olo.h[e] = f2bf(rbf(rbf(xl * c) - rbf(xh * s)));
+      ohi.h[e] = f2bf(rbf(rbf(xh * c) + rbf(xl * s)));
+    }
+    if (q.region == 0) {
+      bf16_t* qo = a.Y + (size_t)m * a.ldy + (size_t)q.head * hd + q.p * 8;
+      if (qvec) {
+        *(uint4*)qo = olo.u;
+        *(uint4*)(qo + half) = ohi.u;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          qo[e] = olo.h[e];
+          qo[half + e] = ohi.h[e];
+        }
+      }
+    } else {
+      const int slot = pos0 + m;  // inside the cache (checked on the host)
+      bf16_t* kc = a.k_cache + (size_t)q.head * a.max_len * hd;
+      *(uint4*)(kc + k_off(slot, q.p * 8, hd)) = olo.u;
+      *(uint4*)(kc + k_off(slot, half + q.p * 8, hd)) = ohi.u;
+    }
+  }
+  // V^T: one (8-slot run, staged column) per item; runs cut by the tile's first or last token, or by
+  // M, are written element by element (the neighbouring tile writes the rest of such a run)
+  const int s_lo = pos0 + m0, s_hi = pos0 + min(m0 + P4_BM, a.M);  // slots [s_lo, s_hi)
+  const int g_lo = s_lo >> 3, n_runs = ((s_hi + 7) >> 3) - g_lo;
+  for (int it = t; it < n_runs * NWT * 16; it += 256) {
+    const int run = it / (NWT * 16), c = it % (NWT * 16), tt = c >> 4, i = c & 15;
+    if (tt >= n_wt) continue;
+    const QkvTile q = qkv_tile(a, nb0 + tt);
+    if (q.region != 2) continue;
+    const int d = q.p * 8 + (i & 7) + (i >= 8 ? half : 0);
+    const int s0 = (g_lo + run) * 8;
+    bf16_t* vt = a.vt_cache + (size_t)q.head * hd * a.max_len;
+    if (s0 >= s_lo && s0 + 8 <= s_hi) {
+      Pack8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v.h[e] = stage[(s0 + e - s_lo) * P4_ROW + c];
+      *(uint4*)(vt + v_off(s0, d, hd)) = v.u;
+    } else {
+      for (int e = 0; e < 8; ++e) {
+        const int s = s0 + e;
+        if (s >= s_lo && s < s_hi) vt[v_off(s, d, hd)] = stage[(s - s_lo) * P4_ROW + c];
+      }
+    }
+  }
+}
+
+template <int EPI, bool RS, int XT>
 __global__ __launch_bounds__(256, 1) void prefill_gemm4_kernel(GemmArgs a, int group, int n_mt, int n_nt, int pos0,
                                                                int sb_n, int sb_m) {
+  static_assert(XT == 8 || XT == 6, "8 or 6 weight tiles per wave");
+  static_assert(EPI != EPI_SWIGLU || XT == 8, "SwiGLU pairs need whole 16-column output groups");
+  constexpr int WR = XT / 2, PER = WR + 4;  // W tiles each wave loads per k-block; loads per k-block
   __shared__ __align__(16) unsigned char smem[P4_SLOTS * P4_SLOT_BYTES];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int j = lane & 15, g = lane >> 4;
@@ -355,57 +255,57 @@ __global__ __launch_bounds__(256, 1) void prefill_gemm4_kernel(GemmArgs a, int g
   };
   float* rn_s = (float*)(smem + P4_RN_OFF);
   bf16_t* stage = (bf16_t*)smem;  // [256 tokens][P4_ROW] after the k loop
-  // the same XCD-aware persistent schedule as prefill_gemm_kernel
+  // persistent and XCD-aware: the workgroups resident on one XCD sweep blocks of sb_n x sb_m output
+  // tiles together, so the weight and activation tiles they share are fetched into that XCD's L2
+  // once per block
   const int xcd = blockIdx.x % 8, jw = blockIdx.x / 8;
   const int n_bn = (n_nt + sb_n - 1) / sb_n, n_bm = (n_mt + sb_m - 1) / sb_m;
   for (int blk = xcd; blk < n_bn * n_bm; blk += 8) {
   const int bn = (blk / n_bm) * sb_n + jw % sb_n, bm = (blk % n_bm) * sb_m + jw / sb_n;
   if (bn >= n_nt || bm >= n_mt || jw >= sb_n * sb_m) continue;  // uniform per workgroup
-  const int nb0 = bn * 16, m0 = bm * P4_BM;
-  // wave w loads W tiles 4w .. 4w + 3 and X tiles 4w .. 4w + 3 of every k-block (row tiles past
-  // the weight's last load that one; tokens past M load the last row: neither is stored)
-  const u32x4_t* wsrc[4];
+  const int nb0 = bn * 2 * XT, m0 = bm * P4_BM;
+  // wave w loads W tiles WR w .. WR w + WR - 1 and X tiles 4w .. 4w + 3 of every k-block (row tiles
+  // past the weight's last load that one; tokens past M load the last row: neither is stored)
+  const u32x4_t* wsrc[WR];
   const bf16_t* xsrc[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int nb = min(nb0 + 4 * w + r, n_rt - 1);
+  for (int r = 0; r < WR; ++r) {
+    const int nb = min(nb0 + WR * w + r, n_rt - 1);
     wsrc[r] = W + packed_tile(nb, 0, kbt, group) * 64 + lane;
-    xsrc[r] = a.X + (size_t)min(m0 + 16 * (4 * w + r) + j, a.M - 1) * a.ldx + g * 8;
   }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) xsrc[r] = a.X + (size_t)min(m0 + 16 * (4 * w + r) + j, a.M - 1) * a.ldx + g * 8;
   const size_t wstep = (size_t)group * 64;
 
-  f32x4_t acc[8][8];  // written first by k-block 0's srcC = 0 MFMAs
-  float ss[4] = {};
+  f32x4_t acc[XT][8];  // written first by k-block 0's srcC = 0 MFMAs
 
   // prologue: loads of k-blocks 0 .. 3, fragments of k-block 0
-  u32x4_t a0[8], b0[8], a1[8], b1[8];
+  u32x4_t a0[XT], b0[8], a1[XT], b1[8];
   for (int p = 0; p < P4_AHEAD; ++p)
     if (p < kbt) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
+      for (int r = 0; r < WR; ++r)
         __builtin_amdgcn_global_load_lds((const void*)(wsrc[r] + p * wstep),
-                                         (__attribute__((address_space(3))) void*)(slotA(p, 4 * w) + r * 64), 16, 0, 0);
+                                         (__attribute__((address_space(3))) void*)(slotA(p, WR * w) + r * 64), 16, 0, 0);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         __builtin_amdgcn_global_load_lds((const void*)(xsrc[r] + (size_t)p * 32),
                                          (__attribute__((address_space(3))) void*)(slotB(p, 4 * w) + r * 64), 16, 0, 0);
     }
   // k-block 0 landed (up to three later ones may still run), fragments of 0
-  if (kbt >= 4) asm volatile("s_waitcnt vmcnt(24)\n\ts_barrier" ::: "memory");
-  else if (kbt == 3) asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
-  else asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+  p4_wait<PER>(min(kbt, P4_AHEAD) - 1);
 #pragma unroll
   for (int y = 0; y < 8; ++y) b0[y] = slotB(0, wm * 8)[y * 64 + lane];
 #pragma unroll
-  for (int x = 0; x < 8; ++x) a0[x] = slotA(0, wn * 8)[x * 64 + lane];
+  for (int x = 0; x < XT; ++x) a0[x] = slotA(0, wn * XT)[x * 64 + lane];
 
-  auto step = [&](auto init, int kb, const u32x4_t (&fa)[8], const u32x4_t (&fb)[8], u32x4_t (&na)[8],
+  auto step = [&](auto init, int kb, const u32x4_t (&fa)[XT], const u32x4_t (&fb)[8], u32x4_t (&na)[XT],
                   u32x4_t (&nb)[8]) {
-    p4_wait(min(kbt - 2 - kb, 2));  // loads of kb + 2 .. kb + 3 may still run
+    p4_wait<PER>(min(kbt - 2 - kb, 2));  // loads of kb + 2 .. kb + 3 may still run
     const int ki = kb + P4_AHEAD;
-    p4_step<NORM, decltype(init)::value>(wsrc, xsrc, (size_t)ki * wstep, (size_t)ki * 32, ki < kbt, slotA(ki, 4 * w),
-                                         slotB(ki, 4 * w), slotA(kb + 1, wn * 8), slotB(kb + 1, wm * 8), kb + 1 < kbt,
-                                         fa, fb, na, nb, acc, ss, wn, lane);
+    p4_step<decltype(init)::value, XT>(wsrc, xsrc, (size_t)ki * wstep, (size_t)ki * 32, ki < kbt, slotA(ki, WR * w),
+                                       slotB(ki, 4 * w), slotA(kb + 1, wn * XT), slotB(kb + 1, wm * 8), kb + 1 < kbt,
+                                       fa, fb, na, nb, acc, lane);
   };
   using first_t = std::integral_constant<bool, true>;
   using rest_t = std::integral_constant<bool, false>;
@@ -416,84 +316,124 @@ __global__ __launch_bounds__(256, 1) void prefill_gemm4_kernel(GemmArgs a, int g
     step(rest_t{}, kb + 1, a0, b0, a1, b1);
   }
   step(rest_t{}, kbt - 1, a1, b1, a0, b0);
-  p4_drain(acc);
+  p4_drain<XT>(acc);
   __syncthreads();  // every wave is done with the slots: the staged tile and the scales reuse LDS
 
-  if constexpr (NORM == 1) {
-    // lanes j, j + 16, j + 32, j + 48 hold the four k-chunks of token 16 y + j
-#pragma unroll
-    for (int y = 0; y < 4; ++y) {
-      float v = ss[y];
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
-      if (g == 0) rn_s[wm * 128 + 16 * (4 * wn + y) + j] = rsqrtf(v / (float)(kbt * 32) + a.norm_eps);
-    }
-    __syncthreads();
-  } else if constexpr (NORM == 2) {
+  if constexpr (RS) {
     rn_s[t] = a.row_scale[min(m0 + t, a.M - 1)];  // 256 threads, 256 rows
     __syncthreads();
   }
-  static_assert(EPI != EPI_QKV, "q/k/v runs on prefill_gemm_kernel");
   {
-    // stage: lane (g, j) of tile (x, y) holds output rows 16 (wn 8 + x) + 4 g + e of token
-    // wm 128 + 16 y + j -- four consecutive columns (plain) or, for SwiGLU, rows r (gate) and
-    // r + 8 (up) meeting through a lane swap, four consecutive intermediate columns on lanes g < 2
-    constexpr int COLS = EPI == EPI_SWIGLU ? 128 : 256;
+    // the epilogue's thread indices pass through an empty asm statement, so that nothing computed
+    // from them is hoisted above the k loop and kept live (spilled) across it
+    int te = t;
+    asm volatile("" : "+v"(te));
+    const int je = te & 15, ge = (te >> 4) & 3, we = te >> 6, wne = we & 1, wme = we >> 1;
+    constexpr int COLS = EPI == EPI_SWIGLU ? 16 * XT : 32 * XT;  // staged columns
+    constexpr int NIT = COLS / 8;                                   // write-out items per thread
+    const int n_out = EPI == EPI_SWIGLU ? a.N / 2 : a.N;
+    const int c0 = (EPI == EPI_SWIGLU ? nb0 * 8 : nb0 * 16);
+    // The residual joins in the staging: lane (g, j)'s four columns of tile (x, y) are one 8-byte
+    // residual piece, loaded two token tiles ahead (clamped addresses, so the loads are
+    // unconditional; columns past N are never stored). The rotary tables of the q/k/v write-out are
+    // loaded before the staging. Either way the loads' latency overlaps the staging.
+    const bool res = EPI == EPI_STORE && a.residual && a.ldr % 4 == 0 && ((uintptr_t)a.residual & 7) == 0 &&
+                     n_out % 4 == 0;  // uniform
+    // 16-byte stores of staged rows (with a residual, only when the staging added it)
+    const bool vec = a.ldy % 8 == 0 && ((uintptr_t)a.Y & 15) == 0 && (!a.residual || res);
+    [[maybe_unused]] uint2 rq[3][EPI == EPI_STORE ? XT : 1];
+    auto load_res = [&](int y, uint2 (&dst)[EPI == EPI_STORE ? XT : 1]) {
+      if constexpr (EPI == EPI_STORE) {
+        const int m = min(m0 + wme * 128 + y * 16 + je, a.M - 1);
+#pragma unroll
+        for (int x = 0; x < XT; ++x) {
+          const int n = min(c0 + (wne * XT + x) * 16 + 4 * ge, n_out - 4);
+          dst[x] = *(const uint2*)(a.residual + (size_t)m * a.ldr + n);
+        }
+      }
+    };
+    [[maybe_unused]] P4Rope<EPI == EPI_QKV ? XT : 1> rope;
+    if constexpr (EPI == EPI_STORE) {
+      if (res) {
+        load_res(0, rq[0]);
+        load_res(1, rq[1]);
+      }
+    } else if constexpr (EPI == EPI_QKV) {
+      p4_qkv_rope<XT>(a, nb0, m0, pos0, te, rope);
+    }
+    // stage: lane (g, j) of tile (x, y) holds output rows 16 (wn XT + x) + 4 g + e of token
+    // wm 128 + 16 y + j -- four consecutive columns (plain, q/k/v). For SwiGLU, rows r (gate) and
+    // r + 8 (up) meet through a lane swap, after which lanes g and g + 2 hold the same four pairs:
+    // lanes g < 2 finish pairs 0, 1 and lanes g >= 2 pairs 2, 3 of them (intermediate columns
+    // 8 (wn XT + x) + 4 (g & 1) + 2 (g >> 1) + 0, 1).
 #pragma unroll
     for (int y = 0; y < 8; ++y) {
-      const int mr = wm * 128 + y * 16 + j;
-      const float sc = NORM ? rn_s[mr] : 1.f;
+      const int mr = wme * 128 + y * 16 + je;
+      const float sc = RS ? rn_s[mr] : 1.f;
+      if constexpr (EPI == EPI_STORE) {
+        __builtin_amdgcn_sched_barrier(0);  // keep each row's loads two rows ahead (not all hoisted)
+        if (res && y + 2 < 8) load_res(y + 2, rq[(y + 2) % 3]);
+      }
 #pragma unroll
-      for (int x = 0; x < 8; ++x) {
+      for (int x = 0; x < XT; ++x) {
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = acc[x][y][e] * sc;
-        uint32_t lo2, hi2;
-        int col;
         if constexpr (EPI == EPI_SWIGLU) {
-          float o[4];
+          float gt[4], up[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[e]), __float_as_uint(v[e]), false, false);
-            const float gt = __uint_as_float(p[0]), up = __uint_as_float(p[1]);
-            o[e] = rbf(silu_f(rbf(gt))) * rbf(up);
+            gt[e] = __uint_as_float(p[0]);
+            up[e] = __uint_as_float(p[1]);
           }
-          lo2 = pack_bf16x2(o[0], o[1]);
-          hi2 = pack_bf16x2(o[2], o[3]);
-          col = (wn * 8 + x) * 8 + 4 * g;
+          const bool hi = ge >= 2;
+          const float g0 = hi ? gt[2] : gt[0], g1 = hi ? gt[3] : gt[1];
+          const float u0 = hi ? up[2] : up[0], u1 = hi ? up[3] : up[1];
+          const float o0 = rbf(pf_silu(rbf(g0))) * rbf(u0), o1 = rbf(pf_silu(rbf(g1))) * rbf(u1);
+          const int col = (wne * XT + x) * 8 + 4 * (ge & 1) + 2 * (ge >> 1);
+          *(uint32_t*)(stage + mr * P4_ROW + col) = pack_bf16x2(o0, o1);
         } else {
-          lo2 = pack_bf16x2(v[0], v[1]);
-          hi2 = pack_bf16x2(v[2], v[3]);
-          col = (wn * 8 + x) * 16 + 4 * g;
+          if constexpr (EPI == EPI_STORE) {
+            if (res) {
+              // out = bf16(residual + bf16(acc sc)), the order of the decode epilogue
+              const uint2 r = rq[y % 3][x];
+              const uint32_t rw[2] = {r.x, r.y};
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v[e] = bf2f((bf16_t)(rw[e >> 1] >> (16 * (e & 1)))) + rbf(v[e]);
+            }
+          }
+          const int col = (wne * XT + x) * 16 + 4 * ge;
+          *(uint2*)(stage + mr * P4_ROW + col) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
         }
-        if (EPI != EPI_SWIGLU || g < 2) *(uint2*)(stage + mr * P4_ROW + col) = make_uint2(lo2, hi2);
       }
     }
     __syncthreads();
-    // write out: 8 columns (16 bytes) per item, a row's items on consecutive threads
-    const int n_out = EPI == EPI_SWIGLU ? a.N / 2 : a.N;
-    const int c0 = (EPI == EPI_SWIGLU ? nb0 * 8 : nb0 * 16);
-    const bool vec = a.ldy % 8 == 0 && ((uintptr_t)a.Y & 15) == 0 &&
-                     (!a.residual || (a.ldr % 8 == 0 && ((uintptr_t)a.residual & 15) == 0));
-    for (int it = t; it < P4_BM * (COLS / 8); it += 256) {
-      const int row = it / (COLS / 8), c8 = (it % (COLS / 8)) * 8;
-      const int m = m0 + row, n = c0 + c8;
-      if (m >= a.M || n >= n_out) continue;
-      Pack8 v;
-      v.u = *(const uint4*)(stage + row * P4_ROW + c8);
-      if (vec && n + 8 <= n_out) {
-        if (EPI == EPI_STORE && a.residual) {
-          Pack8 r;
-          r.u = *(const uint4*)(a.residual + (size_t)m * a.ldr + n);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) v.h[e] = f2bf(bf2f(r.h[e]) + bf2f(v.h[e]));
+    if constexpr (EPI == EPI_QKV) {
+      p4_qkv_out<XT>(a, stage, nb0, m0, pos0, te, rope);
+    } else {
+      // write out: 8 columns (16 bytes) per item, a row's items on consecutive threads
+      if (vec && n_out % 8 == 0) {  // uniform: every item is one whole 16-byte piece
+        for (int i = 0; i < NIT; ++i) {
+          const int it = te + 256 * i, row = it / NIT, c8 = (it % NIT) * 8;
+          const int m = m0 + row, n = c0 + c8;
+          if (m >= a.M || n >= n_out) continue;
+          *(uint4*)(a.Y + (size_t)m * a.ldy + n) = *(const uint4*)(stage + row * P4_ROW + c8);
         }
-        *(uint4*)(a.Y + (size_t)m * a.ldy + n) = v.u;
-      } else {
-        for (int e = 0; e < 8 && n + e < n_out; ++e) {
-          float r = bf2f(v.h[e]);
-          if (EPI == EPI_STORE && a.residual) r = rbf(bf2f(a.residual[(size_t)m * a.ldr + n + e]) + r);
-          a.Y[(size_t)m * a.ldy + n + e] = f2bf(r);
+      } else {  // element by element (unaligned output or residual, or N not a multiple of 8)
+        for (int i = 0; i < NIT; ++i) {
+          const int it = te + 256 * i, row = it / NIT, c8 = (it % NIT) * 8;
+          const int m = m0 + row, n = c0 + c8;
+          if (m >= a.M || n >= n_out) continue;
+          Pack8 v;
+          v.u = *(const uint4*)(stage + row * P4_ROW + c8);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            if (n + e >= n_out) continue;
+            float r = bf2f(v.h[e]);  // the staged value already holds the residual when res
+            if (EPI == EPI_STORE && a.residual && !res) r = rbf(bf2f(a.residual[(size_t)m * a.ldr + n + e]) + r);
+            a.Y[(size_t)m * a.ldy + n + e] = f2bf(r);
+          }
         }
       }
     }
@@ -676,33 +616,31 @@ __global__ __launch_bounds__(256) void prefill_rowscale_kernel(const bf16_t* __r
 }
 
 static int launch_prefill_gemm4(GemmArgs a, int group, int pos0, int epi, int cus, hipStream_t s) {
+  const int xt = epi == EPI_QKV ? 6 : 8;  // weight tiles per wave: 192- or 256-column workgroup tiles
   const int n_mt = (a.M + P4_BM - 1) / P4_BM;
-  const int n_nt = (a.N + 255) / 256;
+  const int n_nt = (a.N + 32 * xt - 1) / (32 * xt);
   const int per_xcd = max((cus / 8) & ~3, 4);  // one workgroup per CU
   const int sb_m = n_mt < 4 ? n_mt : 4;
   const int sb_n = per_xcd / sb_m;
   const int grid = 8 * sb_n * sb_m;
-  const bool norm = a.norm_eps > 0.f;
-#define PF4_LAUNCH(E)                                                                                             \
-  if (norm) SSD_LAUNCH((prefill_gemm4_kernel<E, 1>), dim3(grid), dim3(256), 0, s, a, group, n_mt, n_nt, pos0, sb_n, sb_m); \
-  else SSD_LAUNCH((prefill_gemm4_kernel<E, 0>), dim3(grid), dim3(256), 0, s, a, group, n_mt, n_nt, pos0, sb_n, sb_m);
+#define PF4_LAUNCH(E, R, X)                                                                                     \
+  SSD_LAUNCH((prefill_gemm4_kernel<E, R, X>), dim3(grid), dim3(256), 0, s, a, group, n_mt, n_nt, pos0, sb_n, sb_m)
+#define PF4_SCALES(E, X)                   \
+  if (a.row_scale) PF4_LAUNCH(E, true, X); \
+  else PF4_LAUNCH(E, false, X);
   if (epi == EPI_SWIGLU) {
-    if (a.row_scale)
-      SSD_LAUNCH((prefill_gemm4_kernel<EPI_SWIGLU, 2>), dim3(grid), dim3(256), 0, s, a, group, n_mt, n_nt, pos0, sb_n,
-                 sb_m);
-    else
-      PF4_LAUNCH(EPI_SWIGLU);
+    PF4_SCALES(EPI_SWIGLU, 8);
+  } else if (epi == EPI_QKV) {
+    PF4_SCALES(EPI_QKV, 6);
   } else {
-    PF4_LAUNCH(EPI_STORE);
+    PF4_SCALES(EPI_STORE, 8);
   }
+#undef PF4_SCALES
 #undef PF4_LAUNCH
   return check_launch("prefill_gemm4");
 }
 
 static int launch_prefill_gemm(GemmArgs a, int group, int pos0, int epi, hipStream_t s) {
-  const int n_mt = (a.M + PF_BM - 1) / PF_BM;
-  const int n_nt = (a.N + 64 * PF_WN - 1) / (64 * PF_WN);
-  // 4 / PF_WN workgroups per CU, all resident: 8 XCDs x per_xcd workgroups
   static int cus_of[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return set_error(SSD_EHIP, "prefill gemm: no current device");
@@ -711,32 +649,11 @@ static int launch_prefill_gemm(GemmArgs a, int group, int pos0, int epi, hipStre
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
     if (dev >= 0 && dev < 64) cus_of[dev] = cus;
   }
-  // plain and SwiGLU outputs: the 4-wave 256 x 256 kernel (measured at 4096 tokens, 8B shapes: gate/up
-  // 1295 against 1440 us, o_proj 160 against 226, down 481 against 602); q/k/v keeps the 8-wave
-  // kernel (its RoPE / KV-cache epilogue, and 384 256 x 256 tiles would leave half the CUs idle in a
-  // second round)
-  if (epi != EPI_QKV) return launch_prefill_gemm4(a, group, pos0, epi, cus, s);
-  // 32 on MI355X; at least one block row of 8 M-tiles, so a device reporting fewer CUs (a compute
-  // partition) still gets a nonempty grid (the schedule loops, so any grid size is correct)
-  const int per_xcd = max((4 / PF_WN * cus / 8) & ~7, 8);
-  const int sb_m = n_mt < 8 ? n_mt : 8;
-  const int sb_n = per_xcd / sb_m;
-  const int grid = 8 * sb_n * sb_m;
-  const bool norm = a.norm_eps > 0.f;
-#define PF_LAUNCH(E)                                                                                                   \
-  if (norm) SSD_LAUNCH((prefill_gemm_kernel<E, 1>), dim3(grid), dim3(128 * PF_WN), 0, s, a, group, n_mt, n_nt, pos0, sb_n, sb_m); \
-  else SSD_LAUNCH((prefill_gemm_kernel<E, 0>), dim3(grid), dim3(128 * PF_WN), 0, s, a, group, n_mt, n_nt, pos0, sb_n, sb_m);
-  switch (epi) {
-    case EPI_STORE: PF_LAUNCH(EPI_STORE); break;
-    case EPI_SWIGLU: PF_LAUNCH(EPI_SWIGLU); break;
-    default: PF_LAUNCH(EPI_QKV); break;
-  }
-#undef PF_LAUNCH
-  return check_launch("prefill_gemm");
+  return launch_prefill_gemm4(a, group, pos0, epi, cus, s);
 }
 
 static int check_packed(int N, int K, int group) {
-  if (N <= 0 || K <= 0 || K % (32 * PF_KB)) return set_error(SSD_EINVAL, "prefill gemm: N=%d K=%d (K %% 64 == 0)", N, K);
+  if (N <= 0 || K <= 0 || K % 64) return set_error(SSD_EINVAL, "prefill gemm: N=%d K=%d (K %% 64 == 0)", N, K);
   const int tiles = (N + 127) / 128 * 8;  // packed row tiles (rows padded to 128)
   if (group < 1 || group > 16 || tiles % group)
     return set_error(SSD_EINVAL, "prefill gemm: group %d does not divide the %d row tiles", group, tiles);
@@ -747,21 +664,28 @@ static int check_packed(int N, int K, int group) {
 
 using namespace ssd;
 
-static int prefill_gemm(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int group, int N, int K,
-                        float norm_eps, int epi, uint16_t* Y, int64_t ldy, const uint16_t* residual, int64_t ldr,
-                        const SsdQkvEpilogue* qkv, const float* row_scale, hipStream_t stream);
-
-SSD_API int ssd_prefill_gemm_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int group, int N,
-                                  int K, float norm_eps, int epi, uint16_t* Y, int64_t ldy, const uint16_t* residual,
-                                  int64_t ldr, const SsdQkvEpilogue* qkv, hipStream_t stream) {
-  return prefill_gemm(X, ldx, M, W_packed, group, N, K, norm_eps, epi, Y, ldy, residual, ldr, qkv, nullptr, stream);
+static int launch_row_scale(const uint16_t* X, int64_t ldx, int M, int K, float eps, float* rs, hipStream_t s) {
+  SSD_LAUNCH(prefill_rowscale_kernel, dim3((M + 3) / 4), dim3(256), 0, s, (const bf16_t*)X, ldx, M, K, eps, rs);
+  return check_launch("prefill_row_scale");
 }
 
-// ssd_prefill_gemm_bf16 with the folded RMSNorm's row scales given (row_scale, [M] floats, with
-// norm_eps > 0; used by the 4-wave kernel's plain and SwiGLU outputs instead of in-loop sums).
-static int prefill_gemm(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int group, int N, int K,
-                        float norm_eps, int epi, uint16_t* Y, int64_t ldy, const uint16_t* residual, int64_t ldr,
-                        const SsdQkvEpilogue* qkv, const float* row_scale, hipStream_t stream) {
+// Row scales of the RMSNorm folded into a prefill GEMM's packed weight: rs[m] = rsqrt(mean(X[m, :K]^2)
+// + eps), one wave per row in a fixed order (a row's scale does not depend on M).
+SSD_API int ssd_prefill_row_scale_bf16(const uint16_t* X, int64_t ldx, int M, int K, float eps, float* row_scale,
+                                       hipStream_t stream) {
+  if (!X || !row_scale) return set_error(SSD_EINVAL, "prefill row scale: null pointer");
+  if (M <= 0 || K <= 0 || K % 8 || ldx < K || ldx % 8 || ((uintptr_t)X & 15) || !(eps > 0.f))
+    return set_error(SSD_EINVAL, "prefill row scale: M=%d K=%d ldx=%lld eps=%g (16-byte rows, eps > 0)", M, K,
+                     (long long)ldx, (double)eps);
+  return launch_row_scale(X, ldx, M, K, eps, row_scale, stream);
+}
+
+// Y = epilogue(X W^T) with the folded RMSNorm's row scales (row_scale, [M] floats from
+// ssd_prefill_row_scale_bf16) applied to the products, or none (row_scale null).
+SSD_API int ssd_prefill_gemm_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packed, int group, int N,
+                                  int K, const float* row_scale, int epi, uint16_t* Y, int64_t ldy,
+                                  const uint16_t* residual, int64_t ldr, const SsdQkvEpilogue* qkv,
+                                  hipStream_t stream) {
   if (!X || !W_packed || !Y) return set_error(SSD_EINVAL, "prefill gemm: null pointer");
   if (M <= 0) return set_error(SSD_EINVAL, "prefill gemm: M=%d", M);
   int rc = check_packed(N, K, group);
@@ -774,8 +698,8 @@ static int prefill_gemm(const uint16_t* X, int64_t ldx, int M, const uint16_t* W
   if (epi != SSD_EPI_STORE && residual) return set_error(SSD_EINVAL, "prefill gemm: residual only with a plain store");
   GemmArgs a{};
   a.X = X; a.ldx = ldx; a.M = M; a.W = (const uint4*)W_packed; a.N = N; a.kb_total = K / 32;
-  a.Y = Y; a.ldy = ldy; a.residual = residual; a.ldr = ldr; a.norm_eps = norm_eps;
-  a.row_scale = norm_eps > 0.f ? row_scale : nullptr;
+  a.Y = Y; a.ldy = ldy; a.residual = residual; a.ldr = ldr;
+  a.row_scale = row_scale;
   int pos0 = 0;
   if (epi == SSD_EPI_QKV) {
     if (!qkv || !qkv->cos || !qkv->sin || !qkv->k_cache || !qkv->vt_cache)
@@ -785,6 +709,9 @@ static int prefill_gemm(const uint16_t* X, int64_t ldx, int M, const uint16_t* W
         N != (qkv->heads + 2 * qkv->kv_heads) * hd || ldy < (int64_t)qkv->heads * hd)
       return set_error(SSD_EINVAL, "prefill gemm: q/k/v shape N=%d heads=%d kv=%d hd=%d", N, qkv->heads,
                        qkv->kv_heads, hd);
+    if (((uintptr_t)qkv->k_cache & 15) || ((uintptr_t)qkv->vt_cache & 15) || ((uintptr_t)qkv->cos & 15) ||
+        ((uintptr_t)qkv->sin & 15))
+      return set_error(SSD_EINVAL, "prefill gemm: caches and rotary tables must be 16-byte aligned");
     if (qkv->pos0 < 0 || qkv->pos0 + M > qkv->max_len || qkv->pos0 + M > qkv->rope_rows || qkv->max_len % 64)
       return set_error(SSD_EINVAL, "prefill gemm: rows [%d, %d) outside the cache (%lld) or rotary table (%lld)",
                        qkv->pos0, qkv->pos0 + M, (long long)qkv->max_len, (long long)qkv->rope_rows);
@@ -854,23 +781,27 @@ SSD_API int ssd_prefill(const SsdModel* md, const uint16_t* head_w, const SsdPre
     const SsdLayerW& L = md->layers[li];
     SsdQkvEpilogue qe{H, KV, hd, md->cos, md->sin, md->rope_rows, pos0, pb->k_arena + li * layer_elems,
                       pb->vt_arena + li * layer_elems, pb->cache_cap};
-    if ((rc = ssd_prefill_gemm_bf16(pb->h, d, m, L.wqkv, g_qkv, nqkv, d, md->eps, SSD_EPI_QKV, pb->q, qdim, nullptr, 0,
+    // the input norm's row scales, computed once per row into the attention buffer (free until the
+    // attention writes it)
+    float* rs_qkv = (float*)pb->attn;
+    if ((rc = launch_row_scale(pb->h, d, m, d, md->eps, rs_qkv, s))) return rc;
+    if ((rc = ssd_prefill_gemm_bf16(pb->h, d, m, L.wqkv, g_qkv, nqkv, d, rs_qkv, SSD_EPI_QKV, pb->q, qdim, nullptr, 0,
                                     &qe, s)))
       return rc;
     if ((rc = ssd_prefill_attention_bf16(pb->q, qdim, m, pos0, H, KV, hd, qe.k_cache, qe.vt_cache, pb->cache_cap,
                                          md->attn_scale, pb->attn, qdim, s)))
       return rc;
-    if ((rc = ssd_prefill_gemm_bf16(pb->attn, qdim, m, L.wo, g_o, d, (int)qdim, 0.f, SSD_EPI_STORE, pb->h, d, pb->h, d,
-                                    nullptr, s)))
+    if ((rc = ssd_prefill_gemm_bf16(pb->attn, qdim, m, L.wo, g_o, d, (int)qdim, nullptr, SSD_EPI_STORE, pb->h, d, pb->h,
+                                    d, nullptr, s)))
       return rc;
     // gate/up's norm scales computed once per row into the q buffer (free after the attention)
     float* rs = (float*)pb->q;
-    SSD_LAUNCH(prefill_rowscale_kernel, dim3((m + 3) / 4), dim3(256), 0, s, pb->h, (int64_t)d, m, d, md->eps, rs);
-    if ((rc = check_launch("prefill_rowscale"))) return rc;
-    if ((rc = prefill_gemm(pb->h, d, m, L.wgu, g_gu, 2 * I, d, md->eps, SSD_EPI_SWIGLU, pb->act, I, nullptr, 0, nullptr,
-                           rs, s)))
+    if ((rc = launch_row_scale(pb->h, d, m, d, md->eps, rs, s))) return rc;
+    if ((rc = ssd_prefill_gemm_bf16(pb->h, d, m, L.wgu, g_gu, 2 * I, d, rs, SSD_EPI_SWIGLU, pb->act, I, nullptr, 0,
+                                    nullptr, s)))
       return rc;
-    if ((rc = ssd_prefill_gemm_bf16(pb->act, I, m, L.wd, g_d, d, I, 0.f, SSD_EPI_STORE, pb->h, d, pb->h, d, nullptr, s)))
+    if ((rc = ssd_prefill_gemm_bf16(pb->act, I, m, L.wd, g_d, d, I, nullptr, SSD_EPI_STORE, pb->h, d, pb->h, d, nullptr,
+                                    s)))
       return rc;
   }
   if (head_w)

@@ -144,15 +144,16 @@ _PROTOS = {
     "ssd_accept_sample_trials": (I32, [P, I64, P, I64, I32, P, P, I32, C.POINTER(C.c_int32), U64, U64, I32, P, P, P]),
     "ssd_forward": (I32, [C.POINTER(SsdModel), C.POINTER(SsdPlan), C.POINTER(SsdBuffers), C.POINTER(SsdRows), I32,
                           I32, I32, I32, I32, P]),
-    "ssd_prefill_gemm_bf16": (I32, [P, I64, I32, P, I32, I32, I32, F32, I32, P, I64, P, I64,
+    "ssd_prefill_row_scale_bf16": (I32, [P, I64, I32, I32, F32, P, P]),
+    "ssd_prefill_gemm_bf16": (I32, [P, I64, I32, P, I32, I32, I32, P, I32, P, I64, P, I64,
                                     C.POINTER(SsdQkvEpilogue), P]),
     "ssd_prefill_attention_bf16": (I32, [P, I64, I32, I32, I32, I32, I32, P, P, I64, F32, P, I64, P]),
     "ssd_prefill": (I32, [C.POINTER(SsdModel), P, C.POINTER(SsdPrefillBuffers), P, I32, I32, P]),
 }
 
 EXPORTED = tuple(_PROTOS)
-ABI_VERSION = 5  # descriptor struct layouts (SsdModel.mlp_fused, SsdBuffers.sync, SsdRows.kv_off); pos_base
-# arguments; ssd_tree_level_topk's record count S
+ABI_VERSION = 6  # descriptor struct layouts (SsdModel.mlp_fused, SsdBuffers.sync, SsdRows.kv_off); pos_base
+# arguments; ssd_tree_level_topk's record count S; ssd_prefill_gemm_bf16 takes row scales
 
 _lib = None
 

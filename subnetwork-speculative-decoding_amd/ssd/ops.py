@@ -164,8 +164,13 @@ def prefill_gemm(x, m, wp, group, n, k, out, epi="store", residual=None, norm_ep
         ep = _lib.SsdQkvEpilogue(c["heads"], c["kv_heads"], c["head_dim"], c["cos"].data_ptr(), c["sin"].data_ptr(),
                                  c["cos"].shape[0], int(c["pos0"]), c["k_cache"].data_ptr(), c["vt_cache"].data_ptr(),
                                  int(c["max_len"]))
-    _lib.call("ssd_prefill_gemm_bf16", x.data_ptr(), _rows(x, "x", k, m), m, wp.data_ptr(), int(group), n, k,
-              float(norm_eps), EPI[epi], out.data_ptr(), _rows(out, "out", cols, m), _p(residual), ldr,
+    ldx = _rows(x, "x", k, m)
+    rs = None
+    if norm_eps > 0:  # the folded RMSNorm's row scales, one pass before the GEMM
+        rs = torch.empty(m, dtype=torch.float32, device=x.device)
+        _lib.call("ssd_prefill_row_scale_bf16", x.data_ptr(), ldx, m, k, float(norm_eps), rs.data_ptr(), stream())
+    _lib.call("ssd_prefill_gemm_bf16", x.data_ptr(), ldx, m, wp.data_ptr(), int(group), n, k, _p(rs), EPI[epi],
+              out.data_ptr(), _rows(out, "out", cols, m), _p(residual), ldr,
               ctypes.byref(ep) if ep is not None else None, stream())
     return out
 

@@ -42,7 +42,7 @@ def test_host_only_entry_points():
     from ssd import _lib
 
     lib = _lib.load()
-    assert lib.ssd_abi_version() == _lib.ABI_VERSION == 5
+    assert lib.ssd_abi_version() == _lib.ABI_VERSION == 6
     assert lib.ssd_packed_weight_elems(17, 40) == 128 * 64  # rows padded to 128, K to 32
     assert [lib.ssd_gemm_weight_group(n, 4096) for n in (4096, 8192, 28672, 128256)] == [1, 2, 4, 8]
     assert lib.ssd_gemm_weight_group(4096, 100) == 0

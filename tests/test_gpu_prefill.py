@@ -109,12 +109,15 @@ def test_prefill_gemm_norm_swiglu_matches_decode(hidden, inter, m):
     close_bf16(got, ref, frac=0.95, rtol=1.6e-2)
 
 
-@pytest.mark.parametrize("heads,kv,hd,hidden", [(4, 2, 64, 256), (32, 8, 128, 4096)])
-def test_prefill_gemm_qkv_rope_matches_decode(heads, kv, hd, hidden):
-    """q/k/v + RoPE + KV-cache write at positions pos0 + row against the decode q/k/v GEMM."""
+@pytest.mark.parametrize("heads,kv,hd,hidden,m,pos0", [(4, 2, 64, 256, 150, 70), (32, 8, 128, 4096, 150, 70),
+                                                      (8, 2, 128, 512, 600, 37)])
+def test_prefill_gemm_qkv_rope_matches_decode(heads, kv, hd, hidden, m, pos0):
+    """q/k/v + RoPE + KV-cache write at positions pos0 + row against the decode q/k/v GEMM. Unaligned
+    pos0: the V^T cache's 8-slot runs are cut at the first and last row and, with m > 256, between
+    the two row tiles' workgroups."""
     from ssd.models.llama import qkv_row_map, rope_tables
     ops = _ops()
-    m, pos0, cap = 150, 70, 320
+    cap = (pos0 + m + 63) // 64 * 64 + 64
     n = (heads + 2 * kv) * hd
     h = bf(rand(m, hidden, seed=10)).to(DEV)
     ln = bf(1 + 0.1 * rand(hidden, seed=11)).to(DEV)
@@ -142,6 +145,7 @@ def test_prefill_gemm_qkv_rope_matches_decode(heads, kv, hd, hidden):
     close_bf16(ka[:, pos0:pos0 + m], kb[:, pos0:pos0 + m])
     close_bf16(va[:, pos0:pos0 + m], vb[:, pos0:pos0 + m])
     assert not ka[:, :pos0].any() and not ka[:, pos0 + m:].any()  # nothing written outside the rows
+    assert not va[:, :pos0].any() and not va[:, pos0 + m:].any()
 
 
 @pytest.mark.parametrize("heads,kv,hd", [(4, 2, 64), (32, 8, 128), (64, 8, 128)])
