@@ -525,13 +525,22 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
   // it back with readlane (no registers per superblock).
   float v[CH][PER];
   // Unconditional loads from clamped indices (a per-lane conditional load would be waited for
-  // one by one); entries past n are masked where they are used.
+  // one by one); entries past n are masked where they are used. At head_dim 128 lane l owns dims
+  // 2l and 2l + 1 (one 4-byte load per record), otherwise dims l + 64 i.
+  constexpr bool PAIRS = HD == 128;
+  auto dim = [&](int i) { return PAIRS ? 2 * lane + i : min(lane + 64 * i, HD - 1); };
   auto load_chunk = [&](int s0) {
 #pragma unroll
     for (int q = 0; q < CH; ++q) {
       const int sq = min(s0 + q, n - 1);
+      if constexpr (PAIRS) {
+        const uint32_t w = *(const uint32_t*)(O + (size_t)sq * HD + 2 * lane);
+        v[q][0] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+        v[q][1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+      } else {
 #pragma unroll
-      for (int i = 0; i < PER; ++i) v[q][i] = (float)O[(size_t)sq * HD + min(lane + 64 * i, HD - 1)];
+        for (int i = 0; i < PER; ++i) v[q][i] = (float)O[(size_t)sq * HD + dim(i)];
+      }
     }
   };
   float2 win = ml[min(lane, n - 1)];
@@ -561,9 +570,13 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
     load_chunk(s0);
   }
   bf16_t* dst = out + (size_t)tok * ldo + (size_t)hq * HD;
+  if constexpr (PAIRS) {
+    *(uint32_t*)(dst + 2 * lane) = pack_bf16x2(l > 0.f ? o[0] / l : 0.f, l > 0.f ? o[1] / l : 0.f);
+  } else {
 #pragma unroll
-  for (int i = 0; i < PER; ++i)
-    if (lane + 64 * i < HD) dst[lane + 64 * i] = f2bf(l > 0.f ? o[i] / l : 0.f);
+    for (int i = 0; i < PER; ++i)
+      if (lane + 64 * i < HD) dst[lane + 64 * i] = f2bf(l > 0.f ? o[i] / l : 0.f);
+  }
 }
 
 template <int HD>
@@ -635,6 +648,8 @@ int ssd::tree_attention(const uint16_t* q, int64_t ldq, int M, int heads, int kv
     return set_error(SSD_EINVAL, "attention: bad M=%d heads=%d kv_heads=%d", M, heads, kv_heads);
   if (max_len % 64 || ((uintptr_t)vt_cache & 15) || ((uintptr_t)k_cache & 15) || ((uintptr_t)q & 15) || ldq % 8)
     return set_error(SSD_EINVAL, "attention: caches/q must be 16-byte aligned, max_len %% 64 == 0");
+  if (((uintptr_t)out & 3) || ldo % 2 || ldo < (int64_t)heads * head_dim)
+    return set_error(SSD_EINVAL, "attention: out must be 4-byte aligned with an even row stride >= heads * head_dim");
   if (l_max > max_len || p_min < 0 || l_max < 1 || p_min > l_max)
     return set_error(SSD_EINVAL, "attention: bad bounds p_min=%d l_max=%d max_len=%lld", p_min, l_max,
                      (long long)max_len);
