@@ -464,7 +464,152 @@ __device__ __forceinline__ float pf_sum_lanes(float v) {
 
 constexpr int PF_TOK = 32;  // tokens per wave (two 16-row tiles)
 
+// Per-wave state of the causal attention: the query fragments of two 16-row tiles, their running
+// max / sum and output accumulators, and each lane's last attended key.
 template <int HD>
+struct PfAttnState {
+  static constexpr int KS = HD / 32, DT = HD / 16, NT = PF_TOK / 16;
+  u32x4_t qf[NT][KS];
+  float m_run[NT], l_run[NT];
+  f32x4_t o[NT][DT];
+  int lim[NT];
+};
+
+// One 64-key block b for both row tiles. K / V fragments come from `ck` / `cv` (the block in LDS,
+// SHARED) or from the cache rows `kb` / `vb`; with SHARED the copy of block b + 1 into `nk` / `nv`
+// is issued first. The LDS pointers are restrict, so the compiler sees that the fragment reads do
+// not touch the buffer being filled and does not wait for that copy before them.
+template <int HD, bool SHARED>
+__device__ __forceinline__ void pf_attend_block(PfAttnState<HD>& st, int b, int n_blk, int full_blk, int last,
+                                                float scale_log2, int lane, const bf16_t* kb, const bf16_t* vb,
+                                                const u32x4_t* ksrc, const u32x4_t* vsrc,
+                                                const lds_u32x4* __restrict__ ck, const lds_u32x4* __restrict__ cv,
+                                                lds_u32x4* __restrict__ nk, lds_u32x4* __restrict__ nv) {
+  constexpr int KS = HD / 32, DT = HD / 16, NT = PF_TOK / 16;
+  constexpr int PIECES = 64 * HD / 8;  // 16-byte pieces of one block's K (and of its V^T)
+  const int g = lane >> 4, w = threadIdx.x >> 6;
+  if constexpr (SHARED) {
+    // this block's copy landed (the only loads in flight: an explicit wait, since a workgroup
+    // barrier does not wait for global-to-LDS loads) and every wave is done with the buffer the next
+    // copy overwrites (it held block b - 1). The barrier is __syncthreads (not inline assembly) so
+    // the compiler sees it and places its own wait for the copy there, not before the fragment reads.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (b + 1 < n_blk) {
+      // wave w, load i copies pieces 256 i + 64 w + lane of block b + 1's K and V^T
+      const size_t off = (size_t)(b + 1) * PIECES + 64 * w;
+#pragma unroll
+      for (int i = 0; i < PIECES / 256; ++i) {
+        __builtin_amdgcn_global_load_lds((const void*)(ksrc + off + 256 * i),
+                                         (__attribute__((address_space(3))) void*)(nk + 256 * i + 64 * w), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(vsrc + off + 256 * i),
+                                         (__attribute__((address_space(3))) void*)(nv + 256 * i + 64 * w), 16, 0, 0);
+      }
+    }
+  }
+  // K first: the scores of both row tiles; V is read while the softmax runs (K and V are not live
+  // together, which keeps the wave inside 256 registers)
+  u32x4_t kf[4][KS];
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if constexpr (SHARED) kf[kt][ks] = ck[(kt * KS + ks) * 64 + lane];
+      else kf[kt][ks] = *(const u32x4_t*)(kb + (size_t)b * 64 * HD + (kt * KS + ks) * 512);
+    }
+  // k-step outer: consecutive MFMAs go to different accumulators (each sum keeps its ks order)
+  f32x4_t s[NT][4];
+#pragma unroll
+  for (int rt = 0; rt < NT; ++rt)
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) s[rt][kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+    for (int rt = 0; rt < NT; ++rt)
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) s[rt][kt] = mfma16x16x32(bits_bf16x8(kf[kt][ks]), bits_bf16x8(st.qf[rt][ks]), s[rt][kt]);
+  u32x4_t vf[DT][2];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    if constexpr (SHARED) {
+      vf[dt][0] = cv[(dt * 2) * 64 + lane];
+      vf[dt][1] = cv[(dt * 2 + 1) * 64 + lane];
+    } else {
+      vf[dt][0] = *(const u32x4_t*)(vb + (size_t)b * 64 * HD + (dt * 2) * 512);
+      vf[dt][1] = *(const u32x4_t*)(vb + (size_t)b * 64 * HD + (dt * 2 + 1) * 512);
+    }
+  }
+  if (b == n_blk - 1) {
+    // slots past the tile's last key hold whatever the cache held (not yet written): their
+    // probabilities are 0, and 0 * V must stay 0, so V is zeroed there. Lane (g, i) of V tile
+    // (dt, c) holds slots 64 b + 32 c + 8 g .. + 8.
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int s0 = b * 64 + c * 32 + g * 8;
+      u32x4_t keep;
+#pragma unroll
+      for (int w2 = 0; w2 < 4; ++w2)
+        keep[w2] = (s0 + 2 * w2 <= last ? 0x0000ffffu : 0u) | (s0 + 2 * w2 + 1 <= last ? 0xffff0000u : 0u);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) vf[dt][c] &= keep;
+    }
+  }
+  const bool masked = b >= full_blk;
+#pragma unroll
+  for (int rt = 0; rt < NT; ++rt) {
+    // Softmax in base 2 with the score scale folded into the exponent: p = 2^(s c - m), m a running
+    // reference in scaled units. The reference only moves up when a block's maximum exceeds it by
+    // more than 8 (so p <= 2^8 stays exact enough in fp32 and in the bf16 P operand); otherwise O
+    // and l keep their scale and O is not rescaled -- for the whole wave when no row of it moved.
+    // Every row attends key 0, so the first block sets a finite reference.
+    float sv[16], mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float v = s[rt][kt][e];
+        if (masked && b * 64 + pf_perm_key(kt, 4 * g + e) > st.lim[rt]) v = -INFINITY;
+        sv[kt * 4 + e] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = pf_max_lanes(mx) * scale_log2;
+    const bool grow = mx > st.m_run[rt] + 8.f;  // true in the first block (m_run = -inf)
+    const float m_use = grow ? mx : st.m_run[rt];
+    const float alpha = grow ? __builtin_amdgcn_exp2f(st.m_run[rt] - mx) : 1.f;
+    float l = 0.f;
+    uint32_t pw[2][4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int e = 0; e < 4; e += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(sv[kt * 4 + e], scale_log2, -m_use));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(sv[kt * 4 + e + 1], scale_log2, -m_use));
+        l += p0 + p1;
+        pw[kt >> 1][(kt & 1) * 2 + e / 2] = pack_bf16x2(p0, p1);
+      }
+    l = pf_sum_lanes(l);
+    st.l_run[rt] = st.l_run[rt] * alpha + l;
+    st.m_run[rt] = m_use;
+    if (__builtin_amdgcn_ballot_w64(grow)) {  // wave-uniform: multiplying by alpha = 1 is exact
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) st.o[rt][dt] = st.o[rt][dt] * alpha;
+    }
+    const u32x4_t pb0 = {pw[0][0], pw[0][1], pw[0][2], pw[0][3]};
+    const u32x4_t pb1 = {pw[1][0], pw[1][1], pw[1][2], pw[1][3]};
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) st.o[rt][dt] = mfma16x16x32(bits_bf16x8(vf[dt][0]), bits_bf16x8(pb0), st.o[rt][dt]);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) st.o[rt][dt] = mfma16x16x32(bits_bf16x8(vf[dt][1]), bits_bf16x8(pb1), st.o[rt][dt]);
+  }
+}
+
+// SHARED: the workgroup's four waves are four q heads of one kv head, so each 64-key block of K and
+// V^T is copied once per workgroup into LDS (direct global-to-LDS loads, 16 bytes per lane, the
+// cache layout kept) one block ahead of its use, and the waves read their MFMA fragments from there;
+// otherwise every wave loads its block's K and V straight into registers when it needs them. The
+// fragments and their order are the same either way, so the outputs are bit-identical.
+template <int HD, bool SHARED>
 __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(const bf16_t* __restrict__ Q, int64_t ldq, int M,
                                                                    int pos0, int heads, int kv_heads,
                                                                    const bf16_t* __restrict__ Kc,
@@ -472,130 +617,71 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(const bf16_t*
                                                                    float scale_log2, bf16_t* __restrict__ out,
                                                                    int64_t ldo, int n_tt) {
   constexpr int KS = HD / 32, DT = HD / 16, NT = PF_TOK / 16;
+  constexpr int PIECES = 64 * HD / 8;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int n_hg = (heads + 3) / 4;
   // the longest token tiles first (their rows attend the most keys)
   const int tt = n_tt - 1 - (int)blockIdx.x / n_hg;
   const int h = ((int)blockIdx.x % n_hg) * 4 + w;
-  if (h >= heads) return;
+  if (!SHARED && h >= heads) return;  // SHARED launches have heads % 4 == 0 (no wave leaves early)
   const int kvh = h / (heads / kv_heads);
   const int t0 = tt * PF_TOK;
   const bf16_t* kb = Kc + (size_t)kvh * max_len * HD + lane * 8;
   const bf16_t* vb = Vt + (size_t)kvh * max_len * HD + lane * 8;
+  // this kv head's blocks as 16-byte pieces (per lane) for the LDS copies
+  const u32x4_t* ksrc = (const u32x4_t*)(Kc + (size_t)kvh * max_len * HD) + lane;
+  const u32x4_t* vsrc = (const u32x4_t*)(Vt + (size_t)kvh * max_len * HD) + lane;
 
-  u32x4_t qf[NT][KS];
-  int lim[NT];  // last attended key of this lane's row in tile rt
+  PfAttnState<HD> st;
 #pragma unroll
   for (int rt = 0; rt < NT; ++rt) {
     const int tok = min(t0 + rt * 16 + j, M - 1);
-    lim[rt] = pos0 + t0 + rt * 16 + j;
+    st.lim[rt] = pos0 + t0 + rt * 16 + j;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[rt][ks] = *(const u32x4_t*)(Q + (size_t)tok * ldq + (size_t)h * HD + ks * 32 + g * 8);
-  }
-  float m_run[NT], l_run[NT];
-  f32x4_t o[NT][DT];
+    for (int ks = 0; ks < KS; ++ks)
+      st.qf[rt][ks] = *(const u32x4_t*)(Q + (size_t)tok * ldq + (size_t)h * HD + ks * 32 + g * 8);
+    st.m_run[rt] = -INFINITY;
+    st.l_run[rt] = 0.f;
 #pragma unroll
-  for (int rt = 0; rt < NT; ++rt) {
-    m_run[rt] = -INFINITY;
-    l_run[rt] = 0.f;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) o[rt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int dt = 0; dt < DT; ++dt) st.o[rt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
   const int last = pos0 + min(t0 + PF_TOK, M) - 1;  // the tile's last attended key
   const int n_blk = last / 64 + 1;
   const int full_blk = (pos0 + t0) / 64;  // blocks every row of the tile attends entirely
-  for (int b = 0; b < n_blk; ++b) {
-    // K first: the scores of both row tiles; V is loaded while the softmax runs (K and V are not
-    // live together, which keeps the wave inside 256 registers)
-    u32x4_t kf[4][KS];
+
+  // two K / V^T buffers (SHARED): blocks alternate between them
+  constexpr int BUF = SHARED ? PIECES : 1;
+  [[maybe_unused]] __shared__ __align__(16) u32x4_t kA[BUF], vA[BUF], kB[BUF], vB[BUF];
+  typedef __attribute__((address_space(3))) u32x4_t* lp;
+  if constexpr (SHARED) {
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kf[kt][ks] = *(const u32x4_t*)(kb + (size_t)b * 64 * HD + (kt * KS + ks) * 512);
-    // k-step outer: consecutive MFMAs go to different accumulators (each sum keeps its ks order)
-    f32x4_t s[NT][4];
-#pragma unroll
-    for (int rt = 0; rt < NT; ++rt)
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) s[rt][kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int rt = 0; rt < NT; ++rt)
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt) s[rt][kt] = mfma16x16x32(bits_bf16x8(kf[kt][ks]), bits_bf16x8(qf[rt][ks]), s[rt][kt]);
-    u32x4_t vf[DT][2];
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      vf[dt][0] = *(const u32x4_t*)(vb + (size_t)b * 64 * HD + (dt * 2) * 512);
-      vf[dt][1] = *(const u32x4_t*)(vb + (size_t)b * 64 * HD + (dt * 2 + 1) * 512);
+    for (int i = 0; i < PIECES / 256; ++i) {
+      __builtin_amdgcn_global_load_lds((const void*)(ksrc + 256 * i + 64 * w),
+                                       (__attribute__((address_space(3))) void*)((lp)kA + 256 * i + 64 * w), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(vsrc + 256 * i + 64 * w),
+                                       (__attribute__((address_space(3))) void*)((lp)vA + 256 * i + 64 * w), 16, 0, 0);
     }
-    if (b == n_blk - 1) {
-      // slots past the tile's last key hold whatever the cache held (not yet written): their
-      // probabilities are 0, and 0 * V must stay 0, so V is zeroed there. Lane (g, i) of V tile
-      // (dt, c) holds slots 64 b + 32 c + 8 g .. + 8.
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const int s0 = b * 64 + c * 32 + g * 8;
-        u32x4_t keep;
-#pragma unroll
-        for (int w2 = 0; w2 < 4; ++w2)
-          keep[w2] = (s0 + 2 * w2 <= last ? 0x0000ffffu : 0u) | (s0 + 2 * w2 + 1 <= last ? 0xffff0000u : 0u);
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) vf[dt][c] &= keep;
-      }
-    }
-    const bool masked = b >= full_blk;
-#pragma unroll
-    for (int rt = 0; rt < NT; ++rt) {
-      float sv[16], mx = -INFINITY;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float v = s[rt][kt][e] * scale_log2;
-          if (masked && b * 64 + pf_perm_key(kt, 4 * g + e) > lim[rt]) v = -INFINITY;
-          sv[kt * 4 + e] = v;
-          mx = fmaxf(mx, v);
-        }
-      mx = pf_max_lanes(mx);
-      const float m_new = fmaxf(m_run[rt], mx);
-      // every row attends key 0, so m_new is finite from the first block on
-      const float alpha = __builtin_amdgcn_exp2f(m_run[rt] - m_new);
-      float l = 0.f;
-      uint32_t pw[2][4];
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int e = 0; e < 4; e += 2) {
-          const float p0 = __builtin_amdgcn_exp2f(sv[kt * 4 + e] - m_new);
-          const float p1 = __builtin_amdgcn_exp2f(sv[kt * 4 + e + 1] - m_new);
-          l += p0 + p1;
-          pw[kt >> 1][(kt & 1) * 2 + e / 2] = pack_bf16x2(p0, p1);
-        }
-      l = pf_sum_lanes(l);
-      l_run[rt] = l_run[rt] * alpha + l;
-      m_run[rt] = m_new;
-      const u32x4_t pb0 = {pw[0][0], pw[0][1], pw[0][2], pw[0][3]};
-      const u32x4_t pb1 = {pw[1][0], pw[1][1], pw[1][2], pw[1][3]};
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o[rt][dt] = mfma16x16x32(bits_bf16x8(vf[dt][0]), bits_bf16x8(pb0), o[rt][dt] * alpha);
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o[rt][dt] = mfma16x16x32(bits_bf16x8(vf[dt][1]), bits_bf16x8(pb1), o[rt][dt]);
-    }
+  }
+  // blocks in pairs: each instance of the body reads one buffer and fills the other
+  for (int b = 0; b < n_blk; b += 2) {
+    pf_attend_block<HD, SHARED>(st, b, n_blk, full_blk, last, scale_log2, lane, kb, vb, ksrc, vsrc, (lp)kA, (lp)vA,
+                                (lp)kB, (lp)vB);
+    if (b + 1 < n_blk)
+      pf_attend_block<HD, SHARED>(st, b + 1, n_blk, full_blk, last, scale_log2, lane, kb, vb, ksrc, vsrc, (lp)kB,
+                                  (lp)vB, (lp)kA, (lp)vA);
   }
   // lane (g, j) of o[rt][dt] holds dims 16 dt + 4 g + e of row j
 #pragma unroll
   for (int rt = 0; rt < NT; ++rt) {
     const int tok = t0 + rt * 16 + j;
     if (tok >= M) continue;
-    const float inv = 1.f / l_run[rt];
+    const float inv = 1.f / st.l_run[rt];
     bf16_t* dst = out + (size_t)tok * ldo + (size_t)h * HD;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      const uint32_t lo = pack_bf16x2(o[rt][dt][0] * inv, o[rt][dt][1] * inv);
-      const uint32_t hi = pack_bf16x2(o[rt][dt][2] * inv, o[rt][dt][3] * inv);
+      const uint32_t lo = pack_bf16x2(st.o[rt][dt][0] * inv, st.o[rt][dt][1] * inv);
+      const uint32_t hi = pack_bf16x2(st.o[rt][dt][2] * inv, st.o[rt][dt][3] * inv);
       *(uint2*)(dst + dt * 16 + 4 * g) = make_uint2(lo, hi);
     }
   }
@@ -737,19 +823,24 @@ SSD_API int ssd_prefill_attention_bf16(const uint16_t* q, int64_t ldq, int M, in
   const int n_tt = (M + PF_TOK - 1) / PF_TOK;
   const dim3 grid((unsigned)(n_tt * ((heads + 3) / 4))), block(256);
   const float sl2 = scale * 1.4426950408889634f;
+  // a workgroup's four waves share one kv head's K/V when 4 divides the q heads per kv head
+  const bool shared = (heads / kv_heads) % 4 == 0;
+#define PF_ATT(D, SH)                                                                                         \
+  SSD_LAUNCH((prefill_attention_kernel<D, SH>), grid, block, 0, stream, (const bf16_t*)q, ldq, M, pos0, heads, \
+             kv_heads, (const bf16_t*)k_cache, (const bf16_t*)vt_cache, max_len, sl2, (bf16_t*)out, ldo, n_tt)
   switch (head_dim) {
     case 64:
-      SSD_LAUNCH((prefill_attention_kernel<64>), grid, block, 0, stream, (const bf16_t*)q, ldq, M, pos0, heads,
-                         kv_heads, (const bf16_t*)k_cache, (const bf16_t*)vt_cache, max_len, sl2, (bf16_t*)out, ldo, n_tt);
+      if (shared) PF_ATT(64, true);
+      else PF_ATT(64, false);
       break;
     case 128:
-      SSD_LAUNCH((prefill_attention_kernel<128>), grid, block, 0, stream, (const bf16_t*)q, ldq, M, pos0,
-                         heads, kv_heads, (const bf16_t*)k_cache, (const bf16_t*)vt_cache, max_len, sl2, (bf16_t*)out,
-                         ldo, n_tt);
+      if (shared) PF_ATT(128, true);
+      else PF_ATT(128, false);
       break;
     default:
       return set_error(SSD_EINVAL, "prefill attention: head_dim %d unsupported (64, 128)", head_dim);
   }
+#undef PF_ATT
   return check_launch("prefill_attention");
 }
 

@@ -169,6 +169,36 @@ def test_prefill_attention_matches_oracle(heads, kv, hd, m, pos0):
     torch.testing.assert_close(got, ref, atol=1e-2 * scale, rtol=2e-2)
 
 
+@pytest.mark.parametrize("heads,kv,hd,m,pos0", [(32, 8, 128, 300, 0), (64, 8, 128, 161, 77), (16, 4, 64, 97, 40),
+                                               (32, 8, 128, 1, 500)])
+def test_prefill_attention_shared_kv_equals_per_wave_loads(heads, kv, hd, m, pos0):
+    """With 4 | (q heads per kv head) a workgroup's four waves share their kv head's K/V blocks
+    through LDS (copied one block ahead); the same heads run as 2-head, 1-kv-head problems take the
+    kernel whose waves load their own K/V. The fragments and their order are the same, so every
+    head's output is bit-identical (unwritten cache slots hold NaN, as in the test above)."""
+    ops = _ops()
+    L = pos0 + m
+    cap = (L + 63) // 64 * 64 + 64
+    q = bf(rand(m, heads, hd, seed=21))
+    k = bf(rand(kv, cap, hd, seed=22))
+    v = bf(rand(kv, cap, hd, seed=23))
+    k[:, L:] = float("nan")
+    v[:, L:] = float("nan")
+    kd, vd = ops.kv_tile(k.to(DEV), "k"), ops.kv_tile(v.to(DEV), "v")
+    out = torch.zeros(m, heads * hd, dtype=torch.bfloat16, device=DEV)
+    ops.prefill_attention(q.reshape(m, -1).to(DEV), m, pos0, heads, kv, hd, kd, vd, cap, out)
+    out = out.view(m, heads, hd)
+    assert torch.isfinite(out.float()).all()
+    rep = heads // kv
+    for kvh in range(kv):
+        kh, vh = kd[kvh:kvh + 1].contiguous(), vd[kvh:kvh + 1].contiguous()
+        for h0 in range(kvh * rep, (kvh + 1) * rep, 2):
+            o2 = torch.zeros(m, 2 * hd, dtype=torch.bfloat16, device=DEV)
+            ops.prefill_attention(q[:, h0:h0 + 2].reshape(m, -1).contiguous().to(DEV), m, pos0, 2, 1, hd, kh, vh, cap,
+                                  o2)
+            assert torch.equal(o2.view(m, 2, hd), out[:, h0:h0 + 2]), (kvh, h0)
+
+
 def _small_hf(layers=4):
     from transformers import LlamaConfig, LlamaForCausalLM
     torch.manual_seed(0)
