@@ -481,22 +481,27 @@ __global__ __launch_bounds__(256, 2) void attn_partial_kernel(AttnArgs a) {
     }
   } else {
     // Shared workgroups run many tiles: software-pipelined, each wave folds tile i in the same
-    // straight-line code that computes tile i + 1, so the fold's LDS reads and stores overlap the
-    // next tile's MFMAs.
+    // straight-line code that computes tile i + 1 (fold first, so its LDS reads and record stores
+    // are issued before the next query loads and the MFMAs they overlap).
     load_qf(r_begin + 16, qa);
     block_attend<HD, false>(f, qn, bits, a.scale_log2, m, l, o);
     publish(0, m, l, o);
+    // Nothing outstanding on entry to the loop: the compiler's wait counts at the loop head then
+    // follow the loop's own order (query loads, then the fold's stores) and wait for the query
+    // fragments only. With the prologue's loads still counted, its merged state placed a wait for
+    // the previous tile's record stores in front of every other tile's MFMAs.
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0), lgkmcnt and expcnt not waited for
     for (int t0 = r_begin;; t0 += 32) {
       // tile t0 is in area 0, tile t0 + 16's query fragments in qa
-      if (t0 + 16 >= r_end) { fold(t0, 0); break; }  // uniform
+      fold(t0, 0);
+      if (t0 + 16 >= r_end) break;  // uniform
       load_qf(t0 + 32, qn);
       block_attend<HD, false>(f, qa, bits, a.scale_log2, m, l, o);
-      fold(t0, 0);
       publish(1, m, l, o);
-      if (t0 + 32 >= r_end) { fold(t0 + 16, 1); break; }
+      fold(t0 + 16, 1);
+      if (t0 + 32 >= r_end) break;
       load_qf(t0 + 48, qa);
       block_attend<HD, false>(f, qn, bits, a.scale_log2, m, l, o);
-      fold(t0 + 16, 1);
       publish(0, m, l, o);
     }
   }
