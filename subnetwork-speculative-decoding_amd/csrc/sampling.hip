@@ -685,8 +685,8 @@ __global__ void draw_merge_kernel(int rows, SmpWs ws, int* __restrict__ out_tok)
 // and bonus[j] = the categorical draw from p_j (one shared Exp(1) vector per round: only one
 // state's draw is ever used, and which one is decided by the acceptance uniforms alone).
 // Pass j (one launch over all rows and chunks) produces the chunk partials of zr[j] and
-// bonus[j]; partials are combined in chunk order by whoever needs them (the next pass, the
-// walk), always by the same sequential loop, so every reader sees the same values.
+// bonus[j]; partials are combined by whoever needs them (the next pass, the walk), always by
+// the same wave reduction (combine_states), so every reader sees the same values.
 struct AcceptArgs {
   SsdTree tree;
   const float* P;
@@ -715,34 +715,9 @@ __device__ __forceinline__ const float* q_row(const AcceptArgs& a, int cur) {
 }
 
 // Children of cur in rank order (ranks are distinct among siblings: they are draw order),
-// skipping those with q0(x) <= 0 (verify.py:77-78). One thread (the walk).
-__device__ __forceinline__ void node_kids(const AcceptArgs& a, int cur, NodeKids& k) {
-  const int vn = verify_nodes(a.tree);
-  const float* q0 = q_row(a, cur);
-  int cnt = 0, prev_rank = -1;
-  for (int s = 0; s < a.max_kids; ++s) {  // the next larger rank each time
-    int best = -1, best_rank = 0x7fffffff;
-    for (int v = 0; v < vn; ++v) {
-      const int rk = a.tree.vranks[v];
-      if (a.tree.vparents[v] == cur && rk > prev_rank && rk < best_rank) {
-        best = v;
-        best_rank = rk;
-      }
-    }
-    if (best < 0) break;
-    prev_rank = best_rank;
-    const int x = a.tree.vtokens[best];
-    if (q0[x] > 0.f) {
-      k.kid[cnt] = best;
-      k.tok[cnt] = x;
-      ++cnt;
-    }
-  }
-  k.n = cnt;
-}
-
-// The same list built by a whole workgroup (tree nodes staged in LDS; each child finds its
-// position by counting siblings of lower rank). Result in `k` (shared), valid after return.
+// skipping those with q0(x) <= 0 (verify.py:77-78), built by a whole workgroup of at least 64
+// threads (tree nodes staged in LDS; each child finds its position by counting siblings of lower
+// rank). Result in `k` (shared), valid after return.
 __device__ __forceinline__ void node_kids_block(const AcceptArgs& a, int cur, NodeKids& k, int* sh_par,
                                                 int* sh_rank, int* sh_pos) {
   const int vn = verify_nodes(a.tree);
@@ -759,20 +734,49 @@ __device__ __forceinline__ void node_kids_block(const AcceptArgs& a, int cur, No
     if (pos < SMP_MAXK) sh_pos[pos] = t;
   }
   __syncthreads();
-  if (t == 0) {
+  if (t < 64) {  // wave 0: lane i takes rank position i (positions are dense from 0), loads in parallel
     const float* q0 = q_row(a, cur);
-    int cnt = 0;
-    for (int i = 0; i < a.max_kids && sh_pos[i] >= 0; ++i) {
-      const int x = a.tree.vtokens[sh_pos[i]];
-      if (q0[x] > 0.f) {
-        k.kid[cnt] = sh_pos[i];
-        k.tok[cnt] = x;
-        ++cnt;
-      }
+    int pos = t < a.max_kids && t < SMP_MAXK ? sh_pos[t] : -1;
+    // the list ends at the first empty position, as a rank-order scan would stop there
+    const uint64_t filled = __ballot(pos >= 0);
+    if (t >= __ffsll((unsigned long long)~filled) - 1) pos = -1;
+    const int x = pos >= 0 ? a.tree.vtokens[pos] : 0;
+    const bool keep = pos >= 0 && q0[x] > 0.f;
+    const uint64_t m = __ballot(keep);
+    if (keep) {
+      const int slot = __popcll(m & ((1ull << t) - 1));  // kept children of lower rank
+      k.kid[slot] = pos;
+      k.tok[slot] = x;
     }
-    k.n = cnt;
+    if (t == 0) k.n = __popcll(m);
   }
   __syncthreads();
+}
+
+// Wave reductions: a butterfly of exchanges, so every lane ends with the same value (each step adds
+// the same two partials on both lanes, and floating-point addition is commutative) and the order
+// of the additions is fixed.
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
+  return v;
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
+  return v;
+}
+__device__ __forceinline__ KeyIdx wave_argmax(float k, int i) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float ok = __shfl_xor(k, o);
+    const int oi = __shfl_xor(i, o);
+    if (better(ok, oi, k, i)) {
+      k = ok;
+      i = oi;
+    }
+  }
+  return KeyIdx{k, i};
 }
 
 struct StateScalars {
@@ -782,28 +786,39 @@ struct StateScalars {
   float zq[SMP_MAXK + 1];  // zq[0] = 1
 };
 
-// Combine the chunk partials of row r: q0's mass and support, and states 1..upto. One thread;
-// the same sequential loops wherever the values are needed.
+// Combine the chunk partials of row r: q0's mass and support, and states 1..upto. Called by a
+// whole wave: lane l sums chunks l, l + 64, ..., then the wave reduces; every lane returns the
+// same values, and every reader (the passes and the walk) uses this code, so all see the same.
 __device__ __forceinline__ void combine_states(const AcceptArgs& a, int r, const float* q0, const NodeKids& k,
                                                int upto, StateScalars& s) {
-  const int C = a.ws.C;
+  const int C = a.ws.C, lane = threadIdx.x & 63;
   double s0 = 0.0;
   int supp = 0;
-  for (int c = 0; c < C; ++c) {
+  for (int c = lane; c < C; c += 64) {
     s0 += a.ws.s0[(size_t)r * C + c];
     supp += a.ws.supp[(size_t)r * C + c];
   }
+  double z[SMP_MAXK + 1];
+#pragma unroll
+  for (int j = 1; j <= SMP_MAXK; ++j) {
+    z[j] = 0.0;
+    if (j <= upto)
+      for (int c = lane; c < C; c += 64) z[j] += a.ws.zr[((size_t)r * (SMP_MAXK + 1) + j) * C + c];
+  }
+  s0 = wave_sum_d(s0);
   s.s0 = s0;
-  s.supp = supp;
+  s.supp = wave_sum_i(supp);
   s.zr[0] = 0.f;
   s.zq[0] = 1.f;
   double zq = s0;
-  for (int j = 1; j <= upto; ++j) {
-    double z = 0.0;
-    for (int c = 0; c < C; ++c) z += a.ws.zr[((size_t)r * (SMP_MAXK + 1) + j) * C + c];
-    s.zr[j] = z > 0.0 ? (float)z : 0.f;
-    zq -= (double)q0[k.tok[j - 1]];
-    s.zq[j] = (float)zq;
+#pragma unroll
+  for (int j = 1; j <= SMP_MAXK; ++j) {
+    if (j <= upto) {  // uniform
+      const double zj = wave_sum_d(z[j]);
+      s.zr[j] = zj > 0.0 ? (float)zj : 0.f;
+      zq -= (double)q0[k.tok[j - 1]];
+      s.zq[j] = (float)zq;
+    }
   }
 }
 
@@ -886,7 +901,7 @@ __global__ __launch_bounds__(SMP_THREADS) void statej_kernel(AcceptArgs a, int j
   node_kids_block(a, cur, kids, sh_par, sh_rank, sh_pos);
   if (kids.n < j) return;  // uniform: this node has fewer children
   const float* q0 = q_row(a, cur);
-  if (t == 0) combine_states(a, r, q0, kids, j - 1, st);
+  if (t < 64) combine_states(a, r, q0, kids, j - 1, st);  // wave 0; its lanes store the same values
   __syncthreads();
   const int i = c * SMP_CHUNK + t * 4;
   float p[4], q[4];
@@ -927,34 +942,38 @@ __global__ __launch_bounds__(SMP_THREADS) void statej_kernel(AcceptArgs a, int j
 }
 
 // The walk of sample_verify over the state scalars, then the same bookkeeping as the greedy
-// walk: result = [n_new, tokens...], compaction sources, next root token.
-__global__ void sample_walk_kernel(AcceptArgs a, int committed, int* result, int* keep_src, int* n_keep,
-                                   int* root_token) {
-  if (threadIdx.x != 0) return;
+// walk: result = [n_new, tokens...], compaction sources, next root token. One wave: every lane
+// walks the same path with the same values (the child lists, the state sums and the bonus merge
+// are wave-wide operations), lane 0 writes the result.
+__global__ __launch_bounds__(64) void sample_walk_kernel(AcceptArgs a, int committed, int* result, int* keep_src,
+                                                        int* n_keep, int* root_token) {
+  __shared__ int sh_par[64], sh_rank[64], sh_pos[SMP_MAXK];
+  __shared__ NodeKids kids;
+  const int lane = threadIdx.x;
   const int C = a.ws.C;
   int cur = -1, n_acc = 0, bonus = 0;
   int rej[SMP_MAXK];
-  NodeKids k;
   StateScalars s;
   for (int step = 0; step <= SMP_MAXDEPTH; ++step) {
     const int r = cur + 1;
     if (r >= a.rows) break;  // a tree larger than the launch's rows (the engine never makes one)
-    node_kids(a, cur, k);
+    node_kids_block(a, cur, kids, sh_par, sh_rank, sh_pos);
+    const int kn = kids.n;
     const float* q0 = q_row(a, cur);
     const float* p = a.P + (size_t)r * a.ldp;
     s.supp = 0;
     s.zr[0] = 0.f;
     s.zq[0] = 1.f;
-    if (k.n > 0) combine_states(a, r, q0, k, k.n, s);
+    if (kn > 0) combine_states(a, r, q0, kids, kn, s);
     int chosen = -1, j = 0;
-    for (int i = 0; i < k.n; ++i) {
-      const int x = k.tok[i];
+    for (int i = 0; i < kn; ++i) {
+      const int x = kids.tok[i];
       const float q0x = q0[x];
       const float pj = chain_p(p[x], q0x, x, j, s.zr, s.zq, rej);
       const float qj = j == 0 ? q0x : q0x / s.zq[j];
       const double u = uniform_from_bits(rng_block(a.rng, (uint32_t)j, (uint32_t)r, TAG_ACCEPT).x);
       if (u < (double)fminf(1.f, pj / qj)) {
-        chosen = k.kid[i];
+        chosen = kids.kid[i];
         break;
       }
       rej[j] = x;
@@ -964,20 +983,30 @@ __global__ void sample_walk_kernel(AcceptArgs a, int committed, int* result, int
     if (chosen < 0) {
       int jj = j;
       while (jj > 0 && !(s.zr[jj] > 0.f)) --jj;  // p_j == p_{j-1} when the residual had no mass
-      const KeyIdx b = merge_chunks(a.ws.bon + ((size_t)r * (SMP_MAXK + 1) + jj) * C, C);
+      // the categorical draw from p_jj: the best of the chunks' records (a strict order on
+      // (key, column), so any merge order gives the same record)
+      const KeyIdx* part = a.ws.bon + ((size_t)r * (SMP_MAXK + 1) + jj) * C;
+      KeyIdx b{-1.f, NO_IDX};
+      for (int c = lane; c < C; c += 64)
+        if (better(part[c].key, part[c].idx, b.key, b.idx)) b = part[c];
+      b = wave_argmax(b.key, b.idx);
       bonus = b.idx == NO_IDX ? 0 : b.idx;
       break;
     }
-    result[1 + n_acc] = a.tree.vtokens[chosen];
-    keep_src[1 + n_acc] = committed + 1 + chosen;
+    if (lane == 0) {
+      result[1 + n_acc] = a.tree.vtokens[chosen];
+      keep_src[1 + n_acc] = committed + 1 + chosen;
+    }
     ++n_acc;
     cur = chosen;
   }
-  result[1 + n_acc] = bonus;
-  result[0] = n_acc + 1;
-  keep_src[0] = committed;
-  *n_keep = n_acc + 1;
-  *root_token = bonus;
+  if (lane == 0) {
+    result[1 + n_acc] = bonus;
+    result[0] = n_acc + 1;
+    keep_src[0] = committed;
+    *n_keep = n_acc + 1;
+    *root_token = bonus;
+  }
 }
 
 // ------------------------------------------------------ batched acceptance trials
@@ -1012,28 +1041,6 @@ struct TrialArgs {
   int* out_n;    // [trials]
 };
 
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
-  return v;
-}
-__device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
-  return v;
-}
-__device__ __forceinline__ KeyIdx wave_argmax(float k, int i) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const float ok = __shfl_xor(k, o);
-    const int oi = __shfl_xor(i, o);
-    if (better(ok, oi, k, i)) {
-      k = ok;
-      i = oi;
-    }
-  }
-  return KeyIdx{k, i};
-}
 
 // q_{j-1}(y) as statej_kernel computes it: rejected tokens have no draft mass left.
 __device__ __forceinline__ float trial_qprev(float q0, int y, int j, const float* zq, const int* rej) {
