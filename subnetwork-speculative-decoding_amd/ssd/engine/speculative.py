@@ -223,6 +223,9 @@ class DecodeSession:
         self.cand_tok = torch.zeros(TREE_CAP, dtype=torch.int32, device=dev)
         self.cand_lp = torch.zeros(TREE_CAP, dtype=torch.float32, device=dev)
         self.argmax = torch.zeros(ROW_CAP_VERIFY, dtype=torch.int32, device=dev)
+        # greedy verify: the head's per-slab argmax records (the head fused with its chunk pass)
+        self.verify_parts = None if self.sampler is not None else torch.empty(
+            ops.gemm_topk_bytes(ROW_CAP_VERIFY, self.target._head_n()), dtype=torch.uint8, device=dev)
         self.keep_src = torch.zeros(cfg.depth + 2, dtype=torch.int32, device=dev)
         self.n_keep = torch.zeros(1, dtype=torch.int32, device=dev)
         self.phases = _Phases()
@@ -282,12 +285,21 @@ class DecodeSession:
                               pos_base=self.pos_base, window=window)
         m = drafter.finalize_device(self.tree, 0, self.root_rows, self.verify_rows, pos_base=self.pos_base)
         cache.check_room(hi + m)
-        logits = target.forward_rows(self.verify_rows, m, lo + 1, hi + 1 + cfg.depth, cache, ws)
-        ops.row_topk(logits, m, logits.shape[1], 1, 0, None, self.argmax)
+        self._verify_argmax(m, lo + 1, hi + 1 + cfg.depth)
         _lib.call("ssd_accept_greedy", self.tree.struct, self.argmax.data_ptr(), 0, self.record[2:].data_ptr(),
                   self.keep_src.data_ptr(), self.n_keep.data_ptr(), self.root_rows.ids.data_ptr(),
                   self.pos_base.data_ptr(), ops.stream())
         cache.compact_device(0, self.keep_src, self.n_keep, cfg.depth + 1, pos_base=self.pos_base)
+
+    def _verify_argmax(self, m: int, p_min: int, l_max: int) -> None:
+        """Target forward over the verify rows and each row's first-index argmax into self.argmax
+        (greedy_verify, reference verify.py:45-57): the head runs fused with its top-k chunk pass
+        (k = 1 over the bf16-rounded logits, ties to the lower column, as ssd_row_topk_bf16 on
+        stored logits) and the records are merged, so the [m, V] logits are never written."""
+        target, ws = self.target, self.ws
+        target.forward_rows(self.verify_rows, m, p_min, l_max, self.cache, ws, head_rows=0)
+        s = target.head_topk(ws.h, m, 1, self.verify_parts, mode=0)
+        ops.row_topk_merge(self.verify_parts, m, s, 1, 0, None, self.argmax)
 
     def _capture(self, committed: int) -> bool:
         """Capture the round of the segment holding root position ``committed`` (nothing in flight).
@@ -372,12 +384,12 @@ class DecodeSession:
         ph.mark("verify")
         m = drafter.finalize_device(self.tree, committed, self.root_rows, self.verify_rows)
         cache.check_room(committed + m)
-        logits = target.forward_rows(self.verify_rows, m, committed + 1, committed + 1 + cfg.depth, cache, ws)
         if self.sampler is not None:
+            logits = target.forward_rows(self.verify_rows, m, committed + 1, committed + 1 + cfg.depth, cache, ws)
             self.sampler.accept(self.tree, logits, m, committed, self.record[2:], self.keep_src, self.n_keep,
                                 self.root_rows.ids)
         else:
-            ops.row_topk(logits, m, logits.shape[1], 1, 0, None, self.argmax)
+            self._verify_argmax(m, committed + 1, committed + 1 + cfg.depth)
             _lib.call("ssd_accept_greedy", self.tree.struct, self.argmax.data_ptr(), committed,
                       self.record[2:].data_ptr(), self.keep_src.data_ptr(), self.n_keep.data_ptr(),
                       self.root_rows.ids.data_ptr(), None, ops.stream())
