@@ -77,7 +77,8 @@ int ssd_gemm_bf16(const uint16_t* X, int64_t ldx, int M, const uint16_t* W_packe
  * through memory. parts (8-byte aligned, >= M * ssd_gemm_topk_parts(N) * 136 bytes) gets, for row m
  * and slab s (consecutive 128-column groups, the slabs a function of N only), the slab's k best
  * (value, column) keys of the bf16-rounded logits, its maximum and (mode 1) its sum of exp(x - max);
- * merge them with ssd_tree_level_topk or ssd_row_topk_merge (S = ssd_gemm_topk_parts(N)). The keys
+ * merge them with ssd_tree_level_topk or ssd_row_topk_merge (S = ssd_gemm_topk_parts(N), the same
+ * k: records are stored packed for k, 8 + 8 k bytes each). The keys
  * are exact; the sums of exp differ from ssd_row_topk_partial_bf16's only in summation order.
  * W_packed as for ssd_gemm_bf16 (tiles grouped by ssd_gemm_weight_group(N, K)). Y (NULL or ldy >= N)
  * also receives the logits, bit-identical to ssd_gemm_bf16's for N >= 65536.

@@ -540,11 +540,11 @@ __global__ __launch_bounds__(64 * WIDE_WAVES) void gemm_wide_kernel(GemmArgs a, 
   if constexpr (TOPK) {
     // each row's state was last written by its own wave: no barrier needed to read it here
     for (int m = w; m < Mv; m += WIDE_WAVES) {
-      TopkPart* o = tk.parts + (size_t)m * tk.S + slab;
-      if (lane < TOPK_MAX) o->key[lane] = tkey[m][lane];
+      const TopkRec o = topk_rec(tk.parts, (size_t)m * tk.S + slab, tk.k);
+      if (lane < tk.k) o.key[lane] = tkey[m][lane];
       if (lane == 0) {
-        o->mx = tmx[m];
-        o->se = tk.mode == 1 ? tse[m] : 0.f;
+        *o.mx = tmx[m];
+        *o.se = tk.mode == 1 ? tse[m] : 0.f;
       }
     }
     __syncthreads();  // the next slab's reset follows every wave's record
@@ -1000,7 +1000,7 @@ SSD_API int ssd_gemm_topk_bf16(const uint16_t* X, int64_t ldx, int M, const uint
     a.N = N; a.kb_total = K / 32;
     a.Y = Y ? Y + (size_t)m0 * ldy : nullptr; a.ldy = ldy;
     a.norm_eps = norm_eps > 0.f ? norm_eps : 0.f;
-    t.parts = (TopkPart*)parts + (size_t)m0 * t.S;
+    t.parts = (TopkPart*)((char*)parts + (size_t)m0 * t.S * (size_t)(8 + 8 * k));
     if ((rc = launch_wide<EPI_STORE>(a, n_groups, stream, &t))) return rc;
   }
   return SSD_OK;

@@ -229,7 +229,7 @@ __global__ __launch_bounds__(256) void row_topk_partial_kernel(const bf16_t* __r
       key[h * 8 + t] = ok ? rank_key(val[h * 8 + t], col + t) : 0ull;
     }
   }
-  TopkPart* out = parts + (size_t)row * S + s;
+  const TopkRec out = topk_rec(parts, (size_t)row * S + s, k);
   uint32_t taken = 0;
   float mx = -INFINITY;
   for (int q = 0; q < k; ++q) {
@@ -245,7 +245,7 @@ __global__ __launch_bounds__(256) void row_topk_partial_kernel(const bf16_t* __r
 #pragma unroll
     for (int w = 1; w < 4; ++w) m = wbest[q & 1][w] > m ? wbest[q & 1][w] : m;
     if (bj >= 0 && b == m) taken |= 1u << bj;  // keys are distinct: one thread retires it
-    if (threadIdx.x == 0) out->key[q] = m;
+    if (threadIdx.x == 0) out.key[q] = m;
     if (q == 0) mx = m ? key_value(m) : -INFINITY;
   }
   float se = 0.f;
@@ -255,7 +255,7 @@ __global__ __launch_bounds__(256) void row_topk_partial_kernel(const bf16_t* __r
     for (int j = 0; j < TOPK_PER; ++j) acc += __expf(val[j] - mx);
     se = block_sum_256(acc, sh);
   }
-  if (threadIdx.x == 0) { out->mx = mx; out->se = se; }
+  if (threadIdx.x == 0) { *out.mx = mx; *out.se = se; }
 }
 
 // Merge pass, one wave per row (topk_merge_row).
@@ -263,7 +263,8 @@ __global__ __launch_bounds__(64) void row_topk_merge_kernel(const TopkPart* __re
                                                             const int* __restrict__ vocab_ids, int* __restrict__ out_tok,
                                                             float* __restrict__ out_val, float* __restrict__ out_lse) {
   const int row = blockIdx.x;
-  topk_merge_row(parts + (size_t)row * S, S, k, mode, vocab_ids, threadIdx.x, out_tok + row * k,
+  topk_merge_row((const char*)parts + (size_t)row * S * (size_t)(8 + 8 * k), S, k, mode, vocab_ids, threadIdx.x,
+                 out_tok + row * k,
                  out_val ? out_val + row * k : nullptr, out_lse ? out_lse + row : nullptr);
 }
 
@@ -312,6 +313,7 @@ SSD_API int ssd_row_topk_merge(const void* parts, int64_t parts_bytes, int M, in
                                const int32_t* vocab_ids, int32_t* out_tok, float* out_val, float* out_lse,
                                hipStream_t stream) {
   if (!parts || !out_tok) return set_error(SSD_EINVAL, "row_topk_merge: null pointer");
+  if ((uintptr_t)parts & 7) return set_error(SSD_EINVAL, "row_topk_merge: parts must be 8-byte aligned");
   if (M < 0 || k < 1 || k > TOPK_MAX || (mode != 0 && mode != 1))
     return set_error(SSD_EINVAL, "row_topk_merge: M=%d k=%d mode=%d", M, k, mode);
   if (S < 1 || S > TOPK_MAX_PARTS || S * k > 64 * TOPK_MAX)

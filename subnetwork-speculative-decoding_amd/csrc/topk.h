@@ -44,6 +44,23 @@ struct TopkPart {
   uint64_t key[TOPK_MAX];  // the chunk's k best, best first
 };
 
+// Records are stored packed for the k of the call: 8 + 8 k bytes each (the maximum, the sum of exp,
+// then the k keys, 8-byte aligned), so a merge reads the bytes it uses (32 B a record at k = 3
+// instead of a 136-byte TopkPart's line). Buffers stay sized for sizeof(TopkPart) records, which
+// covers every k <= TOPK_MAX.
+struct TopkRec {
+  float* mx;
+  float* se;
+  uint64_t* key;
+};
+__device__ __forceinline__ TopkRec topk_rec(void* parts, size_t idx, int k) {
+  char* r = (char*)parts + idx * (size_t)(8 + 8 * k);
+  return TopkRec{(float*)r, (float*)r + 1, (uint64_t*)(r + 8)};
+}
+__device__ __forceinline__ TopkRec topk_rec(const void* parts, size_t idx, int k) {
+  return topk_rec(const_cast<void*>(parts), idx, k);
+}
+
 constexpr int TOPK_MAX_PARTS = 256;  // records per row a merge takes (S * k <= 64 * TOPK_MAX as well)
 
 // Merge of one row's S <= 256 partial records (each the k best keys and the max / sum of exp of a
@@ -53,7 +70,7 @@ constexpr int TOPK_MAX_PARTS = 256;  // records per row a merge takes (S * k <= 
 // of a wave maximum. Lane 0 writes token q (vocab_ids[column] when vocab_ids is set) to tok[q]
 // and, when val is set, its value to val[q]: mode 0 the raw value, mode 1 the log-softmax value
 // (x - M) - log(sum); lse (mode 1, when set) gets M + log(sum).
-__device__ __forceinline__ void topk_merge_row(const TopkPart* __restrict__ p, int S, int k, int mode,
+__device__ __forceinline__ void topk_merge_row(const void* __restrict__ p, int S, int k, int mode,
                                                const int* __restrict__ vocab_ids, int lane, int* tok, float* val,
                                                float* lse_out) {
   // Every load is issued up front from a clamped index (one memory round trip instead of one per
@@ -63,15 +80,15 @@ __device__ __forceinline__ void topk_merge_row(const TopkPart* __restrict__ p, i
   float mx_o[PER], se_o[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
-    const TopkPart& own = p[min(lane + 64 * i, S - 1)];
-    mx_o[i] = own.mx;
-    se_o[i] = own.se;
+    const TopkRec own = topk_rec(p, min(lane + 64 * i, S - 1), k);
+    mx_o[i] = *own.mx;
+    se_o[i] = *own.se;
   }
   uint64_t key[TOPK_MAX];
 #pragma unroll
   for (int j = 0; j < TOPK_MAX; ++j) {
     const int c = min(lane + 64 * j, total - 1);
-    key[j] = p[c / k].key[c % k];
+    key[j] = topk_rec(p, c / k, k).key[c % k];
   }
 #pragma unroll
   for (int j = 0; j < TOPK_MAX; ++j)

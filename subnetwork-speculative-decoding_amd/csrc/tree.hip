@@ -167,7 +167,8 @@ __global__ __launch_bounds__(1024) void tree_level_topk_kernel(SsdTree t, int d,
   tree_level_counts(t, d, n0, F, prev_start);
   tree_level_stage(t, L);
   for (int f = w; f < f_rows; f += 16)
-    topk_merge_row(parts + (size_t)f * S, S, k, 1, vocab_ids, lane, s_tok + f * k, s_lp + f * k, nullptr);
+    topk_merge_row((const char*)parts + (size_t)f * S * (size_t)(8 + 8 * k), S, k, 1, vocab_ids, lane, s_tok + f * k,
+                   s_lp + f * k, nullptr);
   __syncthreads();
   tree_level_body(t, d, s_tok, s_lp, k, width, feed, root_pos, tree_start, past, rows, rows_max, n0, F, prev_start,
                   L);
@@ -341,6 +342,7 @@ SSD_API int ssd_tree_level_topk(const SsdTree* tree, int d, const void* parts, i
                                 int tree_start, int past, const SsdRows* rows, int rows_max, const int32_t* pos_base,
                                 hipStream_t stream) {
   if (!tree || !parts || (feed && !rows)) return set_error(SSD_EINVAL, "tree_level_topk: null pointer");
+  if ((uintptr_t)parts & 7) return set_error(SSD_EINVAL, "tree_level_topk: parts must be 8-byte aligned");
   if (d < 0 || d >= TREE_MAXDEPTH || d + 1 > ROW_MAXD)
     return set_error(SSD_ERANGE, "tree_level_topk: depth %d too deep", d);
   if (F_max < 1 || k < 1 || k > TOPK_MAX || F_max * k > TREE_CAP)

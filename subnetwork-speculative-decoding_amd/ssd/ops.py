@@ -337,7 +337,7 @@ def row_topk_merge(parts, m, s, k, mode, vocab_ids, out_tok, out_val=None, out_l
               _p(out_val), _p(out_lse), stream())
 
 
-TOPK_PART_BYTES = 136  # TopkPart: max, sum of exp, 16 keys
+TOPK_PART_BYTES = 136  # room per record: max, sum of exp, up to 16 keys (stored packed for the call's k)
 
 
 def gemm_topk_parts(n: int) -> int:

@@ -17,7 +17,6 @@ from oracle import kernels as ok
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
-PART = 136  # bytes per record
 
 
 def bf(t):
@@ -79,10 +78,13 @@ def test_gemm_topk_records_merge_like_the_chunk_pass(seed, m, n, kd, k, norm, ti
         else:
             diff = (yt.float() - y.float()).abs()
             assert (diff <= 2e-2 * y.float().abs() + 1e-3).all()
-        # the records do not depend on whether the logits are stored
+        # the records do not depend on whether the logits are stored (the records are packed for k:
+        # m * S records of 8 + 8 k bytes, every byte written; the rest of the buffer is untouched)
+        used = m * S * (8 + 8 * k)
         bare = torch.full_like(parts, 7)
         ops.gemm_topk(x, m, wp, n, kd, k, mode, bare, norm_eps=eps)
-        assert torch.equal(bare, parts)
+        assert torch.equal(bare[:used], parts[:used])
+        assert (bare[used:] == 7).all()
         # merged records == the chunk pass over the logits the fused launch computed
         tok = torch.zeros(m * k, dtype=torch.int32, device=DEV)
         val = torch.zeros(m * k, dtype=torch.float32, device=DEV)
@@ -109,10 +111,11 @@ def test_gemm_topk_records_merge_like_the_chunk_pass(seed, m, n, kd, k, norm, ti
             want = sorted(ties)[:k]
             assert tok.view(m, k)[0, :len(want)].tolist() == want
         # a row's records are the same computed alone (batch invariance of the head)
+        row_bytes = S * (8 + 8 * k)  # records are packed for the call's k (max, sum of exp, k keys)
         for r in sorted({0, m - 1}):
             one = torch.zeros(ops.gemm_topk_bytes(1, n), dtype=torch.uint8, device=DEV)
             ops.gemm_topk(x[r:r + 1].contiguous(), 1, wp, n, kd, k, mode, one, norm_eps=eps)
-            assert torch.equal(one, parts[r * S * PART:(r + 1) * S * PART]), f"row {r}"
+            assert torch.equal(one[:row_bytes], parts[r * row_bytes:(r + 1) * row_bytes]), f"row {r}"
 
 
 def test_gemm_topk_argument_errors():
@@ -128,7 +131,7 @@ def test_gemm_topk_argument_errors():
         ops.gemm_topk(x, 2, wp, 4096, 64, 2, 1, parts[:100])  # records do not fit
     tok = torch.zeros(2 * 16, dtype=torch.int32, device=DEV)
     with pytest.raises(ValueError):  # 256 records x 16 keys exceed the merge's 1024 candidates
-        ops.row_topk_merge(torch.zeros(2 * 256 * PART, dtype=torch.uint8, device=DEV), 2, 256, 16, 1, None, tok)
+        ops.row_topk_merge(torch.zeros(2 * 256 * ops.TOPK_PART_BYTES, dtype=torch.uint8, device=DEV), 2, 256, 16, 1, None, tok)
 
 
 @pytest.mark.parametrize("seed,V,mapped", [(0, 128256, False), (1, 32768, True)])
